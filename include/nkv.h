@@ -1,0 +1,226 @@
+/*
+ * nkv.h -- C ABI of libnkv_amd.so, the MI355X (gfx950) attention hot path of
+ * nano-kvllm: paged K/V store, paged decode attention, varlen causal prefill
+ * over the paged cache, and the window-based periodic KV-compression step.
+ *
+ * Conventions (every entry point):
+ *   - All tensor pointers are DEVICE pointers. Element types are fixed per
+ *     argument: bf16 for q/k/v/cache/out, int32 for metadata, fp32 for scores.
+ *   - Strides are in ELEMENTS of the pointed-to type.
+ *   - `stream` is a hipStream_t (NULL = the null stream). Every call is
+ *     asynchronous on that stream, performs no host<->device synchronisation
+ *     and allocates no memory; callers pass workspaces explicitly.
+ *   - Return value: NKV_OK (0) or a negative NKV_E* code; nkv_last_error()
+ *     then holds a human-readable message (thread-local).
+ *   - K/V cache layout is the reference's [num_blocks, block_size, Hk, D]
+ *     with the token row contiguous (stride(1) == Hk*D), i.e. slot s of the
+ *     flattened cache holds Hk*D elements starting at s*Hk*D.
+ *     (nanokvllm/engine/model_runner.py:145, nanokvllm/layers/attention.py:38)
+ */
+#ifndef NKV_H
+#define NKV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NKV_OK 0
+#define NKV_EINVAL (-1)  /* bad argument: shape, stride, alignment, null pointer */
+#define NKV_ELAUNCH (-2) /* HIP launch / runtime error */
+#define NKV_EWORKSPACE (-3) /* workspace missing or too small */
+#define NKV_EUNSUPPORTED (-4) /* valid but unsupported configuration */
+
+/* Thread-local text of the last error raised on this thread ("" if none). */
+const char* nkv_last_error(void);
+
+/* Library version string. */
+const char* nkv_version(void);
+
+/*
+ * store_kvcache: for every token i < n_tokens with slot_mapping[i] != -1,
+ * copy key[i] and value[i] (n_kv_heads*head_dim contiguous elements each)
+ * into row slot_mapping[i] of k_cache / v_cache. Rows with slot -1 are
+ * skipped; slots outside [0, n_slots) are skipped as well (the reference
+ * would write out of bounds there).
+ * key/value rows may be strided views (e.g. the v part of a fused qkv
+ * projection): element (i, h, d) lives at ptr[i*row_stride + h*head_dim + d].
+ * Replaces: store_kvcache / store_kvcache_kernel,
+ *           nanokvllm/layers/attention.py:10-40
+ */
+int nkv_store_kvcache(const void* key, int64_t key_row_stride,
+                      const void* value, int64_t value_row_stride,
+                      void* k_cache, void* v_cache,
+                      const int32_t* slot_mapping, int64_t n_tokens,
+                      int32_t n_kv_heads, int32_t head_dim, int64_t n_slots,
+                      void* stream);
+
+/*
+ * Paged decode attention (one query token per sequence, GQA, causal with the
+ * new token already stored): for b < batch, query head h,
+ *   out[b,h] = sum_{t<ctx_b} softmax_t(scale * q[b,h].K[b,t,h/g]) V[b,t,h/g]
+ * with K[b,t] = k_cache row (block_tables[b, t/block_size]*block_size
+ * + t%block_size). Sequences with context_lens[b] <= 0 produce zeros.
+ * Split-K: one work unit per 256 tokens of a sequence and KV head, then a
+ * combine pass. workspace must hold nkv_paged_decode_workspace_bytes(...).
+ * q[b,h,d] at q[b*q_row_stride + h*head_dim + d]; out likewise with
+ * out_row_stride. head_dim must be 128; n_q_heads/n_kv_heads in {1,2,4,8,16}.
+ * Replaces: flash_attn_with_kvcache(q.unsqueeze(1), k_cache, v_cache,
+ *           cache_seqlens=context_lens, block_table=block_tables,
+ *           softmax_scale=scale, causal=True),
+ *           nanokvllm/layers/attention.py:104-107
+ */
+size_t nkv_paged_decode_workspace_bytes(int32_t batch, int32_t n_q_heads,
+                                        int32_t head_dim, int32_t max_blocks_per_seq,
+                                        int32_t block_size);
+
+int nkv_paged_decode(const void* q, int64_t q_row_stride,
+                     const void* k_cache, const void* v_cache,
+                     const int32_t* block_tables, int64_t bt_row_stride,
+                     const int32_t* context_lens, int32_t batch,
+                     int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                     int32_t block_size, int32_t max_blocks_per_seq,
+                     int64_t n_blocks, float scale,
+                     void* out, int64_t out_row_stride,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* The two stages nkv_paged_decode launches, exported so a caller can time or
+ * schedule them separately. Same arguments as nkv_paged_decode.
+ * Replaces: the same flash_attn_with_kvcache call (attention.py:104-107). */
+int nkv_paged_decode_split(const void* q, int64_t q_row_stride,
+                           const void* k_cache, const void* v_cache,
+                           const int32_t* block_tables, int64_t bt_row_stride,
+                           const int32_t* context_lens, int32_t batch,
+                           int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                           int32_t block_size, int32_t max_blocks_per_seq,
+                           int64_t n_blocks, float scale,
+                           void* workspace, size_t workspace_bytes, void* stream);
+int nkv_paged_decode_combine(const int32_t* context_lens, int32_t batch,
+                             int32_t n_q_heads, int32_t head_dim,
+                             int32_t block_size, int32_t max_blocks_per_seq,
+                             void* out, int64_t out_row_stride,
+                             const void* workspace, size_t workspace_bytes,
+                             void* stream);
+
+/*
+ * Varlen causal prefill over K/V rows (flash-attn bottom-right causal):
+ * sequence i has Lq = cu_seqlens_q[i+1]-cu_seqlens_q[i] query rows and
+ * Lk = cu_seqlens_k[i+1]-cu_seqlens_k[i] keys; query j attends keys
+ * 0 .. Lk-Lq+j. If block_tables != NULL, key t of sequence i is k_cache row
+ * block_tables[i, t/block_size]*block_size + t%block_size (paged); otherwise
+ * it is row cu_seqlens_k[i]+t of k_cache/v_cache (contiguous [sum Lk, Hk, D]
+ * with row stride kv_row_stride). q/out are [sum Lq, Hq, D] with row strides.
+ * head_dim must be 128.
+ * Replaces: flash_attn_varlen_func(q, k, v, max_seqlen_q, cu_seqlens_q,
+ *           max_seqlen_k, cu_seqlens_k, softmax_scale, causal=True,
+ *           block_table), nanokvllm/layers/attention.py:96-102
+ */
+int nkv_prefill_varlen(const void* q, int64_t q_row_stride,
+                       const void* k_cache, const void* v_cache, int64_t kv_row_stride,
+                       const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                       const int32_t* block_tables, int64_t bt_row_stride,
+                       int32_t n_seqs, int32_t max_seqlen_q,
+                       int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                       int32_t block_size, int64_t n_rows, float scale,
+                       void* out, int64_t out_row_stride, void* stream);
+
+/* Aggregation of key importance over query heads (compression scoring). */
+#define NKV_AGG_ALL 0   /* sum over all Hq heads -> one kept set per sequence
+                           (nanokvllm/layers/CompressMethod.py:41-42) */
+#define NKV_AGG_GROUP 1 /* sum over the g query heads of each KV head -> one
+                           kept set per (sequence, KV head) */
+
+/*
+ * Compression scoring (SnapKV with window = 1): for selected sequence j
+ * (batch row seq_idx[j]) the window is its last `window_blocks` FULL blocks,
+ * located from base_context_lens[seq_idx[j]] and block_tables. Keys
+ * t < W*B-1 of the window are scored with the sequence's current query:
+ *   imp[j, s, t] = sum_{h in set s} softmax_t(scale * q[h].K[t, h/g])
+ * with key 0 masked to -inf (attention sink) before the softmax.
+ * importance_out: fp32 [m, n_sets, W*B-1], n_sets = 1 (ALL) or n_kv_heads
+ * (GROUP). workspace: nkv_compress_workspace_bytes(...).
+ * If block_tables == NULL the keys come from a contiguous K tensor
+ * [m, Hk, L, D] (k_cache points at it, L = window_blocks*block_size), as in
+ * SnapKV(Q, K, V, ...) called directly; seq_idx and base_context_lens are
+ * then ignored.
+ * Replaces: get_tail_window_and_tail_slots + gather_kv_by_slots + the scoring
+ *           half of SnapKV, nanokvllm/layers/compress_utils.py:9-97,155-173,
+ *           nanokvllm/layers/CompressMethod.py:4-42
+ */
+size_t nkv_compress_workspace_bytes(int32_t m, int32_t n_q_heads,
+                                    int32_t window_blocks, int32_t block_size);
+
+int nkv_compress_score(const void* q, int64_t q_row_stride,
+                       const void* k_cache, const int32_t* block_tables,
+                       int64_t bt_row_stride, int32_t max_blocks_per_seq,
+                       const int32_t* base_context_lens,
+                       const int32_t* seq_idx, int32_t m,
+                       int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                       int32_t block_size, int32_t window_blocks, int64_t n_blocks,
+                       float scale, int32_t agg_mode, float* importance_out,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Top-k selection on importance [m*n_sets, n_cand] (fp32): keep the num_keep
+ * largest (ties -> lower index first), sorted ascending, and emit
+ *   keep_idx[r] = [0, kept..., n_cand]  (1 + num_keep + 1 int32 entries)
+ * i.e. the reference's [bos, sorted top-k, last window token].
+ * Requires num_keep < n_cand <= 4096.
+ * Replaces: the topk/sort/cat tail of SnapKV, CompressMethod.py:44-57
+ */
+int nkv_compress_topk(const float* importance, int32_t n_rows, int32_t n_cand,
+                      int32_t num_keep, int32_t* keep_idx, void* stream);
+
+/*
+ * In-place compaction of the window of each selected sequence, K and V:
+ * kept window token keep_idx[j,s,i] moves to window position i
+ * (i < keep_tokens); the tail partial block (tail = len % B tokens, block
+ * block_tables[seq, len/B]) moves right after the last kept slot. Reads of a
+ * (sequence, KV head) complete before any of its writes, so overlapping
+ * sources and destinations behave like the reference's two-phase
+ * index_select().clone() / index_copy_. Then
+ *   context_lens[seq_idx[j]] = len - W*B + keep_tokens.
+ * keep_idx: int32 [m, n_sets, keep_tokens] with n_sets 1 (shared by all KV
+ * heads) or n_kv_heads. Requires keep_tokens + block_size - 1 <= 1024.
+ * Replaces: MyCompressCompact's compaction and context_lens update,
+ *           nanokvllm/layers/compress_utils.py:186-263
+ */
+int nkv_compress_compact(void* k_cache, void* v_cache,
+                         const int32_t* block_tables, int64_t bt_row_stride,
+                         int32_t max_blocks_per_seq,
+                         const int32_t* base_context_lens, int32_t* context_lens,
+                         const int32_t* seq_idx, int32_t m,
+                         const int32_t* keep_idx, int32_t n_sets, int32_t keep_tokens,
+                         int32_t n_kv_heads, int32_t head_dim, int32_t block_size,
+                         int32_t window_blocks, int64_t n_blocks, void* stream);
+
+/*
+ * Last-layer bookkeeping of a compression step, after the compaction of every
+ * layer: for selected sequence j (new_len = len - W*B + keep_tokens,
+ * keep_blocks = ceil(new_len / B)) write
+ *   events[j, :] = [seq_idx[j], new_len, keep_blocks, n_freed, freed ids...,
+ *                   -1 padding]   (int32, row length 4 + max_blocks_per_seq)
+ * where the freed ids are block_tables[seq, keep_blocks:] entries >= 0; then,
+ * if rewrite_tables != 0, set those block_tables entries to -1 and, if
+ * slot_mapping != NULL, set slot_mapping[seq] to the slot of token position
+ * new_len (-1 if that position starts a new block).
+ * Replaces: the event construction of MyCompressCompact
+ *           (compress_utils.py:266-288) and the table/slot effect of
+ *           Scheduler.postprocess + BlockManager.truncate_blocks
+ *           (nanokvllm/engine/scheduler.py:104-125,
+ *            nanokvllm/engine/block_manager.py:117-138)
+ */
+int nkv_compress_finalize(int32_t* block_tables, int64_t bt_row_stride,
+                          int32_t max_blocks_per_seq,
+                          const int32_t* base_context_lens, const int32_t* seq_idx,
+                          int32_t m, int32_t keep_tokens, int32_t block_size,
+                          int32_t window_blocks, int32_t rewrite_tables,
+                          int32_t* slot_mapping, int32_t* events, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NKV_H */

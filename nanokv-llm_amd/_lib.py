@@ -1,0 +1,88 @@
+"""ctypes binding of libnkv_amd.so (declared in include/nkv.h).
+
+The library is the only compute path of this package: if it is missing the
+loader raises, there is no CPU or PyTorch fallback. torch is imported first
+so that the HIP runtime torch ships (SONAME libamdhip64.so.7) is the one the
+library binds to; the streams handed over are torch's own.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import torch  # noqa: F401  (must be loaded before the HIP library)
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG_DIR, "libnkv_amd.so")
+
+NKV_OK = 0
+NKV_AGG_ALL = 0
+NKV_AGG_GROUP = 1
+
+_p = C.c_void_p
+_i32 = C.c_int32
+_i64 = C.c_int64
+_f32 = C.c_float
+_sz = C.c_size_t
+
+# name -> (restype, argtypes); mirrors include/nkv.h
+SIGNATURES = {
+    "nkv_last_error": (C.c_char_p, []),
+    "nkv_version": (C.c_char_p, []),
+    "nkv_store_kvcache": (C.c_int, [_p, _i64, _p, _i64, _p, _p, _p, _i64, _i32, _i32, _i64, _p]),
+    "nkv_paged_decode_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
+    "nkv_paged_decode": (C.c_int, [_p, _i64, _p, _p, _p, _i64, _p, _i32, _i32, _i32, _i32, _i32,
+                                   _i32, _i64, _f32, _p, _i64, _p, _sz, _p]),
+    "nkv_paged_decode_split": (C.c_int, [_p, _i64, _p, _p, _p, _i64, _p, _i32, _i32, _i32, _i32,
+                                         _i32, _i32, _i64, _f32, _p, _sz, _p]),
+    "nkv_paged_decode_combine": (C.c_int, [_p, _i32, _i32, _i32, _i32, _i32, _p, _i64, _p, _sz,
+                                           _p]),
+    "nkv_prefill_varlen": (C.c_int, [_p, _i64, _p, _p, _i64, _p, _p, _p, _i64, _i32, _i32, _i32,
+                                     _i32, _i32, _i32, _i64, _f32, _p, _i64, _p]),
+    "nkv_compress_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32]),
+    "nkv_compress_score": (C.c_int, [_p, _i64, _p, _p, _i64, _i32, _p, _p, _i32, _i32, _i32, _i32,
+                                     _i32, _i32, _i64, _f32, _i32, _p, _p, _sz, _p]),
+    "nkv_compress_topk": (C.c_int, [_p, _i32, _i32, _i32, _p, _p]),
+    "nkv_compress_compact": (C.c_int, [_p, _p, _p, _i64, _i32, _p, _p, _p, _i32, _p, _i32, _i32,
+                                       _i32, _i32, _i32, _i32, _i64, _p]),
+    "nkv_compress_finalize": (C.c_int, [_p, _i64, _i32, _p, _p, _i32, _i32, _i32, _i32, _i32, _p,
+                                        _p, _p]),
+}
+
+_LIB = None
+
+
+class NkvError(RuntimeError):
+    pass
+
+
+def lib() -> C.CDLL:
+    """Load libnkv_amd.so once; raise if it has not been built."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise NkvError(
+                f"{LIB_PATH} is missing: build it with `python __graft_entry__.py build` "
+                "(or nanokv-llm_amd/build.py); there is no fallback path")
+        handle = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _LIB = handle
+    return _LIB
+
+
+def check(rc: int, what: str) -> None:
+    if rc != NKV_OK:
+        msg = lib().nkv_last_error().decode(errors="replace")
+        raise NkvError(f"{what} failed (code {rc}): {msg}")
+
+
+def stream_of(t: torch.Tensor) -> int:
+    """HIP stream handle of torch's current stream on t's device."""
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()

@@ -1,0 +1,500 @@
+// Window-based periodic KV compression step (SnapKV scoring, wave-level top-k
+// selection, in-place compaction, last-layer bookkeeping).
+//
+// Reference: MyCompressCompact + helpers, nanokvllm/layers/compress_utils.py:
+// 9-290, and SnapKV, nanokvllm/layers/CompressMethod.py:4-57.
+//
+// MI355X design. The step is HBM-bound (read the K window, move the kept K/V
+// rows) and tiny in flops, so it is organised around bytes and launches:
+//  * score: one workgroup per (selected sequence, KV head, 256-key chunk of
+//    the window). K is read IN PLACE from the paged cache (the reference
+//    first gathers K and V of the window into new tensors) straight into the
+//    MFMA B layout; q K^T runs on v_mfma_f32_16x16x32_bf16 exactly as in
+//    paged decode. Scaled scores (log2 domain) go to a small fp32 workspace.
+//  * importance: one workgroup per kept set (sequence, or sequence x KV
+//    head): per-head softmax statistics by wavefront reductions, then
+//    importance[t] = sum_h softmax_h[t] over the set's query heads.
+//  * top-k: one wavefront per kept set selects the num_keep largest
+//    importances with a 32-step bitwise radix select on order-preserving
+//    integer keys held in registers (ballot-free counts via shuffles), ties
+//    broken by lower index, and writes the kept positions in ascending order
+//    with a wave prefix sum -- no sort.
+//  * compact: one workgroup per (sequence, KV head, K|V, 128-byte half of the
+//    head row). Every source row of the unit is loaded into registers before
+//    any destination row is written (s_waitcnt 0 + barrier), which gives the
+//    reference's two-phase index_select().clone() / index_copy_ semantics
+//    without a staging buffer, at one read + one write per moved byte.
+//  * finalize (last layer): events, freed blocks, block-table and slot rewrite.
+#include "nkv_common.h"
+
+namespace nkv {
+
+constexpr int kCD = 128;      // head_dim
+constexpr int kChunk = 256;   // keys per scoring workgroup
+
+// ------------------------------------------------------------------ score
+// scores[j][h][t] for t < Lw (window tokens); t == 0 and t == Lw-1 are -inf
+// (sink mask; the last window token is not scored).
+template <int G>
+__global__ __launch_bounds__(256) void compress_score_kernel(
+    const bf16_t* __restrict__ q, int64_t q_row_stride, const bf16_t* __restrict__ k,
+    const int32_t* __restrict__ block_tables, int64_t bt_row_stride, int32_t max_blocks,
+    const int32_t* __restrict__ base_context_lens, const int32_t* __restrict__ seq_idx,
+    int32_t Hk, int32_t block_size, int32_t window_blocks, int64_t n_blocks, float scale_log2,
+    float* __restrict__ scores) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int Lw = window_blocks * block_size;
+  const int n_chunks = Lw / kChunk;
+  const int c = blockIdx.x % n_chunks;
+  const int kvh = (blockIdx.x / n_chunks) % Hk;
+  const int j = blockIdx.x / (n_chunks * Hk);
+  const int Hq = Hk * G;
+  const int t0 = c * kChunk;
+
+  int64_t base;            // element offset of key t0 (this KV head)
+  int64_t tok_stride;      // elements between consecutive keys
+  int64_t qrow;
+  bool valid = true;
+  if (block_tables) {
+    const int seq = seq_idx[j];
+    const int len = base_context_lens[seq];
+    const int full = len / block_size;
+    const int wblk = full - window_blocks + t0 / block_size;
+    int64_t pb = -1;
+    if (full >= window_blocks && full <= max_blocks)
+      pb = block_tables[(int64_t)seq * bt_row_stride + wblk];
+    valid = pb >= 0 && pb < n_blocks;
+    base = ((pb * block_size + t0 % block_size) * Hk + kvh) * (int64_t)kCD;
+    tok_stride = (int64_t)Hk * kCD;
+    qrow = seq;
+  } else {  // contiguous K [m, Hk, Lw, D]
+    base = (((int64_t)j * Hk + kvh) * Lw + t0) * kCD;
+    tok_stride = kCD;
+    qrow = j;
+  }
+  float* srow = scores + ((int64_t)j * Hq + (int64_t)kvh * G) * Lw + t0;
+  if (!valid) {
+    for (int i = threadIdx.x; i < G * kChunk; i += blockDim.x)
+      srow[(int64_t)(i / kChunk) * Lw + i % kChunk] = -INFINITY;
+    return;
+  }
+  const uint4 zero4 = make_uint4(0, 0, 0, 0);
+  uint4 kreg[4][4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int tw = wave * 64 + g * 16 + (lane & 15);
+    const bf16_t* kp = k + base + tw * tok_stride + (lane >> 4) * 8;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) kreg[g][ks] = *reinterpret_cast<const uint4*>(kp + ks * 32);
+  }
+  uint4 qreg[4];
+  {
+    const int hr = lane & 15;
+    const bf16_t* qp = q + qrow * q_row_stride + (int64_t)(kvh * G + hr) * kCD + (lane >> 4) * 8;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      qreg[ks] = (hr < G) ? *reinterpret_cast<const uint4*>(qp + ks * 32) : zero4;
+  }
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(qreg[ks]), as_bf16x8(kreg[g][ks]),
+                                                     acc, 0, 0, 0);
+    const int tw = wave * 64 + g * 16 + (lane & 15);
+    const int t = t0 + tw;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int h = (lane >> 4) * 4 + r;
+      if (h < G)
+        srow[(int64_t)h * Lw + tw] = (t == 0 || t == Lw - 1) ? -INFINITY : acc[r] * scale_log2;
+    }
+  }
+}
+
+// -------------------------------------------------------------- importance
+// importance[r][t] (t < Lw-1) for kept set r = j*n_sets + s, heads of the set
+// are [s*hps, (s+1)*hps) with hps = Hq / n_sets.
+__global__ __launch_bounds__(256) void compress_importance_kernel(
+    const float* __restrict__ scores, int32_t Hq, int32_t n_sets, int32_t Lw,
+    float* __restrict__ importance) {
+  extern __shared__ float stats[];  // [hps][2]: max, 1/sum
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int r = blockIdx.x;
+  const int j = r / n_sets, s = r % n_sets;
+  const int hps = Hq / n_sets;
+  const float* sbase = scores + ((int64_t)j * Hq + (int64_t)s * hps) * Lw;
+  for (int h = wave; h < hps; h += 4) {
+    const float* sr = sbase + (int64_t)h * Lw;
+    float mx = -INFINITY;
+    for (int t = lane; t < Lw; t += 64) mx = fmaxf(mx, sr[t]);
+    mx = wave_max(mx);
+    float sum = 0.f;
+    if (mx != -INFINITY)
+      for (int t = lane; t < Lw; t += 64) sum += fast_exp2(sr[t] - mx);
+    sum = wave_sum(sum);
+    if (lane == 0) {
+      stats[2 * h] = mx;
+      stats[2 * h + 1] = sum > 0.f ? 1.f / sum : 0.f;
+    }
+  }
+  __syncthreads();
+  const int n_cand = Lw - 1;
+  float* irow = importance + (int64_t)r * n_cand;
+  for (int t = threadIdx.x; t < n_cand; t += blockDim.x) {
+    float acc = 0.f;
+    for (int h = 0; h < hps; ++h) {
+      const float mx = stats[2 * h];
+      const float sv = sbase[(int64_t)h * Lw + t];
+      if (mx != -INFINITY && sv != -INFINITY) acc += fast_exp2(sv - mx) * stats[2 * h + 1];
+    }
+    irow[t] = acc;
+  }
+}
+
+// ------------------------------------------------------------------- top-k
+__device__ __forceinline__ uint32_t order_key(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ int wave_excl_scan_i(int v) {
+  const int lane = threadIdx.x & 63;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  return x - v;
+}
+
+// One wavefront per row; lane l holds candidates [l*ITEMS, (l+1)*ITEMS).
+template <int ITEMS>
+__global__ __launch_bounds__(64) void compress_topk_kernel(
+    const float* __restrict__ importance, int32_t n_cand, int32_t num_keep,
+    int32_t* __restrict__ keep_idx) {
+  const int lane = threadIdx.x;
+  const int r = blockIdx.x;
+  const float* irow = importance + (int64_t)r * n_cand;
+  uint32_t key[ITEMS];
+#pragma unroll
+  for (int e = 0; e < ITEMS; ++e) {
+    const int i = lane * ITEMS + e;
+    key[e] = (i < n_cand) ? order_key(irow[i]) : 0u;  // padding sorts last
+  }
+  // k-th largest key by bitwise radix select
+  uint32_t T = 0;
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t cand = T | (1u << bit);
+    int cnt = 0;
+#pragma unroll
+    for (int e = 0; e < ITEMS; ++e) cnt += key[e] >= cand;
+    if (wave_sum_i(cnt) >= num_keep) T = cand;
+  }
+  int gt = 0, eq = 0;
+#pragma unroll
+  for (int e = 0; e < ITEMS; ++e) {
+    gt += key[e] > T;
+    eq += key[e] == T;
+  }
+  const int need = num_keep - wave_sum_i(gt);  // ties at T taken lowest index first
+  int eq_rank = wave_excl_scan_i(eq);
+  uint64_t selmask = 0;
+#pragma unroll
+  for (int e = 0; e < ITEMS; ++e) {
+    const int i = lane * ITEMS + e;
+    bool sel = key[e] > T;
+    if (key[e] == T) {
+      sel = eq_rank < need;
+      ++eq_rank;
+    }
+    if (i >= n_cand) sel = false;
+    selmask |= (uint64_t)sel << e;
+  }
+  int pos = wave_excl_scan_i(__builtin_popcountll(selmask));
+  int32_t* out = keep_idx + (int64_t)r * (num_keep + 2);
+#pragma unroll
+  for (int e = 0; e < ITEMS; ++e)
+    if (selmask & (1ull << e)) out[1 + pos++] = lane * ITEMS + e;
+  if (lane == 0) {
+    out[0] = 0;
+    out[num_keep + 1] = n_cand;
+  }
+}
+
+// ----------------------------------------------------------------- compact
+// Unit = (selected j, KV head, K|V, half row). Rows i < keep_tokens move from
+// window position keep_idx[i] to window position i; rows keep_tokens + u
+// (u < tail) move from the tail block offset u to slot(window pos keep-1)+1+u.
+template <int ROUNDS>
+__global__ __launch_bounds__(256) void compress_compact_kernel(
+    bf16_t* __restrict__ k_cache, bf16_t* __restrict__ v_cache,
+    const int32_t* __restrict__ block_tables, int64_t bt_row_stride, int32_t max_blocks,
+    const int32_t* __restrict__ base_context_lens, int32_t* __restrict__ context_lens,
+    const int32_t* __restrict__ seq_idx, const int32_t* __restrict__ keep_idx, int32_t n_sets,
+    int32_t keep_tokens, int32_t Hk, int32_t block_size, int32_t window_blocks,
+    int64_t n_blocks) {
+  const int half = blockIdx.x & 1;
+  const int is_v = (blockIdx.x >> 1) & 1;
+  const int kvh = (blockIdx.x >> 2) % Hk;
+  const int j = (blockIdx.x >> 2) / Hk;
+  const int seq = seq_idx[j];
+  const int len = base_context_lens[seq];
+  const int B = block_size;
+  const int full = len / B;
+  const int tail = len - full * B;
+  // not compressible, or inconsistent with the table width: leave untouched
+  if (full < window_blocks || full > max_blocks || (tail > 0 && full >= max_blocks)) return;
+  const int32_t* bt = block_tables + (int64_t)seq * bt_row_stride;
+  const int wb0 = full - window_blocks;
+  const int64_t n_slots = n_blocks * B;
+  const int32_t* kidx = keep_idx + ((int64_t)j * n_sets + (n_sets > 1 ? kvh : 0)) * keep_tokens;
+  const int Lw = window_blocks * B;
+
+  auto window_slot = [&](int p) -> int64_t {
+    const int64_t pb = bt[wb0 + p / B];
+    return (pb >= 0 && pb < n_blocks) ? pb * B + p % B : -1;
+  };
+  const int64_t tail_pb = tail > 0 ? (int64_t)bt[full] : -1;
+  const int64_t last_dst = window_slot(keep_tokens - 1);
+  const int nrows = keep_tokens + tail;
+
+  bf16_t* cache = is_v ? v_cache : k_cache;
+  const int64_t row = (int64_t)Hk * kCD;
+  const int64_t col = (int64_t)kvh * kCD + half * 64 + (threadIdx.x & 7) * 8;
+  const int rsub = threadIdx.x >> 3;  // 0..31
+
+  uint4 reg[ROUNDS];
+  int64_t dst[ROUNDS];
+#pragma unroll
+  for (int rr = 0; rr < ROUNDS; ++rr) {
+    const int i = rr * 32 + rsub;
+    int64_t src = -1, d = -1;
+    if (i < keep_tokens) {
+      const int p = kidx[i];
+      if (p >= 0 && p < Lw) src = window_slot(p);
+      d = window_slot(i);
+    } else if (i < nrows) {
+      const int u = i - keep_tokens;
+      if (tail_pb >= 0 && tail_pb < n_blocks) src = tail_pb * B + u;
+      if (last_dst >= 0) d = last_dst + 1 + u;
+    }
+    if (src < 0 || src >= n_slots || d < 0 || d >= n_slots) d = -1;
+    dst[rr] = d;
+    reg[rr] = (d >= 0) ? *reinterpret_cast<const uint4*>(cache + src * row + col)
+                       : make_uint4(0, 0, 0, 0);
+  }
+  // all reads of the unit land before any write (two-phase semantics)
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+#pragma unroll
+  for (int rr = 0; rr < ROUNDS; ++rr)
+    if (dst[rr] >= 0) *reinterpret_cast<uint4*>(cache + dst[rr] * row + col) = reg[rr];
+
+  if (blockIdx.x % (4 * Hk) == 0 && threadIdx.x == 0)
+    context_lens[seq] = len - Lw + keep_tokens;
+}
+
+// ---------------------------------------------------------------- finalize
+__global__ __launch_bounds__(64) void compress_finalize_kernel(
+    int32_t* __restrict__ block_tables, int64_t bt_row_stride, int32_t max_blocks,
+    const int32_t* __restrict__ base_context_lens, const int32_t* __restrict__ seq_idx,
+    int32_t m, int32_t keep_tokens, int32_t block_size, int32_t window_blocks,
+    int32_t rewrite_tables, int32_t* __restrict__ slot_mapping, int32_t* __restrict__ events) {
+  const int B = block_size;
+  const int ev_len = 4 + max_blocks;
+  for (int j = threadIdx.x; j < m; j += blockDim.x) {
+    const int seq = seq_idx[j];
+    const int len = base_context_lens[seq];
+    int32_t* ev = events + (int64_t)j * ev_len;
+    int32_t* bt = block_tables + (int64_t)seq * bt_row_stride;
+    const int full = len / B, tail = len - (len / B) * B;
+    // same skip rule as the compaction: not compressible -> report unchanged
+    if (full < window_blocks || full > max_blocks || (tail > 0 && full >= max_blocks)) {
+      ev[0] = seq; ev[1] = len; ev[2] = (len + B - 1) / B; ev[3] = 0;
+      for (int i = 0; i < max_blocks; ++i) ev[4 + i] = -1;
+      continue;
+    }
+    const int new_len = len - window_blocks * B + keep_tokens;
+    const int keep_blocks = (new_len + B - 1) / B;
+    int n = 0;
+    for (int i = keep_blocks; i < max_blocks; ++i) {
+      const int id = bt[i];
+      if (id >= 0) ev[4 + n++] = id;
+    }
+    for (int i = n; i < max_blocks; ++i) ev[4 + i] = -1;
+    ev[0] = seq; ev[1] = new_len; ev[2] = keep_blocks; ev[3] = n;
+    if (rewrite_tables)
+      for (int i = keep_blocks; i < max_blocks; ++i) bt[i] = -1;
+    if (slot_mapping) {
+      const int blk = new_len / B, off = new_len % B;
+      slot_mapping[seq] = (off == 0 || blk >= max_blocks || bt[blk] < 0) ? -1 : bt[blk] * B + off;
+    }
+  }
+}
+
+}  // namespace nkv
+
+// ============================================================= C ABI
+using namespace nkv;
+
+extern "C" size_t nkv_compress_workspace_bytes(int32_t m, int32_t n_q_heads,
+                                               int32_t window_blocks, int32_t block_size) {
+  if (m <= 0 || n_q_heads <= 0 || window_blocks <= 0 || block_size <= 0) return 0;
+  return (size_t)m * n_q_heads * window_blocks * block_size * sizeof(float);
+}
+
+extern "C" int nkv_compress_score(const void* q, int64_t q_row_stride, const void* k_cache,
+                                  const int32_t* block_tables, int64_t bt_row_stride,
+                                  int32_t max_blocks_per_seq,
+                                  const int32_t* base_context_lens, const int32_t* seq_idx,
+                                  int32_t m, int32_t n_q_heads, int32_t n_kv_heads,
+                                  int32_t head_dim, int32_t block_size, int32_t window_blocks,
+                                  int64_t n_blocks, float scale, int32_t agg_mode,
+                                  float* importance_out, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  clear_error();
+  NKV_REQUIRE(m >= 0 && n_q_heads > 0 && n_kv_heads > 0 && window_blocks > 0 && block_size > 0,
+              NKV_EINVAL, "compress_score: bad sizes");
+  if (m == 0) return NKV_OK;
+  NKV_REQUIRE(head_dim == kCD, NKV_EUNSUPPORTED, "compress_score: head_dim must be 128");
+  NKV_REQUIRE(n_q_heads % n_kv_heads == 0, NKV_EINVAL, "compress_score: Hq %% Hk != 0");
+  const int g = n_q_heads / n_kv_heads;
+  NKV_REQUIRE(g == 1 || g == 2 || g == 4 || g == 8 || g == 16, NKV_EUNSUPPORTED,
+              "compress_score: GQA group %d not in {1,2,4,8,16}", g);
+  NKV_REQUIRE(block_size % kChunk == 0, NKV_EUNSUPPORTED,
+              "compress_score: block_size must be a multiple of 256");
+  NKV_REQUIRE(agg_mode == NKV_AGG_ALL || agg_mode == NKV_AGG_GROUP, NKV_EINVAL,
+              "compress_score: bad agg_mode %d", agg_mode);
+  NKV_REQUIRE(q && k_cache && importance_out, NKV_EINVAL, "compress_score: null pointer");
+  NKV_REQUIRE(!block_tables || (seq_idx && base_context_lens && max_blocks_per_seq > 0 &&
+                                 bt_row_stride >= max_blocks_per_seq),
+              NKV_EINVAL, "compress_score: paged mode needs seq_idx, base_context_lens and a "
+              "block table width");
+  NKV_REQUIRE(aligned16(q) && aligned16(k_cache) && q_row_stride % 8 == 0, NKV_EINVAL,
+              "compress_score: q/k must be 16-byte aligned");
+  const size_t need = nkv_compress_workspace_bytes(m, n_q_heads, window_blocks, block_size);
+  NKV_REQUIRE(workspace && workspace_bytes >= need, NKV_EWORKSPACE,
+              "compress_score: workspace needs %zu bytes (got %zu)", need, workspace_bytes);
+  const int Lw = window_blocks * block_size;
+  NKV_REQUIRE(Lw >= 2, NKV_EINVAL, "compress_score: window too short");
+  float* scores = (float*)workspace;
+  hipStream_t s = as_stream(stream);
+  const unsigned grid = (unsigned)(m * n_kv_heads * (Lw / kChunk));
+  const float sl2 = scale * kLog2e;
+#define NKV_SCORE_LAUNCH(G)                                                                    \
+  hipLaunchKernelGGL(compress_score_kernel<G>, dim3(grid), dim3(256), 0, s, (const bf16_t*)q,   \
+                     q_row_stride, (const bf16_t*)k_cache, block_tables, bt_row_stride,         \
+                     max_blocks_per_seq, base_context_lens, seq_idx, n_kv_heads, block_size, window_blocks,         \
+                     n_blocks, sl2, scores)
+  switch (g) {
+    case 1: NKV_SCORE_LAUNCH(1); break;
+    case 2: NKV_SCORE_LAUNCH(2); break;
+    case 4: NKV_SCORE_LAUNCH(4); break;
+    case 8: NKV_SCORE_LAUNCH(8); break;
+    default: NKV_SCORE_LAUNCH(16); break;
+  }
+#undef NKV_SCORE_LAUNCH
+  int rc = check_launch("nkv_compress_score");
+  if (rc) return rc;
+  const int n_sets = agg_mode == NKV_AGG_ALL ? 1 : n_kv_heads;
+  const int hps = n_q_heads / n_sets;
+  hipLaunchKernelGGL(compress_importance_kernel, dim3((unsigned)(m * n_sets)), dim3(256),
+                     (size_t)hps * 2 * sizeof(float), s, scores, n_q_heads, n_sets, Lw,
+                     importance_out);
+  return check_launch("nkv_compress_score(importance)");
+}
+
+extern "C" int nkv_compress_topk(const float* importance, int32_t n_rows, int32_t n_cand,
+                                 int32_t num_keep, int32_t* keep_idx, void* stream) {
+  clear_error();
+  NKV_REQUIRE(n_rows >= 0 && n_cand > 0 && n_cand <= 4096, NKV_EINVAL,
+              "compress_topk: need 0 < n_cand <= 4096 (got %d)", n_cand);
+  NKV_REQUIRE(num_keep > 0 && num_keep < n_cand, NKV_EINVAL,
+              "compress_topk: need 0 < num_keep < n_cand (got %d, %d)", num_keep, n_cand);
+  if (n_rows == 0) return NKV_OK;
+  NKV_REQUIRE(importance && keep_idx, NKV_EINVAL, "compress_topk: null pointer");
+  hipStream_t s = as_stream(stream);
+  if (n_cand <= 64 * 16) {
+    hipLaunchKernelGGL(compress_topk_kernel<16>, dim3((unsigned)n_rows), dim3(64), 0, s,
+                       importance, n_cand, num_keep, keep_idx);
+  } else {
+    hipLaunchKernelGGL(compress_topk_kernel<64>, dim3((unsigned)n_rows), dim3(64), 0, s,
+                       importance, n_cand, num_keep, keep_idx);
+  }
+  return check_launch("nkv_compress_topk");
+}
+
+extern "C" int nkv_compress_compact(void* k_cache, void* v_cache, const int32_t* block_tables,
+                                    int64_t bt_row_stride, int32_t max_blocks_per_seq,
+                                    const int32_t* base_context_lens,
+                                    int32_t* context_lens, const int32_t* seq_idx, int32_t m,
+                                    const int32_t* keep_idx, int32_t n_sets,
+                                    int32_t keep_tokens, int32_t n_kv_heads, int32_t head_dim,
+                                    int32_t block_size, int32_t window_blocks, int64_t n_blocks,
+                                    void* stream) {
+  clear_error();
+  NKV_REQUIRE(m >= 0 && n_kv_heads > 0 && block_size > 0 && window_blocks > 0, NKV_EINVAL,
+              "compress_compact: bad sizes");
+  if (m == 0) return NKV_OK;
+  NKV_REQUIRE(head_dim == kCD, NKV_EUNSUPPORTED, "compress_compact: head_dim must be 128");
+  NKV_REQUIRE(n_sets == 1 || n_sets == n_kv_heads, NKV_EINVAL,
+              "compress_compact: n_sets must be 1 or n_kv_heads");
+  NKV_REQUIRE(keep_tokens > 0 && keep_tokens <= window_blocks * block_size, NKV_EINVAL,
+              "compress_compact: need 0 < keep_tokens <= window tokens");
+  const int max_rows = keep_tokens + block_size - 1;
+  NKV_REQUIRE(max_rows <= 1024, NKV_EUNSUPPORTED,
+              "compress_compact: keep_tokens + block_size - 1 = %d exceeds 1024", max_rows);
+  NKV_REQUIRE(k_cache && v_cache && block_tables && base_context_lens && context_lens &&
+                  seq_idx && keep_idx,
+              NKV_EINVAL, "compress_compact: null pointer");
+  NKV_REQUIRE(aligned16(k_cache) && aligned16(v_cache), NKV_EINVAL,
+              "compress_compact: caches must be 16-byte aligned");
+  NKV_REQUIRE(max_blocks_per_seq > 0 && bt_row_stride >= max_blocks_per_seq, NKV_EINVAL,
+              "compress_compact: bad block table width/stride");
+  hipStream_t s = as_stream(stream);
+  const unsigned grid = (unsigned)(m * n_kv_heads * 4);
+#define NKV_COMPACT_LAUNCH(R)                                                                  \
+  hipLaunchKernelGGL(compress_compact_kernel<R>, dim3(grid), dim3(256), 0, s, (bf16_t*)k_cache, \
+                     (bf16_t*)v_cache, block_tables, bt_row_stride, max_blocks_per_seq,         \
+                     base_context_lens,                                                         \
+                     context_lens, seq_idx, keep_idx, n_sets, keep_tokens, n_kv_heads,          \
+                     block_size, window_blocks, n_blocks)
+  if (max_rows <= 256) NKV_COMPACT_LAUNCH(8);
+  else if (max_rows <= 512) NKV_COMPACT_LAUNCH(16);
+  else if (max_rows <= 768) NKV_COMPACT_LAUNCH(24);
+  else NKV_COMPACT_LAUNCH(32);
+#undef NKV_COMPACT_LAUNCH
+  return check_launch("nkv_compress_compact");
+}
+
+extern "C" int nkv_compress_finalize(int32_t* block_tables, int64_t bt_row_stride,
+                                     int32_t max_blocks_per_seq,
+                                     const int32_t* base_context_lens, const int32_t* seq_idx,
+                                     int32_t m, int32_t keep_tokens, int32_t block_size,
+                                     int32_t window_blocks, int32_t rewrite_tables,
+                                     int32_t* slot_mapping, int32_t* events, void* stream) {
+  clear_error();
+  NKV_REQUIRE(m >= 0 && block_size > 0 && window_blocks > 0 && max_blocks_per_seq > 0,
+              NKV_EINVAL, "compress_finalize: bad sizes");
+  if (m == 0) return NKV_OK;
+  NKV_REQUIRE(block_tables && base_context_lens && seq_idx && events, NKV_EINVAL,
+              "compress_finalize: null pointer");
+  NKV_REQUIRE(bt_row_stride >= max_blocks_per_seq, NKV_EINVAL,
+              "compress_finalize: bt_row_stride < max_blocks_per_seq");
+  hipLaunchKernelGGL(compress_finalize_kernel, dim3(1), dim3(64), 0, as_stream(stream),
+                     block_tables, bt_row_stride, max_blocks_per_seq, base_context_lens, seq_idx,
+                     m, keep_tokens, block_size, window_blocks, rewrite_tables, slot_mapping,
+                     events);
+  return check_launch("nkv_compress_finalize");
+}

@@ -1,0 +1,141 @@
+"""Engine hooks of the periodic compression step (host side).
+
+* ``CompressionScheduler.prepare`` -- the compression block of the
+  reference's ``ModelRunner.prepare_decode`` (model_runner.py:291-332): a
+  decode-step counter fires every ``kv_compress_period`` steps; a sequence is
+  eligible iff ``len % B != B-1``, ``tail_uncompressed_len >= W*B`` and it has
+  at least W full blocks; the first ``kv_compress_topk`` eligible sequences in
+  batch order are selected (``policy="first"``, the reference), or the
+  longest ones (``policy="longest"``). It fills the Context fields
+  ``is_compress_step``, ``compress_selected_batch_indices``,
+  ``compress_selected_seq_ids`` and ``compress_base_context_lens``.
+* ``apply_compression_events`` -- ``Scheduler.postprocess``'s event handling
+  (scheduler.py:103-125) plus ``BlockManager.truncate_blocks``: dedup by
+  batch index, free the tail blocks, ``num_tokens = new_len``,
+  ``tail_uncompressed_len = 0``. It also rebases ``num_computed_tokens`` by
+  the number of tokens removed, which the reference leaves at the
+  uncompressed count (its prepare_step would then index past the truncated
+  block table).
+* ``prepare_decode_metadata`` -- decode metadata as in prepare_decode
+  (model_runner.py:265-285): positions = rope_pos, context_lens = physical
+  length, slot = last block * B + last_block_num_tokens - 1, block tables
+  right-padded with -1.
+* ``prepare_step_metadata`` -- the mixed prefill/decode builder of
+  prepare_step (model_runner.py:160-219).
+"""
+from __future__ import annotations
+
+import torch
+
+from .sequence import ScheduledSeq, Sequence
+
+
+def prepare_block_tables(seqs: list[Sequence], pad: int = -1) -> list[list[int]]:
+    """model_runner.py:154-158 (host lists; the caller moves them to the device)."""
+    max_len = max(len(s.block_table) for s in seqs)
+    return [s.block_table + [pad] * (max_len - len(s.block_table)) for s in seqs]
+
+
+def prepare_decode_metadata(seqs: list[Sequence], block_size: int, device="cuda"):
+    positions, slot_mapping, context_lens = [], [], []
+    for seq in seqs:
+        positions.append(seq.rope_pos)
+        context_lens.append(len(seq))
+        slot_mapping.append(seq.block_table[-1] * block_size + seq.last_block_num_tokens - 1)
+    to = dict(device=device)
+    return dict(
+        positions=torch.tensor(positions, dtype=torch.int64).to(**to),
+        slot_mapping=torch.tensor(slot_mapping, dtype=torch.int32).to(**to),
+        context_lens=torch.tensor(context_lens, dtype=torch.int32).to(**to),
+        block_tables=torch.tensor(prepare_block_tables(seqs), dtype=torch.int32).to(**to),
+    )
+
+
+def prepare_step_metadata(scheduled: list[ScheduledSeq], block_size: int, device="cuda"):
+    positions, slot_mapping, context_lens = [], [], []
+    cu_q, cu_k = [0], [0]
+    max_q = max_k = 0
+    for sched in scheduled:
+        seq, n = sched.seq, sched.num_new_tokens
+        start = seq.num_computed_tokens
+        end = start + n
+        positions.extend(range(start, end))
+        cu_q.append(cu_q[-1] + n)
+        cu_k.append(cu_k[-1] + end)
+        max_q, max_k = max(max_q, n), max(max_k, end)
+        for pos in range(start, end):
+            slot_mapping.append(seq.block_table[pos // block_size] * block_size + pos % block_size)
+        context_lens.append(end)
+    to = dict(device=device)
+    return dict(
+        positions=torch.tensor(positions, dtype=torch.int64).to(**to),
+        slot_mapping=torch.tensor(slot_mapping, dtype=torch.int32).to(**to),
+        context_lens=torch.tensor(context_lens, dtype=torch.int32).to(**to),
+        cu_seqlens_q=torch.tensor(cu_q, dtype=torch.int32).to(**to),
+        cu_seqlens_k=torch.tensor(cu_k, dtype=torch.int32).to(**to),
+        max_seqlen_q=max_q, max_seqlen_k=max_k,
+        block_tables=torch.tensor(prepare_block_tables([s.seq for s in scheduled]),
+                                  dtype=torch.int32).to(**to),
+    )
+
+
+class CompressionScheduler:
+    """Decode-step counter + selection of the sequences to compress."""
+
+    def __init__(self, config, policy: str = "first"):
+        self.block_size = config.kvcache_block_size
+        self.window_blocks = config.kv_compress_window_blocks
+        self.topk = config.kv_compress_topk
+        self.period = config.kv_compress_period
+        self.policy = policy
+        self.decode_step_counter = 0
+
+    def select(self, seqs: list[Sequence]) -> tuple[bool, list[int], list[int]]:
+        B = self.block_size
+        window_tokens = self.window_blocks * B
+        self.decode_step_counter += 1
+        is_compress_step = self.decode_step_counter % self.period == 0
+        selected: list[tuple[int, int]] = []
+        if is_compress_step:
+            candidates = []
+            for i, seq in enumerate(seqs):
+                cur = len(seq)
+                full_blocks, tail_len = cur // B, cur % B
+                if tail_len == B - 1:
+                    continue
+                if seq.tail_uncompressed_len >= window_tokens and full_blocks >= self.window_blocks:
+                    candidates.append((i, seq.seq_id))
+            if self.policy == "longest":
+                candidates.sort(key=lambda c: (-len(seqs[c[0]]), c[0]))
+            selected = candidates[:self.topk]
+        return is_compress_step, [x[0] for x in selected], [x[1] for x in selected]
+
+    def prepare(self, context, seqs: list[Sequence]) -> None:
+        """Fill the compression fields of ``context`` for this decode step."""
+        context.compress_need_mask = None
+        context.compress_any = False
+        is_step, idx, ids = self.select(seqs)
+        context.is_compress_step = is_step
+        context.compress_selected_batch_indices = idx
+        context.compress_selected_seq_ids = ids
+        context.compress_base_context_lens = (context.context_lens.clone()
+                                              if is_step and idx else None)
+
+
+def apply_compression_events(scheduled: list, events: list[dict] | None, block_manager) -> None:
+    """Apply the last layer's events to the host state (scheduler.py:104-125)."""
+    if not events:
+        return
+    dedup = {}
+    for ev in events:
+        bidx = ev["batch_index"]
+        if 0 <= bidx < len(scheduled):
+            dedup[bidx] = ev
+    for bidx, ev in dedup.items():
+        item = scheduled[bidx]
+        seq = item.seq if isinstance(item, ScheduledSeq) or hasattr(item, "seq") else item
+        removed = len(seq) - ev["new_context_len"]
+        block_manager.truncate_blocks(seq, ev["keep_blocks"])
+        seq.num_tokens = ev["new_context_len"]
+        seq.num_computed_tokens = max(0, seq.num_computed_tokens - removed)
+        seq.tail_uncompressed_len = ev.get("tail_uncompressed_len_after", 0)

@@ -1,0 +1,183 @@
+"""Drop-in Attention layer and the functional ops behind it.
+
+Mirrors nanokvllm/layers/attention.py: ``store_kvcache`` (:33-40) and
+``Attention`` (:42-108) with the same constructor, attributes
+(``k_cache``/``v_cache`` assigned by the model runner) and ``forward(q, k, v,
+Layer)``. Every op runs in libnkv_amd.so on the caller's current HIP stream;
+nothing here computes on the CPU.
+"""
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from .. import _lib
+from ..utils.context import get_context
+from .compress_utils import MyCompressCompact
+
+_BF16 = torch.bfloat16
+
+
+def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
+                  v_cache: torch.Tensor, slot_mapping: torch.Tensor) -> None:
+    """k_cache/v_cache row slot_mapping[i] <- key[i]/value[i]; -1 slots skipped.
+
+    Same checks as the reference (attention.py:33-40): last dim contiguous,
+    head stride == head_dim, cache token stride == Hk*D, one slot per token.
+    """
+    N, num_heads, head_dim = key.shape
+    D = num_heads * head_dim
+    assert key.stride(-1) == 1 and value.stride(-1) == 1
+    assert key.stride(1) == head_dim and value.stride(1) == head_dim
+    assert k_cache.stride(1) == D and v_cache.stride(1) == D
+    assert slot_mapping.numel() == N
+    assert key.dtype == _BF16 and value.dtype == _BF16 and k_cache.dtype == _BF16
+    assert slot_mapping.dtype == torch.int32 and slot_mapping.is_contiguous()
+    n_slots = k_cache.numel() // D
+    rc = _lib.lib().nkv_store_kvcache(
+        key.data_ptr(), key.stride(0), value.data_ptr(), value.stride(0),
+        k_cache.data_ptr(), v_cache.data_ptr(), slot_mapping.data_ptr(), N,
+        num_heads, head_dim, n_slots, _lib.stream_of(key))
+    _lib.check(rc, "store_kvcache")
+
+
+def _decode_args(q, k_cache, block_tables, context_lens):
+    bs, Hq, D = q.shape
+    NB, B, Hk, Dk = k_cache.shape
+    assert Dk == D and q.stride(-1) == 1 and q.stride(1) == D
+    assert k_cache.is_contiguous()
+    assert block_tables.dtype == torch.int32 and block_tables.stride(1) == 1
+    assert context_lens.dtype == torch.int32 and context_lens.is_contiguous()
+    assert block_tables.size(0) >= bs and context_lens.numel() >= bs
+    return bs, Hq, D, NB, B, Hk
+
+
+def paged_decode_workspace(q: torch.Tensor, k_cache: torch.Tensor,
+                           block_tables: torch.Tensor) -> torch.Tensor:
+    bs, Hq, D = q.shape
+    nbytes = _lib.lib().nkv_paged_decode_workspace_bytes(bs, Hq, D, block_tables.size(1),
+                                                          k_cache.size(1))
+    return torch.empty(max(nbytes, 4), dtype=torch.uint8, device=q.device)
+
+
+def paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                 context_lens: torch.Tensor, block_tables: torch.Tensor, scale: float,
+                 out: torch.Tensor | None = None,
+                 workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Paged GQA decode: q [bs, Hq, D] -> out [bs, Hq, D] (bf16).
+
+    Same math as flash_attn_with_kvcache(q.unsqueeze(1), k_cache, v_cache,
+    cache_seqlens=context_lens, block_table=block_tables, softmax_scale=scale,
+    causal=True) at attention.py:104-107.
+    """
+    bs, Hq, D, NB, B, Hk = _decode_args(q, k_cache, block_tables, context_lens)
+    if out is None:
+        out = torch.empty(bs, Hq, D, dtype=_BF16, device=q.device)
+    if workspace is None:
+        workspace = paged_decode_workspace(q, k_cache, block_tables)
+    rc = _lib.lib().nkv_paged_decode(
+        q.data_ptr(), q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(),
+        block_tables.data_ptr(), block_tables.stride(0), context_lens.data_ptr(), bs, Hq, Hk, D,
+        B, block_tables.size(1), NB, float(scale), out.data_ptr(), out.stride(0),
+        workspace.data_ptr(), workspace.numel(), _lib.stream_of(q))
+    _lib.check(rc, "paged_decode")
+    return out
+
+
+def varlen_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                   cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor, max_seqlen_q: int,
+                   scale: float, block_tables: torch.Tensor | None = None,
+                   out: torch.Tensor | None = None) -> torch.Tensor:
+    """Varlen causal (bottom-right) attention: q [sum Lq, Hq, D] -> [sum Lq, Hq, D].
+
+    With ``block_tables`` k/v are the paged caches [NB, B, Hk, D]; without,
+    they are contiguous [sum Lk, Hk, D] rows. Same math as
+    flash_attn_varlen_func(..., causal=True, block_table) at attention.py:96-102.
+    """
+    N, Hq, D = q.shape
+    assert q.stride(-1) == 1 and q.stride(1) == D
+    assert cu_seqlens_q.dtype == torch.int32 and cu_seqlens_k.dtype == torch.int32
+    n_seqs = cu_seqlens_q.numel() - 1
+    if block_tables is not None:
+        NB, B, Hk, Dk = k.shape
+        assert k.is_contiguous() and v.is_contiguous()
+        kv_row_stride = Hk * Dk
+        n_rows = NB * B
+        bt_ptr, bt_stride = block_tables.data_ptr(), block_tables.stride(0)
+        assert block_tables.dtype == torch.int32 and block_tables.stride(1) == 1
+    else:
+        _, Hk, Dk = k.shape
+        assert k.stride(1) == Dk and k.stride(2) == 1 and v.stride() == k.stride()
+        kv_row_stride = k.stride(0)
+        n_rows = k.size(0)
+        B = 0
+        bt_ptr, bt_stride = None, 0
+    assert Dk == D
+    if out is None:
+        out = torch.empty(N, Hq, D, dtype=_BF16, device=q.device)
+    rc = _lib.lib().nkv_prefill_varlen(
+        q.data_ptr(), q.stride(0), k.data_ptr(), v.data_ptr(), kv_row_stride,
+        cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), bt_ptr, bt_stride, n_seqs,
+        int(max_seqlen_q), Hq, Hk, D, B, n_rows, float(scale), out.data_ptr(), out.stride(0),
+        _lib.stream_of(q))
+    _lib.check(rc, "varlen_prefill")
+    return out
+
+
+class Attention(nn.Module):
+    """Per-layer attention: store -> (periodic compression) -> prefill or decode.
+
+    Constructor and forward follow nanokvllm/layers/attention.py:44-108.
+    """
+
+    def __init__(self, num_heads, head_dim, scale, num_kv_heads, vllm_config, num_layers):
+        super().__init__()
+        self.num_heads = num_heads
+        self.head_dim = head_dim
+        self.scale = scale
+        self.num_kv_heads = num_kv_heads
+        self.k_cache = self.v_cache = torch.tensor([])
+
+        self.kv_compress_enabled = vllm_config.kv_compress_enabled
+        if self.kv_compress_enabled:
+            self.num_layers = num_layers
+            self.kv_compress_window_blocks = vllm_config.kv_compress_window_blocks
+            self.kv_compress_keep_blocks = vllm_config.kv_compress_keep_blocks
+            self.kv_compress_keep_extra_tokens = vllm_config.kv_compress_keep_extra_tokens
+            self.kv_compress_agg = getattr(vllm_config, "kv_compress_agg", "all")
+        self._decode_ws = None
+
+    def _workspace(self, q, block_tables):
+        nbytes = _lib.lib().nkv_paged_decode_workspace_bytes(
+            q.size(0), q.size(1), q.size(2), block_tables.size(1), self.k_cache.size(1))
+        ws = self._decode_ws
+        if ws is None or ws.numel() < nbytes or ws.device != q.device:
+            ws = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=q.device)
+            self._decode_ws = ws
+        return ws
+
+    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, Layer):
+        context = get_context()
+        k_cache, v_cache = self.k_cache, self.v_cache
+        if k_cache.numel() and v_cache.numel():
+            store_kvcache(k, v, k_cache, v_cache, context.slot_mapping)
+
+        if (context.use_decode_kernel and self.kv_compress_enabled and context.is_compress_step
+                and context.compress_selected_batch_indices):
+            MyCompressCompact(
+                q_current=q, k_cache=k_cache, v_cache=v_cache, layer_id=Layer,
+                block_size=k_cache.size(1), window_blocks=self.kv_compress_window_blocks,
+                keep_blocks=self.kv_compress_keep_blocks,
+                keep_extra_tokens=self.kv_compress_keep_extra_tokens,
+                num_layers=self.num_layers, context=context, agg=self.kv_compress_agg)
+
+        if not context.use_decode_kernel:
+            if context.block_tables is not None:  # K/V read back from the paged cache
+                return varlen_prefill(q, k_cache, v_cache, context.cu_seqlens_q,
+                                      context.cu_seqlens_k, context.max_seqlen_q, self.scale,
+                                      block_tables=context.block_tables)
+            return varlen_prefill(q, k, v, context.cu_seqlens_q, context.cu_seqlens_k,
+                                  context.max_seqlen_q, self.scale)
+        o = paged_decode(q, k_cache, v_cache, context.context_lens, context.block_tables,
+                         self.scale, workspace=self._workspace(q, context.block_tables))
+        return o.unsqueeze(1)

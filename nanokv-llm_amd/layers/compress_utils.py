@@ -1,0 +1,170 @@
+"""Window-based periodic KV compression, run per layer inside Attention.forward.
+
+Drop-in for ``MyCompressCompact`` (nanokvllm/layers/compress_utils.py:100-290):
+same arguments, same return value, same side effects -- the layer's K/V cache
+is compacted in place, ``context.context_lens`` of the selected sequences is
+set to ``len - W*B + keep_tokens`` (from the base lengths captured before the
+first layer), and on the last layer one event dict per selected sequence is
+appended to ``context.compression_events``.
+
+The reference's helpers ``get_tail_window_and_tail_slots`` and
+``gather_kv_by_slots`` (:9-97) have no counterpart: window location is done
+inside the kernels, and K is scored in place instead of being gathered.
+Kernels (libnkv_amd.so): nkv_compress_score -> nkv_compress_topk ->
+nkv_compress_compact (every layer) -> nkv_compress_finalize (last layer).
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+
+AGG_MODES = {"all": _lib.NKV_AGG_ALL, "group": _lib.NKV_AGG_GROUP}
+
+
+class _StepBuffers:
+    """Device buffers of one compression step, shared by all layers."""
+
+    def __init__(self, selected, device, m, n_sets, n_cand, keep_tokens, ws_bytes, ev_len):
+        self.key = (tuple(selected), device, n_sets, n_cand, keep_tokens, ws_bytes, ev_len)
+        self.seq_idx = torch.tensor(selected, dtype=torch.int32).to(device, non_blocking=True)
+        self.importance = torch.empty(m, n_sets, n_cand, dtype=torch.float32, device=device)
+        self.keep_idx = torch.empty(m, n_sets, keep_tokens, dtype=torch.int32, device=device)
+        self.workspace = torch.empty(max(ws_bytes, 4), dtype=torch.uint8, device=device)
+        self.events = torch.empty(m, ev_len, dtype=torch.int32, device=device)
+
+
+def _buffers(context, selected, device, m, n_sets, n_cand, keep_tokens, ws_bytes, ev_len):
+    key = (tuple(selected), device, n_sets, n_cand, keep_tokens, ws_bytes, ev_len)
+    buf = getattr(context, "_nkv_compress_buffers", None)
+    if buf is None or buf.key != key:
+        buf = _StepBuffers(selected, device, m, n_sets, n_cand, keep_tokens, ws_bytes, ev_len)
+        context._nkv_compress_buffers = buf
+    return buf
+
+
+def compress_select(q, k_cache, block_tables, base_context_lens, seq_idx, window_blocks,
+                    num_keep, scale, agg="all", importance=None, keep_idx=None, workspace=None):
+    """Score the window of each selected sequence and pick the kept positions.
+
+    Returns (keep_idx int32 [m, n_sets, 1+num_keep+1], importance fp32
+    [m, n_sets, W*B-1]). keep_idx rows are [0, ascending top-num_keep, W*B-1].
+    """
+    m = seq_idx.numel()
+    NB, B, Hk, D = k_cache.shape
+    Hq = q.size(1)
+    n_sets = 1 if agg == "all" else Hk
+    n_cand = window_blocks * B - 1
+    L = _lib.lib()
+    if importance is None:
+        importance = torch.empty(m, n_sets, n_cand, dtype=torch.float32, device=q.device)
+    if keep_idx is None:
+        keep_idx = torch.empty(m, n_sets, num_keep + 2, dtype=torch.int32, device=q.device)
+    ws_bytes = L.nkv_compress_workspace_bytes(m, Hq, window_blocks, B)
+    if workspace is None:
+        workspace = torch.empty(max(ws_bytes, 4), dtype=torch.uint8, device=q.device)
+    stream = _lib.stream_of(q)
+    rc = L.nkv_compress_score(
+        q.data_ptr(), q.stride(0), k_cache.data_ptr(), block_tables.data_ptr(),
+        block_tables.stride(0), block_tables.size(1), base_context_lens.data_ptr(),
+        seq_idx.data_ptr(), m, Hq, Hk, D, B, window_blocks, NB, float(scale), AGG_MODES[agg],
+        importance.data_ptr(), workspace.data_ptr(), workspace.numel(), stream)
+    _lib.check(rc, "compress_score")
+    rc = L.nkv_compress_topk(importance.data_ptr(), m * n_sets, n_cand, num_keep,
+                             keep_idx.data_ptr(), stream)
+    _lib.check(rc, "compress_topk")
+    return keep_idx, importance
+
+
+def compress_compact(k_cache, v_cache, block_tables, base_context_lens, context_lens, seq_idx,
+                     keep_idx, window_blocks):
+    """Move the kept window rows (and the tail block) into place, K and V."""
+    NB, B, Hk, D = k_cache.shape
+    m, n_sets, keep_tokens = keep_idx.shape
+    rc = _lib.lib().nkv_compress_compact(
+        k_cache.data_ptr(), v_cache.data_ptr(), block_tables.data_ptr(), block_tables.stride(0),
+        block_tables.size(1), base_context_lens.data_ptr(), context_lens.data_ptr(),
+        seq_idx.data_ptr(), m, keep_idx.data_ptr(), n_sets, keep_tokens, Hk, D, B,
+        window_blocks, NB, _lib.stream_of(k_cache))
+    _lib.check(rc, "compress_compact")
+
+
+def compress_finalize(block_tables, base_context_lens, seq_idx, keep_tokens, block_size,
+                      window_blocks, events, rewrite_tables=True, slot_mapping=None):
+    rc = _lib.lib().nkv_compress_finalize(
+        block_tables.data_ptr(), block_tables.stride(0), block_tables.size(1),
+        base_context_lens.data_ptr(), seq_idx.data_ptr(), seq_idx.numel(), keep_tokens,
+        block_size, window_blocks, int(bool(rewrite_tables)), _lib.ptr(slot_mapping),
+        events.data_ptr(), _lib.stream_of(block_tables))
+    _lib.check(rc, "compress_finalize")
+
+
+def events_to_dicts(events: torch.Tensor, layer_id: int) -> list[dict]:
+    """Decode the int32 event rows into the reference's event dicts (:280-287)."""
+    out = []
+    for row in events.cpu().tolist():
+        n = row[3]
+        out.append({
+            "batch_index": int(row[0]),
+            "layer": int(layer_id),
+            "new_context_len": int(row[1]),
+            "keep_blocks": int(row[2]),
+            "freed_block_ids": [int(x) for x in row[4:4 + n]],
+            "tail_uncompressed_len_after": 0,
+        })
+    return out
+
+
+def MyCompressCompact(q_current: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                      layer_id: int, block_size: int, window_blocks: int, keep_blocks: int,
+                      keep_extra_tokens: int, num_layers: int, context=None, agg: str = "all",
+                      rewrite_tables: bool = True) -> bool:
+    """Compress the last ``window_blocks`` full blocks of each selected sequence.
+
+    agg="all" sums key importance over every query head (the reference,
+    CompressMethod.py:41-42); agg="group" keeps a separate set per KV head.
+    A selected sequence whose base length has fewer than ``window_blocks``
+    full blocks is left unchanged (the reference asserts instead, :39-41).
+    """
+    if context is None:
+        from ..utils.context import get_context
+        context = get_context()
+    if (not context.use_decode_kernel) or context.context_lens is None \
+            or context.block_tables is None:
+        return False
+    selected = context.compress_selected_batch_indices
+    if not selected:
+        return False
+    m = len(selected)
+    bs = context.context_lens.numel()
+    assert all(0 <= i < bs for i in selected) and len(set(selected)) == m, \
+        f"selected batch indices must be distinct and < {bs}: {selected}"
+    B = block_size
+    window_tokens = window_blocks * B
+    keep_tokens = keep_blocks * B + keep_extra_tokens
+    num_keep = keep_tokens - 2  # bos + selected + latest token
+    # SnapKV's own skip rule with window = 1 (CompressMethod.py:17-18)
+    if window_tokens - 1 <= 0 or window_tokens <= num_keep + 1:
+        return False
+    base = context.compress_base_context_lens
+    assert base is not None, "compress_base_context_lens is None during compress step"
+    device = k_cache.device
+    Hq, D = q_current.size(1), q_current.size(2)
+    Hk = k_cache.size(2)
+    n_sets = 1 if agg == "all" else Hk
+    ws_bytes = _lib.lib().nkv_compress_workspace_bytes(m, Hq, window_blocks, B)
+    buf = _buffers(context, selected, device, m, n_sets, window_tokens - 1, keep_tokens,
+                   ws_bytes, 4 + context.block_tables.size(1))
+    compress_select(q_current, k_cache, context.block_tables, base, buf.seq_idx, window_blocks,
+                    num_keep, D ** -0.5, agg, importance=buf.importance, keep_idx=buf.keep_idx,
+                    workspace=buf.workspace)
+    compress_compact(k_cache, v_cache, context.block_tables, base, context.context_lens,
+                     buf.seq_idx, buf.keep_idx, window_blocks)
+    if layer_id + 1 >= num_layers:
+        compress_finalize(context.block_tables, base, buf.seq_idx, keep_tokens, B, window_blocks,
+                          buf.events, rewrite_tables=rewrite_tables,
+                          slot_mapping=context.slot_mapping if rewrite_tables else None)
+        if context.compression_events is None:
+            context.compression_events = []
+        context.compression_events.extend(events_to_dicts(buf.events, layer_id))
+    return True

@@ -1,0 +1,176 @@
+"""Seeded synthetic inputs for the paged-attention workloads (no checkpoints).
+
+Each generator builds a paged K/V pool ``[n_blocks, 256, Hk, 128]`` (bf16),
+assigns every sequence ``ceil(ctx / B)`` physical blocks drawn without
+replacement from a random permutation of the pool, and derives block tables
+(right-padded with -1) and the slot of the newest token. Integer choices use
+a CPU ``torch.Generator`` seeded with ``seed`` so they are identical on every
+machine; the bulk random values are drawn on ``device``.
+
+Workloads (sizes from the reference's Qwen3 geometries, block size 256):
+  decode_qwen3_0_6b   bs 4,  Hq 16, Hk 8, ctx U[300, 1000], pool 16 blocks,
+                      q/K/V ~ N(0,1)/sqrt(128)
+  decode_qwen3_8b     bs 64, Hq 32, Hk 8, ctx U[2048, 8192], pool 4096 blocks,
+                      q/K/V ~ N(0,1); one new token per sequence stored first
+  compress_qwen3_8b   bs 500, Hq 32, Hk 8, ctx U[1500, 4096], top-20 longest,
+                      W = 4 blocks, keep 2*256+1
+  prefill_qwen3_8b    16 sequences, L U[512, 4096]; chunked: 2048-token chunks
+                      on paged prefixes of U[0, 8192] tokens
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+BLOCK = 256
+HEAD_DIM = 128
+
+
+def _randn(shape, gen_seed, device, dtype=torch.bfloat16, scale=1.0):
+    g = torch.Generator(device=device)
+    g.manual_seed(gen_seed)
+    x = torch.randn(shape, generator=g, device=device, dtype=torch.float32)
+    if scale != 1.0:
+        x.mul_(scale)
+    return x.to(dtype)
+
+
+def assign_blocks(ctx_lens: list[int], n_blocks: int, gen: torch.Generator, block=BLOCK,
+                  extra_tokens: int = 0):
+    """Block tables for sequences of the given lengths (+extra_tokens headroom)."""
+    need = [math.ceil((c + extra_tokens) / block) for c in ctx_lens]
+    total = sum(need)
+    if total > n_blocks:
+        raise ValueError(f"pool of {n_blocks} blocks cannot hold {total} blocks")
+    perm = torch.randperm(n_blocks, generator=gen)[:total].tolist()
+    width = max(need)
+    tables, pos = [], 0
+    for n in need:
+        tables.append(perm[pos:pos + n] + [-1] * (width - n))
+        pos += n
+    return torch.tensor(tables, dtype=torch.int32)
+
+
+def slot_of(block_tables: torch.Tensor, positions: torch.Tensor, block=BLOCK):
+    """slot = block_table[b, pos // B] * B + pos % B (model_runner.py:192-194)."""
+    pos = positions.to(torch.int64)
+    blk = torch.gather(block_tables.to(torch.int64), 1, (pos // block).view(-1, 1)).view(-1)
+    return (blk * block + pos % block).to(torch.int32)
+
+
+def decode_workload(bs, Hq, Hk, ctx_lo, ctx_hi, n_blocks, seed, device="cpu", value_scale=1.0,
+                    n_table_sets=1):
+    """Paged decode inputs; context lengths include the token stored this step.
+
+    Returns a dict with q [bs,Hq,D], new key/value [bs,Hk,D], k_cache/v_cache,
+    context_lens [bs] (int32), slot_mapping [bs] and block_tables (a list of
+    n_table_sets independent random assignments of the same lengths).
+    """
+    gen = torch.Generator().manual_seed(seed)
+    ctx = torch.randint(ctx_lo, ctx_hi + 1, (bs,), generator=gen, dtype=torch.int64)
+    tables = [assign_blocks(ctx.tolist(), n_blocks, gen) for _ in range(n_table_sets)]
+    D = HEAD_DIM
+    k_cache = _randn((n_blocks, BLOCK, Hk, D), seed * 7 + 1, device, scale=value_scale)
+    v_cache = _randn((n_blocks, BLOCK, Hk, D), seed * 7 + 2, device, scale=value_scale)
+    q = _randn((bs, Hq, D), seed * 7 + 3, "cpu", scale=value_scale)
+    key = _randn((bs, Hk, D), seed * 7 + 4, "cpu", scale=value_scale)
+    value = _randn((bs, Hk, D), seed * 7 + 5, "cpu", scale=value_scale)
+    ctx32 = ctx.to(torch.int32)
+    return dict(q=q, key=key, value=value, k_cache=k_cache, v_cache=v_cache,
+                context_lens=ctx32, block_tables=tables,
+                slot_mappings=[slot_of(t, ctx - 1) for t in tables],
+                scale=D ** -0.5, Hq=Hq, Hk=Hk)
+
+
+def decode_qwen3_0_6b(seed=1, device="cpu"):
+    return decode_workload(4, 16, 8, 300, 1000, 16, seed, device, value_scale=HEAD_DIM ** -0.5)
+
+
+def decode_qwen3_8b(seed=2, device="cpu", bs=64, n_blocks=4096, n_table_sets=1):
+    return decode_workload(bs, 32, 8, 2048, 8192, n_blocks, seed, device,
+                           n_table_sets=n_table_sets)
+
+
+def compress_workload(bs, Hq, Hk, ctx_lo, ctx_hi, topk, seed, device="cpu", n_blocks=None,
+                      selected_only=False):
+    """Decode state for a compression step; selection = the topk longest sequences.
+
+    With selected_only, only the selected sequences get blocks (the others
+    keep their lengths but own no cache) -- enough for the step itself.
+    """
+    gen = torch.Generator().manual_seed(seed)
+    ctx = torch.randint(ctx_lo, ctx_hi + 1, (bs,), generator=gen, dtype=torch.int64)
+    order = sorted(range(bs), key=lambda i: (-int(ctx[i]), i))
+    selected = sorted(order[:topk])
+    lens_for_tables = [int(ctx[i]) if (not selected_only or i in selected) else 0
+                       for i in range(bs)]
+    need = sum(math.ceil(c / BLOCK) for c in lens_for_tables)
+    n_blocks = n_blocks or need + 8
+    table = assign_blocks(lens_for_tables, n_blocks, gen)
+    D = HEAD_DIM
+    k_cache = _randn((n_blocks, BLOCK, Hk, D), seed * 7 + 1, device)
+    v_cache = _randn((n_blocks, BLOCK, Hk, D), seed * 7 + 2, device)
+    q = _randn((bs, Hq, D), seed * 7 + 3, "cpu")
+    return dict(q=q, k_cache=k_cache, v_cache=v_cache, context_lens=ctx.to(torch.int32),
+                block_tables=table, seq_idx=selected, Hq=Hq, Hk=Hk)
+
+
+def compress_qwen3_8b(seed=3, device="cpu", selected_only=True):
+    return compress_workload(500, 32, 8, 1500, 4096, 20, seed, device,
+                             selected_only=selected_only)
+
+
+def prefill_workload(n_seqs, Hq, Hk, len_lo, len_hi, seed, device="cpu", prefix_lo=None,
+                     prefix_hi=None, chunk=None):
+    """Varlen prefill over the paged cache.
+
+    One-shot: Lq = Lk = L ~ U[len_lo, len_hi]. Chunked (chunk given): prefix
+    P ~ U[prefix_lo, prefix_hi] already in cache, Lq = chunk, Lk = P + chunk.
+    The new chunk's K/V rows (key/value) are what store_kvcache writes before
+    the attention; the cache holds N(0,1) values for the prefix.
+    """
+    gen = torch.Generator().manual_seed(seed)
+    if chunk is None:
+        Lq = torch.randint(len_lo, len_hi + 1, (n_seqs,), generator=gen).tolist()
+        Lk = list(Lq)
+    else:
+        P = torch.randint(prefix_lo, prefix_hi + 1, (n_seqs,), generator=gen).tolist()
+        Lq = [chunk] * n_seqs
+        Lk = [p + chunk for p in P]
+    need = sum(math.ceil(k / BLOCK) for k in Lk)
+    n_blocks = need + 8
+    table = assign_blocks(Lk, n_blocks, gen)
+    cu_q = torch.tensor([0] + list(torch.tensor(Lq).cumsum(0).tolist()), dtype=torch.int32)
+    cu_k = torch.tensor([0] + list(torch.tensor(Lk).cumsum(0).tolist()), dtype=torch.int32)
+    N = int(cu_q[-1])
+    D = HEAD_DIM
+    positions = torch.cat([torch.arange(k - q, k) for q, k in zip(Lq, Lk)])
+    seq_of = torch.cat([torch.full((q,), i, dtype=torch.int64) for i, q in enumerate(Lq)])
+    blk = table.to(torch.int64)[seq_of, positions // BLOCK]
+    slots = (blk * BLOCK + positions % BLOCK).to(torch.int32)
+    return dict(
+        q=_randn((N, Hq, D), seed * 7 + 3, device),
+        key=_randn((N, Hk, D), seed * 7 + 4, device),
+        value=_randn((N, Hk, D), seed * 7 + 5, device),
+        k_cache=_randn((n_blocks, BLOCK, Hk, D), seed * 7 + 1, device),
+        v_cache=_randn((n_blocks, BLOCK, Hk, D), seed * 7 + 2, device),
+        block_tables=table, cu_seqlens_q=cu_q, cu_seqlens_k=cu_k, slot_mapping=slots,
+        max_seqlen_q=max(Lq), max_seqlen_k=max(Lk), Lq=Lq, Lk=Lk, Hq=Hq, Hk=Hk,
+        scale=D ** -0.5)
+
+
+def prefill_qwen3_8b(seed=4, device="cpu", n_seqs=16):
+    return prefill_workload(n_seqs, 32, 8, 512, 4096, seed, device)
+
+
+def prefill_chunked_qwen3_8b(seed=5, device="cpu", n_seqs=16):
+    return prefill_workload(n_seqs, 32, 8, 0, 0, seed, device, prefix_lo=0, prefix_hi=8192,
+                            chunk=2048)
+
+
+def decode_bytes(context_lens, Hq, Hk, D=HEAD_DIM, max_blocks=0):
+    """Algorithmic HBM bytes of one paged decode call (K+V rows, q, out, tables)."""
+    ctx = int(torch.as_tensor(context_lens).to(torch.int64).clamp(min=0).sum())
+    bs = int(torch.as_tensor(context_lens).numel())
+    return ctx * Hk * D * 2 * 2 + bs * Hq * D * 2 * 2 + bs * 4 * (max_blocks + 1)

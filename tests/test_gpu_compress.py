@@ -1,0 +1,159 @@
+"""Compression step on the GPU vs the oracle.
+
+* importance (fp32) within rtol 1e-4 of the oracle's fp32 SnapKV importance;
+* kept-index sets bit-exact given identical scores (the oracle's selection
+  applied to the GPU importance);
+* compaction, context_lens, events, block tables and slot maps bit-exact given
+  identical kept indices;
+* kept sets vs the reference's bf16 scoring chain: overlap reported and
+  bounded below (bf16 ties make exact equality impossible).
+"""
+import importlib
+from types import SimpleNamespace
+
+import pytest
+import torch
+
+from oracle.compress_ref import (compress_compact_ref, get_tail_window_and_tail_slots_ref,
+                                 gather_kv_by_slots_ref, select_topk_ref, snapkv_importance_ref)
+
+pytestmark = pytest.mark.gpu
+wl_mod = importlib.import_module("nanokv-llm_amd.workloads")
+cu = importlib.import_module("nanokv-llm_amd.layers.compress_utils")
+
+W, KEEP = 4, 2 * 256 + 1
+
+
+def _state(seed=3, bs=64, topk=8):
+    return wl_mod.compress_workload(bs, 32, 8, 1500, 4096, topk, seed, selected_only=True)
+
+
+def _oracle_importance(wl, agg, dtype="fp32"):
+    sel = torch.tensor(wl["seq_idx"])
+    slots, *_ = get_tail_window_and_tail_slots_ref(wl["block_tables"], wl["context_lens"], sel,
+                                                   256, W)
+    k_sub, _ = gather_kv_by_slots_ref(wl["k_cache"], wl["v_cache"], slots)
+    q_sub = wl["q"].index_select(0, sel).unsqueeze(2)
+    return snapkv_importance_ref(q_sub, k_sub, 1, dtype, agg)
+
+
+@pytest.mark.parametrize("agg", ["all", "group"])
+def test_select_matches_oracle(nkv, dev, agg):
+    wl = _state()
+    kg = wl["k_cache"].to(dev)
+    keep, imp = cu.compress_select(
+        wl["q"].to(dev), kg, wl["block_tables"].to(dev), wl["context_lens"].to(dev),
+        torch.tensor(wl["seq_idx"], dtype=torch.int32, device=dev), W, KEEP - 2, 128 ** -0.5,
+        agg)
+    torch.cuda.synchronize()
+    ref_imp = _oracle_importance(wl, agg, "fp32")
+    assert torch.allclose(imp.cpu(), ref_imp, rtol=1e-4, atol=1e-7)
+    # bit-exact selection given identical scores
+    exp = select_topk_ref(imp.cpu(), KEEP - 2)
+    got = keep.cpu().to(torch.int64)
+    assert torch.equal(got[..., 1:-1], exp)
+    assert torch.all(got[..., 0] == 0) and torch.all(got[..., -1] == W * 256 - 1)
+    # against the reference's bf16 chain: overlap of the kept middles
+    b16 = select_topk_ref(_oracle_importance(wl, agg, "bf16"), KEEP - 2)
+    for r in range(exp.size(0)):
+        for s in range(exp.size(1)):
+            a, b = set(exp[r, s].tolist()), set(b16[r, s].tolist())
+            assert len(a & b) / len(a) >= 0.85
+
+
+def test_topk_ties_and_extremes(nkv, dev):
+    imp = torch.zeros(3, 1023)
+    imp[0] = 1.0  # all tied -> lowest indices
+    imp[1] = torch.arange(1023).float()  # strictly increasing -> the last ones
+    imp[2, ::2] = 0.5
+    imp[2, 1::2] = -0.25  # negative values order correctly
+    out = torch.empty(3, 513, dtype=torch.int32, device=dev)
+    lib = importlib.import_module("nanokv-llm_amd._lib")
+    rc = lib.lib().nkv_compress_topk(imp.to(dev).data_ptr(), 3, 1023, 511, out.data_ptr(),
+                                     lib.stream_of(out))
+    lib.check(rc, "topk")
+    torch.cuda.synchronize()
+    exp = select_topk_ref(imp, 511)
+    assert torch.equal(out.cpu()[:, 1:-1].long(), exp)
+
+
+@pytest.mark.parametrize("agg", ["all", "group"])
+def test_compact_and_finalize_bit_exact(nkv, dev, agg):
+    wl = _state(seed=5)
+    bt = wl["block_tables"]
+    kg, vg = wl["k_cache"].to(dev), wl["v_cache"].to(dev)
+    btg = bt.to(dev)
+    base = wl["context_lens"].to(dev)
+    ctx = base.clone()
+    sel = torch.tensor(wl["seq_idx"], dtype=torch.int32, device=dev)
+    keep, _ = cu.compress_select(wl["q"].to(dev), kg, btg, base, sel, W, KEEP - 2, 128 ** -0.5,
+                                 agg)
+    cu.compress_compact(kg, vg, btg, base, ctx, sel, keep, W)
+    events = torch.empty(len(wl["seq_idx"]), 4 + bt.size(1), dtype=torch.int32, device=dev)
+    slots = torch.arange(bt.size(0), dtype=torch.int32, device=dev) * 7
+    cu.compress_finalize(btg, base, sel, KEEP, 256, W, events, rewrite_tables=True,
+                         slot_mapping=slots)
+    torch.cuda.synchronize()
+    kc, vc = wl["k_cache"].clone(), wl["v_cache"].clone()
+    ctx_ref = wl["context_lens"].clone()
+    ok, _, ev_ref = compress_compact_ref(None, kc, vc, bt, wl["context_lens"], ctx_ref,
+                                         wl["seq_idx"], 256, W, 2, 1, 0, 1,
+                                         keep_idx=keep.cpu().long())
+    assert ok
+    assert torch.equal(kg.cpu(), kc) and torch.equal(vg.cpu(), vc)
+    assert torch.equal(ctx.cpu(), ctx_ref)
+    assert cu.events_to_dicts(events, 0) == ev_ref
+    bt_exp = bt.clone()
+    slot_exp = (torch.arange(bt.size(0), dtype=torch.int32) * 7)
+    for ev in ev_ref:
+        s = ev["batch_index"]
+        bt_exp[s, ev["keep_blocks"]:] = -1
+        n = ev["new_context_len"]
+        slot_exp[s] = int(bt[s, n // 256]) * 256 + n % 256
+    assert torch.equal(btg.cpu(), bt_exp)
+    assert torch.equal(slots.cpu(), slot_exp)
+
+
+def test_my_compress_compact_drop_in(nkv, dev):
+    """MyCompressCompact through the Context over 2 layers; events on the last one."""
+    wl = _state(seed=7, bs=48, topk=6)
+    base = wl["context_lens"].to(dev)
+    nkv.set_context(True, slot_mapping=torch.zeros(48, dtype=torch.int32, device=dev),
+                    context_lens=base.clone(), block_tables=wl["block_tables"].to(dev))
+    ctx = nkv.get_context()
+    ctx.is_compress_step = True
+    ctx.compress_selected_batch_indices = list(wl["seq_idx"])
+    ctx.compress_base_context_lens = base
+    caches = [(wl["k_cache"].to(dev), wl["v_cache"].to(dev)) for _ in range(2)]
+    q = wl["q"].to(dev)
+    for layer, (kg, vg) in enumerate(caches):
+        assert nkv.MyCompressCompact(q, kg, vg, layer, 256, W, 2, 1, 2, context=ctx)
+        if layer == 0:
+            assert ctx.compression_events == []
+    torch.cuda.synchronize()
+    evs = ctx.compression_events
+    assert [e["batch_index"] for e in evs] == list(wl["seq_idx"])
+    assert all(e["layer"] == 1 for e in evs)
+    lens = wl["context_lens"]
+    for e in evs:
+        assert e["new_context_len"] == int(lens[e["batch_index"]]) - 1024 + KEEP
+    assert torch.equal(ctx.context_lens.cpu()[wl["seq_idx"]],
+                       lens[wl["seq_idx"]] - 1024 + KEEP)
+    # both layers compacted identically (same q, same K)
+    assert torch.equal(caches[0][0], caches[1][0]) and torch.equal(caches[0][1], caches[1][1])
+    nkv.reset_context()
+
+
+def test_snapkv_plugin_api(nkv, dev):
+    g = torch.Generator().manual_seed(9)
+    Q = torch.randn(3, 32, 1, 128, generator=g).to(torch.bfloat16)
+    K = torch.randn(3, 8, 1024, 128, generator=g).to(torch.bfloat16)
+    out = nkv.SnapKV(Q.to(dev), K.to(dev), None, num_keep=511, window=1)
+    assert out.dtype == torch.int64 and out.shape == (3, 513)
+    imp = snapkv_importance_ref(Q, K, 1, "fp32", "all")
+    ref = select_topk_ref(imp, 511)[:, 0]
+    got = out.cpu()[:, 1:-1]
+    for r in range(3):
+        overlap = len(set(got[r].tolist()) & set(ref[r].tolist())) / 511
+        assert overlap >= 0.99
+    assert nkv.SnapKV(Q.to(dev), K[:, :, :256].contiguous().to(dev), None, 300, 1) is False

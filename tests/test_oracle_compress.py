@@ -1,0 +1,195 @@
+"""Pins the oracle's compression step against brute force and closed forms (CPU).
+
+Inputs plant the mistakes a restatement could make: a sink token with the
+largest raw score (dropped -inf mask), heads that disagree (wrong head sum),
+heads with different score spreads (dropped scale), the last window token
+with a huge score (scored instead of always kept), and a per-slot brute force
+of the two-phase compaction on tiny blocks.
+"""
+import math
+
+import pytest
+import torch
+
+from oracle.compress_ref import (compress_compact_ref, get_tail_window_and_tail_slots_ref,
+                                 select_topk_ref, snapkv_importance_ref, snapkv_ref)
+
+
+def _brute_importance(Q, K, scale, agg):
+    """float64 loops: softmax over keys 1..L-2 (key 0 masked, key L-1 unscored)."""
+    m, Hk, L, D = K.shape
+    Hq = Q.size(1)
+    g = Hq // Hk
+    n_sets = 1 if agg == "all" else Hk
+    imp = torch.zeros(m, n_sets, L - 1, dtype=torch.float64)
+    for b in range(m):
+        for h in range(Hq):
+            s = [float((Q[b, h, 0].double() * K[b, h // g, t].double()).sum()) * scale
+                 for t in range(L - 1)]
+            mx = max(s[1:])
+            w = [0.0] + [math.exp(x - mx) for x in s[1:]]
+            z = sum(w)
+            for t in range(L - 1):
+                imp[b, 0 if agg == "all" else h // g, t] += w[t] / z
+    return imp
+
+
+def _brute_topk(imp_row, k):
+    idx = sorted(range(len(imp_row)), key=lambda i: (-float(imp_row[i]), i))[:k]
+    return sorted(idx)
+
+
+def _planted(seed, m=2, Hq=4, Hk=2, L=12, D=8):
+    g = torch.Generator().manual_seed(seed)
+    Q = torch.randn(m, Hq, 1, D, generator=g)
+    K = torch.randn(m, Hk, L, D, generator=g)
+    # sink: key 0 aligned with every query -> largest raw score
+    K[:, :, 0] = Q[:, ::Hq // Hk, 0] * 4
+    # last window token: huge score, must not influence the softmax
+    K[:, :, L - 1] = Q[:, ::Hq // Hk, 0] * 8
+    # head 1 of KV group 0 gets a 3x sharper spread (scale matters)
+    Q[:, 1] *= 3
+    return Q, K
+
+
+@pytest.mark.parametrize("agg", ["all", "group"])
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_importance_fp32_matches_brute_force(agg, seed):
+    Q, K = _planted(seed)
+    imp = snapkv_importance_ref(Q, K, 1, "fp32", agg)
+    exp = _brute_importance(Q, K, K.size(-1) ** -0.5, agg)
+    assert torch.allclose(imp.double(), exp, atol=1e-6)
+    assert torch.all(imp[..., 0] == 0)  # sink masked
+
+
+@pytest.mark.parametrize("agg", ["all", "group"])
+def test_snapkv_fp32_matches_brute_force(agg):
+    Q, K = _planted(3, m=3, L=16)
+    num_keep = 5
+    final = snapkv_ref(Q, K, None, num_keep=num_keep, window=1, score_dtype="fp32", agg=agg)
+    exp_imp = _brute_importance(Q, K, K.size(-1) ** -0.5, agg)
+    final = final.view(3, -1, num_keep + 2)
+    for b in range(3):
+        for s in range(final.size(1)):
+            row = final[b, s].tolist()
+            assert row[0] == 0 and row[-1] == 15 and len(row) == num_keep + 2
+            assert row[1:-1] == _brute_topk(exp_imp[b, s].tolist(), num_keep)
+            assert row[1:-1] == sorted(row[1:-1])
+
+
+def test_snapkv_skip_rule():
+    Q, K = _planted(4, L=8)
+    assert snapkv_ref(Q, K, None, num_keep=7, window=1) is False  # L <= num_keep + window
+    assert snapkv_ref(Q, K, None, num_keep=6, window=1) is not False
+
+
+def test_topk_tie_rule_lower_index():
+    imp = torch.tensor([[0.0, 0.5, 0.2, 0.5, 0.5, 0.1, 0.2]])
+    assert select_topk_ref(imp, 2).tolist() == [[1, 3]]
+    assert select_topk_ref(imp, 4).tolist() == [[1, 2, 3, 4]]
+    assert select_topk_ref(imp, 5).tolist() == [[1, 2, 3, 4, 6]]
+
+
+def test_bf16_path_equals_fp32_on_separated_scores():
+    # keys of distinct, well separated strengths: bf16 rounding cannot reorder
+    m, Hq, Hk, L, D = 2, 4, 2, 32, 16
+    g = torch.Generator().manual_seed(5)
+    Q = torch.zeros(m, Hq, 1, D)
+    Q[:, :, 0, 0] = 1.0
+    K = torch.zeros(m, Hk, L, D)
+    strengths = torch.randperm(L, generator=g).float() * 0.5
+    K[:, :, :, 0] = strengths * (D ** 0.5) / 4
+    f32 = snapkv_ref(Q, K, None, num_keep=9, window=1, score_dtype="fp32")
+    b16 = snapkv_ref(Q, K, None, num_keep=9, window=1, score_dtype="bf16")
+    assert torch.equal(f32, b16)
+
+
+# --------------------------------------------------------------- compaction
+def _brute_compact(kc, vc, bt, lens, seq_idxs, B, W, keep_idx, keep_tokens):
+    """Per-slot loop: snapshot the sources, then write the destinations."""
+    kf, vf = kc.view(-1, kc.size(2), kc.size(3)), vc.view(-1, vc.size(2), vc.size(3))
+    snap_k, snap_v = kf.clone(), vf.clone()
+    for j, s in enumerate(seq_idxs):
+        n = int(lens[s])
+        full, tail = n // B, n % B
+        wslot = [int(bt[s, full - W + p // B]) * B + p % B for p in range(W * B)]
+        for i in range(keep_tokens):
+            src = wslot[int(keep_idx[j, i])]
+            kf[wslot[i]] = snap_k[src]
+            vf[wslot[i]] = snap_v[src]
+        for u in range(tail):
+            src = int(bt[s, full]) * B + u
+            dst = wslot[keep_tokens - 1] + 1 + u
+            kf[dst] = snap_k[src]
+            vf[dst] = snap_v[src]
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_compaction_matches_brute_force(seed):
+    B, W, keep_blocks, extra = 4, 4, 2, 1
+    keep_tokens = keep_blocks * B + extra  # 9 of a 16-token window
+    g = torch.Generator().manual_seed(seed)
+    nb, Hk, D = 24, 2, 4
+    kc = torch.randn(nb, B, Hk, D, generator=g)
+    vc = torch.randn(nb, B, Hk, D, generator=g)
+    lens = torch.tensor([19, 16, 22, 9], dtype=torch.int32)  # tails 3, 0, 2, (too short)
+    perm = torch.randperm(nb, generator=g).tolist()
+    bt = torch.full((4, 6), -1, dtype=torch.int32)
+    p = 0
+    for i, n in enumerate(lens.tolist()):
+        nblk = math.ceil(n / B)
+        bt[i, :nblk] = torch.tensor(perm[p:p + nblk])
+        p += nblk
+    seq_idxs = [0, 1, 2]
+    q = torch.randn(4, 4, D, generator=g)
+    kc2, vc2 = kc.clone(), vc.clone()
+    ctx = lens.clone()
+    ok, keep_idx, events = compress_compact_ref(
+        q, kc2, vc2, bt, lens, ctx, seq_idxs, B, W, keep_blocks, extra, 0, 1,
+        score_dtype="fp32")
+    assert ok
+    exp_k, exp_v = kc.clone(), vc.clone()
+    _brute_compact(exp_k, exp_v, bt, lens, seq_idxs, B, W, keep_idx[:, 0], keep_tokens)
+    assert torch.equal(kc2, exp_k) and torch.equal(vc2, exp_v)
+    # closed forms: new_len = len - W*B + keep; keep_blocks = ceil(new_len / B)
+    assert ctx.tolist() == [19 - 16 + 9, 16 - 16 + 9, 22 - 16 + 9, 9]
+    for ev, s in zip(events, seq_idxs):
+        n = int(lens[s])
+        new_len = n - W * B + keep_tokens
+        kb = math.ceil(new_len / B)
+        assert ev["batch_index"] == s and ev["new_context_len"] == new_len
+        assert ev["keep_blocks"] == kb
+        nblk = math.ceil(n / B)
+        assert ev["freed_block_ids"] == bt[s, kb:nblk].tolist()
+        # full=F, tail=t: frees 1 block if t == 0 else 2 (W=4, keep=2B+1)
+        assert len(ev["freed_block_ids"]) == (1 if n % B == 0 else 2)
+
+
+def test_compaction_group_mode_moves_heads_independently():
+    B, W = 4, 4
+    g = torch.Generator().manual_seed(7)
+    kc = torch.randn(8, B, 2, 4, generator=g)
+    vc = torch.randn(8, B, 2, 4, generator=g)
+    bt = torch.tensor([[0, 1, 2, 3, 4]], dtype=torch.int32)
+    lens = torch.tensor([18], dtype=torch.int32)
+    keep = torch.stack([torch.tensor([0, 2, 3, 5, 7, 8, 9, 12, 14, 15]),
+                        torch.tensor([0, 1, 4, 6, 10, 11, 12, 13, 14, 15])]).unsqueeze(0)
+    kc2, vc2 = kc.clone(), vc.clone()
+    compress_compact_ref(None, kc2, vc2, bt, lens, lens.clone(), [0], B, W, 2, 2, 0, 2,
+                         keep_idx=keep)
+    kf, kf2 = kc.view(-1, 2, 4), kc2.view(-1, 2, 4)
+    for h in range(2):
+        for i in range(10):
+            assert torch.equal(kf2[i, h], kf[int(keep[0, h, i]), h])
+        for u in range(2):  # tail rows of block 4 follow the kept rows
+            assert torch.equal(kf2[10 + u, h], kf[16 + u, h])
+
+
+def test_window_location_closed_form():
+    bt = torch.tensor([[7, 3, 9, 1, 4, 2], [5, 6, 8, 0, -1, -1]], dtype=torch.int32)
+    lens = torch.tensor([21, 16], dtype=torch.int32)
+    slots, old, tail, tail_ids = get_tail_window_and_tail_slots_ref(
+        bt, lens, torch.tensor([0, 1]), 4, 3)
+    assert slots[0].tolist() == [b * 4 + o for b in (9, 1, 4) for o in range(4)]
+    assert slots[1].tolist() == [b * 4 + o for b in (6, 8, 0) for o in range(4)]
+    assert tail.tolist() == [1, 0] and tail_ids.tolist() == [2, -1]
