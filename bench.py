@@ -86,7 +86,7 @@ def run_decode(args, dev):
                    "split")
         if ev:
             ev[2].record(stream)
-        _lib.check(lib.nkv_paged_decode_combine(ctx.data_ptr(), bs, Hq, D, B, width,
+        _lib.check(lib.nkv_paged_decode_combine(ctx.data_ptr(), bs, Hq, Hk, D, B, width,
                                                 out.data_ptr(), out.stride(0), ws.data_ptr(),
                                                 ws.numel(), sh), "combine")
         if ev:
@@ -257,7 +257,7 @@ def main():
         "store_us": round(r["store_ms"] * 1e3, 2),
         "parity_max_abs_err": r["parity_max_abs_err"],
         "roofline": {
-            "kernel": "paged_decode_split_kernel<4>",
+            "kernel": "paged_decode_split_kernel<4> (stream-K split)",
             "bound": "hbm",
             "achieved": round(split_gbs, 1),
             "peak": HBM_PEAK_GBS,

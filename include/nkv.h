@@ -63,10 +63,12 @@ int nkv_store_kvcache(const void* key, int64_t key_row_stride,
  *   out[b,h] = sum_{t<ctx_b} softmax_t(scale * q[b,h].K[b,t,h/g]) V[b,t,h/g]
  * with K[b,t] = k_cache row (block_tables[b, t/block_size]*block_size
  * + t%block_size). Sequences with context_lens[b] <= 0 produce zeros.
- * Split-K: one work unit per 256 tokens of a sequence and KV head, then a
- * combine pass. workspace must hold nkv_paged_decode_workspace_bytes(...).
+ * Balanced split-K over 16-token chunks, then a combine pass; workspace
+ * must hold nkv_paged_decode_workspace_bytes(...).
  * q[b,h,d] at q[b*q_row_stride + h*head_dim + d]; out likewise with
- * out_row_stride. head_dim must be 128; n_q_heads/n_kv_heads in {1,2,4,8,16}.
+ * out_row_stride. head_dim must be 128; n_q_heads/n_kv_heads in {1,2,4,8,16};
+ * block_size a multiple of 16. Block-table entries outside [0, n_blocks)
+ * contribute nothing.
  * Replaces: flash_attn_with_kvcache(q.unsqueeze(1), k_cache, v_cache,
  *           cache_seqlens=context_lens, block_table=block_tables,
  *           softmax_scale=scale, causal=True),
@@ -98,7 +100,7 @@ int nkv_paged_decode_split(const void* q, int64_t q_row_stride,
                            int64_t n_blocks, float scale,
                            void* workspace, size_t workspace_bytes, void* stream);
 int nkv_paged_decode_combine(const int32_t* context_lens, int32_t batch,
-                             int32_t n_q_heads, int32_t head_dim,
+                             int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
                              int32_t block_size, int32_t max_blocks_per_seq,
                              void* out, int64_t out_row_stride,
                              const void* workspace, size_t workspace_bytes,

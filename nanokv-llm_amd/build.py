@@ -21,9 +21,12 @@ LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 ARCH = os.environ.get("NKV_OFFLOAD_ARCH", "gfx950")
 
 # -packed-fp32-ops: keep the compiler from forming v_pk_{add,mul,fma}_f32.
+# -amdgpu-mfma-vgpr-form: MFMA accumulators stay in VGPRs, so the online-softmax
+#   rescale of an accumulator needs no AGPR<->VGPR copies.
 HIP_FLAGS = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-munsafe-fp-atomics", "-Wall", "-Wno-unused-function",
 ]
 

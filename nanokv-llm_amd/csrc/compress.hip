@@ -31,6 +31,8 @@ namespace nkv {
 
 constexpr int kCD = 128;      // head_dim
 constexpr int kChunk = 256;   // keys per scoring workgroup
+constexpr int kMaxWindowBlocks = 64;
+constexpr int kMaxRows = 1024;  // kept tokens + tail rows per compaction unit
 
 // ------------------------------------------------------------------ score
 // scores[j][h][t] for t < Lw (window tokens); t == 0 and t == Lw-1 are -inf
@@ -79,7 +81,6 @@ __global__ __launch_bounds__(256) void compress_score_kernel(
       srow[(int64_t)(i / kChunk) * Lw + i % kChunk] = -INFINITY;
     return;
   }
-  const uint4 zero4 = make_uint4(0, 0, 0, 0);
   uint4 kreg[4][4];
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
@@ -88,13 +89,14 @@ __global__ __launch_bounds__(256) void compress_score_kernel(
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) kreg[g][ks] = *reinterpret_cast<const uint4*>(kp + ks * 32);
   }
+  __builtin_amdgcn_sched_barrier(0);  // all loads issued before the first MFMA
   uint4 qreg[4];
   {
     const int hr = lane & 15;
-    const bf16_t* qp = q + qrow * q_row_stride + (int64_t)(kvh * G + hr) * kCD + (lane >> 4) * 8;
+    const int hc = hr < G ? hr : 0;  // MFMA rows >= g are computed and discarded
+    const bf16_t* qp = q + qrow * q_row_stride + (int64_t)(kvh * G + hc) * kCD + (lane >> 4) * 8;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-      qreg[ks] = (hr < G) ? *reinterpret_cast<const uint4*>(qp + ks * 32) : zero4;
+    for (int ks = 0; ks < 4; ++ks) qreg[ks] = *reinterpret_cast<const uint4*>(qp + ks * 32);
   }
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
@@ -257,49 +259,72 @@ __global__ __launch_bounds__(256) void compress_compact_kernel(
   if (full < window_blocks || full > max_blocks || (tail > 0 && full >= max_blocks)) return;
   const int32_t* bt = block_tables + (int64_t)seq * bt_row_stride;
   const int wb0 = full - window_blocks;
-  const int64_t n_slots = n_blocks * B;
   const int32_t* kidx = keep_idx + ((int64_t)j * n_sets + (n_sets > 1 ? kvh : 0)) * keep_tokens;
   const int Lw = window_blocks * B;
 
-  auto window_slot = [&](int p) -> int64_t {
-    const int64_t pb = bt[wb0 + p / B];
-    return (pb >= 0 && pb < n_blocks) ? pb * B + p % B : -1;
-  };
-  const int64_t tail_pb = tail > 0 ? (int64_t)bt[full] : -1;
-  const int64_t last_dst = window_slot(keep_tokens - 1);
-  const int nrows = keep_tokens + tail;
+  // phase 0: the unit's physical blocks (window, then tail) into LDS
+  __shared__ int32_t win_pb[kMaxWindowBlocks + 1];
+  __shared__ int32_t src_lds[kMaxRows];
+  __shared__ int32_t dst_lds[kMaxRows];
+  if (threadIdx.x <= window_blocks) {
+    int32_t pb = -1;
+    if (threadIdx.x < window_blocks) pb = bt[wb0 + threadIdx.x];
+    else if (tail > 0) pb = bt[full];
+    win_pb[threadIdx.x] = (pb >= 0 && pb < n_blocks) ? pb : -1;
+  }
+  __syncthreads();
 
+  // phase 1: source and destination slot of every row of the unit into LDS
+  // (-1 = row not moved). block_size is a power of two (checked on the host).
+  const int lb = 31 - __builtin_clz(B);
+  const int32_t tail_pb = win_pb[window_blocks];
+  const int32_t last_pb = win_pb[(keep_tokens - 1) >> lb];
+  const int32_t last_dst = last_pb >= 0 ? last_pb * B + ((keep_tokens - 1) & (B - 1)) : -1;
+  const int nrows = keep_tokens + tail;
+  const int64_t n_slots = n_blocks * B;
+  for (int i = threadIdx.x; i < ROUNDS * 32; i += blockDim.x) {
+    int32_t sv = -1, d = -1;
+    if (i < keep_tokens) {
+      const int p = kidx[i];
+      if (p >= 0 && p < Lw) {
+        const int32_t pb = win_pb[p >> lb];
+        if (pb >= 0) sv = pb * B + (p & (B - 1));
+      }
+      const int32_t pd = win_pb[i >> lb];
+      if (pd >= 0) d = pd * B + (i & (B - 1));
+    } else if (i < nrows) {
+      const int u = i - keep_tokens;
+      if (tail_pb >= 0) sv = tail_pb * B + u;
+      if (last_dst >= 0 && (int64_t)last_dst + 1 + u < n_slots) d = last_dst + 1 + u;
+    }
+    const bool ok = sv >= 0 && d >= 0;
+    src_lds[i] = ok ? sv : -1;
+    dst_lds[i] = ok ? d : -1;
+  }
+  __syncthreads();
+
+  // phase 2: every source row of the unit, as unconditional 128-bit loads
+  // (rows that are not moved re-read slot 0, always valid)
   bf16_t* cache = is_v ? v_cache : k_cache;
   const int64_t row = (int64_t)Hk * kCD;
   const int64_t col = (int64_t)kvh * kCD + half * 64 + (threadIdx.x & 7) * 8;
-  const int rsub = threadIdx.x >> 3;  // 0..31
-
-  uint4 reg[ROUNDS];
-  int64_t dst[ROUNDS];
+  const int rsub = threadIdx.x >> 3;  // 0..31: row within a round
+  u32x4_t reg[ROUNDS];
 #pragma unroll
   for (int rr = 0; rr < ROUNDS; ++rr) {
-    const int i = rr * 32 + rsub;
-    int64_t src = -1, d = -1;
-    if (i < keep_tokens) {
-      const int p = kidx[i];
-      if (p >= 0 && p < Lw) src = window_slot(p);
-      d = window_slot(i);
-    } else if (i < nrows) {
-      const int u = i - keep_tokens;
-      if (tail_pb >= 0 && tail_pb < n_blocks) src = tail_pb * B + u;
-      if (last_dst >= 0) d = last_dst + 1 + u;
-    }
-    if (src < 0 || src >= n_slots || d < 0 || d >= n_slots) d = -1;
-    dst[rr] = d;
-    reg[rr] = (d >= 0) ? *reinterpret_cast<const uint4*>(cache + src * row + col)
-                       : make_uint4(0, 0, 0, 0);
+    const int32_t sv = max(src_lds[rr * 32 + rsub], 0);
+    reg[rr] = *reinterpret_cast<const u32x4_t*>(cache + (int64_t)sv * row + col);
   }
+  __builtin_amdgcn_sched_barrier(0);
   // all reads of the unit land before any write (two-phase semantics)
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  // phase 3: writes
 #pragma unroll
-  for (int rr = 0; rr < ROUNDS; ++rr)
-    if (dst[rr] >= 0) *reinterpret_cast<uint4*>(cache + dst[rr] * row + col) = reg[rr];
+  for (int rr = 0; rr < ROUNDS; ++rr) {
+    const int32_t d = dst_lds[rr * 32 + rsub];
+    if (d >= 0) *reinterpret_cast<u32x4_t*>(cache + (int64_t)d * row + col) = reg[rr];
+  }
 
   if (blockIdx.x % (4 * Hk) == 0 && threadIdx.x == 0)
     context_lens[seq] = len - Lw + keep_tokens;
@@ -462,6 +487,12 @@ extern "C" int nkv_compress_compact(void* k_cache, void* v_cache, const int32_t*
               "compress_compact: caches must be 16-byte aligned");
   NKV_REQUIRE(max_blocks_per_seq > 0 && bt_row_stride >= max_blocks_per_seq, NKV_EINVAL,
               "compress_compact: bad block table width/stride");
+  NKV_REQUIRE((block_size & (block_size - 1)) == 0, NKV_EUNSUPPORTED,
+              "compress_compact: block_size must be a power of two (got %d)", block_size);
+  NKV_REQUIRE(window_blocks <= kMaxWindowBlocks, NKV_EUNSUPPORTED,
+              "compress_compact: window_blocks > %d", kMaxWindowBlocks);
+  NKV_REQUIRE(n_blocks * block_size < (1ll << 31), NKV_EUNSUPPORTED,
+              "compress_compact: pool of %lld slots exceeds 2^31", (long long)(n_blocks * block_size));
   hipStream_t s = as_stream(stream);
   const unsigned grid = (unsigned)(m * n_kv_heads * 4);
 #define NKV_COMPACT_LAUNCH(R)                                                                  \

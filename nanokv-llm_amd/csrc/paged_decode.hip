@@ -6,228 +6,315 @@
 // causal=True) at nanokvllm/layers/attention.py:104-107.
 //
 // MI355X design (HBM-bound: every K/V byte is read exactly once):
-//  * Split-K work unit = (sequence b, KV head, 256-token split). One
-//    workgroup of 4 wave64s per unit; wave w owns tokens [64w, 64w+64).
-//    A unit streams 64 KiB of K + 64 KiB of V (256 rows x 256 B, rows 2 KiB
-//    apart in the cache), issued up front as 16+16 128-bit loads per lane so
-//    each wave keeps 16 KiB in flight.
-//  * QK^T runs on the matrix cores: v_mfma_f32_16x16x32_bf16 with the g query
-//    heads of the KV head as rows (rows >= g are zero) and 16 keys as columns;
-//    the B operand is loaded straight from HBM in the MFMA lane layout
-//    (lane l: key l%16, dims 8*(l/16)..+8 of each 32-dim step).
-//  * Softmax max/sum are wavefront shuffle reductions over the split's 256
-//    scores staged in LDS; probabilities go back to LDS for the PV product.
-//  * PV is VALU FMA on fp32 (V rows are token-major, the wrong orientation
-//    for the MFMA B operand); lanes reduce with shuffles, waves through LDS.
-//  * Partial (m, l, O) per split go to the workspace; a combine kernel merges
-//    the splits of each (sequence, query head) and writes bf16.
+//  * Balanced split-K ("stream-K"): the K/V stream of the batch is cut into
+//    16-token chunks ordered (sequence, KV head, chunk). Persistent one-wave
+//    workgroups, as many as are resident at once, each take an equal
+//    contiguous range of C chunks, so every wave moves the same number of
+//    bytes whatever the context-length mix. A range crosses at most a few
+//    (sequence, KV head) segments; each segment it touches yields one
+//    partial (m, l, O) in slot  wave - first_wave_of_the_segment.
+//  * Within a segment the wave streams chunks through a register ring of
+//    DEPTH chunks: K (4 x 16 B per lane) and V (4 x 16 B per lane) of chunk
+//    j+DEPTH are issued as soon as chunk j has been consumed. Loads are
+//    raw buffer loads whose per-chunk descriptor covers only the chunk's
+//    valid rows: keys past the context, chunks of other waves and invalid
+//    block-table entries read as zero without touching memory.
+//  * Both contractions run on the matrix cores:
+//      S^T = K q^T   v_mfma_f32_16x16x32_bf16, A = 16 keys (straight from
+//                    the K loads), B = the g query heads of the KV head;
+//                    lane l ends up with head l%16, keys 4(l/16)..+3.
+//      O^T += V^T P^T v_mfma_f32_16x16x16_bf16 per 16-dim block; the B
+//                    operand is exactly the lane's 4 softmax weights (bf16),
+//                    the A operand V^T comes from LDS with ds_read_b64_tr_b16
+//                    (the chunk's V rows are staged row-major in LDS).
+//    Every lane holds state for one head (its column): the online softmax
+//    needs no cross-lane traffic except one xor-max over the 4 key groups.
+//  * A combine kernel merges the few partials of each (sequence, query head).
 // Scores are kept in the log2 domain (scale * log2 e folded in) so the
 // exponentials are single v_exp_f32 instructions.
 #include "nkv_common.h"
 
+#include <algorithm>
+
 namespace nkv {
 
-constexpr int kD = 128;       // head_dim
-constexpr int kSplit = 256;   // tokens per split-K work unit
-constexpr int kWaves = 4;     // wave64s per workgroup
-constexpr int kTokPerWave = kSplit / kWaves;
+constexpr int kD = 128;                  // head_dim
+constexpr int kChunk = 16;               // tokens per pipeline stage
+constexpr int kMinChunks = 16;           // minimum chunks per wave range
+constexpr int kWinBlocks = 64;           // block ids held per window (one per lane)
+constexpr int kVRow = kD + 16;           // LDS row stride of a staged V chunk (elements)
+constexpr int kBufferFlags = 0x00020000; // raw buffer resource word 3 (dword data)
+constexpr int kDepth = 4;                // ring depth (chunks in flight per wave)
 
-static inline int64_t decode_max_splits(int32_t max_blocks, int32_t block_size) {
-  return ((int64_t)max_blocks * block_size + kSplit - 1) / kSplit;
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
+typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
+
+// Partial slots per (sequence, query head): a head of n chunks is touched by
+// at most ceil(n / kMinChunks) + 1 waves.
+static inline int64_t decode_slots(int32_t max_blocks, int32_t block_size) {
+  const int64_t max_chunks = ((int64_t)max_blocks * block_size + kChunk - 1) / kChunk;
+  return (max_chunks + kMinChunks - 1) / kMinChunks + 1;
+}
+
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(v, o, 64);
+    if (lane >= o) v += y;
+  }
+  return v;
+}
+
+// Cursor over sequences in batches of 64 (one per lane): sequence s owns the
+// global chunks [g_s, g_s + nc_s * Hk), KV-head-major inside.
+struct SeqCursor {
+  int cb;    // first sequence of the loaded batch (uniform)
+  int base;  // global chunk index of sequence cb (uniform)
+  int tot;   // chunks of the batch (uniform)
+  int ctx;   // lane: context length of sequence cb + lane
+  int nc;    // lane: chunks per KV head
+  int incl;  // lane: inclusive prefix of nc * Hk over the batch
+};
+
+__device__ __forceinline__ void seq_load(SeqCursor& c, const int32_t* __restrict__ ctx_lens,
+                                         int batch, int Hk, int max_tokens) {
+  const int s = c.cb + (int)threadIdx.x;
+  c.ctx = s < batch ? ctx_lens[s] : 0;
+  c.nc = c.ctx > 0 ? (min(c.ctx, max_tokens) + kChunk - 1) / kChunk : 0;
+  c.incl = wave_incl_scan(c.nc * Hk);
+  c.tot = __builtin_amdgcn_readlane(c.incl, 63);
 }
 
 template <int G>
-__global__ __launch_bounds__(256) void paged_decode_split_kernel(
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2)))
+void paged_decode_split_kernel(
     const bf16_t* __restrict__ q, int64_t q_row_stride,
     const bf16_t* __restrict__ k_cache, const bf16_t* __restrict__ v_cache,
     const int32_t* __restrict__ block_tables, int64_t bt_row_stride,
     const int32_t* __restrict__ context_lens, int32_t batch, int32_t Hk,
-    int32_t block_size, int32_t max_blocks, int32_t max_splits, int64_t n_blocks,
-    float scale_log2, float* __restrict__ part_o, float* __restrict__ part_ml) {
-  __shared__ float s_lds[G][kSplit];            // scores (log2 domain)
-  __shared__ float p_lds[kSplit][G];            // probabilities, token-major
-  __shared__ float o_lds[kWaves][G][kD];        // per-wave PV partials
-  __shared__ float ml_lds[G][2];
+    int32_t block_size, int32_t max_blocks, int64_t n_blocks, int32_t slots, float scale_log2,
+    float* __restrict__ part_o, float* __restrict__ part_ml, int32_t* __restrict__ nslots) {
+  __shared__ __attribute__((aligned(16))) bf16_t vbuf[kChunk * kVRow];
 
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int kvh = blockIdx.x % Hk;
-  const int rest = blockIdx.x / Hk;
-  const int b = rest % batch;
-  const int split = rest / batch;
-  const int ctx = context_lens[b];
-  const int t0 = split * kSplit;
-  if (t0 >= ctx) return;  // uniform over the workgroup
-
+  const int lane = threadIdx.x;
+  const int g4 = lane >> 4;   // key group: keys 4*g4 .. 4*g4+3 of a chunk
+  const int col = lane & 15;  // MFMA column: query head (S^T, O^T) / key row (K)
   const int Hq = Hk * G;
   const int64_t row = (int64_t)Hk * kD;
-  const int blk = t0 / block_size;
-  const int off0 = t0 - blk * block_size;
-  const int64_t pb = (blk < max_blocks) ? (int64_t)block_tables[(int64_t)b * bt_row_stride + blk] : -1;
-  const int64_t obase = ((int64_t)b * Hq + (int64_t)kvh * G) * max_splits + split;
-  if (pb < 0 || pb >= n_blocks) {  // invalid table entry: empty split
-    for (int i = threadIdx.x; i < G * kD; i += blockDim.x) {
-      const int h = i / kD, d = i % kD;
-      part_o[(obase + (int64_t)h * max_splits) * kD + d] = 0.f;
-      if (d == 0) {
-        part_ml[(obase + (int64_t)h * max_splits) * 2 + 0] = -INFINITY;
-        part_ml[(obase + (int64_t)h * max_splits) * 2 + 1] = 0.f;
+  const int row_b = (int)(row * 2);
+  const int max_tokens = max_blocks * block_size;
+
+  // ---- this wave's chunk range
+  SeqCursor cur;
+  int T = 0;
+  for (cur.cb = 0; cur.cb < batch; cur.cb += 64) {
+    seq_load(cur, context_lens, batch, Hk, max_tokens);
+    T += cur.tot;
+  }
+  const int W = gridDim.x;
+  const int C = max((T + W - 1) / W, kMinChunks);
+  const int k_begin = blockIdx.x * C;
+  if (k_begin >= T) return;
+  const int k_end = min(T, k_begin + C);
+  cur.cb = 0;
+  cur.base = 0;
+  seq_load(cur, context_lens, batch, Hk, max_tokens);
+
+  // per-lane constant load offsets: K as the A operand (lane l: key l%16,
+  // dims 8*(l/16) + 32*ks), V as 4 rows x 256 B (lane l: key 4r + l/16, dims 8*(l%16))
+  const int koff = col * row_b + g4 * 16;
+  const int voff = g4 * row_b + col * 16;
+  const int tr_row = 4 * g4 + (col >> 2);  // ds_read_b64_tr_b16 source row / column
+  const int tr_col = (col & 3) * 4;
+
+  for (int k = k_begin; k < k_end;) {
+    // ---- locate the segment holding global chunk k (wave-uniform)
+    while (k >= cur.base + cur.tot) {
+      cur.base += cur.tot;
+      cur.cb += 64;
+      seq_load(cur, context_lens, batch, Hk, max_tokens);
+    }
+    const int ln = __builtin_amdgcn_readfirstlane(__builtin_ctzll(__ballot(cur.base + cur.incl > k)));
+    const int b = cur.cb + ln;
+    const int ctx = __builtin_amdgcn_readlane(cur.ctx, ln);
+    const int nc = __builtin_amdgcn_readlane(cur.nc, ln);
+    const int gb = cur.base + __builtin_amdgcn_readlane(cur.incl, ln) - nc * Hk;
+    const int kvh = (k - gb) / nc;
+    const int c_lo = k - gb - kvh * nc;
+    const int n_seg = min(nc - c_lo, k_end - k);
+    const int g0 = gb + kvh * nc;
+    const int slot = (int)blockIdx.x - g0 / C;
+
+    // q^T as the MFMA B operand: lane l -> head l%16 (columns >= g re-read
+    // head 0 and are discarded), dims 8*(l/16) + 32*ks .. +8
+    u32x4_t qreg[4];
+    {
+      const int hc = col < G ? col : 0;
+      const u32x4_t* qp = reinterpret_cast<const u32x4_t*>(
+          q + (int64_t)b * q_row_stride + (int64_t)(kvh * G + hc) * kD + g4 * 8);
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) qreg[ks] = qp[ks * 4];
+    }
+    const bf16_t* kbase = k_cache + (int64_t)kvh * kD;
+    const bf16_t* vbase = v_cache + (int64_t)kvh * kD;
+    const int32_t* bt_row = block_tables + (int64_t)b * bt_row_stride;
+
+    f32x4_t acc[8];  // O^T: lane l -> head l%16, dims 16*db + 4*(l/16) .. +3
+#pragma unroll
+    for (int db = 0; db < 8; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.f;
+
+    // windows of at most kWinBlocks cache blocks (block ids one per lane)
+    const int win_cap = (kWinBlocks - 1) * (block_size / kChunk);
+    for (int wc = 0; wc < n_seg; wc += win_cap) {
+      const int wlo = c_lo + wc;                 // first chunk of the window
+      const int wn = min(n_seg - wc, win_cap);   // chunks in the window
+      const int blk0 = wlo * kChunk / block_size;
+      int blk_id = -1;
+      {
+        const int bi = blk0 + lane;
+        if (bi < max_blocks && bi * block_size < (wlo + wn) * kChunk) {
+          const int id = bt_row[bi];
+          blk_id = (id >= 0 && id < n_blocks) ? id : -1;
+        }
+      }
+
+      u32x4_t kreg[kDepth][4];
+      u32x4_t vreg[kDepth][4];
+      int nv[kDepth];  // valid keys of the chunk in each ring slot (0: masked)
+      auto issue = [&](int j, int s) {
+        const int t0 = (wlo + j) * kChunk;
+        const int pb = __builtin_amdgcn_readlane(blk_id, min(t0 / block_size - blk0, 63));
+        const int n = (j < wn && pb >= 0) ? min(max(ctx - t0, 0), kChunk) : 0;
+        nv[s] = n;
+        const int64_t r0 = (int64_t)(pb < 0 ? 0 : pb) * block_size + t0 % block_size;
+        const uint32_t bytes = (uint32_t)(n * row_b);
+        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(kbase + r0 * row), (short)0, bytes, kBufferFlags);
+        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(vbase + r0 * row), (short)0, bytes, kBufferFlags);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+          kreg[s][ks] = __builtin_bit_cast(
+              u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rk, koff + ks * 64, 0, 0));
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          vreg[s][r] = __builtin_bit_cast(
+              u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rv, voff + r * 4 * row_b, 0, 0));
+      };
+
+      auto consume = [&](int s) {
+        // S^T for 16 keys x 16 heads
+        f32x4_t st = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+          st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8_v(kreg[s][ks]),
+                                                        as_bf16x8_v(qreg[ks]), st, 0, 0, 0);
+        // stage V rows (row-major) for the transposed reads
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          *reinterpret_cast<u32x4_t*>(&vbuf[(4 * r + g4) * kVRow + col * 8]) = vreg[s][r];
+        // online softmax for head `col` over keys 4*g4 .. +3 of the chunk
+        float sv[4];
+        float cmax = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          sv[r] = (4 * g4 + r < nv[s]) ? st[r] * scale_log2 : -INFINITY;
+          cmax = fmaxf(cmax, sv[r]);
+        }
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
+        const float m_new = fmaxf(m_run, cmax);
+        const float alpha = (m_new == -INFINITY) ? 1.f : fast_exp2(m_run - m_new);
+        float p[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) p[r] = (sv[r] == -INFINITY) ? 0.f : fast_exp2(sv[r] - m_new);
+        l_run = l_run * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+        m_run = m_new;
+        if (alpha != 1.f) {
+#pragma unroll
+          for (int db = 0; db < 8; ++db) acc[db] *= alpha;
+        }
+        const bf16x2v_t p01 = {(__bf16)p[0], (__bf16)p[1]};
+        const bf16x2v_t p23 = {(__bf16)p[2], (__bf16)p[3]};
+        const uint2 pw = {__builtin_bit_cast(uint32_t, p01), __builtin_bit_cast(uint32_t, p23)};
+        const i16x4_t pb4 = __builtin_bit_cast(i16x4_t, pw);
+        // O^T[dims][heads] += V^T[dims][keys] P^T[keys][heads], 16 dims per MFMA
+#pragma unroll
+        for (int db = 0; db < 8; ++db) {
+          const i16x4_t va = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_i16x4_t*)&vbuf[tr_row * kVRow + db * 16 + tr_col]);
+          acc[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb4, acc[db], 0, 0, 0);
+        }
+      };
+
+      // Ring schedule over the window padded to a multiple of kDepth: every
+      // group but the last refills each slot right after consuming it
+      // (branch-free, so the wait counts stay exact); the last group drains.
+      const int n_groups = (wn + kDepth - 1) / kDepth;
+#pragma unroll
+      for (int s = 0; s < kDepth; ++s) issue(s, s);
+      for (int gi = 0; gi + 1 < n_groups; ++gi) {
+#pragma unroll
+        for (int s = 0; s < kDepth; ++s) {
+          consume(s);
+          __builtin_amdgcn_sched_barrier(0);  // refill only after the slot is consumed
+          issue((gi + 1) * kDepth + s, s);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+#pragma unroll
+      for (int s = 0; s < kDepth; ++s) consume(s);
+    }
+
+    // ---- segment epilogue: l over the four key groups, then the partial
+    l_run += __shfl_xor(l_run, 16, 64);
+    l_run += __shfl_xor(l_run, 32, 64);
+    const int64_t obase = ((int64_t)b * Hq + (int64_t)kvh * G) * slots + slot;
+    if (col < G) {
+      const int64_t prow = obase + (int64_t)col * slots;
+#pragma unroll
+      for (int db = 0; db < 8; ++db)
+        *reinterpret_cast<f32x4_t*>(&part_o[prow * kD + db * 16 + g4 * 4]) = acc[db];
+      if (g4 == 0) {
+        part_ml[prow * 2 + 0] = m_run;
+        part_ml[prow * 2 + 1] = l_run;
       }
     }
-    return;
-  }
-  const int n_valid = min(ctx - t0, kSplit);
-  const int64_t row0 = pb * block_size + off0;  // cache row of the split's first token
-
-  // ---- issue all K and V loads of this wave (16 + 16 x 16 B per lane)
-  uint4 kreg[4][4];  // [16-key group][32-dim step]
-  uint4 vreg[16];
-  const uint4 zero4 = make_uint4(0, 0, 0, 0);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int tw = wave * kTokPerWave + j * 16 + (lane & 15);
-    const bf16_t* kp = k_cache + (row0 + tw) * row + (int64_t)kvh * kD + (lane >> 4) * 8;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-      kreg[j][ks] = (tw < n_valid) ? *reinterpret_cast<const uint4*>(kp + ks * 32) : zero4;
-  }
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int tw = wave * kTokPerWave + (lane >> 4) + 4 * i;
-    const bf16_t* vp = v_cache + (row0 + tw) * row + (int64_t)kvh * kD + (lane & 15) * 8;
-    vreg[i] = (tw < n_valid) ? *reinterpret_cast<const uint4*>(vp) : zero4;
-  }
-
-  // ---- q in the MFMA A layout: lane l -> head row l%16, dims 8*(l/16) of each step
-  uint4 qreg[4];
-  {
-    const int hr = lane & 15;
-    const bf16_t* qp = q + (int64_t)b * q_row_stride + (int64_t)(kvh * G + hr) * kD + (lane >> 4) * 8;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-      qreg[ks] = (hr < G) ? *reinterpret_cast<const uint4*>(qp + ks * 32) : zero4;
-  }
-
-  // ---- S = q K^T on MFMA; lane l holds rows 4*(l/16)+r, key column l%16
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(qreg[ks]), as_bf16x8(kreg[j][ks]),
-                                                     acc, 0, 0, 0);
-    const int tw = wave * kTokPerWave + j * 16 + (lane & 15);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int h = (lane >> 4) * 4 + r;
-      if (h < G) s_lds[h][tw] = (tw < n_valid) ? acc[r] * scale_log2 : -INFINITY;
-    }
-  }
-  __syncthreads();
-
-  // ---- softmax statistics per head (one wave per head)
-  for (int h = wave; h < G; h += kWaves) {
-    float sv[4];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      sv[k] = s_lds[h][lane + 64 * k];
-      mx = fmaxf(mx, sv[k]);
-    }
-    mx = wave_max(mx);
-    float sum = 0.f;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const float p = (mx == -INFINITY) ? 0.f : fast_exp2(sv[k] - mx);
-      p_lds[lane + 64 * k][h] = p;
-      sum += p;
-    }
-    sum = wave_sum(sum);
-    if (lane == 0) {
-      ml_lds[h][0] = mx;
-      ml_lds[h][1] = sum;
-    }
-  }
-  __syncthreads();
-
-  // ---- O = P V on VALU: lane l owns dims 8*(l%16)..+8 of keys (l/16)+4i
-  float acc_o[G][8];
-#pragma unroll
-  for (int h = 0; h < G; ++h)
-#pragma unroll
-    for (int d = 0; d < 8; ++d) acc_o[h][d] = 0.f;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int tw = wave * kTokPerWave + (lane >> 4) + 4 * i;
-    float p[G];
-#pragma unroll
-    for (int h = 0; h < G; ++h) p[h] = p_lds[tw][h];
-    const uint32_t w[4] = {vreg[i].x, vreg[i].y, vreg[i].z, vreg[i].w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float v0 = bf16_lo(w[e]), v1 = bf16_hi(w[e]);
-#pragma unroll
-      for (int h = 0; h < G; ++h) {
-        acc_o[h][2 * e] = fmaf(p[h], v0, acc_o[h][2 * e]);
-        acc_o[h][2 * e + 1] = fmaf(p[h], v1, acc_o[h][2 * e + 1]);
-      }
-    }
-  }
-#pragma unroll
-  for (int h = 0; h < G; ++h)
-#pragma unroll
-    for (int d = 0; d < 8; ++d) {
-      float v = acc_o[h][d];
-      v += __shfl_xor(v, 16, 64);
-      v += __shfl_xor(v, 32, 64);
-      acc_o[h][d] = v;
-    }
-  if (lane < 16) {
-#pragma unroll
-    for (int h = 0; h < G; ++h)
-#pragma unroll
-      for (int d = 0; d < 8; ++d) o_lds[wave][h][lane * 8 + d] = acc_o[h][d];
-  }
-  __syncthreads();
-
-  for (int i = threadIdx.x; i < G * kD; i += blockDim.x) {
-    const int h = i / kD, d = i % kD;
-    float o = 0.f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) o += o_lds[w][h][d];
-    part_o[(obase + (int64_t)h * max_splits) * kD + d] = o;
-    if (d == 0) {
-      part_ml[(obase + (int64_t)h * max_splits) * 2 + 0] = ml_lds[h][0];
-      part_ml[(obase + (int64_t)h * max_splits) * 2 + 1] = ml_lds[h][1];
-    }
+    if (c_lo + n_seg == nc && lane == 0) nslots[(int64_t)b * Hk + kvh] = slot + 1;
+    k += n_seg;
   }
 }
 
-// Merge the splits of one (sequence, query head): O = sum_s 2^(m_s-M) O_s /
-// sum_s 2^(m_s-M) l_s. One workgroup of kD lanes (one dim each) per pair.
-__global__ __launch_bounds__(kD) void paged_decode_combine_kernel(
-    const int32_t* __restrict__ context_lens, int32_t Hq, int32_t max_splits,
+// Merge the partials of one (sequence, query head): O = sum_s 2^(m_s-M) O_s /
+// sum_s 2^(m_s-M) l_s. One wave per pair; each lane owns two output dims.
+__global__ __launch_bounds__(64) void paged_decode_combine_kernel(
+    const int32_t* __restrict__ context_lens, int32_t Hq, int32_t Hk, int32_t slots,
     const float* __restrict__ part_o, const float* __restrict__ part_ml,
-    bf16_t* __restrict__ out, int64_t out_row_stride) {
+    const int32_t* __restrict__ nslots, bf16_t* __restrict__ out, int64_t out_row_stride) {
   const int b = blockIdx.x / Hq;
   const int h = blockIdx.x % Hq;
-  const int d = threadIdx.x;
+  const int lane = threadIdx.x;
   const int ctx = context_lens[b];
-  const int ns = ctx > 0 ? min((ctx + kSplit - 1) / kSplit, max_splits) : 0;
-  const int64_t base = ((int64_t)b * Hq + h) * max_splits;
+  const int ns = ctx > 0 ? min(nslots[(int64_t)b * Hk + h / (Hq / Hk)], slots) : 0;
+  const int64_t base = ((int64_t)b * Hq + h) * slots;
   float M = -INFINITY;
   for (int s = 0; s < ns; ++s) M = fmaxf(M, part_ml[(base + s) * 2]);
-  float L = 0.f, acc = 0.f;
-  if (M != -INFINITY) {
-    for (int s = 0; s < ns; ++s) {
-      const float ms = part_ml[(base + s) * 2];
-      const float w = (ms == -INFINITY) ? 0.f : fast_exp2(ms - M);
-      L = fmaf(w, part_ml[(base + s) * 2 + 1], L);
-      acc = fmaf(w, part_o[(base + s) * kD + d], acc);
-    }
+  float L = 0.f, o0 = 0.f, o1 = 0.f;
+  const float* po = part_o + base * kD + 2 * lane;
+  for (int s = 0; s < ns; ++s) {
+    const float ms = part_ml[(base + s) * 2];
+    const float wv = (ms == -INFINITY) ? 0.f : fast_exp2(ms - M);
+    L = fmaf(wv, part_ml[(base + s) * 2 + 1], L);
+    const float2 v = *reinterpret_cast<const float2*>(po + (int64_t)s * kD);
+    o0 = fmaf(wv, v.x, o0);
+    o1 = fmaf(wv, v.y, o1);
   }
-  const float o = (L > 0.f) ? acc / L : 0.f;
-  out[(int64_t)b * out_row_stride + (int64_t)h * kD + d] = (bf16_t)f32_to_bf16_bits(o);
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  bf16_t* op = out + (int64_t)b * out_row_stride + (int64_t)h * kD + 2 * lane;
+  *reinterpret_cast<uint32_t*>(op) = pack_bf16x2(o0 * inv, o1 * inv);
 }
 
 static int decode_check(const void* q, const void* k_cache, const void* v_cache,
@@ -244,11 +331,15 @@ static int decode_check(const void* q, const void* k_cache, const void* v_cache,
   const int g = n_q_heads / n_kv_heads;
   NKV_REQUIRE(g == 1 || g == 2 || g == 4 || g == 8 || g == 16, NKV_EUNSUPPORTED,
               "paged_decode: GQA group %d not in {1,2,4,8,16}", g);
-  NKV_REQUIRE(block_size > 0 && block_size % kSplit == 0, NKV_EUNSUPPORTED,
-              "paged_decode: block_size must be a multiple of 256 (got %d)", block_size);
+  NKV_REQUIRE(block_size > 0 && block_size % kChunk == 0, NKV_EUNSUPPORTED,
+              "paged_decode: block_size must be a multiple of 16 (got %d)", block_size);
   NKV_REQUIRE(max_blocks_per_seq > 0 && bt_row_stride >= max_blocks_per_seq, NKV_EINVAL,
               "paged_decode: bad block table width/stride (%d, %lld)", max_blocks_per_seq,
               (long long)bt_row_stride);
+  NKV_REQUIRE((int64_t)max_blocks_per_seq * block_size < (1ll << 30), NKV_EUNSUPPORTED,
+              "paged_decode: max_blocks_per_seq * block_size too large");
+  NKV_REQUIRE((int64_t)block_size * n_kv_heads * kD * 2 < (1ll << 31), NKV_EUNSUPPORTED,
+              "paged_decode: cache block too large for 32-bit buffer offsets");
   NKV_REQUIRE(q_row_stride >= (int64_t)n_q_heads * kD && q_row_stride % 8 == 0, NKV_EINVAL,
               "paged_decode: q row stride must be >= Hq*D and a multiple of 8");
   NKV_REQUIRE(q && k_cache && v_cache && block_tables && context_lens, NKV_EINVAL,
@@ -258,14 +349,53 @@ static int decode_check(const void* q, const void* k_cache, const void* v_cache,
   return NKV_OK;
 }
 
+// Persistent grid: as many one-wave workgroups as are resident at once.
+template <int G>
+static int decode_grid() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cached[dev] == 0) {
+    int n_cu = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n_cu <= 0)
+      n_cu = 256;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, reinterpret_cast<const void*>(paged_decode_split_kernel<G>), 64, 0) !=
+            hipSuccess ||
+        per_cu <= 0)
+      per_cu = 8;
+    cached[dev] = n_cu * per_cu;
+  }
+  return cached[dev];
+}
+
+struct DecodeWorkspace {
+  float* part_o;
+  float* part_ml;
+  int32_t* nslots;
+};
+
+static DecodeWorkspace decode_workspace(void* ws, int32_t batch, int32_t Hq, int32_t Hk,
+                                        int64_t slots) {
+  DecodeWorkspace w;
+  w.part_o = (float*)ws;
+  w.part_ml = w.part_o + (int64_t)batch * Hq * slots * kD;
+  w.nslots = (int32_t*)(w.part_ml + (int64_t)batch * Hq * slots * 2);
+  (void)Hk;
+  return w;
+}
+
 }  // namespace nkv
 
 extern "C" size_t nkv_paged_decode_workspace_bytes(int32_t batch, int32_t n_q_heads,
                                                    int32_t head_dim, int32_t max_blocks_per_seq,
                                                    int32_t block_size) {
   if (batch <= 0 || n_q_heads <= 0 || max_blocks_per_seq <= 0 || block_size <= 0) return 0;
-  const int64_t ms = nkv::decode_max_splits(max_blocks_per_seq, block_size);
-  return (size_t)batch * n_q_heads * ms * (head_dim + 2) * sizeof(float);
+  const int64_t slots = nkv::decode_slots(max_blocks_per_seq, block_size);
+  // partial O and (m, l) per slot, then one slot count per (sequence, head)
+  return (size_t)batch * n_q_heads * slots * (head_dim + 2) * sizeof(float) +
+         (size_t)batch * n_q_heads * sizeof(int32_t);
 }
 
 extern "C" int nkv_paged_decode_split(const void* q, int64_t q_row_stride, const void* k_cache,
@@ -286,20 +416,20 @@ extern "C" int nkv_paged_decode_split(const void* q, int64_t q_row_stride, const
                                                        max_blocks_per_seq, block_size);
   NKV_REQUIRE(workspace && workspace_bytes >= need, NKV_EWORKSPACE,
               "paged_decode: workspace needs %zu bytes (got %zu)", need, workspace_bytes);
-  const int64_t ms = decode_max_splits(max_blocks_per_seq, block_size);
-  const int64_t grid = ms * batch * n_kv_heads;
-  NKV_REQUIRE(grid < (1ll << 31), NKV_EUNSUPPORTED, "paged_decode: grid too large");
-  float* part_o = (float*)workspace;
-  float* part_ml = part_o + (int64_t)batch * n_q_heads * ms * kD;
+  const int64_t slots = decode_slots(max_blocks_per_seq, block_size);
+  const int64_t max_chunks = ((int64_t)max_blocks_per_seq * block_size + kChunk - 1) / kChunk;
+  NKV_REQUIRE(max_chunks * batch * n_kv_heads < (1ll << 31), NKV_EUNSUPPORTED,
+              "paged_decode: too many chunks in one call");
+  DecodeWorkspace w = decode_workspace(workspace, batch, n_q_heads, n_kv_heads, slots);
   const float scale_log2 = scale * kLog2e;
   const int g = n_q_heads / n_kv_heads;
   hipStream_t s = as_stream(stream);
-#define NKV_DECODE_LAUNCH(G)                                                                   \
-  hipLaunchKernelGGL(paged_decode_split_kernel<G>, dim3((unsigned)grid), dim3(256), 0, s,      \
-                     (const bf16_t*)q, q_row_stride, (const bf16_t*)k_cache,                    \
+#define NKV_DECODE_LAUNCH(G)                                                                  \
+  hipLaunchKernelGGL((paged_decode_split_kernel<G>), dim3((unsigned)decode_grid<G>()),        \
+                     dim3(64), 0, s, (const bf16_t*)q, q_row_stride, (const bf16_t*)k_cache,  \
                      (const bf16_t*)v_cache, block_tables, bt_row_stride, context_lens, batch, \
-                     n_kv_heads, block_size, max_blocks_per_seq, (int32_t)ms, n_blocks,        \
-                     scale_log2, part_o, part_ml)
+                     n_kv_heads, block_size, max_blocks_per_seq, n_blocks, (int32_t)slots,    \
+                     scale_log2, w.part_o, w.part_ml, w.nslots)
   switch (g) {
     case 1: NKV_DECODE_LAUNCH(1); break;
     case 2: NKV_DECODE_LAUNCH(2); break;
@@ -312,29 +442,33 @@ extern "C" int nkv_paged_decode_split(const void* q, int64_t q_row_stride, const
 }
 
 extern "C" int nkv_paged_decode_combine(const int32_t* context_lens, int32_t batch,
-                                        int32_t n_q_heads, int32_t head_dim, int32_t block_size,
-                                        int32_t max_blocks_per_seq, void* out,
-                                        int64_t out_row_stride, const void* workspace,
+                                        int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                                        int32_t block_size, int32_t max_blocks_per_seq,
+                                        void* out, int64_t out_row_stride, const void* workspace,
                                         size_t workspace_bytes, void* stream) {
   using namespace nkv;
   clear_error();
   NKV_REQUIRE(head_dim == kD, NKV_EUNSUPPORTED, "paged_decode: head_dim must be 128");
-  NKV_REQUIRE(batch >= 0 && n_q_heads > 0 && block_size > 0 && max_blocks_per_seq > 0,
+  NKV_REQUIRE(batch >= 0 && n_q_heads > 0 && n_kv_heads > 0 && n_q_heads % n_kv_heads == 0 &&
+                  block_size > 0 && max_blocks_per_seq > 0,
               NKV_EINVAL, "paged_decode_combine: bad sizes");
   if (batch == 0) return NKV_OK;
   NKV_REQUIRE(out && context_lens, NKV_EINVAL, "paged_decode_combine: null pointer");
-  NKV_REQUIRE(out_row_stride >= (int64_t)n_q_heads * kD, NKV_EINVAL,
-              "paged_decode_combine: out row stride must be >= Hq*D");
+  NKV_REQUIRE(out_row_stride >= (int64_t)n_q_heads * kD && out_row_stride % 2 == 0 &&
+                  (reinterpret_cast<uintptr_t>(out) & 3) == 0,
+              NKV_EINVAL,
+              "paged_decode_combine: out must be 4-byte aligned with an even row stride "
+              ">= Hq*D");
   const size_t need = nkv_paged_decode_workspace_bytes(batch, n_q_heads, head_dim,
                                                        max_blocks_per_seq, block_size);
   NKV_REQUIRE(workspace && workspace_bytes >= need, NKV_EWORKSPACE,
               "paged_decode: workspace needs %zu bytes (got %zu)", need, workspace_bytes);
-  const int64_t ms = decode_max_splits(max_blocks_per_seq, block_size);
-  const float* part_o = (const float*)workspace;
-  const float* part_ml = part_o + (int64_t)batch * n_q_heads * ms * kD;
-  hipLaunchKernelGGL(paged_decode_combine_kernel, dim3((unsigned)(batch * n_q_heads)), dim3(kD),
-                     0, as_stream(stream), context_lens, n_q_heads, (int32_t)ms, part_o, part_ml,
-                     (bf16_t*)out, out_row_stride);
+  const int64_t slots = decode_slots(max_blocks_per_seq, block_size);
+  DecodeWorkspace w =
+      decode_workspace(const_cast<void*>(workspace), batch, n_q_heads, n_kv_heads, slots);
+  hipLaunchKernelGGL(paged_decode_combine_kernel, dim3((unsigned)(batch * n_q_heads)), dim3(64),
+                     0, as_stream(stream), context_lens, n_q_heads, n_kv_heads, (int32_t)slots,
+                     w.part_o, w.part_ml, w.nslots, (bf16_t*)out, out_row_stride);
   return check_launch("nkv_paged_decode_combine");
 }
 
@@ -350,7 +484,7 @@ extern "C" int nkv_paged_decode(const void* q, int64_t q_row_stride, const void*
                                   block_size, max_blocks_per_seq, n_blocks, scale, workspace,
                                   workspace_bytes, stream);
   if (rc) return rc;
-  return nkv_paged_decode_combine(context_lens, batch, n_q_heads, head_dim, block_size,
-                                  max_blocks_per_seq, out, out_row_stride, workspace,
+  return nkv_paged_decode_combine(context_lens, batch, n_q_heads, n_kv_heads, head_dim,
+                                  block_size, max_blocks_per_seq, out, out_row_stride, workspace,
                                   workspace_bytes, stream);
 }

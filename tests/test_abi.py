@@ -57,4 +57,6 @@ def test_host_side_argument_checks_without_gpu():
     # zero tokens is a no-op
     assert lib.nkv_store_kvcache(None, 0, None, 0, None, None, None, 0, 8, 128, 0, None) == 0
     # workspace sizing is pure host arithmetic
-    assert lib.nkv_paged_decode_workspace_bytes(64, 32, 128, 32, 256) == 64 * 32 * 32 * 130 * 4
+    slots = (32 * 256 // 16 + 15) // 16 + 1
+    assert lib.nkv_paged_decode_workspace_bytes(64, 32, 128, 32, 256) == \
+        64 * 32 * slots * 130 * 4 + 64 * 32 * 4

@@ -105,3 +105,29 @@ def test_decode_attention_module(nkv, dev):
     ref = paged_decode_ref(wl["q"].float(), kc, vc, wl["context_lens"], bt, wl["scale"])
     assert o.shape == (4, 1, 16, 128)
     assert (o[:, 0].float().cpu() - ref).abs().max().item() <= TOL
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_decode_ragged_batch_over_64(nkv, dev, seed):
+    """200 sequences (several 64-sequence cursor batches), lengths 0..700 with many
+    short ones: every wave crosses many (sequence, KV head) segments."""
+    g = torch.Generator().manual_seed(100 + seed)
+    bs, Hq, Hk, D, B = 200, 32, 8, 128, 256
+    ctx = torch.randint(0, 700, (bs,), generator=g, dtype=torch.int32)
+    ctx[::7] = torch.randint(1, 20, (len(ctx[::7]),), generator=g, dtype=torch.int32)
+    ctx[5] = 0
+    ctx[64] = 0
+    ctx[199] = 0
+    need = [(int(c) + B - 1) // B for c in ctx]
+    nb = sum(need) + 3
+    perm = torch.randperm(nb, generator=g).tolist()
+    bt = torch.full((bs, 3), -1, dtype=torch.int32)
+    p = 0
+    for i, n in enumerate(need):
+        bt[i, :n] = torch.tensor(perm[p:p + n], dtype=torch.int32)
+        p += n
+    kc = torch.randn(nb, B, Hk, D, generator=g).to(torch.bfloat16)
+    vc = torch.randn(nb, B, Hk, D, generator=g).to(torch.bfloat16)
+    q = torch.randn(bs, Hq, D, generator=g).to(torch.bfloat16)
+    out = _check(nkv, dev, q, kc, vc, ctx, bt, D ** -0.5)
+    assert torch.all(out[ctx == 0] == 0)
