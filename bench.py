@@ -43,7 +43,22 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--compress-reps", type=int, default=30)
+    p.add_argument("--only", choices=["all", "decode", "compress"], default="all",
+                   help="run one part only (for profiling)")
+    p.add_argument("--copy-calibration-mib", type=int, default=0,
+                   help="also run 5 device-to-device copies of this many MiB (a kernel of "
+                        "known traffic, to scale hardware byte counters)")
     return p.parse_args()
+
+
+def copy_calibration(mib, dev):
+    """Five plain copies of `mib` MiB: reads and writes exactly mib MiB each."""
+    src = torch.empty(mib * 1024 * 1024, dtype=torch.uint8, device=dev).fill_(3)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"[bench] copy calibration: 5 x {mib} MiB device copies", file=sys.stderr, flush=True)
 
 
 def decode_setup(dev):
@@ -218,12 +233,21 @@ def main():
               "collective, see the design notes).", file=sys.stderr)
         sys.exit(2)
     dev = torch.device("cuda:0")
+    if args.copy_calibration_mib:
+        copy_calibration(args.copy_calibration_mib, dev)
+    if args.only == "compress":
+        comp = run_compress(args, dev)
+        print(json.dumps(comp), flush=True)
+        return
     print(f"[bench] decode workload: bs 64, Hq 32, Hk 8, ctx U[2048,8192], pool 4096 blocks",
           file=sys.stderr, flush=True)
     wl, sets, r = run_decode(args, dev)
     print(f"[bench] decode done: {r['decode_ms'] * 1e3:.1f} us/decode, "
           f"split {r['split_ms'] * 1e3:.1f} us, parity err {r['parity_max_abs_err']:.3e}",
           file=sys.stderr, flush=True)
+    if args.only == "decode":
+        print(json.dumps(r), flush=True)
+        return
     comp = run_compress(args, dev)
     print(f"[bench] compress done: {comp['compress_step_us']} us", file=sys.stderr, flush=True)
     cpu = None

@@ -14,19 +14,19 @@
 //    (sequence, KV head) segments; each segment it touches yields one
 //    partial (m, l, O) in slot  wave - first_wave_of_the_segment.
 //  * Within a segment the wave streams chunks through a register ring of
-//    DEPTH chunks: K (4 x 16 B per lane) and V (4 x 16 B per lane) of chunk
-//    j+DEPTH are issued as soon as chunk j has been consumed. Loads are
-//    raw buffer loads whose per-chunk descriptor covers only the chunk's
-//    valid rows: keys past the context, chunks of other waves and invalid
-//    block-table entries read as zero without touching memory.
+//    DEPTH chunks: K and V of chunk j+DEPTH (4 whole 256-byte rows per load
+//    instruction, 8 x 16 B per lane) are issued as soon as chunk j has been
+//    consumed. Loads are non-temporal raw buffer loads whose per-chunk
+//    descriptor covers only the chunk's valid rows: keys past the context,
+//    padding chunks and invalid block-table entries read as zero without
+//    touching memory. Each consumed chunk is staged row-major in LDS.
 //  * Both contractions run on the matrix cores:
-//      S^T = K q^T   v_mfma_f32_16x16x32_bf16, A = 16 keys (straight from
-//                    the K loads), B = the g query heads of the KV head;
-//                    lane l ends up with head l%16, keys 4(l/16)..+3.
+//      S^T = K q^T   v_mfma_f32_16x16x32_bf16, A = 16 keys (read back from
+//                    LDS, one key row per lane), B = the g query heads of the
+//                    KV head; lane l ends up with head l%16, keys 4(l/16)..+3.
 //      O^T += V^T P^T v_mfma_f32_16x16x16_bf16 per 16-dim block; the B
 //                    operand is exactly the lane's 4 softmax weights (bf16),
-//                    the A operand V^T comes from LDS with ds_read_b64_tr_b16
-//                    (the chunk's V rows are staged row-major in LDS).
+//                    the A operand V^T comes from LDS with ds_read_b64_tr_b16.
 //    Every lane holds state for one head (its column): the online softmax
 //    needs no cross-lane traffic except one xor-max over the 4 key groups.
 //  * A combine kernel merges the few partials of each (sequence, query head).
@@ -44,6 +44,7 @@ constexpr int kMinChunks = 16;           // minimum chunks per wave range
 constexpr int kWinBlocks = 64;           // block ids held per window (one per lane)
 constexpr int kVRow = kD + 16;           // LDS row stride of a staged V chunk (elements)
 constexpr int kBufferFlags = 0x00020000; // raw buffer resource word 3 (dword data)
+constexpr int kStreamPolicy = 2;         // cache policy "nt": K/V are read exactly once
 constexpr int kDepth = 4;                // ring depth (chunks in flight per wave)
 
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
@@ -67,23 +68,23 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
   return v;
 }
 
-// Cursor over sequences in batches of 64 (one per lane): sequence s owns the
-// global chunks [g_s, g_s + nc_s * Hk), KV-head-major inside.
+// Cursor over sequences in batches of 64 (one per lane): in the chunk stream
+// of one KV head, sequence s owns chunks [g_s, g_s + nc_s).
 struct SeqCursor {
   int cb;    // first sequence of the loaded batch (uniform)
-  int base;  // global chunk index of sequence cb (uniform)
+  int base;  // stream index of sequence cb's first chunk (uniform)
   int tot;   // chunks of the batch (uniform)
   int ctx;   // lane: context length of sequence cb + lane
-  int nc;    // lane: chunks per KV head
-  int incl;  // lane: inclusive prefix of nc * Hk over the batch
+  int nc;    // lane: chunks of that sequence
+  int incl;  // lane: inclusive prefix of nc over the batch
 };
 
 __device__ __forceinline__ void seq_load(SeqCursor& c, const int32_t* __restrict__ ctx_lens,
-                                         int batch, int Hk, int max_tokens) {
+                                         int batch, int max_tokens) {
   const int s = c.cb + (int)threadIdx.x;
   c.ctx = s < batch ? ctx_lens[s] : 0;
   c.nc = c.ctx > 0 ? (min(c.ctx, max_tokens) + kChunk - 1) / kChunk : 0;
-  c.incl = wave_incl_scan(c.nc * Hk);
+  c.incl = wave_incl_scan(c.nc);
   c.tot = __builtin_amdgcn_readlane(c.incl, 63);
 }
 
@@ -96,6 +97,7 @@ void paged_decode_split_kernel(
     const int32_t* __restrict__ context_lens, int32_t batch, int32_t Hk,
     int32_t block_size, int32_t max_blocks, int64_t n_blocks, int32_t slots, float scale_log2,
     float* __restrict__ part_o, float* __restrict__ part_ml, int32_t* __restrict__ nslots) {
+  __shared__ __attribute__((aligned(16))) bf16_t kbuf[kChunk * kVRow];
   __shared__ __attribute__((aligned(16))) bf16_t vbuf[kChunk * kVRow];
 
   const int lane = threadIdx.x;
@@ -106,46 +108,50 @@ void paged_decode_split_kernel(
   const int row_b = (int)(row * 2);
   const int max_tokens = max_blocks * block_size;
 
-  // ---- this wave's chunk range
+  // ---- this wave's KV head and chunk range. Every KV head has the same
+  // chunk stream (sequence-major); waves kvh, kvh+Hk, kvh+2Hk, ... split it
+  // into equal ranges, so the Hk waves i*Hk .. i*Hk+Hk-1 read the same cache
+  // blocks (the Hk heads of a block) at the same time.
+  const int kvh = blockIdx.x % Hk;
+  const int wi = blockIdx.x / Hk;
+  const int Wh = gridDim.x / Hk;
+  if (wi >= Wh) return;
   SeqCursor cur;
   int T = 0;
   for (cur.cb = 0; cur.cb < batch; cur.cb += 64) {
-    seq_load(cur, context_lens, batch, Hk, max_tokens);
+    seq_load(cur, context_lens, batch, max_tokens);
     T += cur.tot;
   }
-  const int W = gridDim.x;
-  const int C = max((T + W - 1) / W, kMinChunks);
-  const int k_begin = blockIdx.x * C;
+  const int C = max((T + Wh - 1) / Wh, kMinChunks);
+  const int k_begin = wi * C;
   if (k_begin >= T) return;
   const int k_end = min(T, k_begin + C);
   cur.cb = 0;
   cur.base = 0;
-  seq_load(cur, context_lens, batch, Hk, max_tokens);
+  seq_load(cur, context_lens, batch, max_tokens);
 
-  // per-lane constant load offsets: K as the A operand (lane l: key l%16,
-  // dims 8*(l/16) + 32*ks), V as 4 rows x 256 B (lane l: key 4r + l/16, dims 8*(l%16))
-  const int koff = col * row_b + g4 * 16;
-  const int voff = g4 * row_b + col * 16;
+  // per-lane constant load offset: K and V are both read as 4 whole 256-byte
+  // rows per load instruction (lane l: key 4r + l/16, dims 8*(l%16)) and
+  // staged row-major in LDS; K is re-read from there in the MFMA A layout.
+  const int roff = g4 * row_b + col * 16;
   const int tr_row = 4 * g4 + (col >> 2);  // ds_read_b64_tr_b16 source row / column
   const int tr_col = (col & 3) * 4;
 
   for (int k = k_begin; k < k_end;) {
-    // ---- locate the segment holding global chunk k (wave-uniform)
+    // ---- locate the sequence holding stream chunk k (wave-uniform)
     while (k >= cur.base + cur.tot) {
       cur.base += cur.tot;
       cur.cb += 64;
-      seq_load(cur, context_lens, batch, Hk, max_tokens);
+      seq_load(cur, context_lens, batch, max_tokens);
     }
     const int ln = __builtin_amdgcn_readfirstlane(__builtin_ctzll(__ballot(cur.base + cur.incl > k)));
     const int b = cur.cb + ln;
     const int ctx = __builtin_amdgcn_readlane(cur.ctx, ln);
     const int nc = __builtin_amdgcn_readlane(cur.nc, ln);
-    const int gb = cur.base + __builtin_amdgcn_readlane(cur.incl, ln) - nc * Hk;
-    const int kvh = (k - gb) / nc;
-    const int c_lo = k - gb - kvh * nc;
+    const int g0 = cur.base + __builtin_amdgcn_readlane(cur.incl, ln) - nc;
+    const int c_lo = k - g0;
     const int n_seg = min(nc - c_lo, k_end - k);
-    const int g0 = gb + kvh * nc;
-    const int slot = (int)blockIdx.x - g0 / C;
+    const int slot = wi - g0 / C;
 
     // q^T as the MFMA B operand: lane l -> head l%16 (columns >= g re-read
     // head 0 and are discarded), dims 8*(l/16) + 32*ks .. +8
@@ -196,26 +202,32 @@ void paged_decode_split_kernel(
         const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
             (void*)(vbase + r0 * row), (short)0, bytes, kBufferFlags);
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
-          kreg[s][ks] = __builtin_bit_cast(
-              u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rk, koff + ks * 64, 0, 0));
+        for (int r = 0; r < 4; ++r)
+          kreg[s][r] = __builtin_bit_cast(
+              u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rk, roff + r * 4 * row_b, 0,
+                                                             kStreamPolicy));
 #pragma unroll
         for (int r = 0; r < 4; ++r)
           vreg[s][r] = __builtin_bit_cast(
-              u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rv, voff + r * 4 * row_b, 0, 0));
+              u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rv, roff + r * 4 * row_b, 0,
+                                                             kStreamPolicy));
       };
 
       auto consume = [&](int s) {
-        // S^T for 16 keys x 16 heads
+        // stage the chunk's K and V rows (row-major) in LDS
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          *reinterpret_cast<u32x4_t*>(&kbuf[(4 * r + g4) * kVRow + col * 8]) = kreg[s][r];
+          *reinterpret_cast<u32x4_t*>(&vbuf[(4 * r + g4) * kVRow + col * 8]) = vreg[s][r];
+        }
+        // S^T for 16 keys x 16 heads; A operand: lane l -> key l%16, dims 8*(l/16) + 32*ks
         f32x4_t st = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
-          st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8_v(kreg[s][ks]),
-                                                        as_bf16x8_v(qreg[ks]), st, 0, 0, 0);
-        // stage V rows (row-major) for the transposed reads
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          *reinterpret_cast<u32x4_t*>(&vbuf[(4 * r + g4) * kVRow + col * 8]) = vreg[s][r];
+        for (int ks = 0; ks < 4; ++ks) {
+          const u32x4_t ka = *reinterpret_cast<const u32x4_t*>(&kbuf[col * kVRow + g4 * 8 + ks * 32]);
+          st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8_v(ka), as_bf16x8_v(qreg[ks]), st,
+                                                        0, 0, 0);
+        }
         // online softmax for head `col` over keys 4*g4 .. +3 of the chunk
         float sv[4];
         float cmax = -INFINITY;
@@ -289,7 +301,9 @@ void paged_decode_split_kernel(
 }
 
 // Merge the partials of one (sequence, query head): O = sum_s 2^(m_s-M) O_s /
-// sum_s 2^(m_s-M) l_s. One wave per pair; each lane owns two output dims.
+// sum_s 2^(m_s-M) l_s. One wave per pair: lane s reads partial s's (m, l),
+// the weights are combined with wave reductions, then each lane accumulates
+// two output dims over the partials (all loads independent).
 __global__ __launch_bounds__(64) void paged_decode_combine_kernel(
     const int32_t* __restrict__ context_lens, int32_t Hq, int32_t Hk, int32_t slots,
     const float* __restrict__ part_o, const float* __restrict__ part_ml,
@@ -298,22 +312,59 @@ __global__ __launch_bounds__(64) void paged_decode_combine_kernel(
   const int h = blockIdx.x % Hq;
   const int lane = threadIdx.x;
   const int ctx = context_lens[b];
-  const int ns = ctx > 0 ? min(nslots[(int64_t)b * Hk + h / (Hq / Hk)], slots) : 0;
+  const int cnt = nslots[(int64_t)b * Hk + h / (Hq / Hk)];
+  const int ns = ctx > 0 ? min(cnt, slots) : 0;
   const int64_t base = ((int64_t)b * Hq + h) * slots;
-  float M = -INFINITY;
-  for (int s = 0; s < ns; ++s) M = fmaxf(M, part_ml[(base + s) * 2]);
-  float L = 0.f, o0 = 0.f, o1 = 0.f;
+  bf16_t* op = out + (int64_t)b * out_row_stride + (int64_t)h * kD + 2 * lane;
+  if (ns == 0) {
+    *reinterpret_cast<uint32_t*>(op) = 0u;
+    return;
+  }
+  float o0 = 0.f, o1 = 0.f, L = 0.f;
   const float* po = part_o + base * kD + 2 * lane;
-  for (int s = 0; s < ns; ++s) {
-    const float ms = part_ml[(base + s) * 2];
-    const float wv = (ms == -INFINITY) ? 0.f : fast_exp2(ms - M);
-    L = fmaf(wv, part_ml[(base + s) * 2 + 1], L);
+  // pass 1: the global max over all partials
+  float M = -INFINITY;
+  for (int s = lane; s < ns; s += 64) M = fmaxf(M, part_ml[(base + s) * 2]);
+  M = wave_max(M);
+  // pass 2: weights (lane s holds w_s for s < 64) and the weighted sums
+  const int n1 = min(ns, 64);
+  float wl = 0.f;
+  if (lane < n1) {
+    const float2 ml = *reinterpret_cast<const float2*>(&part_ml[(base + lane) * 2]);
+    wl = (ml.x == -INFINITY) ? 0.f : fast_exp2(ml.x - M);
+    L = wl * ml.y;
+  }
+  for (int s = 64 + lane; s < ns; s += 64) {
+    const float2 ml = *reinterpret_cast<const float2*>(&part_ml[(base + s) * 2]);
+    L += (ml.x == -INFINITY) ? 0.f : fast_exp2(ml.x - M) * ml.y;
+  }
+  L = wave_sum(L);
+  int s = 0;
+  for (; s + 4 <= n1; s += 4) {
+    float2 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const float2*>(po + (int64_t)(s + u) * kD);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float w = __shfl(wl, s + u, 64);
+      o0 = fmaf(w, v[u].x, o0);
+      o1 = fmaf(w, v[u].y, o1);
+    }
+  }
+  for (; s < n1; ++s) {
     const float2 v = *reinterpret_cast<const float2*>(po + (int64_t)s * kD);
-    o0 = fmaf(wv, v.x, o0);
-    o1 = fmaf(wv, v.y, o1);
+    const float w = __shfl(wl, s, 64);
+    o0 = fmaf(w, v.x, o0);
+    o1 = fmaf(w, v.y, o1);
+  }
+  for (; s < ns; ++s) {  // more than 64 partials (very long contexts)
+    const float ms = part_ml[(base + s) * 2];
+    const float w = (ms == -INFINITY) ? 0.f : fast_exp2(ms - M);
+    const float2 v = *reinterpret_cast<const float2*>(po + (int64_t)s * kD);
+    o0 = fmaf(w, v.x, o0);
+    o1 = fmaf(w, v.y, o1);
   }
   const float inv = L > 0.f ? 1.f / L : 0.f;
-  bf16_t* op = out + (int64_t)b * out_row_stride + (int64_t)h * kD + 2 * lane;
   *reinterpret_cast<uint32_t*>(op) = pack_bf16x2(o0 * inv, o1 * inv);
 }
 
@@ -425,7 +476,9 @@ extern "C" int nkv_paged_decode_split(const void* q, int64_t q_row_stride, const
   const int g = n_q_heads / n_kv_heads;
   hipStream_t s = as_stream(stream);
 #define NKV_DECODE_LAUNCH(G)                                                                  \
-  hipLaunchKernelGGL((paged_decode_split_kernel<G>), dim3((unsigned)decode_grid<G>()),        \
+  hipLaunchKernelGGL((paged_decode_split_kernel<G>),                                          \
+                     dim3((unsigned)std::max(n_kv_heads, decode_grid<G>() / n_kv_heads *      \
+                                                             n_kv_heads)),                    \
                      dim3(64), 0, s, (const bf16_t*)q, q_row_stride, (const bf16_t*)k_cache,  \
                      (const bf16_t*)v_cache, block_tables, bt_row_stride, context_lens, batch, \
                      n_kv_heads, block_size, max_blocks_per_seq, n_blocks, (int32_t)slots,    \
