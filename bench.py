@@ -36,6 +36,21 @@ HBM_PEAK_GBS = 8000.0
 METRIC = "paged decode-attn GB/s (% HBM peak) @Qwen3-8B; KV-compress step µs @bs500"
 
 
+def measured_traffic(profile, kernel):
+    """HBM bytes per launch of `kernel`, as recorded by the rocprofv3 byte-counter
+    runs summarised in profiles/<profile> (None if absent)."""
+    path = os.path.join(ROOT, "profiles", profile)
+    key = f"traffic_bytes_per_launch {kernel}:"
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith(key):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
@@ -281,13 +296,14 @@ def main():
         "store_us": round(r["store_ms"] * 1e3, 2),
         "parity_max_abs_err": r["parity_max_abs_err"],
         "roofline": {
-            "kernel": "paged_decode_split_kernel<4> (stream-K split)",
+            "kernel": "paged_decode_split_kernel<4>",
             "bound": "hbm",
             "achieved": round(split_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(split_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic("paged_decode_qwen3_8b_bs64.txt",
+                                        "paged_decode_split_kernel<4>"),
             "avg_us": round(r["split_ms"] * 1e3, 2),
             "algorithmic_bytes": r["split_bytes"],
         },
