@@ -113,8 +113,10 @@ int nkv_paged_decode_combine(const int32_t* context_lens, int32_t batch,
  * 0 .. Lk-Lq+j. If block_tables != NULL, key t of sequence i is k_cache row
  * block_tables[i, t/block_size]*block_size + t%block_size (paged); otherwise
  * it is row cu_seqlens_k[i]+t of k_cache/v_cache (contiguous [sum Lk, Hk, D]
- * with row stride kv_row_stride). q/out are [sum Lq, Hq, D] with row strides.
- * head_dim must be 128.
+ * with row stride kv_row_stride). Table entries at or beyond
+ * max_blocks_per_seq, negative, or past n_rows read as zero keys/values.
+ * q/out are [sum Lq, Hq, D] with row strides. head_dim must be 128;
+ * Hq/Hk in {1, 2, 4, 8}. Rows with no visible key (Lk < Lq) are zero.
  * Replaces: flash_attn_varlen_func(q, k, v, max_seqlen_q, cu_seqlens_q,
  *           max_seqlen_k, cu_seqlens_k, softmax_scale, causal=True,
  *           block_table), nanokvllm/layers/attention.py:96-102
@@ -123,7 +125,7 @@ int nkv_prefill_varlen(const void* q, int64_t q_row_stride,
                        const void* k_cache, const void* v_cache, int64_t kv_row_stride,
                        const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
                        const int32_t* block_tables, int64_t bt_row_stride,
-                       int32_t n_seqs, int32_t max_seqlen_q,
+                       int32_t max_blocks_per_seq, int32_t n_seqs, int32_t max_seqlen_q,
                        int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
                        int32_t block_size, int64_t n_rows, float scale,
                        void* out, int64_t out_row_stride, void* stream);

@@ -38,7 +38,7 @@ SIGNATURES = {
     "nkv_paged_decode_combine": (C.c_int, [_p, _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64, _p,
                                            _sz, _p]),
     "nkv_prefill_varlen": (C.c_int, [_p, _i64, _p, _p, _i64, _p, _p, _p, _i64, _i32, _i32, _i32,
-                                     _i32, _i32, _i32, _i64, _f32, _p, _i64, _p]),
+                                     _i32, _i32, _i32, _i32, _i64, _f32, _p, _i64, _p]),
     "nkv_compress_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32]),
     "nkv_compress_score": (C.c_int, [_p, _i64, _p, _p, _i64, _i32, _p, _p, _i32, _i32, _i32, _i32,
                                      _i32, _i32, _i64, _f32, _i32, _p, _p, _sz, _p]),

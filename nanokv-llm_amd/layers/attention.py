@@ -104,6 +104,7 @@ def varlen_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         kv_row_stride = Hk * Dk
         n_rows = NB * B
         bt_ptr, bt_stride = block_tables.data_ptr(), block_tables.stride(0)
+        max_blocks = block_tables.size(1)
         assert block_tables.dtype == torch.int32 and block_tables.stride(1) == 1
     else:
         _, Hk, Dk = k.shape
@@ -111,13 +112,13 @@ def varlen_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         kv_row_stride = k.stride(0)
         n_rows = k.size(0)
         B = 0
-        bt_ptr, bt_stride = None, 0
+        bt_ptr, bt_stride, max_blocks = None, 0, 0
     assert Dk == D
     if out is None:
         out = torch.empty(N, Hq, D, dtype=_BF16, device=q.device)
     rc = _lib.lib().nkv_prefill_varlen(
         q.data_ptr(), q.stride(0), k.data_ptr(), v.data_ptr(), kv_row_stride,
-        cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), bt_ptr, bt_stride, n_seqs,
+        cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), bt_ptr, bt_stride, max_blocks, n_seqs,
         int(max_seqlen_q), Hq, Hk, D, B, n_rows, float(scale), out.data_ptr(), out.stride(0),
         _lib.stream_of(q))
     _lib.check(rc, "varlen_prefill")

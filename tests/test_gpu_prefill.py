@@ -1,0 +1,166 @@
+"""Varlen causal prefill on the GPU vs the fp32 oracle: max abs err <= 2e-2 (bf16 output)."""
+import importlib
+from types import SimpleNamespace
+
+import pytest
+import torch
+
+from oracle.attention_ref import store_kvcache_ref, varlen_prefill_ref
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-2
+wl_mod = importlib.import_module("nanokv-llm_amd.workloads")
+
+
+def _err(out, ref):
+    return (out.float().cpu() - ref).abs().max().item()
+
+
+def _paged(nkv, dev, wl, q=None):
+    q = wl["q"] if q is None else q
+    kc, vc = wl["k_cache"].clone(), wl["v_cache"].clone()
+    store_kvcache_ref(wl["key"], wl["value"], kc, vc, wl["slot_mapping"])
+    out = nkv.varlen_prefill(q.to(dev), kc.to(dev), vc.to(dev), wl["cu_seqlens_q"].to(dev),
+                             wl["cu_seqlens_k"].to(dev), wl["max_seqlen_q"], wl["scale"],
+                             block_tables=wl["block_tables"].to(dev))
+    torch.cuda.synchronize()
+    ref = varlen_prefill_ref(q.float(), kc, vc, wl["cu_seqlens_q"], wl["cu_seqlens_k"],
+                             wl["scale"], block_tables=wl["block_tables"])
+    return out, ref
+
+
+@pytest.mark.parametrize("Hq,Hk", [(32, 8), (8, 8), (16, 8), (64, 8), (16, 2)])
+def test_prefill_paged_one_shot(nkv, dev, Hq, Hk):
+    wl = wl_mod.prefill_workload(3, Hq, Hk, 1, 700, seed=11)
+    out, ref = _paged(nkv, dev, wl)
+    assert _err(out, ref) <= TOL
+
+
+def test_prefill_paged_chunked(nkv, dev):
+    """Chunk of 200 queries after a random prefix: bottom-right causal alignment."""
+    wl = wl_mod.prefill_workload(4, 32, 8, 0, 0, seed=12, prefix_lo=0, prefix_hi=900, chunk=200)
+    out, ref = _paged(nkv, dev, wl)
+    assert _err(out, ref) <= TOL
+
+
+def test_prefill_contiguous(nkv, dev):
+    """No block table: K/V are the new rows themselves (attention.py:96-102 without cache)."""
+    wl = wl_mod.prefill_workload(3, 32, 8, 1, 600, seed=13)
+    q, k, v = wl["q"], wl["key"], wl["value"]
+    cu = wl["cu_seqlens_q"]
+    out = nkv.varlen_prefill(q.to(dev), k.to(dev), v.to(dev), cu.to(dev), cu.to(dev),
+                             wl["max_seqlen_q"], wl["scale"])
+    ref = varlen_prefill_ref(q.float(), k, v, cu, cu, wl["scale"])
+    assert _err(out, ref) <= TOL
+
+
+def test_prefill_edge_lengths(nkv, dev):
+    """Empty, single-token and tile-boundary sequences; Lk < Lq rows are zero."""
+    g = torch.Generator().manual_seed(14)
+    Hq, Hk, D = 32, 8, 128
+    Lq = [0, 1, 31, 32, 33, 127, 128, 129, 5, 40]
+    Lk = [0, 1, 31, 32, 33, 127, 128, 129, 300, 17]  # last: 23 queries see nothing
+    cu_q = torch.tensor([0] + torch.tensor(Lq).cumsum(0).tolist(), dtype=torch.int32)
+    cu_k = torch.tensor([0] + torch.tensor(Lk).cumsum(0).tolist(), dtype=torch.int32)
+    q = torch.randn(int(cu_q[-1]), Hq, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(int(cu_k[-1]), Hk, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(int(cu_k[-1]), Hk, D, generator=g).to(torch.bfloat16)
+    out = nkv.varlen_prefill(q.to(dev), k.to(dev), v.to(dev), cu_q.to(dev), cu_k.to(dev),
+                             max(Lq), D ** -0.5)
+    ref = varlen_prefill_ref(q.float(), k, v, cu_q, cu_k, D ** -0.5)
+    assert _err(out, ref) <= TOL
+    o = out.cpu()
+    last = int(cu_q[-2])
+    assert torch.all(o[last:last + 23] == 0)
+    # one query over one key -> exactly that value row
+    assert torch.equal(o[0], v[0].repeat_interleave(Hq // Hk, dim=0))
+
+
+def test_prefill_strided_q_and_out(nkv, dev):
+    """q is a view into a fused qkv buffer and out a view into a wider buffer."""
+    wl = wl_mod.prefill_workload(2, 32, 8, 100, 400, seed=15)
+    N = wl["q"].size(0)
+    qkv = torch.randn(N, 48 * 128, generator=torch.Generator().manual_seed(16)).to(torch.bfloat16)
+    q = qkv[:, :32 * 128].view(N, 32, 128)
+    qg = qkv.to(dev)[:, :32 * 128].view(N, 32, 128)
+    wide = torch.zeros(N, 40 * 128, dtype=torch.bfloat16, device=dev)
+    outv = wide[:, :32 * 128].view(N, 32, 128)
+    kc, vc = wl["k_cache"].clone(), wl["v_cache"].clone()
+    store_kvcache_ref(wl["key"], wl["value"], kc, vc, wl["slot_mapping"])
+    nkv.varlen_prefill(qg, kc.to(dev), vc.to(dev), wl["cu_seqlens_q"].to(dev),
+                       wl["cu_seqlens_k"].to(dev), wl["max_seqlen_q"], wl["scale"],
+                       block_tables=wl["block_tables"].to(dev), out=outv)
+    ref = varlen_prefill_ref(q.float(), kc, vc, wl["cu_seqlens_q"], wl["cu_seqlens_k"],
+                             wl["scale"], block_tables=wl["block_tables"])
+    assert _err(outv, ref) <= TOL
+    assert torch.all(wide[:, 32 * 128:] == 0)  # nothing written past the heads
+
+
+def test_prefill_block_permutation_invariance(nkv, dev):
+    wl = wl_mod.prefill_workload(3, 32, 8, 300, 900, seed=17)
+    kc, vc, bt = wl["k_cache"], wl["v_cache"], wl["block_tables"]
+    nb = kc.size(0)
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(18))
+    inv = torch.argsort(perm)
+    bt2 = torch.where(bt >= 0, inv[bt.clamp(min=0).long()].to(torch.int32), bt)
+    args = (wl["cu_seqlens_q"].to(dev), wl["cu_seqlens_k"].to(dev), wl["max_seqlen_q"],
+            wl["scale"])
+    a = nkv.varlen_prefill(wl["q"].to(dev), kc.to(dev), vc.to(dev), *args,
+                           block_tables=bt.to(dev))
+    b = nkv.varlen_prefill(wl["q"].to(dev), kc[perm].to(dev), vc[perm].to(dev), *args,
+                           block_tables=bt2.to(dev))
+    assert torch.equal(a, b)
+
+
+def test_prefill_paged_equals_contiguous(nkv, dev):
+    """The same keys through the block table and as contiguous rows: bitwise equal."""
+    wl = wl_mod.prefill_workload(3, 32, 8, 50, 700, seed=19)
+    kc, vc = wl["k_cache"].clone(), wl["v_cache"].clone()
+    store_kvcache_ref(wl["key"], wl["value"], kc, vc, wl["slot_mapping"])
+    cu = wl["cu_seqlens_q"]
+    a = nkv.varlen_prefill(wl["q"].to(dev), kc.to(dev), vc.to(dev), cu.to(dev), cu.to(dev),
+                           wl["max_seqlen_q"], wl["scale"], block_tables=wl["block_tables"].to(dev))
+    b = nkv.varlen_prefill(wl["q"].to(dev), wl["key"].to(dev), wl["value"].to(dev), cu.to(dev),
+                           cu.to(dev), wl["max_seqlen_q"], wl["scale"])
+    assert torch.equal(a, b)
+
+
+def test_prefill_attention_module(nkv, dev):
+    """Attention.forward prefill branch with a block table: store, then attend over the cache."""
+    wl = wl_mod.prefill_workload(2, 32, 8, 0, 0, seed=20, prefix_lo=100, prefix_hi=600, chunk=150)
+    cfg = SimpleNamespace(kv_compress_enabled=False)
+    attn = nkv.Attention(32, 128, wl["scale"], 8, cfg, 1)
+    attn.k_cache, attn.v_cache = wl["k_cache"].to(dev), wl["v_cache"].to(dev)
+    nkv.set_context(False, cu_seqlens_q=wl["cu_seqlens_q"].to(dev),
+                    cu_seqlens_k=wl["cu_seqlens_k"].to(dev), max_seqlen_q=wl["max_seqlen_q"],
+                    max_seqlen_k=wl["max_seqlen_k"], slot_mapping=wl["slot_mapping"].to(dev),
+                    block_tables=wl["block_tables"].to(dev))
+    o = attn(wl["q"].to(dev), wl["key"].to(dev), wl["value"].to(dev), 0)
+    nkv.reset_context()
+    kc, vc = wl["k_cache"].clone(), wl["v_cache"].clone()
+    store_kvcache_ref(wl["key"], wl["value"], kc, vc, wl["slot_mapping"])
+    ref = varlen_prefill_ref(wl["q"].float(), kc, vc, wl["cu_seqlens_q"], wl["cu_seqlens_k"],
+                             wl["scale"], block_tables=wl["block_tables"])
+    assert _err(o, ref) <= TOL
+
+
+def test_prefill_large_logits(nkv, dev):
+    """Scores spanning ~60 log2 units force the running max to be raised mid-row."""
+    g = torch.Generator().manual_seed(21)
+    Hq, Hk, D, L = 32, 8, 128, 400
+    q = (torch.randn(L, Hq, D, generator=g) * 4).to(torch.bfloat16)
+    k = (torch.randn(L, Hk, D, generator=g) * torch.linspace(0.1, 3, L).view(L, 1, 1)
+         ).to(torch.bfloat16)
+    v = torch.randn(L, Hk, D, generator=g).to(torch.bfloat16)
+    cu = torch.tensor([0, L], dtype=torch.int32)
+    out = nkv.varlen_prefill(q.to(dev), k.to(dev), v.to(dev), cu.to(dev), cu.to(dev), L,
+                             D ** -0.5)
+    ref = varlen_prefill_ref(q.float(), k, v, cu, cu, D ** -0.5)
+    assert _err(out, ref) <= TOL
+
+
+def test_prefill_qwen3_8b_sample(nkv, dev):
+    """Two sequences drawn from the Qwen3-8B prefill workload (lengths 512..4096)."""
+    wl = wl_mod.prefill_workload(2, 32, 8, 512, 4096, seed=4)
+    out, ref = _paged(nkv, dev, wl)
+    assert _err(out, ref) <= TOL
