@@ -32,6 +32,7 @@ namespace nkv {
 
 constexpr int kPD = 128;                // head_dim
 constexpr int kStep = 32;               // keys per step
+constexpr int kBufferFlags = 0x00020000;  // raw buffer descriptor word 3 for gfx950
 constexpr int kRowE = kPD + 16;         // LDS row stride (elements; 288 B)
 constexpr int kRowsPerWave = 32;        // two 16-row groups
 constexpr int kWGRows = 4 * kRowsPerWave;
@@ -52,7 +53,7 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
     const bf16_t* __restrict__ v_cache, int64_t kv_row_stride,
     const int32_t* __restrict__ cu_seqlens_q, const int32_t* __restrict__ cu_seqlens_k,
     const int32_t* __restrict__ block_tables, int64_t bt_row_stride, int32_t Hk,
-    int32_t block_size, int32_t max_blocks, int64_t n_rows, int32_t n_tiles, float scale_log2,
+    int32_t block_size, int32_t max_blocks, int32_t n_limit, int32_t n_tiles, float scale_log2,
     bf16_t* __restrict__ out, int64_t out_row_stride) {
   constexpr int QT = kWGRows / G;  // queries per tile
   constexpr int GPH = QT / 16;     // 16-row groups per head
@@ -98,33 +99,62 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
     for (int ks = 0; ks < 4; ++ks) qreg[rr][ks] = qp[ks * 4];
   }
 
-  // ---- K/V tile loader: thread t moves 16 B of keys t/16 and t/16 + 16
-  const int lk = tid >> 4;        // key 0..15 within a half
-  const int lch = (tid & 15) * 8; // dims offset (elements)
-  const bf16_t* kcol = k_cache + (int64_t)kvh * kPD + lch;
-  const bf16_t* vcol = v_cache + (int64_t)kvh * kPD + lch;
+  // ---- K/V tile loader: thread t moves 16 B of keys t/16 and t/16 + 16 with raw
+  // buffer loads. A step's 32 keys are consecutive rows (one cache block, or the
+  // contiguous K/V), so each step is one uniform base row and a byte window that
+  // covers only its valid keys: keys past Lk and keys of invalid blocks read as 0.
+  const int lk = tid >> 4;         // key 0..15 within a half
+  const int lch = (tid & 15) * 8;  // dims offset (elements)
+  const uint32_t row_b = (uint32_t)kv_row_stride * 2u;
+  const uint32_t voff = (uint32_t)lk * row_b + (uint32_t)(kvh * kPD + lch) * 2u;
+  const uint32_t voff16 = voff + 16u * row_b;
+  // Block ids: lane i holds entry bt_base + i of the sequence's table row, read
+  // by the uniform v_readlane of the step's block (reloaded every 64 blocks).
   const int32_t* bt = block_tables ? block_tables + (int64_t)seq * bt_row_stride : nullptr;
+  int bt_base = 0;
+  int bt_lane = -1;
+  auto load_window = [&]() {
+    const int e = bt_base + lane;
+    const int id = e < max_blocks ? bt[e] : -1;
+    bt_lane = (id >= 0 && id < n_limit) ? id : -1;
+  };
+  if (bt) load_window();
+  // cursor: the step loaded next (first key c_t0, block c_blk, offset c_off in it)
+  int c_t0 = 0, c_blk = 0, c_off = 0;
   u32x4_t stg[4];  // K(lk), K(lk+16), V(lk), V(lk+16)
-  auto load_step = [&](int s) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int t = s * kStep + lk + 16 * h;
-      int64_t r = -1;
-      if (t < Lk) {
-        if (bt) {
-          const int blk = t / block_size;
-          const int64_t pb = blk < max_blocks ? (int64_t)bt[blk] : -1;
-          if (pb >= 0 && pb * block_size < n_rows) r = pb * block_size + t % block_size;
-        } else {
-          r = (int64_t)kb0 + t;
-        }
+  auto load_step = [&]() {
+    int nv = min(kStep, Lk - c_t0);
+    int64_t row0;
+    if (bt) {
+      if (c_blk - bt_base >= 64) {  // uniform, once per 64 blocks
+        bt_base += 64;
+        load_window();
       }
-      const bool ok = r >= 0 && r < n_rows;
-      const int64_t rc = ok ? r : 0;  // row 0 is always readable
-      u32x4_t kv = *reinterpret_cast<const u32x4_t*>(kcol + rc * kv_row_stride);
-      u32x4_t vv = *reinterpret_cast<const u32x4_t*>(vcol + rc * kv_row_stride);
-      stg[h] = ok ? kv : u32x4_t{0u, 0u, 0u, 0u};
-      stg[2 + h] = ok ? vv : u32x4_t{0u, 0u, 0u, 0u};
+      const int pb = __builtin_amdgcn_readlane(bt_lane, c_blk - bt_base);
+      if (pb < 0) nv = 0;
+      row0 = (int64_t)pb * block_size + c_off;
+    } else {
+      row0 = (int64_t)kb0 + c_t0;
+      if (kb0 + c_t0 < 0 || kb0 + c_t0 > n_limit - nv) nv = 0;  // outside the K/V rows
+    }
+    if (nv <= 0) {
+      nv = 0;
+      row0 = 0;
+    }
+    const uint32_t bytes = (uint32_t)nv * row_b;
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(k_cache + row0 * kv_row_stride), (short)0, bytes, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(v_cache + row0 * kv_row_stride), (short)0, bytes, kBufferFlags);
+    stg[0] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rk, voff, 0, 0));
+    stg[1] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rk, voff16, 0, 0));
+    stg[2] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rv, voff, 0, 0));
+    stg[3] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rv, voff16, 0, 0));
+    c_t0 += kStep;
+    c_off += kStep;
+    if (bt && c_off >= block_size) {  // block_size is a multiple of kStep
+      c_off = 0;
+      c_blk = __builtin_amdgcn_readfirstlane(c_blk + 1);
     }
   };
   auto store_step = [&](int buf) {
@@ -146,13 +176,16 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
   const int tr_col = (col & 3) * 4;
 
   if (n_steps > 0) {
-    load_step(0);
+    load_step();
     store_step(0);
   }
+  // Q and the first tile are in registers/LDS: an explicit full wait here lets the
+  // loop's next-tile loads stay in flight across the whole step.
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   for (int s = 0; s < n_steps; ++s) {
     const int buf = s & 1;
-    if (s + 1 < n_steps) load_step(s + 1);
+    if (s + 1 < n_steps) load_step();
     const bf16_t* kt = kbuf[buf];
     const bf16_t* vt = vbuf[buf];
 
@@ -197,9 +230,7 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
       }
       float cmax = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
                          fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-      cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
-      cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
-      const float cm = cmax * scale_log2;
+      const float cm = col_max4(cmax) * scale_log2;
       const bool raise = cm > m_run[rr] + kLazy;  // false while the row has no visible key
       if (__builtin_amdgcn_ballot_w64(raise) != 0) {
         const float alpha = raise ? fast_exp2(m_run[rr] - cm) : 1.f;  // exp2(-inf) = 0
@@ -237,9 +268,7 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
   // ---- epilogue: normalise and store this lane's 4 dims of each 16-dim block
 #pragma unroll
   for (int rr = 0; rr < 2; ++rr) {
-    float l = l_run[rr];
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
+    const float l = col_sum4(l_run[rr]);
     if (jrow[rr] >= Lq) continue;
     const float inv = l > 0.f ? 1.f / l : 0.f;
     bf16_t* op = out + (int64_t)(q0 + jrow[rr]) * out_row_stride +
@@ -282,13 +311,20 @@ extern "C" int nkv_prefill_varlen(const void* q, int64_t q_row_stride, const voi
                   kv_row_stride >= (int64_t)n_kv_heads * kPD && kv_row_stride % 8 == 0,
               NKV_EINVAL, "prefill_varlen: row strides must cover the heads, multiples of 8");
   NKV_REQUIRE(n_rows > 0, NKV_EINVAL, "prefill_varlen: empty K/V");
+  NKV_REQUIRE(kv_row_stride * 2 * kStep < (1ll << 31), NKV_EUNSUPPORTED,
+              "prefill_varlen: K/V row stride too large");
   int max_blocks = 0;
   if (block_tables) {
-    NKV_REQUIRE(block_size > 0 && max_blocks_per_seq > 0 && bt_row_stride >= max_blocks_per_seq,
+    NKV_REQUIRE(block_size > 0 && block_size % kStep == 0, NKV_EUNSUPPORTED,
+                "prefill_varlen: block_size must be a positive multiple of %d", kStep);
+    NKV_REQUIRE(max_blocks_per_seq > 0 && bt_row_stride >= max_blocks_per_seq,
                 NKV_EINVAL, "prefill_varlen: paged mode needs block_size, max_blocks_per_seq "
                 "and bt_row_stride >= max_blocks_per_seq");
     max_blocks = max_blocks_per_seq;
   }
+  // paged: valid block ids are [0, n_rows / block_size); contiguous: valid rows
+  const int32_t n_limit = (int32_t)std::min<int64_t>(block_tables ? n_rows / block_size : n_rows,
+                                                     INT32_MAX);
   const int qt = kWGRows / g;
   const int n_tiles = (max_seqlen_q + qt - 1) / qt;
   const int64_t grid = (int64_t)n_seqs * n_tiles * n_kv_heads;
@@ -299,7 +335,7 @@ extern "C" int nkv_prefill_varlen(const void* q, int64_t q_row_stride, const voi
   hipLaunchKernelGGL(prefill_varlen_kernel<G>, dim3((unsigned)grid), dim3(256), 0, s,            \
                      (const bf16_t*)q, q_row_stride, (const bf16_t*)k_cache,                     \
                      (const bf16_t*)v_cache, kv_row_stride, cu_seqlens_q, cu_seqlens_k,          \
-                     block_tables, bt_row_stride, n_kv_heads, block_size, max_blocks, n_rows,    \
+                     block_tables, bt_row_stride, n_kv_heads, block_size, max_blocks, n_limit,   \
                      n_tiles, sl2, (bf16_t*)out, out_row_stride)
   switch (g) {
     case 1: NKV_PREFILL_LAUNCH(1); break;
