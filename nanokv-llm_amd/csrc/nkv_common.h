@@ -66,16 +66,21 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// max(a, b, c) as one v_maximum3_f32 (no operand canonicalisation; NaN-propagating)
+__device__ __forceinline__ float fmax3(float a, float b, float c) {
+  return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
+}
+
 // Max over the four 16-lane rows of a wave for each column (lane % 16), without
 // LDS: v_permlane16_swap pairs rows 0/1 and 2/3, v_permlane32_swap pairs the
 // two halves; each swap leaves both values of a pair in (r[0], r[1]).
 __device__ __forceinline__ float col_max4(float v) {
   const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
                                                   false);
-  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  v = __builtin_elementwise_maximum(__uint_as_float(a[0]), __uint_as_float(a[1]));
   const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
                                                   false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+  return __builtin_elementwise_maximum(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 __device__ __forceinline__ float col_sum4(float v) {
   const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,

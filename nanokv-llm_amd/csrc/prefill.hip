@@ -10,16 +10,21 @@
 //    tile's 128 "rows" are its queries for all g query heads of the KV head,
 //    so one K/V tile in LDS serves g heads (GQA sharing). Wave w owns two
 //    16-row groups (32 rows).
-//  * Keys advance in 32-key steps; each step's K and V (2 x 8 KiB) are
-//    loaded by the whole workgroup with 16-byte loads into registers,
-//    written to a double-buffered LDS tile, one barrier per step.
+//  * Keys advance in 32-key steps. Each step's K and V tiles (2 x 8 KiB) go
+//    from HBM straight into LDS with gfx950's 16-byte buffer-load-to-LDS
+//    (no staging registers, no LDS write instructions) through a ring of
+//    kStages tiles, issued kStages-1 steps ahead; one barrier per step.
+//    LDS rows are dense (256 B) with the 16-byte chunks of row r XOR-permuted
+//    by 2*(r & 7), which keeps both the K row reads and the V transpose reads
+//    free of bank conflicts; the permutation is applied on the global side
+//    (each lane fetches the chunk that belongs at its fixed LDS slot).
 //  * S^T = K Q^T  (v_mfma_f32_16x16x32_bf16: A = 16 keys from LDS, B = the
 //    wave's Q^T held in registers for the whole sequence) puts, in lane l,
 //    row l%16 and keys 4(l/16)..+3 of each 16-key half. That is exactly the
 //    B operand of  O^T += V^T P^T  (16x16x32 over the 32 keys) once the two
 //    halves' weights are packed to bf16; V^T (A operand) comes from LDS with
 //    two ds_read_b64_tr_b16 per 16-dim block. Each lane owns one row: the
-//    online softmax needs one xor-max over the 4 key groups per step.
+//    online softmax needs one max over the 4 key groups per step.
 //  * Causal: a tile stops at its last visible key; masks are applied per
 //    element only where needed. Tiles are dispatched largest-first and the
 //    KV head is the fastest grid index, so with 8 KV heads each head's tiles
@@ -27,24 +32,50 @@
 #include "nkv_common.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace nkv {
 
-constexpr int kPD = 128;                // head_dim
-constexpr int kStep = 32;               // keys per step
+constexpr int kPD = 128;                  // head_dim
+constexpr int kStep = 32;                 // keys per step
+constexpr int kStages = 3;                // LDS ring depth (steps)
+constexpr int kTileB = kStep * kPD * 2;   // bytes of one K or V tile
+constexpr int kStageB = 2 * kTileB;       // K tile then V tile
 constexpr int kBufferFlags = 0x00020000;  // raw buffer descriptor word 3 for gfx950
-constexpr int kRowE = kPD + 16;         // LDS row stride (elements; 288 B)
-constexpr int kRowsPerWave = 32;        // two 16-row groups
+constexpr int kRowsPerWave = 32;          // two 16-row groups
 constexpr int kWGRows = 4 * kRowsPerWave;
-constexpr float kLazy = 8.f;             // log2 headroom before the running max is raised
+constexpr float kLazy = 8.f;              // log2 headroom before the running max is raised
 
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
+typedef __attribute__((address_space(3))) u32x4_t lds_u32x4_t;
+typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
   const bf16x2v_t v = {(__bf16)a, (__bf16)b};
   return __builtin_bit_cast(uint32_t, v);
+}
+// acc + lo + hi of a packed bf16 pair (v_dot2c_f32_bf16 against (1, 1))
+__device__ __forceinline__ float sum2_bf16(uint32_t pair, float acc) {
+  const bf16x2v_t ones = {(__bf16)1.f, (__bf16)1.f};
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v_t, pair), ones, acc, false);
+}
+// Raw buffer descriptor over [base, base + bytes): loads past `bytes` return 0.
+__device__ __forceinline__ i32x4_t buffer_desc(const void* base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)(uintptr_t)base;
+  return i32x4_t{__builtin_amdgcn_readfirstlane((int32_t)(uint32_t)a),
+                 __builtin_amdgcn_readfirstlane((int32_t)((a >> 32) & 0xffffu)),
+                 __builtin_amdgcn_readfirstlane((int32_t)bytes), kBufferFlags};
+}
+// 16 bytes per lane from desc+voff into LDS at lds_addr + 16 * lane. Written as
+// asm so that the compiler does not add a wait for it before every barrier;
+// the ring's own s_waitcnt (vmcnt) orders it.
+__device__ __forceinline__ void load_to_lds(i32x4_t desc, uint32_t lds_addr, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(lds_addr), "v"(voff), "s"(desc)
+               : "memory");
 }
 
 template <int G>
@@ -57,12 +88,11 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
     bf16_t* __restrict__ out, int64_t out_row_stride) {
   constexpr int QT = kWGRows / G;  // queries per tile
   constexpr int GPH = QT / 16;     // 16-row groups per head
-  __shared__ __attribute__((aligned(16))) bf16_t kbuf[2][kStep * kRowE];
-  __shared__ __attribute__((aligned(16))) bf16_t vbuf[2][kStep * kRowE];
+  __shared__ __attribute__((aligned(1024))) char ring[kStages * kStageB];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g4 = lane >> 4;
   const int col = lane & 15;
 
@@ -80,34 +110,22 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
   const int last_key = min(Lk - 1, diag + j0 + QT - 1);
   const int n_steps = last_key >= 0 ? last_key / kStep + 1 : 0;
 
-  // ---- this wave's two row groups: head and first query of each
-  int head[2], jrow[2];
-#pragma unroll
-  for (int rr = 0; rr < 2; ++rr) {
-    const int rg = wave * 2 + rr;
-    head[rr] = rg / GPH;
-    jrow[rr] = j0 + (rg % GPH) * 16 + col;  // this lane's query (row)
-  }
-  // Q^T as the MFMA B operand: lane l -> row l%16, dims 8*(l/16) + 32*ks
-  u32x4_t qreg[2][4];
-#pragma unroll
-  for (int rr = 0; rr < 2; ++rr) {
-    const int jc = jrow[rr] < Lq ? jrow[rr] : j0;  // rows past the sequence: discarded
-    const u32x4_t* qp = reinterpret_cast<const u32x4_t*>(
-        q + (int64_t)(q0 + jc) * q_row_stride + (int64_t)(kvh * G + head[rr]) * kPD + g4 * 8);
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) qreg[rr][ks] = qp[ks * 4];
-  }
-
-  // ---- K/V tile loader: thread t moves 16 B of keys t/16 and t/16 + 16 with raw
-  // buffer loads. A step's 32 keys are consecutive rows (one cache block, or the
-  // contiguous K/V), so each step is one uniform base row and a byte window that
-  // covers only its valid keys: keys past Lk and keys of invalid blocks read as 0.
-  const int lk = tid >> 4;         // key 0..15 within a half
-  const int lch = (tid & 15) * 8;  // dims offset (elements)
+  // ---- K/V tile loads. Wave w fills rows 8w .. 8w+7 of a tile with two
+  // 1 KiB loads (4 rows each); lane i lands at row 8w + 4h + i/16, slot i%16,
+  // and fetches the row's chunk (i%16) ^ 2*(row & 7). A step's 32 keys are
+  // consecutive rows (one cache block, or the contiguous K/V), so a step is
+  // one uniform base row and a byte window covering only its valid keys:
+  // keys past Lk and keys of invalid blocks read as 0.
   const uint32_t row_b = (uint32_t)kv_row_stride * 2u;
-  const uint32_t voff = (uint32_t)lk * row_b + (uint32_t)(kvh * kPD + lch) * 2u;
-  const uint32_t voff16 = voff + 16u * row_b;
+  const int lrow = lane >> 4;  // 0..3
+  const int slot = lane & 15;
+  const uint32_t vo0 = (uint32_t)(8 * wave + lrow) * row_b + (uint32_t)kvh * (kPD * 2) +
+                       (uint32_t)(slot ^ (2 * lrow)) * 16u;
+  const uint32_t vo1 = (uint32_t)(8 * wave + 4 + lrow) * row_b + (uint32_t)kvh * (kPD * 2) +
+                       (uint32_t)(slot ^ (2 * (4 + lrow))) * 16u;
+  const uint32_t ring_base =
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)ring + (uint32_t)wave * 2048u;
+
   // Block ids: lane i holds entry bt_base + i of the sequence's table row, read
   // by the uniform v_readlane of the step's block (reloaded every 64 blocks).
   const int32_t* bt = block_tables ? block_tables + (int64_t)seq * bt_row_stride : nullptr;
@@ -121,15 +139,10 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
   if (bt) load_window();
   // cursor: the step loaded next (first key c_t0, block c_blk, offset c_off in it)
   int c_t0 = 0, c_blk = 0, c_off = 0;
-  u32x4_t stg[4];  // K(lk), K(lk+16), V(lk), V(lk+16)
-  auto load_step = [&]() {
+  auto issue = [&](int stage) {
     int nv = min(kStep, Lk - c_t0);
     int64_t row0;
     if (bt) {
-      if (c_blk - bt_base >= 64) {  // uniform, once per 64 blocks
-        bt_base += 64;
-        load_window();
-      }
       const int pb = __builtin_amdgcn_readlane(bt_lane, c_blk - bt_base);
       if (pb < 0) nv = 0;
       row0 = (int64_t)pb * block_size + c_off;
@@ -142,14 +155,13 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
       row0 = 0;
     }
     const uint32_t bytes = (uint32_t)nv * row_b;
-    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(k_cache + row0 * kv_row_stride), (short)0, bytes, kBufferFlags);
-    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(v_cache + row0 * kv_row_stride), (short)0, bytes, kBufferFlags);
-    stg[0] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rk, voff, 0, 0));
-    stg[1] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rk, voff16, 0, 0));
-    stg[2] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rv, voff, 0, 0));
-    stg[3] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rv, voff16, 0, 0));
+    const i32x4_t dk = buffer_desc(k_cache + row0 * kv_row_stride, bytes);
+    const i32x4_t dv = buffer_desc(v_cache + row0 * kv_row_stride, bytes);
+    const uint32_t at = ring_base + (uint32_t)stage * kStageB;
+    load_to_lds(dk, at, vo0);
+    load_to_lds(dk, at + 1024u, vo1);
+    load_to_lds(dv, at + kTileB, vo0);
+    load_to_lds(dv, at + kTileB + 1024u, vo1);
     c_t0 += kStep;
     c_off += kStep;
     if (bt && c_off >= block_size) {  // block_size is a multiple of kStep
@@ -157,13 +169,53 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
       c_blk = __builtin_amdgcn_readfirstlane(c_blk + 1);
     }
   };
-  auto store_step = [&](int buf) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      *reinterpret_cast<u32x4_t*>(&kbuf[buf][(lk + 16 * h) * kRowE + lch]) = stg[h];
-      *reinterpret_cast<u32x4_t*>(&vbuf[buf][(lk + 16 * h) * kRowE + lch]) = stg[2 + h];
+  auto refill_window = [&]() {  // uniform; once per 64 blocks
+    if (bt && c_blk - bt_base >= 64) {
+      bt_base += 64;
+      load_window();
     }
   };
+
+  // ---- prologue: the first kStages-1 steps in flight, then Q
+#pragma unroll
+  for (int st = 0; st < kStages - 1; ++st) {
+    issue(st);
+    refill_window();
+  }
+
+  // ---- this wave's two row groups: head and query of this lane's row
+  int head[2], jrow[2];
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr) {
+    const int rg = wave * 2 + rr;
+    head[rr] = rg / GPH;
+    jrow[rr] = j0 + (rg % GPH) * 16 + col;
+  }
+  // Q^T as the MFMA B operand: lane l -> row l%16, dims 8*(l/16) + 32*ks
+  u32x4_t qreg[2][4];
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr) {
+    const int jc = jrow[rr] < Lq ? jrow[rr] : j0;  // rows past the sequence: discarded
+    const u32x4_t* qp = reinterpret_cast<const u32x4_t*>(
+        q + (int64_t)(q0 + jc) * q_row_stride + (int64_t)(kvh * G + head[rr]) * kPD + g4 * 8);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) qreg[rr][ks] = qp[ks * 4];
+  }
+
+  // LDS read offsets (bytes from a tile's start). K A operand, 16-key half hh,
+  // dims 32ks + 8*g4: row 16hh + col, logical chunk g4 + 4ks.
+  uint32_t ko[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+    ko[ks] = (uint32_t)col * 256u + (uint32_t)((g4 + 4 * ks) ^ (2 * (col & 7))) * 16u;
+  // V^T via ds_read_b64_tr_b16: lane 16g + 4r + c reads row 4g + r (and +16),
+  // dims 16db + 4c .. +3 = logical chunk 2db + c/2, half c%2.
+  const int vrow = 4 * g4 + (col >> 2);
+  const int vc = col & 3;
+  uint32_t vo[8];
+#pragma unroll
+  for (int db = 0; db < 8; ++db)
+    vo[db] = (uint32_t)vrow * 256u + (uint32_t)(db ^ (vrow & 7)) * 32u + (uint32_t)vc * 8u;
 
   f32x4_t acc[2][8];  // O^T: lane l -> row l%16, dims 16*db + 4*(l/16) .. +3
 #pragma unroll
@@ -172,22 +224,25 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
     for (int db = 0; db < 8; ++db) acc[rr][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   float m_run[2] = {-INFINITY, -INFINITY};
   float l_run[2] = {0.f, 0.f};
-  const int tr_row = 4 * g4 + (col >> 2);  // ds_read_b64_tr_b16 source row / column
-  const int tr_col = (col & 3) * 4;
 
-  if (n_steps > 0) {
-    load_step();
-    store_step(0);
-  }
-  // Q and the first tile are in registers/LDS: an explicit full wait here lets the
-  // loop's next-tile loads stay in flight across the whole step.
-  __builtin_amdgcn_s_waitcnt(0);
+  // Q is in registers before the loop: the empty asm uses pin the loads'
+  // completion here, so no wait for them (which would also wait for the ring's
+  // loads) lands inside the loop.
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr)
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) asm volatile("" ::"v"(qreg[rr][ks]));
+  // first step's tile landed (each wave waits for its own loads; the barrier
+  // publishes all of them)
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * (kStages - 2)) : "memory");
   __syncthreads();
-  for (int s = 0; s < n_steps; ++s) {
-    const int buf = s & 1;
-    if (s + 1 < n_steps) load_step();
-    const bf16_t* kt = kbuf[buf];
-    const bf16_t* vt = vbuf[buf];
+
+  const char* lds = (const char*)(__attribute__((address_space(3))) char*)ring;
+  auto step = [&](auto stage_c, int s) {
+    constexpr int ST = decltype(stage_c)::value;
+    issue((ST + kStages - 1) % kStages);  // step s + kStages - 1
+    const char* kt = lds + ST * kStageB;
+    const char* vt = kt + kTileB;
 
     // S^T for both 16-key halves and both row groups
     f32x4_t st[2][2];
@@ -196,7 +251,7 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
       u32x4_t ka[4];
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks)
-        ka[ks] = *reinterpret_cast<const u32x4_t*>(&kt[(16 * h + col) * kRowE + g4 * 8 + ks * 32]);
+        ka[ks] = *reinterpret_cast<const u32x4_t*>(kt + h * 4096 + ko[ks]);
 #pragma unroll
       for (int rr = 0; rr < 2; ++rr) {
         f32x4_t a = {0.f, 0.f, 0.f, 0.f};
@@ -207,10 +262,23 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
         st[rr][h] = a;
       }
     }
+    // V^T operands of the step (A of O^T += V^T P^T), read now so that the LDS
+    // latency hides behind the softmax. k-slot j of lane group g is key 4g+j
+    // (j<4) of the first 16-key half and key 16+4g+(j-4) of the second.
+    u32x4_t va[8];
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+      const i16x4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(vt + vo[db]));
+      const i16x4_t v1 =
+          __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(vt + 4096 + vo[db]));
+      va[db] = u32x4_t{__builtin_bit_cast(uint2, v0).x, __builtin_bit_cast(uint2, v0).y,
+                       __builtin_bit_cast(uint2, v1).x, __builtin_bit_cast(uint2, v1).y};
+    }
     // online softmax per row group (log2 domain, running max m_run kept scaled).
     // The max is only raised when a row's maximum grows by more than kLazy
     // (log2 units): weights then stay <= 2^kLazy, exact after the final 1/l.
-    // P^T is packed as the MFMA B operand (8 bf16 per lane).
+    // P^T is packed as the MFMA B operand (8 bf16 per lane); the row sum is
+    // taken over the same bf16 weights that multiply V.
     const bool edge = (s * kStep + kStep - 1 > diag + j0) || (s * kStep + kStep > Lk);  // uniform
     u32x4_t pb[2];
 #pragma unroll
@@ -228,8 +296,8 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
           for (int r = 0; r < 4; ++r)
             if (s * kStep + 16 * h + 4 * g4 + r > lim) sv[4 * h + r] = -INFINITY;
       }
-      float cmax = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
-                         fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+      const float cmax = fmax3(fmax3(sv[0], sv[1], sv[2]), fmax3(sv[3], sv[4], sv[5]),
+                               fmax3(sv[6], sv[7], -INFINITY));
       const float cm = col_max4(cmax) * scale_log2;
       const bool raise = cm > m_run[rr] + kLazy;  // false while the row has no visible key
       if (__builtin_amdgcn_ballot_w64(raise) != 0) {
@@ -243,27 +311,34 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
       float p[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) p[e] = fast_exp2(fmaf(sv[e], scale_log2, -mb));  // -inf -> 0
-      l_run[rr] += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
       pb[rr] = u32x4_t{pack2(p[0], p[1]), pack2(p[2], p[3]), pack2(p[4], p[5]), pack2(p[6], p[7])};
-    }
-    // O^T[dims][rows] += V^T[dims][keys] P^T[keys][rows]: k-slot j of lane group
-    // g is key 4g+j (j<4) of the first half, key 16+4g+(j-4) of the second
+      float l = l_run[rr];
 #pragma unroll
-    for (int db = 0; db < 8; ++db) {
-      const i16x4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (lds_i16x4_t*)&vt[tr_row * kRowE + db * 16 + tr_col]);
-      const i16x4_t v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (lds_i16x4_t*)&vt[(16 + tr_row) * kRowE + db * 16 + tr_col]);
-      const u32x4_t va = {__builtin_bit_cast(uint2, v0).x, __builtin_bit_cast(uint2, v0).y,
-                          __builtin_bit_cast(uint2, v1).x, __builtin_bit_cast(uint2, v1).y};
+      for (int e = 0; e < 4; ++e) l = sum2_bf16(pb[rr][e], l);
+      l_run[rr] = l;
+    }
+#pragma unroll
+    for (int db = 0; db < 8; ++db)
 #pragma unroll
       for (int rr = 0; rr < 2; ++rr)
-        acc[rr][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8_v(va), as_bf16x8_v(pb[rr]),
-                                                               acc[rr][db], 0, 0, 0);
-    }
-    if (s + 1 < n_steps) store_step(buf ^ 1);
+        acc[rr][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8_v(va[db]),
+                                                               as_bf16x8_v(pb[rr]), acc[rr][db],
+                                                               0, 0, 0);
+    // next step's tile landed (own loads), then publish and free this stage
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * (kStages - 2)) : "memory");
     __syncthreads();
+    refill_window();
+  };
+  static_assert(kStages == 3, "the step loop below is unrolled for 3 stages");
+  for (int s = 0;;) {
+    if (s >= n_steps) break;
+    step(std::integral_constant<int, 0>{}, s++);
+    if (s >= n_steps) break;
+    step(std::integral_constant<int, 1>{}, s++);
+    if (s >= n_steps) break;
+    step(std::integral_constant<int, 2>{}, s++);
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no load into LDS outlives the workgroup
 
   // ---- epilogue: normalise and store this lane's 4 dims of each 16-dim block
 #pragma unroll
