@@ -11,7 +11,11 @@ before timing starts.
 Printed JSON line: decode GB/s (algorithmic K/V/q/out/table bytes over the
 decode time), the roofline of the dominant kernel (split-K decode) with its
 HIP-event duration, the compression step time at batch 500 (top-20, window
-4 blocks, keep 513), and the oracle's CPU decode rate on a bounded sample.
+4 blocks, keep 513), varlen causal prefill over the paged cache at Qwen3-8B
+geometry (16 prompts U[512,4096], and 2048-token chunks after prefixes
+U[0,8192]) in TFLOP/s against the bf16 MFMA peak, the store_kvcache rate of
+the prefill-sized scatter, and the oracle's CPU decode rate on a bounded
+sample.
 """
 from __future__ import annotations
 
@@ -33,6 +37,7 @@ wl_mod = importlib.import_module("nanokv-llm_amd.workloads")
 cu = importlib.import_module("nanokv-llm_amd.layers.compress_utils")
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 METRIC = "paged decode-attn GB/s (% HBM peak) @Qwen3-8B; KV-compress step µs @bs500"
 
 
@@ -58,7 +63,8 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--compress-reps", type=int, default=30)
-    p.add_argument("--only", choices=["all", "decode", "compress"], default="all",
+    p.add_argument("--prefill-reps", type=int, default=20)
+    p.add_argument("--only", choices=["all", "decode", "compress", "prefill"], default="all",
                    help="run one part only (for profiling)")
     p.add_argument("--copy-calibration-mib", type=int, default=0,
                    help="also run 5 device-to-device copies of this many MiB (a kernel of "
@@ -156,14 +162,7 @@ def run_decode(args, dev):
 
 def _gather_sample(wl, bt, kc, vc, n):
     """Copy the blocks of the first n sequences to host: compact pool + remapped table."""
-    btn = bt[:n].cpu()
-    ids = sorted({int(x) for x in btn.flatten().tolist() if x >= 0})
-    remap = {b: i for i, b in enumerate(ids)}
-    idx = torch.tensor(ids, device=kc.device)
-    kh, vh = kc.index_select(0, idx).cpu(), vc.index_select(0, idx).cpu()
-    bt2 = torch.tensor([[remap.get(int(x), -1) for x in row] for row in btn.tolist()],
-                       dtype=torch.int32)
-    return kh, vh, bt2
+    return _gather_sample_rows(bt[:n].cpu(), kc, vc)
 
 
 def parity_sample(wl, bt, out, kc, vc, n):
@@ -240,6 +239,90 @@ def run_compress(args, dev):
             "compress_sequences": m}
 
 
+def prefill_flops(Lq, Lk, Hq, D=128):
+    """4*Hq*D per visible (query, key) pair; query j of a sequence sees Lk-Lq+j+1 keys."""
+    pairs = sum(q * (k - q) + q * (q + 1) // 2 for q, k in zip(Lq, Lk))
+    return 4 * Hq * D * pairs
+
+
+def run_prefill_one(args, dev, name, wl):
+    """store_kvcache of the prompt rows, then varlen causal prefill over the paged cache."""
+    kc, vc = wl["k_cache"], wl["v_cache"]
+    key, value, slots = wl["key"], wl["value"], wl["slot_mapping"].to(dev)
+    q = wl["q"]
+    cq, ck = wl["cu_seqlens_q"].to(dev), wl["cu_seqlens_k"].to(dev)
+    bt = wl["block_tables"].to(dev)
+    out = torch.empty_like(q)
+    stream = torch.cuda.current_stream()
+
+    def ev():
+        return torch.cuda.Event(enable_timing=True)
+
+    store_t, pre_t = [], []
+    for i in range(3 + args.prefill_reps):
+        e0, e1, e2 = ev(), ev(), ev()
+        e0.record(stream)
+        nkv.store_kvcache(key, value, kc, vc, slots)
+        e1.record(stream)
+        nkv.varlen_prefill(q, kc, vc, cq, ck, wl["max_seqlen_q"], wl["scale"], block_tables=bt,
+                           out=out)
+        e2.record(stream)
+        torch.cuda.synchronize()
+        if i >= 3:
+            store_t.append(e0.elapsed_time(e1))
+            pre_t.append(e1.elapsed_time(e2))
+    flops = prefill_flops(wl["Lq"], wl["Lk"], wl["Hq"])
+    pre_ms = statistics.median(pre_t)
+    st_ms = statistics.median(store_t)
+    n_rows = key.size(0)
+    st_bytes = 2 * 2 * n_rows * key.size(1) * key.size(2) * 2 + n_rows * 4  # K,V read+write
+    tflops = flops / (pre_ms * 1e-3) / 1e12
+    # parity: the last min(128, Lq) queries of the shortest sequence vs the oracle
+    from oracle.attention_ref import varlen_prefill_ref
+    i = min(range(len(wl["Lq"])), key=lambda j: wl["Lq"][j])
+    Lq_i, Lk_i = wl["Lq"][i], wl["Lk"][i]
+    nq = min(128, Lq_i)
+    r0 = int(wl["cu_seqlens_q"][i]) + Lq_i - nq
+    btr = wl["block_tables"][i:i + 1]
+    kh, vh, bt2 = _gather_sample_rows(btr, kc, vc)
+    ref = varlen_prefill_ref(q[r0:r0 + nq].float().cpu(), kh, vh,
+                             torch.tensor([0, nq], dtype=torch.int32),
+                             torch.tensor([0, Lk_i], dtype=torch.int32), wl["scale"],
+                             block_tables=bt2)
+    err = float((out[r0:r0 + nq].float().cpu() - ref).abs().max())
+    return {
+        f"{name}_us": round(pre_ms * 1e3, 1),
+        f"{name}_tflops": round(tflops, 1),
+        f"{name}_pct_mfma_peak": round(100.0 * tflops / MFMA_BF16_PEAK_TFLOPS, 1),
+        f"{name}_gflop": round(flops / 1e9, 1),
+        f"{name}_parity_max_abs_err": err,
+        f"{name}_store_us": round(st_ms * 1e3, 1),
+        f"{name}_store_gbs": round(st_bytes / (st_ms * 1e-3) / 1e9, 1),
+    }
+
+
+def _gather_sample_rows(btr, kc, vc):
+    """Blocks of the given table rows copied to host, with the table remapped."""
+    ids = sorted({int(x) for x in btr.flatten().tolist() if x >= 0})
+    remap = {b: j for j, b in enumerate(ids)}
+    idx = torch.tensor(ids, device=kc.device)
+    kh, vh = kc.index_select(0, idx).cpu(), vc.index_select(0, idx).cpu()
+    bt2 = torch.tensor([[remap.get(int(x), -1) for x in row] for row in btr.tolist()],
+                       dtype=torch.int32)
+    return kh, vh, bt2
+
+
+def run_prefill(args, dev):
+    res = {}
+    for name, fn in (("prefill", wl_mod.prefill_qwen3_8b),
+                     ("prefill_chunked", wl_mod.prefill_chunked_qwen3_8b)):
+        wl = fn(device=dev)
+        res.update(run_prefill_one(args, dev, name, wl))
+        del wl
+        torch.cuda.empty_cache()
+    return res
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -254,6 +337,9 @@ def main():
         comp = run_compress(args, dev)
         print(json.dumps(comp), flush=True)
         return
+    if args.only == "prefill":
+        print(json.dumps(run_prefill(args, dev)), flush=True)
+        return
     print(f"[bench] decode workload: bs 64, Hq 32, Hk 8, ctx U[2048,8192], pool 4096 blocks",
           file=sys.stderr, flush=True)
     wl, sets, r = run_decode(args, dev)
@@ -265,6 +351,9 @@ def main():
         return
     comp = run_compress(args, dev)
     print(f"[bench] compress done: {comp['compress_step_us']} us", file=sys.stderr, flush=True)
+    pre = run_prefill(args, dev)
+    print(f"[bench] prefill done: {pre['prefill_tflops']} / {pre['prefill_chunked_tflops']} "
+          f"TFLOP/s", file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(wl, sets[0][0], wl["k_cache"], wl["v_cache"])
@@ -309,6 +398,16 @@ def main():
         },
         "cpu_baseline": cpu,
         **comp,
+        "prefill_roofline": {
+            "kernel": "prefill_varlen_kernel<4>",
+            "bound": "mfma",
+            "achieved": pre["prefill_chunked_tflops"],
+            "peak": MFMA_BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(pre["prefill_chunked_tflops"] / MFMA_BF16_PEAK_TFLOPS, 4),
+            "workload": "2048-token chunks after paged prefixes U[0,8192], 16 sequences",
+        },
+        **pre,
     }
     print(json.dumps(line), flush=True)
 
