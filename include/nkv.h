@@ -178,6 +178,55 @@ int nkv_compress_topk(const float* importance, int32_t n_rows, int32_t n_cand,
                       int32_t num_keep, int32_t* keep_idx, void* stream);
 
 /*
+ * Fused selection: score + importance + top-k in one launch (agg "group") or
+ * two (agg "all": per-KV-head partial importance, then their sum and the
+ * top-k) when
+ * W*B <= 1024, B % 64 == 0 and Hq/Hk is a power of two <= 16 (the reference's
+ * W = 4, B = 256 qualifies); otherwise nkv_compress_score + nkv_compress_topk
+ * run on the same workspace. Outputs are those of the two calls:
+ *   importance_out fp32 [m, n_sets, W*B-1],
+ *   keep_idx int32 [m, n_sets, num_keep+2] = [0, ascending kept..., W*B-1].
+ * Workspace: caller-owned, >= nkv_compress_select_workspace_bytes bytes.
+ * Replaces: the scoring and selection of MyCompressCompact, i.e. SnapKV
+ *           (nanokvllm/layers/CompressMethod.py:4-57) as called from
+ *           nanokvllm/layers/compress_utils.py:133-183
+ */
+size_t nkv_compress_select_workspace_bytes(int32_t m, int32_t n_q_heads, int32_t n_kv_heads,
+                                           int32_t window_blocks, int32_t block_size);
+
+int nkv_compress_select(const void* q, int64_t q_row_stride,
+                        const void* k_cache, const int32_t* block_tables,
+                        int64_t bt_row_stride, int32_t max_blocks_per_seq,
+                        const int32_t* base_context_lens,
+                        const int32_t* seq_idx, int32_t m,
+                        int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                        int32_t block_size, int32_t window_blocks, int64_t n_blocks,
+                        float scale, int32_t agg_mode, int32_t num_keep,
+                        float* importance_out, int32_t* keep_idx,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * One layer's compression step: nkv_compress_select (num_keep = keep_tokens-2)
+ * followed by nkv_compress_compact, fused when the selection is (one launch
+ * for agg "group": each (sequence, KV head) workgroup scores, selects and
+ * compacts its KV head; two for agg "all": per-KV-head partial importance,
+ * then sum + select + compact). Same outputs and cache/context_lens effects
+ * as the two calls; compaction additionally needs keep_tokens + B - 1 <= 768
+ * and B a power of two for the fused form. Workspace as nkv_compress_select.
+ * Replaces: MyCompressCompact's per-layer work (scoring, selection,
+ *           compaction, context_lens), nanokvllm/layers/compress_utils.py:100-263
+ */
+int nkv_compress_step(const void* q, int64_t q_row_stride, void* k_cache, void* v_cache,
+                      const int32_t* block_tables, int64_t bt_row_stride,
+                      int32_t max_blocks_per_seq, const int32_t* base_context_lens,
+                      int32_t* context_lens, const int32_t* seq_idx, int32_t m,
+                      int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                      int32_t block_size, int32_t window_blocks, int64_t n_blocks,
+                      float scale, int32_t agg_mode, int32_t keep_tokens,
+                      float* importance_out, int32_t* keep_idx,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * In-place compaction of the window of each selected sequence, K and V:
  * kept window token keep_idx[j,s,i] moves to window position i
  * (i < keep_tokens); the tail partial block (tail = len % B tokens, block

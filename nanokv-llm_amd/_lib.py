@@ -43,6 +43,13 @@ SIGNATURES = {
     "nkv_compress_score": (C.c_int, [_p, _i64, _p, _p, _i64, _i32, _p, _p, _i32, _i32, _i32, _i32,
                                      _i32, _i32, _i64, _f32, _i32, _p, _p, _sz, _p]),
     "nkv_compress_topk": (C.c_int, [_p, _i32, _i32, _i32, _p, _p]),
+    "nkv_compress_select_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
+    "nkv_compress_select": (C.c_int, [_p, _i64, _p, _p, _i64, _i32, _p, _p, _i32, _i32, _i32,
+                                      _i32, _i32, _i32, _i64, _f32, _i32, _i32, _p, _p, _p, _sz,
+                                      _p]),
+    "nkv_compress_step": (C.c_int, [_p, _i64, _p, _p, _p, _i64, _i32, _p, _p, _p, _i32, _i32, _i32,
+                                    _i32, _i32, _i32, _i64, _f32, _i32, _i32, _p, _p, _p, _sz,
+                                    _p]),
     "nkv_compress_compact": (C.c_int, [_p, _p, _p, _i64, _i32, _p, _p, _p, _i32, _p, _i32, _i32,
                                        _i32, _i32, _i32, _i32, _i64, _p]),
     "nkv_compress_finalize": (C.c_int, [_p, _i64, _i32, _p, _p, _i32, _i32, _i32, _i32, _i32, _p,

@@ -234,6 +234,431 @@ __global__ __launch_bounds__(64) void compress_topk_kernel(
   }
 }
 
+// ------------------------------------------------------------- fused step
+// One 1024-thread workgroup per (selected sequence, KV head) holds that KV
+// head's whole window: wave w scores window keys [64w, 64w + 64) for the G
+// query heads of the KV head (K read in place, q K^T on MFMA), so per-head
+// softmax statistics are two workgroup reductions and the head sum of the
+// group is lane-local plus one permlane step.
+//  * agg "group" (compress_group_kernel): the workgroup owns its kept set:
+//    score -> select -> (step) compact this KV head's K and V rows. One launch.
+//  * agg "all": compress_partial_kernel writes each group's importance; then
+//    compress_sum_kernel, per (sequence, KV head), adds the Hk partials in
+//    KV-head order (every KV head's workgroup derives the same kept set),
+//    selects and compacts. The kernel boundary makes the partials visible
+//    across XCDs; a device-scope fence inside a kernel would write back the
+//    whole L2.
+// Selection: 8-pass 4-bit radix select of the num_keep-th largest order key
+// (one candidate per thread), ties to the lower index, ascending output by a
+// workgroup prefix count -- no sort. Compaction: every source row of the
+// (sequence, KV head) unit, K and V, is loaded into registers before any
+// destination is written (the reference's two-phase index_select().clone() /
+// index_copy_), one 256-byte row per 16 lanes.
+constexpr int kSelThreads = 1024;
+constexpr int kSelWaves = kSelThreads / 64;
+constexpr int kSelKeysPerWave = 64;
+constexpr int kSelMaxWindow = kSelWaves * kSelKeysPerWave;  // 1024
+constexpr int kStepRounds = 12;                             // 64 rows per round
+constexpr int kStepMaxRows = 64 * kStepRounds;              // kept + tail rows
+
+struct SelectLds {
+  float red[kSelWaves][16];
+  __attribute__((aligned(16))) float imp[kSelMaxWindow];
+  __attribute__((aligned(16))) int cnt[2][16][kSelWaves];  // [pass parity][digit][wave]
+  int wcnt[kSelWaves];
+  int32_t keep[kSelMaxWindow];
+  int32_t win_pb[kMaxWindowBlocks + 1];
+  int32_t src[kStepMaxRows];
+  int32_t dst[kStepMaxRows];
+};
+
+__device__ __forceinline__ float row16_max(float v) {  // over the 16 lanes of a row
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float row16_sum(float v) {
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Exclusive prefix count of `flag` over the workgroup (thread order) + total.
+__device__ __forceinline__ int block_excl_count(bool flag, int* wcnt, int& total) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const uint64_t b = __builtin_amdgcn_ballot_w64(flag);
+  const int before = __builtin_popcountll(b & ((1ull << lane) - 1ull));
+  if (lane == 0) wcnt[wave] = __builtin_popcountll(b);
+  __syncthreads();
+  int base = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < kSelWaves; ++w) {
+    const int c = wcnt[w];
+    base += w < wave ? c : 0;
+    tot += c;
+  }
+  __syncthreads();  // wcnt is reused by the next call
+  total = tot;
+  return base + before;
+}
+
+// Selects the num_keep largest of L.imp[0, n_cand) and writes
+// [0, ascending kept indices, n_cand] to L.keep and (if out) to out.
+__device__ __forceinline__ void block_select(SelectLds& L, int n_cand, int num_keep,
+                                             int32_t* __restrict__ out) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const bool real = tid < n_cand;
+  const uint32_t key = real ? order_key(L.imp[tid]) : 0u;  // padding sorts last
+  uint32_t T = 0;
+#pragma unroll 1
+  for (int pass = 0; pass < 8; ++pass) {
+    const int shift = 28 - 4 * pass;
+    // c = number of digits d in 1..15 with key >= T + (d << shift)
+    const uint32_t above = key >= T ? (key - T) >> shift : 0u;
+    int c = (int)(above < 15u ? above : 15u);
+    asm volatile("" : "+v"(c));  // one VGPR: each ballot below is a single v_cmp
+    int mine = 0;  // lane d: this wave's count of candidates with c >= d
+#pragma unroll
+    for (int d = 1; d < 16; ++d) {
+      const int n = __builtin_popcountll(__builtin_amdgcn_ballot_w64(c >= d));
+      asm volatile("v_writelane_b32 %0, %1, %2" : "+v"(mine) : "s"(n), "i"(d));
+    }
+    int(*cnt)[kSelWaves] = L.cnt[pass & 1];
+    if (lane < 16) cnt[lane][wave] = mine;
+    __syncthreads();
+    int tot = 0;
+    const u32x4_t* row = reinterpret_cast<const u32x4_t*>(cnt[lane & 15]);
+#pragma unroll
+    for (int w4 = 0; w4 < kSelWaves / 4; ++w4) {
+      const u32x4_t v = row[w4];
+      tot += (int)(v.x + v.y + v.z + v.w);
+    }
+    const uint64_t ok = __builtin_amdgcn_ballot_w64(lane >= 1 && lane < 16 && tot >= num_keep);
+    const int digit = ok ? 63 - __builtin_clzll(ok) : 0;
+    T += (uint32_t)digit << shift;
+  }
+  const bool gt = real && key > T;
+  const bool eq = real && key == T;
+  int n_gt = 0, n_eq = 0, n_sel = 0;
+  (void)block_excl_count(gt, L.wcnt, n_gt);
+  const int eq_rank = block_excl_count(eq, L.wcnt, n_eq);
+  const bool sel = gt || (eq && eq_rank < num_keep - n_gt);  // ties: lower index first
+  const int pos = block_excl_count(sel, L.wcnt, n_sel);
+  if (sel) {
+    L.keep[1 + pos] = tid;
+    if (out) out[1 + pos] = tid;
+  }
+  if (tid == 0) {
+    L.keep[0] = 0;
+    L.keep[num_keep + 1] = n_cand;
+    if (out) {
+      out[0] = 0;
+      out[num_keep + 1] = n_cand;
+    }
+  }
+  __syncthreads();
+}
+
+// Window of (sequence j, KV head kvh): the importance of each key summed over
+// the G query heads of the group, for this thread's keys t0 + 16g + col
+// (valid in lanes of row group 0). Uses L.red.
+template <int G>
+__device__ __forceinline__ void group_importance(
+    SelectLds& L, const bf16_t* __restrict__ q, int64_t q_row_stride,
+    const bf16_t* __restrict__ k, const int32_t* __restrict__ block_tables,
+    int64_t bt_row_stride, int32_t max_blocks, const int32_t* __restrict__ base_context_lens,
+    const int32_t* __restrict__ seq_idx, int j, int kvh, int Hk, int block_size,
+    int window_blocks, int64_t n_blocks, float scale_log2, float gi[4]) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int hg = lane >> 4;   // MFMA row group: heads 4hg .. 4hg+3
+  const int col = lane & 15;  // key within a 16-key group
+  const int Lw = window_blocks * block_size;
+  const int t0 = wave * kSelKeysPerWave;
+  // ---- locate this wave's 64 keys (one cache block holds them all)
+  int64_t base = 0, tok_stride, qrow;
+  bool valid = t0 < Lw;
+  if (block_tables) {
+    const int seq = seq_idx[j];
+    const int len = base_context_lens[seq];
+    const int full = len / block_size;
+    int64_t pb = -1;
+    if (valid && full >= window_blocks && full <= max_blocks)
+      pb = block_tables[(int64_t)seq * bt_row_stride + full - window_blocks + t0 / block_size];
+    valid = valid && pb >= 0 && pb < n_blocks;
+    base = ((pb * block_size + t0 % block_size) * Hk + kvh) * (int64_t)kCD;
+    tok_stride = (int64_t)Hk * kCD;
+    qrow = seq;
+  } else {  // contiguous K [m, Hk, Lw, D]
+    base = (((int64_t)j * Hk + kvh) * Lw + t0) * kCD;
+    tok_stride = kCD;
+    qrow = j;
+  }
+  f32x4_t acc[4] = {};
+  if (valid) {  // wave-uniform
+    u32x4_t kreg[4][4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const bf16_t* kp = k + base + (g * 16 + col) * tok_stride + hg * 8;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) kreg[g][ks] = *reinterpret_cast<const u32x4_t*>(kp + ks * 32);
+    }
+    u32x4_t qreg[4];
+    const int hc = col < G ? col : 0;  // MFMA rows >= G are computed and discarded
+    const bf16_t* qp = q + qrow * q_row_stride + (int64_t)(kvh * G + hc) * kCD + hg * 8;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) qreg[ks] = *reinterpret_cast<const u32x4_t*>(qp + ks * 32);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      f32x4_t a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+        a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8_v(qreg[ks]), as_bf16x8_v(kreg[g][ks]),
+                                                     a, 0, 0, 0);
+      acc[g] = a;
+    }
+  }
+  // log2-domain scores; -inf for the sink (t = 0), the unscored last token,
+  // invalid keys and the discarded MFMA rows (heads >= G)
+  float sv[4][4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int t = t0 + g * 16 + col;
+    const bool key_ok = valid && t > 0 && t < Lw - 1;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      sv[g][r] = (key_ok && 4 * hg + r < G) ? acc[g][r] * scale_log2 : -INFINITY;
+  }
+  // ---- per-head softmax statistics over the window (heads 4hg + r)
+  float hm[4], hinv[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float v = row16_max(fmaxf(fmaxf(sv[0][r], sv[1][r]), fmaxf(sv[2][r], sv[3][r])));
+    if (col == 0) L.red[wave][4 * hg + r] = v;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float v = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kSelWaves; ++w) v = fmaxf(v, L.red[w][4 * hg + r]);
+    hm[r] = v;
+  }
+  __syncthreads();
+  float p[4][4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float ssum = 0.f;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      p[g][r] = (sv[g][r] == -INFINITY) ? 0.f : fast_exp2(sv[g][r] - hm[r]);
+      ssum += p[g][r];
+    }
+    ssum = row16_sum(ssum);
+    if (col == 0) L.red[wave][4 * hg + r] = ssum;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < kSelWaves; ++w) v += L.red[w][4 * hg + r];
+    hinv[r] = v > 0.f ? 1.f / v : 0.f;
+  }
+  // ---- the group's importance per key (heads summed in order)
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    float v = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v += p[g][r] * hinv[r];
+    gi[g] = col_sum4(v);  // + the other row groups' heads
+  }
+}
+
+// In-place compaction of KV head kvh of sequence seq_idx[j], K and V, with the
+// kept window positions in L.keep; kvh 0 also sets the new context length.
+__device__ __forceinline__ void compact_unit(
+    SelectLds& L, bf16_t* __restrict__ k_cache, bf16_t* __restrict__ v_cache,
+    const int32_t* __restrict__ block_tables, int64_t bt_row_stride, int32_t max_blocks,
+    const int32_t* __restrict__ base_context_lens, int32_t* __restrict__ context_lens,
+    const int32_t* __restrict__ seq_idx, int j, int kvh, int keep_tokens, int Hk, int B,
+    int window_blocks, int64_t n_blocks) {
+  const int tid = threadIdx.x;
+  const int seq = seq_idx[j];
+  const int len = base_context_lens[seq];
+  const int full = len / B;
+  const int tail = len - full * B;
+  // not compressible, or inconsistent with the table width: leave untouched
+  if (full < window_blocks || full > max_blocks || (tail > 0 && full >= max_blocks)) return;
+  const int32_t* bt = block_tables + (int64_t)seq * bt_row_stride;
+  const int wb0 = full - window_blocks;
+  const int Lw = window_blocks * B;
+  if (tid <= window_blocks) {
+    int32_t pb = -1;
+    if (tid < window_blocks) pb = bt[wb0 + tid];
+    else if (tail > 0) pb = bt[full];
+    L.win_pb[tid] = (pb >= 0 && pb < n_blocks) ? pb : -1;
+  }
+  __syncthreads();
+  // source and destination slot of every row (-1 = not moved); B is a power of two
+  const int lb = 31 - __builtin_clz(B);
+  const int32_t tail_pb = L.win_pb[window_blocks];
+  const int32_t last_pb = L.win_pb[(keep_tokens - 1) >> lb];
+  const int32_t last_dst = last_pb >= 0 ? last_pb * B + ((keep_tokens - 1) & (B - 1)) : -1;
+  const int nrows = keep_tokens + tail;
+  const int64_t n_slots = n_blocks * B;
+  for (int i = tid; i < kStepMaxRows; i += kSelThreads) {
+    int32_t sv = -1, d = -1;
+    if (i < keep_tokens) {
+      const int pos = L.keep[i];
+      if (pos >= 0 && pos < Lw) {
+        const int32_t pb = L.win_pb[pos >> lb];
+        if (pb >= 0) sv = pb * B + (pos & (B - 1));
+      }
+      const int32_t pd = L.win_pb[i >> lb];
+      if (pd >= 0) d = pd * B + (i & (B - 1));
+    } else if (i < nrows) {
+      const int u = i - keep_tokens;
+      if (tail_pb >= 0) sv = tail_pb * B + u;
+      if (last_dst >= 0 && (int64_t)last_dst + 1 + u < n_slots) d = last_dst + 1 + u;
+    }
+    const bool ok = sv >= 0 && d >= 0;
+    L.src[i] = ok ? sv : -1;
+    L.dst[i] = ok ? d : -1;
+  }
+  __syncthreads();
+  // all source rows (K and V) as unconditional 16-byte loads (rows that are
+  // not moved re-read slot 0, always valid), then the writes
+  const int64_t row = (int64_t)Hk * kCD;
+  const int64_t col = (int64_t)kvh * kCD + (tid & 15) * 8;
+  const int rsub = tid >> 4;  // 0..63: row within a round
+  u32x4_t kr[kStepRounds], vr[kStepRounds];
+#pragma unroll
+  for (int rr = 0; rr < kStepRounds; ++rr) {
+    const int64_t sv = max(L.src[rr * 64 + rsub], 0);
+    kr[rr] = *reinterpret_cast<const u32x4_t*>(k_cache + sv * row + col);
+    vr[rr] = *reinterpret_cast<const u32x4_t*>(v_cache + sv * row + col);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(0);  // all reads of the unit land before any write
+  __syncthreads();
+#pragma unroll
+  for (int rr = 0; rr < kStepRounds; ++rr) {
+    const int64_t d = L.dst[rr * 64 + rsub];
+    if (d >= 0) {
+      *reinterpret_cast<u32x4_t*>(k_cache + d * row + col) = kr[rr];
+      *reinterpret_cast<u32x4_t*>(v_cache + d * row + col) = vr[rr];
+    }
+  }
+  if (kvh == 0 && tid == 0) context_lens[seq] = len - Lw + keep_tokens;
+}
+
+// agg "group": score -> select -> (if k_cache_w) compact. Grid m * Hk.
+template <int G>
+__global__ __launch_bounds__(kSelThreads) void compress_group_kernel(
+    const bf16_t* __restrict__ q, int64_t q_row_stride, const bf16_t* __restrict__ k,
+    const int32_t* __restrict__ block_tables, int64_t bt_row_stride, int32_t max_blocks,
+    const int32_t* __restrict__ base_context_lens, const int32_t* __restrict__ seq_idx,
+    int32_t Hk, int32_t block_size, int32_t window_blocks, int64_t n_blocks, float scale_log2,
+    int32_t num_keep, float* __restrict__ importance_out, int32_t* __restrict__ keep_idx,
+    bf16_t* __restrict__ k_cache_w, bf16_t* __restrict__ v_cache_w,
+    int32_t* __restrict__ context_lens) {
+  __shared__ SelectLds L;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int kvh = blockIdx.x % Hk;
+  const int j = blockIdx.x / Hk;
+  const int Lw = window_blocks * block_size;
+  const int n_cand = Lw - 1;
+  float gi[4];
+  group_importance<G>(L, q, q_row_stride, k, block_tables, bt_row_stride, max_blocks,
+                      base_context_lens, seq_idx, j, kvh, Hk, block_size, window_blocks,
+                      n_blocks, scale_log2, gi);
+  const int t0 = (tid >> 6) * kSelKeysPerWave;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int t = t0 + g * 16 + (lane & 15);
+    if ((lane >> 4) == 0 && t < Lw) L.imp[t] = gi[g];
+  }
+  __syncthreads();
+  float* irow = importance_out + ((int64_t)j * Hk + kvh) * n_cand;
+  for (int t = tid; t < n_cand; t += kSelThreads) irow[t] = L.imp[t];
+  block_select(L, n_cand, num_keep, keep_idx + ((int64_t)j * Hk + kvh) * (num_keep + 2));
+  if (k_cache_w)
+    compact_unit(L, k_cache_w, v_cache_w, block_tables, bt_row_stride, max_blocks,
+                 base_context_lens, context_lens, seq_idx, j, kvh, num_keep + 2, Hk, block_size,
+                 window_blocks, n_blocks);
+}
+
+// agg "all", first kernel: each group's importance -> partial[j][kvh][Lw]. Grid m * Hk.
+template <int G>
+__global__ __launch_bounds__(kSelThreads) void compress_partial_kernel(
+    const bf16_t* __restrict__ q, int64_t q_row_stride, const bf16_t* __restrict__ k,
+    const int32_t* __restrict__ block_tables, int64_t bt_row_stride, int32_t max_blocks,
+    const int32_t* __restrict__ base_context_lens, const int32_t* __restrict__ seq_idx,
+    int32_t Hk, int32_t block_size, int32_t window_blocks, int64_t n_blocks, float scale_log2,
+    float* __restrict__ partial) {
+  __shared__ SelectLds L;
+  const int lane = threadIdx.x & 63;
+  const int kvh = blockIdx.x % Hk;
+  const int j = blockIdx.x / Hk;
+  const int Lw = window_blocks * block_size;
+  float gi[4];
+  group_importance<G>(L, q, q_row_stride, k, block_tables, bt_row_stride, max_blocks,
+                      base_context_lens, seq_idx, j, kvh, Hk, block_size, window_blocks,
+                      n_blocks, scale_log2, gi);
+  float* prow = partial + ((int64_t)j * Hk + kvh) * Lw;
+  const int t0 = (threadIdx.x >> 6) * kSelKeysPerWave;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int t = t0 + g * 16 + (lane & 15);
+    if ((lane >> 4) == 0 && t < Lw) prow[t] = gi[g];
+  }
+}
+
+// agg "all", second kernel: importance[j] = sum over KV heads (in order) of the
+// partials, the selection, and (if k_cache_w) the compaction of KV head kvh.
+// Grid m (selection only) or m * Hk (step: every KV head derives the same set).
+__global__ __launch_bounds__(kSelThreads) void compress_sum_kernel(
+    const float* __restrict__ partial, int32_t Hk, int32_t n_units_per_seq, int32_t block_size,
+    int32_t window_blocks, int32_t num_keep, float* __restrict__ importance_out,
+    int32_t* __restrict__ keep_idx, bf16_t* __restrict__ k_cache_w,
+    bf16_t* __restrict__ v_cache_w, const int32_t* __restrict__ block_tables,
+    int64_t bt_row_stride, int32_t max_blocks, const int32_t* __restrict__ base_context_lens,
+    int32_t* __restrict__ context_lens, const int32_t* __restrict__ seq_idx, int64_t n_blocks) {
+  __shared__ SelectLds L;
+  const int tid = threadIdx.x;
+  const int j = blockIdx.x / n_units_per_seq;
+  const int kvh = blockIdx.x % n_units_per_seq;
+  const int Lw = window_blocks * block_size;
+  const int n_cand = Lw - 1;
+  const float* pj = partial + (int64_t)j * Hk * Lw;
+  const bool writer = kvh == 0;
+  float* irow = importance_out + (int64_t)j * n_cand;
+  for (int t = tid; t < Lw; t += kSelThreads) {
+    float v = 0.f;
+    for (int h0 = 0; h0 < Hk; h0 += 16) {  // 16 loads in flight, added in KV-head order
+      float part[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) part[i] = pj[(int64_t)min(h0 + i, Hk - 1) * Lw + t];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) v += h0 + i < Hk ? part[i] : 0.f;
+    }
+    L.imp[t] = v;
+    if (writer && t < n_cand) irow[t] = v;
+  }
+  __syncthreads();
+  block_select(L, n_cand, num_keep, writer ? keep_idx + (int64_t)j * (num_keep + 2) : nullptr);
+  if (k_cache_w)
+    compact_unit(L, k_cache_w, v_cache_w, block_tables, bt_row_stride, max_blocks,
+                 base_context_lens, context_lens, seq_idx, j, kvh, num_keep + 2, Hk, block_size,
+                 window_blocks, n_blocks);
+}
+
 // ----------------------------------------------------------------- compact
 // Unit = (selected j, KV head, K|V, half row). Rows i < keep_tokens move from
 // window position keep_idx[i] to window position i; rows keep_tokens + u
@@ -460,6 +885,127 @@ extern "C" int nkv_compress_topk(const float* importance, int32_t n_rows, int32_
   return check_launch("nkv_compress_topk");
 }
 
+extern "C" size_t nkv_compress_select_workspace_bytes(int32_t m, int32_t n_q_heads,
+                                                      int32_t n_kv_heads, int32_t window_blocks,
+                                                      int32_t block_size) {
+  if (m <= 0 || n_q_heads <= 0 || n_kv_heads <= 0 || window_blocks <= 0 || block_size <= 0)
+    return 0;
+  const size_t lw = (size_t)window_blocks * block_size;
+  const size_t partials = (size_t)m * n_kv_heads * lw * sizeof(float);
+  const size_t scores = (size_t)m * n_q_heads * lw * sizeof(float);  // general path
+  return partials > scores ? partials : scores;
+}
+
+namespace nkv {
+// Launches the fused selection (and, with k_cache_w, the compaction) when the
+// shape allows it; returns 1 if the caller must take the general path.
+static int launch_fused(const void* q, int64_t q_row_stride, const void* k_cache,
+                        const int32_t* block_tables, int64_t bt_row_stride,
+                        int32_t max_blocks_per_seq, const int32_t* base_context_lens,
+                        const int32_t* seq_idx, int32_t m, int32_t n_q_heads, int32_t n_kv_heads,
+                        int32_t head_dim, int32_t block_size, int32_t window_blocks,
+                        int64_t n_blocks, float scale, int32_t agg_mode, int32_t num_keep,
+                        float* importance_out, int32_t* keep_idx, void* workspace,
+                        void* k_cache_w, void* v_cache_w, int32_t* context_lens,
+                        hipStream_t s) {
+  const int g = n_q_heads / n_kv_heads;
+  const int Lw = window_blocks * block_size;
+  const bool step = k_cache_w != nullptr;
+  const bool ok = Lw <= kSelMaxWindow && block_size % kSelKeysPerWave == 0 && g <= 16 &&
+                  (g & (g - 1)) == 0 && head_dim == kCD && window_blocks <= kMaxWindowBlocks &&
+                  (!step || (num_keep + 2 + block_size - 1 <= kStepMaxRows &&
+                             (block_size & (block_size - 1)) == 0));
+  if (!ok) return 1;
+  const float sl2 = scale * kLog2e;
+  const unsigned units = (unsigned)(m * n_kv_heads);
+  float* partial = (float*)workspace;
+  bf16_t* kw = (bf16_t*)k_cache_w;
+  bf16_t* vw = (bf16_t*)v_cache_w;
+#define NKV_G_SWITCH(MACRO) \
+  switch (g) {              \
+    case 1: MACRO(1); break; \
+    case 2: MACRO(2); break; \
+    case 4: MACRO(4); break; \
+    case 8: MACRO(8); break; \
+    default: MACRO(16); break; \
+  }
+  if (agg_mode == NKV_AGG_GROUP) {
+#define NKV_GROUP(G)                                                                          \
+  hipLaunchKernelGGL(compress_group_kernel<G>, dim3(units), dim3(kSelThreads), 0, s,           \
+                     (const bf16_t*)q, q_row_stride, (const bf16_t*)k_cache, block_tables,     \
+                     bt_row_stride, max_blocks_per_seq, base_context_lens, seq_idx, n_kv_heads, \
+                     block_size, window_blocks, n_blocks, sl2, num_keep, importance_out,       \
+                     keep_idx, kw, vw, context_lens)
+    NKV_G_SWITCH(NKV_GROUP)
+#undef NKV_GROUP
+    return check_launch("compress (group)") ? -1 : 0;
+  }
+#define NKV_PARTIAL(G)                                                                        \
+  hipLaunchKernelGGL(compress_partial_kernel<G>, dim3(units), dim3(kSelThreads), 0, s,         \
+                     (const bf16_t*)q, q_row_stride, (const bf16_t*)k_cache, block_tables,     \
+                     bt_row_stride, max_blocks_per_seq, base_context_lens, seq_idx, n_kv_heads, \
+                     block_size, window_blocks, n_blocks, sl2, partial)
+  NKV_G_SWITCH(NKV_PARTIAL)
+#undef NKV_PARTIAL
+#undef NKV_G_SWITCH
+  if (check_launch("compress (partial)")) return -1;
+  const int per_seq = step ? n_kv_heads : 1;
+  hipLaunchKernelGGL(compress_sum_kernel, dim3((unsigned)(m * per_seq)), dim3(kSelThreads), 0, s,
+                     (const float*)partial, n_kv_heads, per_seq, block_size, window_blocks,
+                     num_keep, importance_out, keep_idx, kw, vw, block_tables, bt_row_stride,
+                     max_blocks_per_seq, base_context_lens, context_lens, seq_idx, n_blocks);
+  return check_launch("compress (sum)") ? -1 : 0;
+}
+}  // namespace nkv
+
+extern "C" int nkv_compress_select(const void* q, int64_t q_row_stride, const void* k_cache,
+                                   const int32_t* block_tables, int64_t bt_row_stride,
+                                   int32_t max_blocks_per_seq, const int32_t* base_context_lens,
+                                   const int32_t* seq_idx, int32_t m, int32_t n_q_heads,
+                                   int32_t n_kv_heads, int32_t head_dim, int32_t block_size,
+                                   int32_t window_blocks, int64_t n_blocks, float scale,
+                                   int32_t agg_mode, int32_t num_keep, float* importance_out,
+                                   int32_t* keep_idx, void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+  clear_error();
+  NKV_REQUIRE(m >= 0 && n_q_heads > 0 && n_kv_heads > 0 && window_blocks > 0 && block_size > 0,
+              NKV_EINVAL, "compress_select: bad sizes");
+  if (m == 0) return NKV_OK;
+  NKV_REQUIRE(n_q_heads % n_kv_heads == 0, NKV_EINVAL, "compress_select: Hq %% Hk != 0");
+  NKV_REQUIRE(agg_mode == NKV_AGG_ALL || agg_mode == NKV_AGG_GROUP, NKV_EINVAL,
+              "compress_select: bad agg_mode %d", agg_mode);
+  const int Lw = window_blocks * block_size;
+  NKV_REQUIRE(num_keep > 0 && num_keep < Lw - 1, NKV_EINVAL,
+              "compress_select: need 0 < num_keep < window tokens - 1 (got %d)", num_keep);
+  NKV_REQUIRE(keep_idx && importance_out, NKV_EINVAL, "compress_select: null output");
+  NKV_REQUIRE(q && k_cache, NKV_EINVAL, "compress_select: null pointer");
+  NKV_REQUIRE(!block_tables || (seq_idx && base_context_lens && max_blocks_per_seq > 0 &&
+                                 bt_row_stride >= max_blocks_per_seq),
+              NKV_EINVAL, "compress_select: paged mode needs seq_idx, base_context_lens and a "
+              "block table width");
+  NKV_REQUIRE(aligned16(q) && aligned16(k_cache) && q_row_stride % 8 == 0, NKV_EINVAL,
+              "compress_select: q/k must be 16-byte aligned");
+  const size_t need = nkv_compress_select_workspace_bytes(m, n_q_heads, n_kv_heads,
+                                                          window_blocks, block_size);
+  NKV_REQUIRE(workspace && workspace_bytes >= need, NKV_EWORKSPACE,
+              "compress_select: workspace needs %zu bytes (got %zu)", need, workspace_bytes);
+  hipStream_t s = as_stream(stream);
+  const int rc = launch_fused(q, q_row_stride, k_cache, block_tables, bt_row_stride,
+                              max_blocks_per_seq, base_context_lens, seq_idx, m, n_q_heads,
+                              n_kv_heads, head_dim, block_size, window_blocks, n_blocks, scale,
+                              agg_mode, num_keep, importance_out, keep_idx, workspace, nullptr,
+                              nullptr, nullptr, s);
+  if (rc <= 0) return rc < 0 ? NKV_ELAUNCH : NKV_OK;
+  // general path: score + importance kernels, then the one-wave top-k
+  const int n_sets = agg_mode == NKV_AGG_ALL ? 1 : n_kv_heads;
+  int e = nkv_compress_score(q, q_row_stride, k_cache, block_tables, bt_row_stride,
+                             max_blocks_per_seq, base_context_lens, seq_idx, m, n_q_heads,
+                             n_kv_heads, head_dim, block_size, window_blocks, n_blocks, scale,
+                             agg_mode, importance_out, workspace, workspace_bytes, stream);
+  if (e) return e;
+  return nkv_compress_topk(importance_out, m * n_sets, Lw - 1, num_keep, keep_idx, stream);
+}
+
 extern "C" int nkv_compress_compact(void* k_cache, void* v_cache, const int32_t* block_tables,
                                     int64_t bt_row_stride, int32_t max_blocks_per_seq,
                                     const int32_t* base_context_lens,
@@ -528,4 +1074,60 @@ extern "C" int nkv_compress_finalize(int32_t* block_tables, int64_t bt_row_strid
                      m, keep_tokens, block_size, window_blocks, rewrite_tables, slot_mapping,
                      events);
   return check_launch("nkv_compress_finalize");
+}
+
+extern "C" int nkv_compress_step(const void* q, int64_t q_row_stride, void* k_cache,
+                                 void* v_cache, const int32_t* block_tables,
+                                 int64_t bt_row_stride, int32_t max_blocks_per_seq,
+                                 const int32_t* base_context_lens, int32_t* context_lens,
+                                 const int32_t* seq_idx, int32_t m, int32_t n_q_heads,
+                                 int32_t n_kv_heads, int32_t head_dim, int32_t block_size,
+                                 int32_t window_blocks, int64_t n_blocks, float scale,
+                                 int32_t agg_mode, int32_t keep_tokens, float* importance_out,
+                                 int32_t* keep_idx, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+  using namespace nkv;
+  clear_error();
+  NKV_REQUIRE(m >= 0 && n_q_heads > 0 && n_kv_heads > 0 && window_blocks > 0 && block_size > 0,
+              NKV_EINVAL, "compress_step: bad sizes");
+  if (m == 0) return NKV_OK;
+  NKV_REQUIRE(block_tables && v_cache && context_lens && seq_idx && base_context_lens,
+              NKV_EINVAL, "compress_step: null pointer");
+  NKV_REQUIRE(aligned16(v_cache), NKV_EINVAL, "compress_step: caches must be 16-byte aligned");
+  NKV_REQUIRE(n_blocks * block_size < (1ll << 31), NKV_EUNSUPPORTED,
+              "compress_step: cache of %lld slots exceeds int32 slot ids",
+              (long long)(n_blocks * block_size));
+  NKV_REQUIRE(n_q_heads % n_kv_heads == 0, NKV_EINVAL, "compress_step: Hq %% Hk != 0");
+  NKV_REQUIRE(agg_mode == NKV_AGG_ALL || agg_mode == NKV_AGG_GROUP, NKV_EINVAL,
+              "compress_step: bad agg_mode %d", agg_mode);
+  const int n_sets = agg_mode == NKV_AGG_ALL ? 1 : n_kv_heads;
+  const int num_keep = keep_tokens - 2;
+  NKV_REQUIRE(keep_tokens > 2 && num_keep < window_blocks * block_size - 1, NKV_EINVAL,
+              "compress_step: need 2 < keep_tokens <= window tokens");
+  NKV_REQUIRE(q && k_cache && keep_idx && importance_out && aligned16(q) && aligned16(k_cache) &&
+                  q_row_stride % 8 == 0 && max_blocks_per_seq > 0 &&
+                  bt_row_stride >= max_blocks_per_seq,
+              NKV_EINVAL, "compress_step: bad q/k/tables");
+  const size_t need = nkv_compress_select_workspace_bytes(m, n_q_heads, n_kv_heads,
+                                                          window_blocks, block_size);
+  NKV_REQUIRE(workspace && workspace_bytes >= need, NKV_EWORKSPACE,
+              "compress_step: workspace needs %zu bytes (got %zu)", need, workspace_bytes);
+  hipStream_t s = as_stream(stream);
+  int rc = launch_fused(q, q_row_stride, k_cache, block_tables, bt_row_stride, max_blocks_per_seq,
+                    base_context_lens, seq_idx, m, n_q_heads, n_kv_heads, head_dim, block_size,
+                    window_blocks, n_blocks, scale, agg_mode, num_keep, importance_out, keep_idx,
+                    workspace, k_cache, v_cache, context_lens, s);
+  if (rc < 0) return NKV_ELAUNCH;
+  if (rc == 0) return NKV_OK;
+  // general path: selection, then the compaction kernel
+  rc = nkv_compress_select(q, q_row_stride, k_cache, block_tables, bt_row_stride,
+                           max_blocks_per_seq, base_context_lens, seq_idx, m, n_q_heads,
+                           n_kv_heads, head_dim, block_size, window_blocks, n_blocks, scale,
+                           agg_mode, num_keep, importance_out, keep_idx, workspace,
+                           workspace_bytes, stream);
+  if (rc) return rc;
+  return nkv_compress_compact(k_cache, v_cache, block_tables, bt_row_stride, max_blocks_per_seq,
+                              base_context_lens, context_lens, seq_idx, m, keep_idx, n_sets,
+                              keep_tokens, n_kv_heads, head_dim, block_size, window_blocks,
+                              n_blocks, stream);
 }

@@ -10,8 +10,10 @@ appended to ``context.compression_events``.
 The reference's helpers ``get_tail_window_and_tail_slots`` and
 ``gather_kv_by_slots`` (:9-97) have no counterpart: window location is done
 inside the kernels, and K is scored in place instead of being gathered.
-Kernels (libnkv_amd.so): nkv_compress_score -> nkv_compress_topk ->
-nkv_compress_compact (every layer) -> nkv_compress_finalize (last layer).
+Kernels (libnkv_amd.so): nkv_compress_step (scoring, importance, top-k and
+compaction: one launch for agg "group", two for agg "all") on every layer,
+nkv_compress_finalize on the last layer. nkv_compress_select and
+nkv_compress_compact are the same work as separate calls.
 """
 from __future__ import annotations
 
@@ -43,10 +45,17 @@ def _buffers(context, selected, device, m, n_sets, n_cand, keep_tokens, ws_bytes
     return buf
 
 
+def select_workspace_bytes(m, n_q_heads, n_kv_heads, window_blocks, block_size):
+    """Bytes of the workspace nkv_compress_select needs."""
+    return _lib.lib().nkv_compress_select_workspace_bytes(m, n_q_heads, n_kv_heads,
+                                                          window_blocks, block_size)
+
+
 def compress_select(q, k_cache, block_tables, base_context_lens, seq_idx, window_blocks,
                     num_keep, scale, agg="all", importance=None, keep_idx=None, workspace=None):
     """Score the window of each selected sequence and pick the kept positions.
 
+    A caller-provided ``workspace`` is uint8 of >= select_workspace_bytes(...).
     Returns (keep_idx int32 [m, n_sets, 1+num_keep+1], importance fp32
     [m, n_sets, W*B-1]). keep_idx rows are [0, ascending top-num_keep, W*B-1].
     """
@@ -60,19 +69,16 @@ def compress_select(q, k_cache, block_tables, base_context_lens, seq_idx, window
         importance = torch.empty(m, n_sets, n_cand, dtype=torch.float32, device=q.device)
     if keep_idx is None:
         keep_idx = torch.empty(m, n_sets, num_keep + 2, dtype=torch.int32, device=q.device)
-    ws_bytes = L.nkv_compress_workspace_bytes(m, Hq, window_blocks, B)
+    ws_bytes = select_workspace_bytes(m, Hq, Hk, window_blocks, B)
     if workspace is None:
         workspace = torch.empty(max(ws_bytes, 4), dtype=torch.uint8, device=q.device)
-    stream = _lib.stream_of(q)
-    rc = L.nkv_compress_score(
+    rc = L.nkv_compress_select(
         q.data_ptr(), q.stride(0), k_cache.data_ptr(), block_tables.data_ptr(),
         block_tables.stride(0), block_tables.size(1), base_context_lens.data_ptr(),
         seq_idx.data_ptr(), m, Hq, Hk, D, B, window_blocks, NB, float(scale), AGG_MODES[agg],
-        importance.data_ptr(), workspace.data_ptr(), workspace.numel(), stream)
-    _lib.check(rc, "compress_score")
-    rc = L.nkv_compress_topk(importance.data_ptr(), m * n_sets, n_cand, num_keep,
-                             keep_idx.data_ptr(), stream)
-    _lib.check(rc, "compress_topk")
+        num_keep, importance.data_ptr(), keep_idx.data_ptr(), workspace.data_ptr(),
+        workspace.numel(), _lib.stream_of(q))
+    _lib.check(rc, "compress_select")
     return keep_idx, importance
 
 
@@ -87,6 +93,36 @@ def compress_compact(k_cache, v_cache, block_tables, base_context_lens, context_
         seq_idx.data_ptr(), m, keep_idx.data_ptr(), n_sets, keep_tokens, Hk, D, B,
         window_blocks, NB, _lib.stream_of(k_cache))
     _lib.check(rc, "compress_compact")
+
+
+def compress_step(q, k_cache, v_cache, block_tables, base_context_lens, context_lens, seq_idx,
+                  window_blocks, keep_tokens, scale, agg="all", importance=None, keep_idx=None,
+                  workspace=None):
+    """compress_select + compress_compact in one call (fused on the GPU).
+
+    Returns (keep_idx, importance) like compress_select; the caches and
+    context_lens are updated like compress_compact.
+    """
+    m = seq_idx.numel()
+    NB, B, Hk, D = k_cache.shape
+    Hq = q.size(1)
+    n_sets = 1 if agg == "all" else Hk
+    n_cand = window_blocks * B - 1
+    if importance is None:
+        importance = torch.empty(m, n_sets, n_cand, dtype=torch.float32, device=q.device)
+    if keep_idx is None:
+        keep_idx = torch.empty(m, n_sets, keep_tokens, dtype=torch.int32, device=q.device)
+    ws_bytes = select_workspace_bytes(m, Hq, Hk, window_blocks, B)
+    if workspace is None:
+        workspace = torch.empty(max(ws_bytes, 4), dtype=torch.uint8, device=q.device)
+    rc = _lib.lib().nkv_compress_step(
+        q.data_ptr(), q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(), block_tables.data_ptr(),
+        block_tables.stride(0), block_tables.size(1), base_context_lens.data_ptr(),
+        context_lens.data_ptr(), seq_idx.data_ptr(), m, Hq, Hk, D, B, window_blocks, NB,
+        float(scale), AGG_MODES[agg], keep_tokens, importance.data_ptr(), keep_idx.data_ptr(),
+        workspace.data_ptr(), workspace.numel(), _lib.stream_of(q))
+    _lib.check(rc, "compress_step")
+    return keep_idx, importance
 
 
 def compress_finalize(block_tables, base_context_lens, seq_idx, keep_tokens, block_size,
@@ -152,14 +188,12 @@ def MyCompressCompact(q_current: torch.Tensor, k_cache: torch.Tensor, v_cache: t
     Hq, D = q_current.size(1), q_current.size(2)
     Hk = k_cache.size(2)
     n_sets = 1 if agg == "all" else Hk
-    ws_bytes = _lib.lib().nkv_compress_workspace_bytes(m, Hq, window_blocks, B)
+    ws_bytes = select_workspace_bytes(m, Hq, Hk, window_blocks, B)
     buf = _buffers(context, selected, device, m, n_sets, window_tokens - 1, keep_tokens,
                    ws_bytes, 4 + context.block_tables.size(1))
-    compress_select(q_current, k_cache, context.block_tables, base, buf.seq_idx, window_blocks,
-                    num_keep, D ** -0.5, agg, importance=buf.importance, keep_idx=buf.keep_idx,
-                    workspace=buf.workspace)
-    compress_compact(k_cache, v_cache, context.block_tables, base, context.context_lens,
-                     buf.seq_idx, buf.keep_idx, window_blocks)
+    compress_step(q_current, k_cache, v_cache, context.block_tables, base, context.context_lens,
+                  buf.seq_idx, window_blocks, keep_tokens, D ** -0.5, agg,
+                  importance=buf.importance, keep_idx=buf.keep_idx, workspace=buf.workspace)
     if layer_id + 1 >= num_layers:
         compress_finalize(context.block_tables, base, buf.seq_idx, keep_tokens, B, window_blocks,
                           buf.events, rewrite_tables=rewrite_tables,

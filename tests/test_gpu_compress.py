@@ -157,3 +157,51 @@ def test_snapkv_plugin_api(nkv, dev):
         overlap = len(set(got[r].tolist()) & set(ref[r].tolist())) / 511
         assert overlap >= 0.99
     assert nkv.SnapKV(Q.to(dev), K[:, :, :256].contiguous().to(dev), None, 300, 1) is False
+
+
+@pytest.mark.parametrize("agg", ["all", "group"])
+def test_fused_step_equals_select_then_compact(nkv, dev, agg):
+    """nkv_compress_step (fused) == nkv_compress_select + nkv_compress_compact, bitwise,
+    and its compaction matches the oracle given its kept indices."""
+    wl = _state(seed=9, bs=40, topk=7)
+    bt = wl["block_tables"]
+    btg = bt.to(dev)
+    base = wl["context_lens"].to(dev)
+    sel = torch.tensor(wl["seq_idx"], dtype=torch.int32, device=dev)
+    q = wl["q"].to(dev)
+    k1, v1 = wl["k_cache"].to(dev), wl["v_cache"].to(dev)
+    k2, v2 = k1.clone(), v1.clone()
+    ctx1, ctx2 = base.clone(), base.clone()
+    keep1, imp1 = cu.compress_select(q, k1, btg, base, sel, W, KEEP - 2, 128 ** -0.5, agg)
+    cu.compress_compact(k1, v1, btg, base, ctx1, sel, keep1, W)
+    keep2, imp2 = cu.compress_step(q, k2, v2, btg, base, ctx2, sel, W, KEEP, 128 ** -0.5, agg)
+    torch.cuda.synchronize()
+    assert torch.equal(imp1, imp2) and torch.equal(keep1, keep2)
+    assert torch.equal(k1, k2) and torch.equal(v1, v2) and torch.equal(ctx1, ctx2)
+    kc, vc = wl["k_cache"].clone(), wl["v_cache"].clone()
+    ctx_ref = wl["context_lens"].clone()
+    ok, _, _ = compress_compact_ref(None, kc, vc, bt, wl["context_lens"], ctx_ref, wl["seq_idx"],
+                                    256, W, 2, 1, 0, 1, keep_idx=keep2.cpu().long())
+    assert ok
+    assert torch.equal(k2.cpu(), kc) and torch.equal(v2.cpu(), vc)
+    assert torch.equal(ctx2.cpu(), ctx_ref)
+
+
+def test_fused_step_skips_short_sequences(nkv, dev):
+    """A selected sequence with fewer than W full blocks is left untouched."""
+    wl = _state(seed=10, bs=16, topk=4)
+    lens = wl["context_lens"].clone()
+    short = wl["seq_idx"][0]
+    lens[short] = 3 * 256 + 17  # 3 full blocks < W
+    btg = wl["block_tables"].to(dev)
+    base = lens.to(dev)
+    ctx = base.clone()
+    sel = torch.tensor(wl["seq_idx"], dtype=torch.int32, device=dev)
+    kg, vg = wl["k_cache"].to(dev), wl["v_cache"].to(dev)
+    k0, v0 = kg.clone(), vg.clone()
+    cu.compress_step(wl["q"].to(dev), kg, vg, btg, base, ctx, sel, W, KEEP, 128 ** -0.5, "all")
+    torch.cuda.synchronize()
+    assert int(ctx[short]) == int(lens[short])
+    blocks = [int(b) for b in wl["block_tables"][short].tolist() if b >= 0]
+    for b in blocks:
+        assert torch.equal(kg[b], k0[b]) and torch.equal(vg[b], v0[b])

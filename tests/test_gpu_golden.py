@@ -89,3 +89,23 @@ def test_compress_compact_golden(nkv, dev):
     got_slots = slots.cpu().numpy()
     s_idx = fx["seq_idx"]
     assert np.array_equal(got_slots[s_idx], fx["next_slot"][s_idx])
+
+
+def test_compress_step_golden(nkv, dev):
+    """The fused step (agg "all") reproduces the fixture's compaction when its kept sets
+    equal the fixture's (they do unless fp32 near-ties reorder the threshold)."""
+    fx = load("compress_small.npz")
+    wl = wl_mod.compress_workload(6, 8, 2, 1100, 2000, 2, 11, selected_only=True)
+    kg, vg = wl["k_cache"].to(dev), wl["v_cache"].to(dev)
+    btg = torch.from_numpy(fx["block_tables"]).to(dev)
+    base = torch.from_numpy(fx["context_lens"]).to(dev)
+    ctx = base.clone()
+    sel = torch.from_numpy(fx["seq_idx"]).to(dev)
+    keep, imp = cu.compress_step(wl["q"].to(dev), kg, vg, btg, base, ctx, sel, W, KEEP,
+                                 128 ** -0.5, "all")
+    torch.cuda.synchronize()
+    assert np.allclose(imp.cpu().numpy(), fx["importance_all"], rtol=1e-4, atol=1e-7)
+    assert np.array_equal(ctx.cpu().numpy(), fx["context_lens_after"])
+    if np.array_equal(keep.cpu().numpy(), fx["keep_all"]):
+        assert digest(kg.cpu()) == str(fx["digest_k_after"])
+        assert digest(vg.cpu()) == str(fx["digest_v_after"])
