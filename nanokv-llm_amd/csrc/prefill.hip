@@ -10,7 +10,7 @@
 //    tile's 128 "rows" are its queries for all g query heads of the KV head,
 //    so one K/V tile in LDS serves g heads (GQA sharing). Wave w owns two
 //    16-row groups (32 rows).
-//  * Keys advance in 32-key steps. Each step's K and V tiles (2 x 8 KiB) go
+//  * Keys advance in 64-key steps. Each step's K and V tiles (2 x 16 KiB) go
 //    from HBM straight into LDS with gfx950's 16-byte buffer-load-to-LDS
 //    (no staging registers, no LDS write instructions) through a ring of
 //    kStages tiles, issued kStages-1 steps ahead; one barrier per step.
@@ -20,10 +20,10 @@
 //    (each lane fetches the chunk that belongs at its fixed LDS slot).
 //  * S^T = K Q^T  (v_mfma_f32_16x16x32_bf16: A = 16 keys from LDS, B = the
 //    wave's Q^T held in registers for the whole sequence) puts, in lane l,
-//    row l%16 and keys 4(l/16)..+3 of each 16-key half. That is exactly the
-//    B operand of  O^T += V^T P^T  (16x16x32 over the 32 keys) once the two
-//    halves' weights are packed to bf16; V^T (A operand) comes from LDS with
-//    two ds_read_b64_tr_b16 per 16-dim block. Each lane owns one row: the
+//    row l%16 and keys 4(l/16)..+3 of each 16-key quarter. Two quarters make
+//    the B operand of  O^T += V^T P^T  (16x16x32 over 32 keys) once their
+//    weights are packed to bf16; V^T (A operand) comes from LDS with two
+//    ds_read_b64_tr_b16 per 16-dim block and 32-key chunk. Each lane owns one row: the
 //    online softmax needs one max over the 4 key groups per step.
 //  * Causal: a tile stops at its last visible key; masks are applied per
 //    element only where needed. Tiles are dispatched largest-first and the
@@ -37,8 +37,8 @@
 namespace nkv {
 
 constexpr int kPD = 128;                  // head_dim
-constexpr int kStep = 32;                 // keys per step
-constexpr int kStages = 3;                // LDS ring depth (steps)
+constexpr int kStep = 64;                 // keys per step
+constexpr int kStages = 2;                // LDS ring depth (steps)
 constexpr int kTileB = kStep * kPD * 2;   // bytes of one K or V tile
 constexpr int kStageB = 2 * kTileB;       // K tile then V tile
 constexpr int kBufferFlags = 0x00020000;  // raw buffer descriptor word 3 for gfx950
@@ -110,24 +110,27 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
   const int last_key = min(Lk - 1, diag + j0 + QT - 1);
   const int n_steps = last_key >= 0 ? last_key / kStep + 1 : 0;
 
-  // ---- K/V tile loads. Wave w fills rows 8w .. 8w+7 of a tile with two
-  // 1 KiB loads (4 rows each); lane i lands at row 8w + 4h + i/16, slot i%16,
-  // and fetches the row's chunk (i%16) ^ 2*(row & 7). A step's 32 keys are
-  // consecutive rows (one cache block, or the contiguous K/V), so a step is
-  // one uniform base row and a byte window covering only its valid keys:
-  // keys past Lk and keys of invalid blocks read as 0.
+  // ---- K/V tile loads. Wave w fills rows 16w .. 16w+15 of a tile with four
+  // 1 KiB loads (4 rows each); lane i of load h lands at row 16w + 4h + i/16,
+  // slot i%16, and fetches the row's chunk (i%16) ^ 2*(row & 7). A wave's 16
+  // keys are consecutive rows (one cache block, B % 16 == 0, or the contiguous
+  // K/V), so each wave's share of a step is one uniform base row and a byte
+  // window covering only its valid keys: keys past Lk and keys of invalid
+  // blocks read as 0.
   const uint32_t row_b = (uint32_t)kv_row_stride * 2u;
   const int lrow = lane >> 4;  // 0..3
   const int slot = lane & 15;
-  const uint32_t vo0 = (uint32_t)(8 * wave + lrow) * row_b + (uint32_t)kvh * (kPD * 2) +
-                       (uint32_t)(slot ^ (2 * lrow)) * 16u;
-  const uint32_t vo1 = (uint32_t)(8 * wave + 4 + lrow) * row_b + (uint32_t)kvh * (kPD * 2) +
-                       (uint32_t)(slot ^ (2 * (4 + lrow))) * 16u;
+  uint32_t vol[4];
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    const int r = 4 * h + lrow;  // row within the wave's 16 (16w + r within the tile)
+    vol[h] = (uint32_t)r * row_b + (uint32_t)kvh * (kPD * 2) + (uint32_t)(slot ^ (2 * (r & 7))) * 16u;
+  }
   const uint32_t ring_base =
-      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)ring + (uint32_t)wave * 2048u;
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)ring + (uint32_t)wave * 4096u;
 
   // Block ids: lane i holds entry bt_base + i of the sequence's table row, read
-  // by the uniform v_readlane of the step's block (reloaded every 64 blocks).
+  // by the uniform v_readlane of the wave's block (reloaded every 64 blocks).
   const int32_t* bt = block_tables ? block_tables + (int64_t)seq * bt_row_stride : nullptr;
   int bt_base = 0;
   int bt_lane = -1;
@@ -136,11 +139,17 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
     const int id = e < max_blocks ? bt[e] : -1;
     bt_lane = (id >= 0 && id < n_limit) ? id : -1;
   };
-  if (bt) load_window();
-  // cursor: the step loaded next (first key c_t0, block c_blk, offset c_off in it)
-  int c_t0 = 0, c_blk = 0, c_off = 0;
+  // cursor of this wave's rows in the step loaded next: first key c_t0,
+  // block c_blk, offset c_off in it
+  int c_t0 = 16 * wave, c_blk = 0, c_off = 0;
+  if (bt) {
+    c_blk = c_t0 / block_size;
+    c_off = c_t0 - c_blk * block_size;
+    bt_base = c_blk & ~63;
+    load_window();
+  }
   auto issue = [&](int stage) {
-    int nv = min(kStep, Lk - c_t0);
+    int nv = min(16, Lk - c_t0);
     int64_t row0;
     if (bt) {
       const int pb = __builtin_amdgcn_readlane(bt_lane, c_blk - bt_base);
@@ -158,20 +167,22 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
     const i32x4_t dk = buffer_desc(k_cache + row0 * kv_row_stride, bytes);
     const i32x4_t dv = buffer_desc(v_cache + row0 * kv_row_stride, bytes);
     const uint32_t at = ring_base + (uint32_t)stage * kStageB;
-    load_to_lds(dk, at, vo0);
-    load_to_lds(dk, at + 1024u, vo1);
-    load_to_lds(dv, at + kTileB, vo0);
-    load_to_lds(dv, at + kTileB + 1024u, vo1);
+#pragma unroll
+    for (int h = 0; h < 4; ++h) load_to_lds(dk, at + 1024u * h, vol[h]);
+#pragma unroll
+    for (int h = 0; h < 4; ++h) load_to_lds(dv, at + kTileB + 1024u * h, vol[h]);
     c_t0 += kStep;
-    c_off += kStep;
-    if (bt && c_off >= block_size) {  // block_size is a multiple of kStep
-      c_off = 0;
-      c_blk = __builtin_amdgcn_readfirstlane(c_blk + 1);
+    if (bt) {
+      c_off += kStep;
+      while (c_off >= block_size) {  // uniform; block_size is a multiple of 16
+        c_off -= block_size;
+        c_blk = __builtin_amdgcn_readfirstlane(c_blk + 1);
+      }
     }
   };
   auto refill_window = [&]() {  // uniform; once per 64 blocks
     if (bt && c_blk - bt_base >= 64) {
-      bt_base += 64;
+      bt_base = c_blk & ~63;
       load_window();
     }
   };
@@ -234,7 +245,7 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
     for (int ks = 0; ks < 4; ++ks) asm volatile("" ::"v"(qreg[rr][ks]));
   // first step's tile landed (each wave waits for its own loads; the barrier
   // publishes all of them)
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * (kStages - 2)) : "memory");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(8 * (kStages - 2)) : "memory");
   __syncthreads();
 
   const char* lds = (const char*)(__attribute__((address_space(3))) char*)ring;
@@ -244,10 +255,10 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
     const char* kt = lds + ST * kStageB;
     const char* vt = kt + kTileB;
 
-    // S^T for both 16-key halves and both row groups
-    f32x4_t st[2][2];
+    // S^T for the four 16-key quarters and both row groups
+    f32x4_t st[2][4];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < 4; ++h) {
       u32x4_t ka[4];
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks)
@@ -262,42 +273,32 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
         st[rr][h] = a;
       }
     }
-    // V^T operands of the step (A of O^T += V^T P^T), read now so that the LDS
-    // latency hides behind the softmax. k-slot j of lane group g is key 4g+j
-    // (j<4) of the first 16-key half and key 16+4g+(j-4) of the second.
-    u32x4_t va[8];
-#pragma unroll
-    for (int db = 0; db < 8; ++db) {
-      const i16x4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(vt + vo[db]));
-      const i16x4_t v1 =
-          __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(vt + 4096 + vo[db]));
-      va[db] = u32x4_t{__builtin_bit_cast(uint2, v0).x, __builtin_bit_cast(uint2, v0).y,
-                       __builtin_bit_cast(uint2, v1).x, __builtin_bit_cast(uint2, v1).y};
-    }
     // online softmax per row group (log2 domain, running max m_run kept scaled).
     // The max is only raised when a row's maximum grows by more than kLazy
     // (log2 units): weights then stay <= 2^kLazy, exact after the final 1/l.
-    // P^T is packed as the MFMA B operand (8 bf16 per lane); the row sum is
-    // taken over the same bf16 weights that multiply V.
+    // P^T is packed as the MFMA B operand (8 bf16 per lane and 32-key chunk);
+    // the row sum is taken over the same bf16 weights that multiply V.
     const bool edge = (s * kStep + kStep - 1 > diag + j0) || (s * kStep + kStep > Lk);  // uniform
-    u32x4_t pb[2];
+    u32x4_t pb[2][2];
 #pragma unroll
     for (int rr = 0; rr < 2; ++rr) {
-      float sv[8];
+      float sv[16];
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
+      for (int h = 0; h < 4; ++h)
 #pragma unroll
         for (int r = 0; r < 4; ++r) sv[4 * h + r] = st[rr][h][r];
       if (edge) {
         const int lim = min(diag + jrow[rr], Lk - 1);  // last visible key of this row
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+        for (int h = 0; h < 4; ++h)
 #pragma unroll
           for (int r = 0; r < 4; ++r)
             if (s * kStep + 16 * h + 4 * g4 + r > lim) sv[4 * h + r] = -INFINITY;
       }
-      const float cmax = fmax3(fmax3(sv[0], sv[1], sv[2]), fmax3(sv[3], sv[4], sv[5]),
-                               fmax3(sv[6], sv[7], -INFINITY));
+      const float cmax = fmax3(fmax3(fmax3(sv[0], sv[1], sv[2]), fmax3(sv[3], sv[4], sv[5]),
+                                     fmax3(sv[6], sv[7], sv[8])),
+                               fmax3(sv[9], sv[10], sv[11]),
+                               fmax3(fmax3(sv[12], sv[13], sv[14]), sv[15], -INFINITY));
       const float cm = col_max4(cmax) * scale_log2;
       const bool raise = cm > m_run[rr] + kLazy;  // false while the row has no visible key
       if (__builtin_amdgcn_ballot_w64(raise) != 0) {
@@ -308,35 +309,47 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
         for (int db = 0; db < 8; ++db) acc[rr][db] *= alpha;
       }
       const float mb = m_run[rr] == -INFINITY ? 0.f : m_run[rr];
-      float p[8];
+      float p[16];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) p[e] = fast_exp2(fmaf(sv[e], scale_log2, -mb));  // -inf -> 0
-      pb[rr] = u32x4_t{pack2(p[0], p[1]), pack2(p[2], p[3]), pack2(p[4], p[5]), pack2(p[6], p[7])};
+      for (int e = 0; e < 16; ++e) p[e] = fast_exp2(fmaf(sv[e], scale_log2, -mb));  // -inf -> 0
       float l = l_run[rr];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) l = sum2_bf16(pb[rr][e], l);
+      for (int c = 0; c < 2; ++c) {
+        pb[rr][c] = u32x4_t{pack2(p[8 * c + 0], p[8 * c + 1]), pack2(p[8 * c + 2], p[8 * c + 3]),
+                            pack2(p[8 * c + 4], p[8 * c + 5]), pack2(p[8 * c + 6], p[8 * c + 7])};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) l = sum2_bf16(pb[rr][c][e], l);
+      }
       l_run[rr] = l;
     }
+    // O^T[dims][rows] += V^T[dims][keys] P^T[keys][rows] per 32-key chunk c:
+    // k-slot j of lane group g is key 32c+4g+j (j<4), or 32c+16+4g+(j-4)
 #pragma unroll
-    for (int db = 0; db < 8; ++db)
+    for (int c = 0; c < 2; ++c) {
 #pragma unroll
-      for (int rr = 0; rr < 2; ++rr)
-        acc[rr][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8_v(va[db]),
-                                                               as_bf16x8_v(pb[rr]), acc[rr][db],
-                                                               0, 0, 0);
+      for (int db = 0; db < 8; ++db) {
+        const char* vc = vt + c * 8192 + vo[db];
+        const i16x4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)vc);
+        const i16x4_t v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(vc + 4096));
+        const u32x4_t va = {__builtin_bit_cast(uint2, v0).x, __builtin_bit_cast(uint2, v0).y,
+                            __builtin_bit_cast(uint2, v1).x, __builtin_bit_cast(uint2, v1).y};
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr)
+          acc[rr][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              as_bf16x8_v(va), as_bf16x8_v(pb[rr][c]), acc[rr][db], 0, 0, 0);
+      }
+    }
     // next step's tile landed (own loads), then publish and free this stage
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * (kStages - 2)) : "memory");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(8 * (kStages - 2)) : "memory");
     __syncthreads();
     refill_window();
   };
-  static_assert(kStages == 3, "the step loop below is unrolled for 3 stages");
+  static_assert(kStages == 2, "the step loop below is unrolled for 2 stages");
   for (int s = 0;;) {
     if (s >= n_steps) break;
     step(std::integral_constant<int, 0>{}, s++);
     if (s >= n_steps) break;
     step(std::integral_constant<int, 1>{}, s++);
-    if (s >= n_steps) break;
-    step(std::integral_constant<int, 2>{}, s++);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no load into LDS outlives the workgroup
 
@@ -390,8 +403,8 @@ extern "C" int nkv_prefill_varlen(const void* q, int64_t q_row_stride, const voi
               "prefill_varlen: K/V row stride too large");
   int max_blocks = 0;
   if (block_tables) {
-    NKV_REQUIRE(block_size > 0 && block_size % kStep == 0, NKV_EUNSUPPORTED,
-                "prefill_varlen: block_size must be a positive multiple of %d", kStep);
+    NKV_REQUIRE(block_size > 0 && block_size % 16 == 0, NKV_EUNSUPPORTED,
+                "prefill_varlen: block_size must be a positive multiple of 16");
     NKV_REQUIRE(max_blocks_per_seq > 0 && bt_row_stride >= max_blocks_per_seq,
                 NKV_EINVAL, "prefill_varlen: paged mode needs block_size, max_blocks_per_seq "
                 "and bt_row_stride >= max_blocks_per_seq");
