@@ -64,7 +64,9 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--compress-reps", type=int, default=30)
     p.add_argument("--prefill-reps", type=int, default=20)
-    p.add_argument("--only", choices=["all", "decode", "compress", "prefill"], default="all",
+    p.add_argument("--longctx-steps", type=int, default=10)
+    p.add_argument("--only", choices=["all", "decode", "compress", "prefill", "longctx"],
+                   default="all",
                    help="run one part only (for profiling)")
     p.add_argument("--copy-calibration-mib", type=int, default=0,
                    help="also run 5 device-to-device copies of this many MiB (a kernel of "
@@ -335,6 +337,85 @@ def run_prefill(args, dev):
     return res
 
 
+def run_longctx(args, dev):
+    """Qwen3-32B long-context decode at batch 500 on a pool filling most of HBM, and the
+    compression step on that state (20 longest uncompressed sequences, window 4 blocks, keep
+    513, agg "group"), amortised over its 1024-step period."""
+    torch.cuda.empty_cache()
+    wl = wl_mod.decode_qwen3_32b_longctx(seed=6, device=dev)
+    kc, vc = wl["k_cache"], wl["v_cache"]
+    bt, slots = wl["block_tables"][0].to(dev), wl["slot_mappings"][0].to(dev)
+    q, key, value = wl["q"].to(dev), wl["key"].to(dev), wl["value"].to(dev)
+    ctx = wl["context_lens"].to(dev)
+    bs, Hq, D = q.shape
+    NB, B, Hk, _ = kc.shape
+    width = bt.size(1)
+    lib = _lib.lib()
+    ws = torch.empty(lib.nkv_paged_decode_workspace_bytes(bs, Hq, D, width, B), dtype=torch.uint8,
+                     device=dev)
+    out = torch.empty(bs, Hq, D, dtype=torch.bfloat16, device=dev)
+    stream = torch.cuda.current_stream()
+
+    def step():
+        nkv.store_kvcache(key, value, kc, vc, slots)
+        nkv.paged_decode(q, kc, vc, ctx, bt, wl["scale"], out=out, workspace=ws)
+
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.longctx_steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    step_ms = e0.elapsed_time(e1) / args.longctx_steps
+    nbytes = wl_mod.decode_bytes(wl["context_lens"], Hq, Hk, D, width)
+    parity = parity_sample(wl, bt, out, kc, vc, n=4)
+    # compression: the 20 longest sequences eligible under the engine's rule
+    lens = wl["context_lens"].tolist()
+    tail_unc = wl["tail_uncompressed"].tolist()
+    elig = [i for i, n in enumerate(lens)
+            if n % B != B - 1 and tail_unc[i] >= 4 * B and n // B >= 4]
+    sel_list = sorted(sorted(elig, key=lambda i: (-lens[i], i))[:20])
+    sel = torch.tensor(sel_list, dtype=torch.int32, device=dev)
+    base = ctx.clone()
+    cl = ctx.clone()
+    m = sel.numel()
+    cws = torch.empty(cu.select_workspace_bytes(m, Hq, Hk, 4, B), dtype=torch.uint8, device=dev)
+    imp = torch.empty(m, Hk, 4 * B - 1, dtype=torch.float32, device=dev)
+    keep = torch.empty(m, Hk, 513, dtype=torch.int32, device=dev)
+    flush = torch.ones(128 * 1024 * 1024, dtype=torch.int32, device=dev)
+    times = []
+    for i in range(3 + args.compress_reps):
+        flush.sum()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        cu.compress_step(q, kc, vc, bt, base, cl, sel, 4, 513, D ** -0.5, "group",
+                         importance=imp, keep_idx=keep, workspace=cws)
+        b.record(stream)
+        torch.cuda.synchronize()
+        if i >= 3:
+            times.append(a.elapsed_time(b) * 1000.0)
+    comp_us = statistics.median(times)
+    gbs = nbytes / (step_ms * 1e-3) / 1e9
+    res = {
+        "longctx_workload": "Qwen3-32B geometry: Hq 64, Hk 8, batch 500, ctx log-uniform "
+                            "[1024,16384] (seed 6), 20% compressed once, store + decode per step",
+        "longctx_pool_gb": round(2 * NB * B * Hk * D * 2 / 1e9, 1),
+        "longctx_tokens": int(sum(lens)),
+        "longctx_step_us": round(step_ms * 1e3, 1),
+        "longctx_decode_gbs": round(gbs, 1),
+        "longctx_pct_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 1),
+        "longctx_parity_max_abs_err": parity,
+        "longctx_compress_step_us": round(comp_us, 2),
+        "longctx_compress_amortized_us_per_step": round(comp_us / 1024, 3),
+    }
+    del wl, kc, vc, ws, out
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -352,6 +433,9 @@ def main():
     if args.only == "prefill":
         print(json.dumps(run_prefill(args, dev)), flush=True)
         return
+    if args.only == "longctx":
+        print(json.dumps(run_longctx(args, dev)), flush=True)
+        return
     print(f"[bench] decode workload: bs 64, Hq 32, Hk 8, ctx U[2048,8192], pool 4096 blocks",
           file=sys.stderr, flush=True)
     wl, sets, r = run_decode(args, dev)
@@ -366,6 +450,9 @@ def main():
     pre = run_prefill(args, dev)
     print(f"[bench] prefill done: {pre['prefill_tflops']} / {pre['prefill_chunked_tflops']} "
           f"TFLOP/s", file=sys.stderr, flush=True)
+    longctx = run_longctx(args, dev)
+    print(f"[bench] long-context decode done: {longctx['longctx_decode_gbs']} GB/s",
+          file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(wl, sets[0][0], wl["k_cache"], wl["v_cache"])
@@ -420,6 +507,7 @@ def main():
             "workload": "2048-token chunks after paged prefixes U[0,8192], 16 sequences",
         },
         **pre,
+        **longctx,
     }
     print(json.dumps(line), flush=True)
 

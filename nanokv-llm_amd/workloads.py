@@ -16,6 +16,10 @@ Workloads (sizes from the reference's Qwen3 geometries, block size 256):
                       W = 4 blocks, keep 2*256+1
   prefill_qwen3_8b    16 sequences, L U[512, 4096]; chunked: 2048-token chunks
                       on paged prefixes of U[0, 8192] tokens
+  decode_qwen3_32b_longctx  bs 500, Hq 64, Hk 8, ctx log-uniform [1024, 16384], 20%
+                      of the sequences already compressed once (shorter context),
+                      a pool sized to fill most of HBM with only the used blocks
+                      written
 """
 from __future__ import annotations
 
@@ -174,3 +178,55 @@ def decode_bytes(context_lens, Hq, Hk, D=HEAD_DIM, max_blocks=0):
     ctx = int(torch.as_tensor(context_lens).to(torch.int64).clamp(min=0).sum())
     bs = int(torch.as_tensor(context_lens).numel())
     return ctx * Hk * D * 2 * 2 + bs * Hq * D * 2 * 2 + bs * 4 * (max_blocks + 1)
+
+
+def decode_qwen3_32b_longctx(seed=6, device="cpu", bs=500, n_blocks=None, frac_compressed=0.2,
+                             pool_fraction=0.85, window_tokens=1024, keep_tokens=513):
+    """High-concurrency long-context decode state at Qwen3-32B geometry.
+
+    Context lengths exp(U(ln 1024, ln 16384)); a random 20% of the sequences were
+    compressed once before (len - window_tokens + keep_tokens: their kept middle
+    positions are non-contiguous, which for attention is just a shorter context)
+    and have no uncompressed tail yet. The pool defaults to pool_fraction of the
+    device's free memory for K+V (at most 0.85 * 288 GB / 1 MiB blocks); blocks
+    are assigned at random over the whole pool and only the used ones are filled
+    with N(0,1) values. Returns decode_workload's fields plus ``compressed``
+    (bool per sequence) and ``tail_uncompressed`` (tokens since the last
+    compression).
+    """
+    gen = torch.Generator().manual_seed(seed)
+    u = torch.rand(bs, generator=gen, dtype=torch.float64)
+    ctx = torch.exp(math.log(1024) + u * (math.log(16384) - math.log(1024))).to(torch.int64)
+    compressed = torch.rand(bs, generator=gen) < frac_compressed
+    ctx = torch.where(compressed, ctx - window_tokens + keep_tokens, ctx)
+    tail_unc = torch.where(compressed, torch.zeros_like(ctx), ctx)
+    Hq, Hk, D = 64, 8, HEAD_DIM
+    block_bytes = 2 * BLOCK * Hk * D * 2
+    if n_blocks is None:
+        if torch.device(device).type == "cuda":
+            free, _ = torch.cuda.mem_get_info(torch.device(device))
+            n_blocks = int(free * pool_fraction) // block_bytes
+        else:
+            n_blocks = 0
+        n_blocks = min(max(n_blocks, 0), int(0.85 * 288e9) // (1 << 20))
+    need = sum(math.ceil(int(c) / BLOCK) for c in ctx.tolist())
+    n_blocks = max(n_blocks, need + 8)
+    table = assign_blocks(ctx.tolist(), n_blocks, gen)
+    k_cache = torch.empty(n_blocks, BLOCK, Hk, D, dtype=torch.bfloat16, device=device)
+    v_cache = torch.empty_like(k_cache)
+    used = table[table >= 0].to(torch.int64)
+    g = torch.Generator(device=device)
+    g.manual_seed(seed * 7 + 1)
+    for i in range(0, used.numel(), 1024):  # fill the used blocks only, 1 GiB at a time
+        ids = used[i:i + 1024].to(device)
+        k_cache[ids] = torch.randn((ids.numel(), BLOCK, Hk, D), generator=g, device=device,
+                                   dtype=torch.float32).to(torch.bfloat16)
+        v_cache[ids] = torch.randn((ids.numel(), BLOCK, Hk, D), generator=g, device=device,
+                                   dtype=torch.float32).to(torch.bfloat16)
+    q = _randn((bs, Hq, D), seed * 7 + 3, "cpu")
+    key = _randn((bs, Hk, D), seed * 7 + 4, "cpu")
+    value = _randn((bs, Hk, D), seed * 7 + 5, "cpu")
+    return dict(q=q, key=key, value=value, k_cache=k_cache, v_cache=v_cache,
+                context_lens=ctx.to(torch.int32), block_tables=[table],
+                slot_mappings=[slot_of(table, ctx - 1)], scale=D ** -0.5, Hq=Hq, Hk=Hk,
+                compressed=compressed, tail_uncompressed=tail_unc, n_blocks=n_blocks)

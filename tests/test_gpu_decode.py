@@ -131,3 +131,35 @@ def test_decode_ragged_batch_over_64(nkv, dev, seed):
     q = torch.randn(bs, Hq, D, generator=g).to(torch.bfloat16)
     out = _check(nkv, dev, q, kc, vc, ctx, bt, D ** -0.5)
     assert torch.all(out[ctx == 0] == 0)
+
+
+def test_decode_qwen3_32b_long_context(nkv, dev):
+    """Qwen3-32B geometry (Hq 64, Hk 8: GQA group 8), contexts log-uniform up to 16384
+    (64 blocks per sequence, the block-id window's full width), some already compressed."""
+    wl = wl_mod.decode_qwen3_32b_longctx(seed=6, bs=8, n_blocks=400)
+    kc, vc = wl["k_cache"], wl["v_cache"]
+    bt, slots = wl["block_tables"][0], wl["slot_mappings"][0]
+    kg, vg = kc.to(dev), vc.to(dev)
+    nkv.store_kvcache(wl["key"].to(dev), wl["value"].to(dev), kg, vg, slots.to(dev))
+    store_kvcache_ref(wl["key"], wl["value"], kc, vc, slots)
+    _check(nkv, dev, wl["q"], kc, vc, wl["context_lens"], bt, wl["scale"], kg, vg)
+    assert bool(wl["compressed"].any())
+
+
+def test_decode_64_block_window_boundary(nkv, dev):
+    """Contexts of 64*256 +- a few tokens: the block-id window reloads after 64 blocks."""
+    g = torch.Generator().manual_seed(31)
+    Hq, Hk, D, B = 32, 8, 128, 256
+    ctx = torch.tensor([64 * B - 1, 64 * B, 64 * B + 1, 70 * B + 5], dtype=torch.int32)
+    need = [(int(c) + B - 1) // B for c in ctx]
+    nb = sum(need) + 2
+    perm = torch.randperm(nb, generator=g).tolist()
+    bt = torch.full((4, max(need)), -1, dtype=torch.int32)
+    p = 0
+    for i, n in enumerate(need):
+        bt[i, :n] = torch.tensor(perm[p:p + n], dtype=torch.int32)
+        p += n
+    kc = torch.randn(nb, B, Hk, D, generator=g).to(torch.bfloat16)
+    vc = torch.randn(nb, B, Hk, D, generator=g).to(torch.bfloat16)
+    q = torch.randn(4, Hq, D, generator=g).to(torch.bfloat16)
+    _check(nkv, dev, q, kc, vc, ctx, bt, D ** -0.5)
