@@ -273,59 +273,74 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
         st[rr][h] = a;
       }
     }
-    // online softmax per row group (log2 domain, running max m_run kept scaled).
-    // The max is only raised when a row's maximum grows by more than kLazy
-    // (log2 units): weights then stay <= 2^kLazy, exact after the final 1/l.
-    // P^T is packed as the MFMA B operand (8 bf16 per lane and 32-key chunk);
-    // the row sum is taken over the same bf16 weights that multiply V.
+    // online softmax (log2 domain, running max m_run kept scaled). The max is
+    // only raised when a row's maximum grows by more than kLazy (log2 units):
+    // weights then stay <= 2^kLazy, exact after the final 1/l. Both row groups'
+    // maxima first (one rescale branch), then per 32-key chunk the weights,
+    // packed as the P^T B operand (8 bf16 per lane), and that chunk's PV
+    // MFMAs: chunk 1's exp work overlaps chunk 0's MFMAs. The row sum is taken
+    // over the same bf16 weights that multiply V.
     const bool edge = (s * kStep + kStep - 1 > diag + j0) || (s * kStep + kStep > Lk);  // uniform
-    u32x4_t pb[2][2];
+    float sv[2][16];
 #pragma unroll
-    for (int rr = 0; rr < 2; ++rr) {
-      float sv[16];
+    for (int rr = 0; rr < 2; ++rr)
 #pragma unroll
       for (int h = 0; h < 4; ++h)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sv[4 * h + r] = st[rr][h][r];
-      if (edge) {
+        for (int r = 0; r < 4; ++r) sv[rr][4 * h + r] = st[rr][h][r];
+    if (edge) {
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) {
         const int lim = min(diag + jrow[rr], Lk - 1);  // last visible key of this row
 #pragma unroll
         for (int h = 0; h < 4; ++h)
 #pragma unroll
           for (int r = 0; r < 4; ++r)
-            if (s * kStep + 16 * h + 4 * g4 + r > lim) sv[4 * h + r] = -INFINITY;
+            if (s * kStep + 16 * h + 4 * g4 + r > lim) sv[rr][4 * h + r] = -INFINITY;
       }
-      const float cmax = fmax3(fmax3(fmax3(sv[0], sv[1], sv[2]), fmax3(sv[3], sv[4], sv[5]),
-                                     fmax3(sv[6], sv[7], sv[8])),
-                               fmax3(sv[9], sv[10], sv[11]),
-                               fmax3(fmax3(sv[12], sv[13], sv[14]), sv[15], -INFINITY));
-      const float cm = col_max4(cmax) * scale_log2;
-      const bool raise = cm > m_run[rr] + kLazy;  // false while the row has no visible key
-      if (__builtin_amdgcn_ballot_w64(raise) != 0) {
-        const float alpha = raise ? fast_exp2(m_run[rr] - cm) : 1.f;  // exp2(-inf) = 0
-        m_run[rr] = raise ? cm : m_run[rr];
+    }
+    float cm[2];
+    bool raise[2];
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      const float* v = sv[rr];
+      const float cmax = fmax3(fmax3(fmax3(v[0], v[1], v[2]), fmax3(v[3], v[4], v[5]),
+                                     fmax3(v[6], v[7], v[8])),
+                               fmax3(v[9], v[10], v[11]),
+                               fmax3(fmax3(v[12], v[13], v[14]), v[15], -INFINITY));
+      cm[rr] = col_max4(cmax) * scale_log2;
+      raise[rr] = cm[rr] > m_run[rr] + kLazy;  // false while the row has no visible key
+    }
+    if (__builtin_amdgcn_ballot_w64(raise[0] || raise[1]) != 0) {
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) {
+        const float alpha = raise[rr] ? fast_exp2(m_run[rr] - cm[rr]) : 1.f;  // exp2(-inf) = 0
+        m_run[rr] = raise[rr] ? cm[rr] : m_run[rr];
         l_run[rr] *= alpha;
 #pragma unroll
         for (int db = 0; db < 8; ++db) acc[rr][db] *= alpha;
       }
-      const float mb = m_run[rr] == -INFINITY ? 0.f : m_run[rr];
-      float p[16];
-#pragma unroll
-      for (int e = 0; e < 16; ++e) p[e] = fast_exp2(fmaf(sv[e], scale_log2, -mb));  // -inf -> 0
-      float l = l_run[rr];
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        pb[rr][c] = u32x4_t{pack2(p[8 * c + 0], p[8 * c + 1]), pack2(p[8 * c + 2], p[8 * c + 3]),
-                            pack2(p[8 * c + 4], p[8 * c + 5]), pack2(p[8 * c + 6], p[8 * c + 7])};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) l = sum2_bf16(pb[rr][c][e], l);
-      }
-      l_run[rr] = l;
     }
+    float mb[2];
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) mb[rr] = m_run[rr] == -INFINITY ? 0.f : m_run[rr];
     // O^T[dims][rows] += V^T[dims][keys] P^T[keys][rows] per 32-key chunk c:
     // k-slot j of lane group g is key 32c+4g+j (j<4), or 32c+16+4g+(j-4)
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
+      u32x4_t pb[2];
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) {
+        float p[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          p[e] = fast_exp2(fmaf(sv[rr][8 * c + e], scale_log2, -mb[rr]));  // -inf -> 0
+        pb[rr] = u32x4_t{pack2(p[0], p[1]), pack2(p[2], p[3]), pack2(p[4], p[5]), pack2(p[6], p[7])};
+        float l = l_run[rr];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) l = sum2_bf16(pb[rr][e], l);
+        l_run[rr] = l;
+      }
 #pragma unroll
       for (int db = 0; db < 8; ++db) {
         const char* vc = vt + c * 8192 + vo[db];
@@ -336,7 +351,7 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
 #pragma unroll
         for (int rr = 0; rr < 2; ++rr)
           acc[rr][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              as_bf16x8_v(va), as_bf16x8_v(pb[rr][c]), acc[rr][db], 0, 0, 0);
+              as_bf16x8_v(va), as_bf16x8_v(pb[rr]), acc[rr][db], 0, 0, 0);
       }
     }
     // next step's tile landed (own loads), then publish and free this stage
