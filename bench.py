@@ -65,7 +65,8 @@ def parse():
     p.add_argument("--compress-reps", type=int, default=30)
     p.add_argument("--prefill-reps", type=int, default=20)
     p.add_argument("--longctx-steps", type=int, default=10)
-    p.add_argument("--only", choices=["all", "decode", "compress", "prefill", "longctx"],
+    p.add_argument("--only", choices=["all", "decode", "compress", "prefill", "longctx",
+                                      "qkrope"],
                    default="all",
                    help="run one part only (for profiling)")
     p.add_argument("--copy-calibration-mib", type=int, default=0,
@@ -337,6 +338,121 @@ def run_prefill(args, dev):
     return res
 
 
+def qkrope_bytes(n_tokens, Hq, Hk, need_k, D=128):
+    """Algorithmic HBM bytes of one fused norm + rope + store: read the q/k/v head rows,
+    position, slot and cos|sin row; write q', the K and V cache rows (and k' if asked)."""
+    per_tok = (Hq + 2 * Hk) * D * 2 + 8 + 4 + D * 4 + (Hq + 2 * Hk + (Hk if need_k else 0)) * D * 2
+    return n_tokens * per_tok
+
+
+def _qkrope_unfused(pos, q, k, v, cs, qw, kw, kc, vc, slots):
+    """The reference's sequence of separate passes (layernorm.py:21-26 twice,
+    rotary_embedding.py:7-15 twice, then store_kvcache) as eager torch ops on the GPU,
+    timed only to show what the fusion saves."""
+    def norm(x, w):
+        xf = x.float()
+        return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)).to(x.dtype) * w
+
+    def rope(x, c, s_):
+        x1, x2 = torch.chunk(x.float(), 2, dim=-1)
+        return torch.cat((x1 * c - x2 * s_, x2 * c + x1 * s_), dim=-1).to(x.dtype)
+
+    c, s_ = cs[pos].unsqueeze(1).chunk(2, dim=-1)
+    q2, k2 = rope(norm(q, qw), c, s_), rope(norm(k, kw), c, s_)
+    nkv.store_kvcache(k2, v, kc, vc, slots)
+    return q2, k2
+
+
+def _graph_call_ms(fn, n_inner=10, reps=20):
+    """Per-call GPU time of fn() from a HIP graph holding n_inner back-to-back calls
+    (replayed reps times, median): the host's launch latency is not in it."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(n_inner):
+            fn()
+    stream = torch.cuda.current_stream()
+    t = []
+    for i in range(3 + reps):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        g.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        if i >= 3:
+            t.append(e0.elapsed_time(e1) / n_inner)
+    return statistics.median(t), g
+
+
+def run_qkrope(args, dev):
+    """Fused q/k RMSNorm + RoPE + K/V store at Qwen3-8B geometry (Hq 32, Hk 8): the 16-prompt
+    prefill batch (positions 0..L-1, k' also written for the contiguous prefill) and a
+    64-token decode batch (k' only into the cache). The fused op is timed inside a replayed
+    HIP graph; the unfused eager sequence (launch latency included) is shown beside it."""
+    wl = wl_mod.prefill_qwen3_8b(device=dev)
+    N, Hq, Hk, D = wl["q"].size(0), 32, 8, 128
+    g = torch.Generator(device=dev).manual_seed(9)
+    qkv = torch.randn(N, (Hq + 2 * Hk) * D, device=dev, generator=g).to(torch.bfloat16)
+    q = qkv[:, :Hq * D].view(N, Hq, D)
+    k = qkv[:, Hq * D:(Hq + Hk) * D].view(N, Hk, D)
+    v = qkv[:, (Hq + Hk) * D:].view(N, Hk, D)
+    qw = (1 + 0.1 * torch.randn(D, device=dev, generator=g)).to(torch.bfloat16)
+    kw = (1 + 0.1 * torch.randn(D, device=dev, generator=g)).to(torch.bfloat16)
+    rope = nkv.RotaryEmbedding(D, D, 40960, 1e6, device=dev)
+    cs = rope.cos_sin_cache
+    kc, vc = wl["k_cache"], wl["v_cache"]
+    pos, slots = wl["positions"], wl["slot_mapping"].to(dev)
+    q_out = torch.empty(N, Hq, D, dtype=torch.bfloat16, device=dev)
+    stream = torch.cuda.current_stream()
+    res = {}
+    for name, n, need_k in (("qkrope_prefill", N, True), ("qkrope_decode", 64, False)):
+        sl = slice(0, n)
+        fused = lambda: nkv.qk_norm_rope_store(pos[sl], q[sl], k[sl], v[sl], cs, qw, kw,  # noqa
+                                               1e-6, k_cache=kc, v_cache=vc,
+                                               slot_mapping=slots[sl], need_k=need_k,
+                                               q_out=q_out[sl])
+        fused()
+        torch.cuda.synchronize()
+        eager_q = q_out[sl].clone()
+        fused_ms, graph = _graph_call_ms(fused, reps=args.prefill_reps)
+        torch.cuda.synchronize()
+        assert torch.equal(q_out[sl], eager_q), "graph replay differs from the eager call"
+        del graph
+        t = []
+        for i in range(5 + args.prefill_reps):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            _qkrope_unfused(pos[sl], q[sl], k[sl], v[sl], cs.squeeze(1), qw, kw, kc, vc,
+                            slots[sl])
+            e1.record(stream)
+            torch.cuda.synchronize()
+            if i >= 5:
+                t.append(e0.elapsed_time(e1))
+        nbytes = qkrope_bytes(n, Hq, Hk, need_k)
+        res[f"{name}_tokens"] = n
+        res[f"{name}_us"] = round(fused_ms * 1e3, 2)
+        res[f"{name}_gbs"] = round(nbytes / (fused_ms * 1e-3) / 1e9, 1)
+        res[f"{name}_unfused_torch_us"] = round(statistics.median(t) * 1e3, 2)
+    res["qkrope_bytes_per_token"] = qkrope_bytes(1, Hq, Hk, True)
+    # parity on the first 64 prefill tokens against the oracle
+    from oracle.rope_ref import qk_norm_rope_store_ref
+    qo, ko, _ = nkv.qk_norm_rope_store(pos[:64], q[:64], k[:64], v[:64], cs, qw, kw, 1e-6)
+    qr, kr, _ = qk_norm_rope_store_ref(qkv[:64].cpu(), pos[:64].cpu(), qw.cpu(), kw.cpu(), 1e-6,
+                                       cs.squeeze(1).cpu(), Hq, Hk)
+    res["qkrope_parity_max_abs_err"] = max(float((qo.float().cpu() - qr.float()).abs().max()),
+                                           float((ko.float().cpu() - kr.float()).abs().max()))
+    del wl
+    torch.cuda.empty_cache()
+    return res
+
+
 def run_longctx(args, dev):
     """Qwen3-32B long-context decode at batch 500 on a pool filling most of HBM, and the
     compression step on that state (20 longest uncompressed sequences, window 4 blocks, keep
@@ -436,6 +552,9 @@ def main():
     if args.only == "longctx":
         print(json.dumps(run_longctx(args, dev)), flush=True)
         return
+    if args.only == "qkrope":
+        print(json.dumps(run_qkrope(args, dev)), flush=True)
+        return
     print(f"[bench] decode workload: bs 64, Hq 32, Hk 8, ctx U[2048,8192], pool 4096 blocks",
           file=sys.stderr, flush=True)
     wl, sets, r = run_decode(args, dev)
@@ -452,6 +571,9 @@ def main():
           f"TFLOP/s", file=sys.stderr, flush=True)
     longctx = run_longctx(args, dev)
     print(f"[bench] long-context decode done: {longctx['longctx_decode_gbs']} GB/s",
+          file=sys.stderr, flush=True)
+    qkrope = run_qkrope(args, dev)
+    print(f"[bench] norm+rope+store done: {qkrope['qkrope_prefill_gbs']} GB/s",
           file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu_baseline:
@@ -508,6 +630,7 @@ def main():
         },
         **pre,
         **longctx,
+        **qkrope,
     }
     print(json.dumps(line), flush=True)
 

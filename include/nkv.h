@@ -5,7 +5,8 @@
  *
  * Conventions (every entry point):
  *   - All tensor pointers are DEVICE pointers. Element types are fixed per
- *     argument: bf16 for q/k/v/cache/out, int32 for metadata, fp32 for scores.
+ *     argument: bf16 for q/k/v/cache/out, int32 for metadata (int64 for
+ *     token positions), fp32 for scores and the rotary cos/sin table.
  *   - Strides are in ELEMENTS of the pointed-to type.
  *   - `stream` is a hipStream_t (NULL = the null stream). Every call is
  *     asynchronous on that stream, performs no host<->device synchronisation
@@ -56,6 +57,43 @@ int nkv_store_kvcache(const void* key, int64_t key_row_stride,
                       const int32_t* slot_mapping, int64_t n_tokens,
                       int32_t n_kv_heads, int32_t head_dim, int64_t n_slots,
                       void* stream);
+
+/*
+ * Fused q/k RMSNorm + rotary embedding + K/V store, the step between the qkv
+ * projection and attention. q, k, v are row-strided bf16 views: element
+ * (i, h, d) of q at q[i*q_row_stride + h*head_dim + d], likewise k and v
+ * (normally the three parts of one fused qkv row). For every token i and q or
+ * k head (head_dim 128):
+ *   x   = head row (fp32);
+ *   if norm weights are given (both, or neither = no norm):
+ *     x = bf16(bf16(x * rsqrt(mean(x^2) + eps)) * w)   (w = q or k weight)
+ *   x1, x2 = x[:64], x[64:];  c, s = cos_sin_cache[p][:64], [p][64:]
+ *   y   = bf16([x1*c - x2*s | x2*c + x1*s])            (p = positions[i])
+ * q heads -> q_out[i*q_out_row_stride + h*128 ...]; k heads -> k_out
+ * ([n_tokens, n_kv_heads, 128] contiguous, optional) and, with a cache, the
+ * k_cache row slot_mapping[i]; v heads are copied unchanged to the v_cache
+ * row. Slots -1 or outside [0, n_slots) are skipped; positions outside
+ * [0, max_position) are clamped (the reference would raise an index error).
+ * positions is int64 and cos_sin_cache fp32 [max_position, 128] as the
+ * reference builds them. k_cache, v_cache, v and slot_mapping are all given
+ * or all NULL; at least one of k_out and k_cache is given. Pointers are
+ * 16-byte aligned and row strides multiples of 8 elements.
+ * Replaces: q_norm/k_norm + rotary_emb in Qwen3Attention.forward
+ *           (nanokvllm/models/qwen3.py:109-113), RMSNorm.rms_forward
+ *           (nanokvllm/layers/layernorm.py:16-26), apply_rotary_emb /
+ *           RotaryEmbedding.forward (nanokvllm/layers/rotary_embedding.py:7-49)
+ *           and the store_kvcache call at the top of Attention.forward
+ *           (nanokvllm/layers/attention.py:71-73).
+ */
+int nkv_qk_norm_rope_store(const void* q, int64_t q_row_stride, const void* k,
+                           int64_t k_row_stride, const void* v, int64_t v_row_stride,
+                           const int64_t* positions, const void* q_norm_weight,
+                           const void* k_norm_weight, float eps,
+                           const float* cos_sin_cache, int64_t max_position,
+                           void* q_out, int64_t q_out_row_stride, void* k_out,
+                           void* k_cache, void* v_cache, const int32_t* slot_mapping,
+                           int64_t n_slots, int64_t n_tokens, int32_t n_q_heads,
+                           int32_t n_kv_heads, int32_t head_dim, void* stream);
 
 /*
  * Paged decode attention (one query token per sequence, GQA, causal with the
@@ -113,7 +151,8 @@ int nkv_paged_decode_combine(const int32_t* context_lens, int32_t batch,
  * 0 .. Lk-Lq+j. If block_tables != NULL, key t of sequence i is k_cache row
  * block_tables[i, t/block_size]*block_size + t%block_size (paged); otherwise
  * it is row cu_seqlens_k[i]+t of k_cache/v_cache (contiguous [sum Lk, Hk, D]
- * with row stride kv_row_stride). Table entries at or beyond
+ * with row strides k_row_stride / v_row_stride, e.g. a roped K next to V as a
+ * view of the qkv projection; paged caches share one stride). Table entries at or beyond
  * max_blocks_per_seq, negative, or past n_rows read as zero keys/values.
  * q/out are [sum Lq, Hq, D] with row strides. head_dim must be 128;
  * Hq/Hk in {1, 2, 4, 8}. Rows with no visible key (Lk < Lq) are zero.
@@ -122,7 +161,8 @@ int nkv_paged_decode_combine(const int32_t* context_lens, int32_t batch,
  *           block_table), nanokvllm/layers/attention.py:96-102
  */
 int nkv_prefill_varlen(const void* q, int64_t q_row_stride,
-                       const void* k_cache, const void* v_cache, int64_t kv_row_stride,
+                       const void* k_cache, const void* v_cache, int64_t k_row_stride,
+                       int64_t v_row_stride,
                        const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
                        const int32_t* block_tables, int64_t bt_row_stride,
                        int32_t max_blocks_per_seq, int32_t n_seqs, int32_t max_seqlen_q,

@@ -8,9 +8,11 @@ directory name is not a Python identifier; import it with
 from .layers.attention import Attention, store_kvcache, paged_decode, varlen_prefill
 from .layers.compress_utils import MyCompressCompact
 from .layers.CompressMethod import SnapKV
+from .layers.rotary_embedding import RotaryEmbedding, get_rope, qk_norm_rope_store
 from .utils.context import Context, get_context, set_context, reset_context
 
 __all__ = [
     "Attention", "store_kvcache", "paged_decode", "varlen_prefill", "MyCompressCompact",
-    "SnapKV", "Context", "get_context", "set_context", "reset_context",
+    "SnapKV", "Context", "get_context", "set_context", "reset_context", "RotaryEmbedding",
+    "get_rope", "qk_norm_rope_store",
 ]

@@ -30,6 +30,9 @@ SIGNATURES = {
     "nkv_last_error": (C.c_char_p, []),
     "nkv_version": (C.c_char_p, []),
     "nkv_store_kvcache": (C.c_int, [_p, _i64, _p, _i64, _p, _p, _p, _i64, _i32, _i32, _i64, _p]),
+    "nkv_qk_norm_rope_store": (C.c_int, [_p, _i64, _p, _i64, _p, _i64, _p, _p, _p, _f32, _p,
+                                         _i64, _p, _i64, _p, _p, _p, _p, _i64, _i64, _i32,
+                                         _i32, _i32, _p]),
     "nkv_paged_decode_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
     "nkv_paged_decode": (C.c_int, [_p, _i64, _p, _p, _p, _i64, _p, _i32, _i32, _i32, _i32, _i32,
                                    _i32, _i64, _f32, _p, _i64, _p, _sz, _p]),
@@ -37,8 +40,8 @@ SIGNATURES = {
                                          _i32, _i32, _i64, _f32, _p, _sz, _p]),
     "nkv_paged_decode_combine": (C.c_int, [_p, _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64, _p,
                                            _sz, _p]),
-    "nkv_prefill_varlen": (C.c_int, [_p, _i64, _p, _p, _i64, _p, _p, _p, _i64, _i32, _i32, _i32,
-                                     _i32, _i32, _i32, _i32, _i64, _f32, _p, _i64, _p]),
+    "nkv_prefill_varlen": (C.c_int, [_p, _i64, _p, _p, _i64, _i64, _p, _p, _p, _i64, _i32, _i32,
+                                     _i32, _i32, _i32, _i32, _i32, _i64, _f32, _p, _i64, _p]),
     "nkv_compress_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32]),
     "nkv_compress_score": (C.c_int, [_p, _i64, _p, _p, _i64, _i32, _p, _p, _i32, _i32, _i32, _i32,
                                      _i32, _i32, _i64, _f32, _i32, _p, _p, _sz, _p]),

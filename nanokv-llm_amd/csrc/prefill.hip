@@ -81,7 +81,7 @@ __device__ __forceinline__ void load_to_lds(i32x4_t desc, uint32_t lds_addr, uin
 template <int G>
 __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
     const bf16_t* __restrict__ q, int64_t q_row_stride, const bf16_t* __restrict__ k_cache,
-    const bf16_t* __restrict__ v_cache, int64_t kv_row_stride,
+    const bf16_t* __restrict__ v_cache, int64_t k_row_stride, int64_t v_row_stride,
     const int32_t* __restrict__ cu_seqlens_q, const int32_t* __restrict__ cu_seqlens_k,
     const int32_t* __restrict__ block_tables, int64_t bt_row_stride, int32_t Hk,
     int32_t block_size, int32_t max_blocks, int32_t n_limit, int32_t n_tiles, float scale_log2,
@@ -116,8 +116,10 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
   // keys are consecutive rows (one cache block, B % 16 == 0, or the contiguous
   // K/V), so each wave's share of a step is one uniform base row and a byte
   // window covering only its valid keys: keys past Lk and keys of invalid
-  // blocks read as 0.
-  const uint32_t row_b = (uint32_t)kv_row_stride * 2u;
+  // blocks read as 0. vol[] are the K offsets; V rows may have another stride
+  // (contiguous mode), and their offsets differ by r * (row_bv - row_b).
+  const uint32_t row_b = (uint32_t)k_row_stride * 2u;
+  const uint32_t row_bv = (uint32_t)v_row_stride * 2u;
   const int lrow = lane >> 4;  // 0..3
   const int slot = lane & 15;
   uint32_t vol[4];
@@ -163,14 +165,14 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
       nv = 0;
       row0 = 0;
     }
-    const uint32_t bytes = (uint32_t)nv * row_b;
-    const i32x4_t dk = buffer_desc(k_cache + row0 * kv_row_stride, bytes);
-    const i32x4_t dv = buffer_desc(v_cache + row0 * kv_row_stride, bytes);
+    const i32x4_t dk = buffer_desc(k_cache + row0 * k_row_stride, (uint32_t)nv * row_b);
+    const i32x4_t dv = buffer_desc(v_cache + row0 * v_row_stride, (uint32_t)nv * row_bv);
     const uint32_t at = ring_base + (uint32_t)stage * kStageB;
 #pragma unroll
     for (int h = 0; h < 4; ++h) load_to_lds(dk, at + 1024u * h, vol[h]);
 #pragma unroll
-    for (int h = 0; h < 4; ++h) load_to_lds(dv, at + kTileB + 1024u * h, vol[h]);
+    for (int h = 0; h < 4; ++h)
+      load_to_lds(dv, at + kTileB + 1024u * h, vol[h] + (uint32_t)(4 * h + lrow) * (row_bv - row_b));
     c_t0 += kStep;
     if (bt) {
       c_off += kStep;
@@ -388,7 +390,8 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
 }  // namespace nkv
 
 extern "C" int nkv_prefill_varlen(const void* q, int64_t q_row_stride, const void* k_cache,
-                                  const void* v_cache, int64_t kv_row_stride,
+                                  const void* v_cache, int64_t k_row_stride,
+                                  int64_t v_row_stride,
                                   const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
                                   const int32_t* block_tables, int64_t bt_row_stride,
                                   int32_t max_blocks_per_seq, int32_t n_seqs, int32_t max_seqlen_q, int32_t n_q_heads,
@@ -411,11 +414,14 @@ extern "C" int nkv_prefill_varlen(const void* q, int64_t q_row_stride, const voi
               NKV_EINVAL, "prefill_varlen: q/k/v/out must be 16-byte aligned");
   NKV_REQUIRE(q_row_stride >= (int64_t)n_q_heads * kPD && q_row_stride % 8 == 0 &&
                   out_row_stride >= (int64_t)n_q_heads * kPD && out_row_stride % 8 == 0 &&
-                  kv_row_stride >= (int64_t)n_kv_heads * kPD && kv_row_stride % 8 == 0,
+                  k_row_stride >= (int64_t)n_kv_heads * kPD && k_row_stride % 8 == 0 &&
+                  v_row_stride >= (int64_t)n_kv_heads * kPD && v_row_stride % 8 == 0,
               NKV_EINVAL, "prefill_varlen: row strides must cover the heads, multiples of 8");
   NKV_REQUIRE(n_rows > 0, NKV_EINVAL, "prefill_varlen: empty K/V");
-  NKV_REQUIRE(kv_row_stride * 2 * kStep < (1ll << 31), NKV_EUNSUPPORTED,
-              "prefill_varlen: K/V row stride too large");
+  NKV_REQUIRE(k_row_stride * 2 * kStep < (1ll << 31) && v_row_stride * 2 * kStep < (1ll << 31),
+              NKV_EUNSUPPORTED, "prefill_varlen: K/V row stride too large");
+  NKV_REQUIRE(!block_tables || k_row_stride == v_row_stride, NKV_EINVAL,
+              "prefill_varlen: paged K and V caches share one row stride");
   int max_blocks = 0;
   if (block_tables) {
     NKV_REQUIRE(block_size > 0 && block_size % 16 == 0, NKV_EUNSUPPORTED,
@@ -437,7 +443,8 @@ extern "C" int nkv_prefill_varlen(const void* q, int64_t q_row_stride, const voi
 #define NKV_PREFILL_LAUNCH(G)                                                                   \
   hipLaunchKernelGGL(prefill_varlen_kernel<G>, dim3((unsigned)grid), dim3(256), 0, s,            \
                      (const bf16_t*)q, q_row_stride, (const bf16_t*)k_cache,                     \
-                     (const bf16_t*)v_cache, kv_row_stride, cu_seqlens_q, cu_seqlens_k,          \
+                     (const bf16_t*)v_cache, k_row_stride, v_row_stride, cu_seqlens_q,           \
+                     cu_seqlens_k,                                                               \
                      block_tables, bt_row_stride, n_kv_heads, block_size, max_blocks, n_limit,   \
                      n_tiles, sl2, (bf16_t*)out, out_row_stride)
   switch (g) {

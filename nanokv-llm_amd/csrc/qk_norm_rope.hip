@@ -1,0 +1,218 @@
+// Fused q/k RMSNorm + rotary embedding + K/V store: the step just before the
+// attention path.
+//
+// Reference: Qwen3Attention.forward, nanokvllm/models/qwen3.py:104-114 (qkv
+// split, q_norm/k_norm when the projection has no bias, rotary_emb, then
+// Attention.forward's store_kvcache); RMSNorm.rms_forward,
+// nanokvllm/layers/layernorm.py:16-26 (fp32 variance, x * rsqrt(var + eps)
+// rounded to bf16, then * weight rounded to bf16); apply_rotary_emb and
+// RotaryEmbedding.forward, nanokvllm/layers/rotary_embedding.py:7-49 (halves
+// x1 | x2 in fp32, y1 = x1 cos - x2 sin, y2 = x2 cos + x1 sin, rounded to
+// bf16; cos_sin_cache[pos] = [cos | sin] of pos * inv_freq, fp32).
+//
+// MI355X design: one pass over the qkv projection output instead of the
+// reference's five (norm q, norm k, rope q, rope k, store k and v). q, k, v
+// are row-strided views (normally the three parts of one qkv row). HBM-bound:
+// per token it reads the (Hq + 2 Hk) head rows, one 512-byte cos|sin
+// row and writes q, the K and V cache rows and optionally a contiguous K.
+// An 8-lane group owns one (token, head) unit; lane i holds elements
+// [8i, 8i+8) and [64+8i, 64+8i+8) of the 128-wide head, so both halves of a
+// rotary pair sit in the same lane (no exchange), the RMS reduction is a
+// 3-step butterfly and every access is 16 bytes. Consecutive units are
+// consecutive head rows, so a wave reads 2 KiB contiguous.
+#include "nkv_common.h"
+
+namespace nkv {
+
+constexpr int kRD = 128;  // head_dim
+constexpr int kRopeThreads = 256;
+constexpr int kRopeUnitsPerBlock = kRopeThreads / 8;  // one unit per 8-lane group
+
+__device__ __forceinline__ float bf(uint32_t b16) { return __uint_as_float(b16 << 16); }
+__device__ __forceinline__ float round_bf(float f) { return bf(f32_to_bf16_bits(f)); }
+
+struct RopeArgs {
+  const bf16_t* q_in;
+  int64_t q_row_stride;
+  const bf16_t* k_in;
+  int64_t k_row_stride;
+  const bf16_t* v_in;
+  int64_t v_row_stride;
+  const int64_t* positions;
+  const bf16_t* q_weight;
+  const bf16_t* k_weight;
+  float eps;
+  const float* cos_sin;
+  int64_t max_position;
+  bf16_t* q_out;
+  int64_t q_out_row_stride;
+  bf16_t* k_cache;
+  bf16_t* v_cache;
+  const int32_t* slot_mapping;
+  int64_t n_slots;
+  bf16_t* k_out;
+  uint32_t n_units;
+  uint32_t units_per_token;
+  int32_t Hq;
+  int32_t Hk;
+};
+
+// Units per token: Hq q heads, Hk k heads, then (when storing) Hk v heads. An
+// 8-lane group owns one unit; lane i holds elements [8i, 8i+8) and
+// [64+8i, 64+8i+8) of the head (16-byte accesses). The head row, the position
+// and the slot are loaded together; the cos|sin row (which needs the position)
+// is the only dependent load. One unit per group measured fastest at every size
+// (more units per group serialise their dependent loads).
+__global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_store_kernel(const RopeArgs a) {
+  // Every product is rounded on its own, as the reference's separate torch ops are:
+  // no a*b - c*d -> fma contraction.
+#pragma clang fp contract(off)
+  const uint32_t u = blockIdx.x * kRopeUnitsPerBlock + (threadIdx.x >> 3);
+  if (u >= a.n_units) return;
+  const int l8 = threadIdx.x & 7;
+  const uint32_t t = u / a.units_per_token;
+  const int h = (int)(u - t * a.units_per_token);
+  const bool is_q = h < a.Hq;
+  const bool is_k = !is_q && h < a.Hq + a.Hk;
+  const int kvh = is_q ? 0 : (is_k ? h - a.Hq : h - a.Hq - a.Hk);
+  const bf16_t* src = is_q ? a.q_in + (int64_t)t * a.q_row_stride + (int64_t)h * kRD
+                      : is_k ? a.k_in + (int64_t)t * a.k_row_stride + (int64_t)kvh * kRD
+                             : a.v_in + (int64_t)t * a.v_row_stride + (int64_t)kvh * kRD;
+  u32x4_t vlo = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(src + 8 * l8));
+  u32x4_t vhi = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(src + 64 + 8 * l8));
+  const int64_t sl = (!is_q && a.k_cache) ? (int64_t)a.slot_mapping[t] : -1;
+  if (is_q || is_k) {  // uniform over the unit's 8 lanes
+    int64_t pos = a.positions[t];
+    pos = pos < 0 ? 0 : (pos >= a.max_position ? a.max_position - 1 : pos);
+    const float* cs = a.cos_sin + pos * kRD + 8 * l8;
+    const f32x4_t c0 = *reinterpret_cast<const f32x4_t*>(cs);
+    const f32x4_t c1 = *reinterpret_cast<const f32x4_t*>(cs + 4);
+    const f32x4_t s0 = *reinterpret_cast<const f32x4_t*>(cs + 64);
+    const f32x4_t s1 = *reinterpret_cast<const f32x4_t*>(cs + 68);
+    float x[16];  // x[0..7] first half, x[8..15] the rotary partners
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[2 * e] = bf(vlo[e] & 0xffffu);
+      x[2 * e + 1] = bf(vlo[e] >> 16);
+      x[8 + 2 * e] = bf(vhi[e] & 0xffffu);
+      x[9 + 2 * e] = bf(vhi[e] >> 16);
+    }
+    if (a.q_weight) {
+      const bf16_t* w = is_q ? a.q_weight : a.k_weight;
+      const u32x4_t wlo = *reinterpret_cast<const u32x4_t*>(w + 8 * l8);
+      const u32x4_t whi = *reinterpret_cast<const u32x4_t*>(w + 64 + 8 * l8);
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) ss += x[e] * x[e];
+      ss += __shfl_xor(ss, 1, 64);
+      ss += __shfl_xor(ss, 2, 64);
+      ss += __shfl_xor(ss, 4, 64);
+      const float r = rsqrtf(ss * (1.0f / kRD) + a.eps);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x[2 * e] = round_bf(round_bf(x[2 * e] * r) * bf(wlo[e] & 0xffffu));
+        x[2 * e + 1] = round_bf(round_bf(x[2 * e + 1] * r) * bf(wlo[e] >> 16));
+        x[8 + 2 * e] = round_bf(round_bf(x[8 + 2 * e] * r) * bf(whi[e] & 0xffffu));
+        x[9 + 2 * e] = round_bf(round_bf(x[9 + 2 * e] * r) * bf(whi[e] >> 16));
+      }
+    }
+    const float cv[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+    const float sv[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+    float y[16];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float x1 = x[e], x2 = x[8 + e];
+      y[e] = x1 * cv[e] - x2 * sv[e];
+      y[8 + e] = x2 * cv[e] + x1 * sv[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      vlo[e] = pack_bf16x2(y[2 * e], y[2 * e + 1]);
+      vhi[e] = pack_bf16x2(y[8 + 2 * e], y[9 + 2 * e]);
+    }
+  }
+  if (is_q) {
+    bf16_t* dst = a.q_out + (int64_t)t * a.q_out_row_stride + (int64_t)h * kRD;
+    *reinterpret_cast<u32x4_t*>(dst + 8 * l8) = vlo;
+    *reinterpret_cast<u32x4_t*>(dst + 64 + 8 * l8) = vhi;
+    return;
+  }
+  if (sl >= 0 && sl < a.n_slots) {  // -1 (padding) or out of range: skipped
+    bf16_t* dst = (is_k ? a.k_cache : a.v_cache) + (sl * a.Hk + kvh) * (int64_t)kRD;
+    *reinterpret_cast<u32x4_t*>(dst + 8 * l8) = vlo;
+    *reinterpret_cast<u32x4_t*>(dst + 64 + 8 * l8) = vhi;
+  }
+  if (is_k && a.k_out) {
+    bf16_t* dst = a.k_out + ((int64_t)t * a.Hk + kvh) * kRD;
+    *reinterpret_cast<u32x4_t*>(dst + 8 * l8) = vlo;
+    *reinterpret_cast<u32x4_t*>(dst + 64 + 8 * l8) = vhi;
+  }
+}
+
+}  // namespace nkv
+
+extern "C" int nkv_qk_norm_rope_store(const void* q, int64_t q_row_stride, const void* k,
+                                      int64_t k_row_stride, const void* v, int64_t v_row_stride,
+                                      const int64_t* positions, const void* q_norm_weight,
+                                      const void* k_norm_weight, float eps,
+                                      const float* cos_sin_cache, int64_t max_position,
+                                      void* q_out, int64_t q_out_row_stride, void* k_out,
+                                      void* k_cache, void* v_cache, const int32_t* slot_mapping,
+                                      int64_t n_slots, int64_t n_tokens, int32_t n_q_heads,
+                                      int32_t n_kv_heads, int32_t head_dim, void* stream) {
+  using namespace nkv;
+  clear_error();
+  NKV_REQUIRE(n_tokens >= 0 && n_q_heads > 0 && n_kv_heads > 0 && n_slots >= 0, NKV_EINVAL,
+              "qk_norm_rope_store: bad sizes");
+  if (n_tokens == 0) return NKV_OK;
+  NKV_REQUIRE(head_dim == kRD, NKV_EUNSUPPORTED, "qk_norm_rope_store: head_dim must be 128");
+  NKV_REQUIRE(q && k && positions && cos_sin_cache && q_out && max_position > 0, NKV_EINVAL,
+              "qk_norm_rope_store: null pointer or empty rotary cache");
+  NKV_REQUIRE(!q_norm_weight == !k_norm_weight, NKV_EINVAL,
+              "qk_norm_rope_store: give both norm weights or neither");
+  NKV_REQUIRE(!k_cache == !v_cache && (!k_cache || (slot_mapping && v)), NKV_EINVAL,
+              "qk_norm_rope_store: k_cache, v_cache, v and slot_mapping go together");
+  NKV_REQUIRE(k_cache || k_out, NKV_EINVAL,
+              "qk_norm_rope_store: nowhere to put K (no cache and no k_out)");
+  const int64_t per_tok = (int64_t)n_q_heads + n_kv_heads + (k_cache ? n_kv_heads : 0);
+  const int64_t qw = (int64_t)n_q_heads * kRD, kw = (int64_t)n_kv_heads * kRD;
+  NKV_REQUIRE(q_row_stride >= qw && q_out_row_stride >= qw && k_row_stride >= kw &&
+                  (!k_cache || v_row_stride >= kw) &&
+                  ((q_row_stride | q_out_row_stride | k_row_stride | v_row_stride) % 8) == 0,
+              NKV_EINVAL, "qk_norm_rope_store: row strides must cover the heads, multiples of 8");
+  NKV_REQUIRE(n_tokens * per_tok < (int64_t)1 << 31, NKV_EINVAL,
+              "qk_norm_rope_store: tokens x heads must stay below 2^31");
+  NKV_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(q_out) &&
+                  aligned16(cos_sin_cache) && aligned16(k_out) && aligned16(k_cache) &&
+                  aligned16(v_cache) && aligned16(q_norm_weight) && aligned16(k_norm_weight),
+              NKV_EINVAL, "qk_norm_rope_store: pointers must be 16-byte aligned");
+  const uint32_t n_units = (uint32_t)(n_tokens * per_tok);
+  const unsigned grid = (unsigned)((n_units + kRopeUnitsPerBlock - 1) / kRopeUnitsPerBlock);
+  RopeArgs a;
+  a.q_in = (const bf16_t*)q;
+  a.q_row_stride = q_row_stride;
+  a.k_in = (const bf16_t*)k;
+  a.k_row_stride = k_row_stride;
+  a.v_in = (const bf16_t*)v;
+  a.v_row_stride = v_row_stride;
+  a.positions = positions;
+  a.q_weight = (const bf16_t*)q_norm_weight;
+  a.k_weight = (const bf16_t*)k_norm_weight;
+  a.eps = eps;
+  a.cos_sin = cos_sin_cache;
+  a.max_position = max_position;
+  a.q_out = (bf16_t*)q_out;
+  a.q_out_row_stride = q_out_row_stride;
+  a.k_cache = (bf16_t*)k_cache;
+  a.v_cache = (bf16_t*)v_cache;
+  a.slot_mapping = slot_mapping;
+  a.n_slots = k_cache ? n_slots : 0;
+  a.k_out = (bf16_t*)k_out;
+  a.n_units = n_units;
+  a.units_per_token = (uint32_t)per_tok;
+  a.Hq = n_q_heads;
+  a.Hk = n_kv_heads;
+  hipLaunchKernelGGL(qk_norm_rope_store_kernel, dim3(grid), dim3(kRopeThreads), 0,
+                     as_stream(stream), a);
+  return check_launch("nkv_qk_norm_rope_store");
+}

@@ -91,7 +91,8 @@ def varlen_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     """Varlen causal (bottom-right) attention: q [sum Lq, Hq, D] -> [sum Lq, Hq, D].
 
     With ``block_tables`` k/v are the paged caches [NB, B, Hk, D]; without,
-    they are contiguous [sum Lk, Hk, D] rows. Same math as
+    they are [sum Lk, Hk, D] rows, each with its own row stride (k roped and
+    contiguous, v a view of the qkv projection). Same math as
     flash_attn_varlen_func(..., causal=True, block_table) at attention.py:96-102.
     """
     N, Hq, D = q.shape
@@ -100,16 +101,17 @@ def varlen_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     n_seqs = cu_seqlens_q.numel() - 1
     if block_tables is not None:
         NB, B, Hk, Dk = k.shape
-        assert k.is_contiguous() and v.is_contiguous()
-        kv_row_stride = Hk * Dk
+        assert k.is_contiguous() and v.is_contiguous() and v.shape == k.shape
+        k_row_stride = v_row_stride = Hk * Dk
         n_rows = NB * B
         bt_ptr, bt_stride = block_tables.data_ptr(), block_tables.stride(0)
         max_blocks = block_tables.size(1)
         assert block_tables.dtype == torch.int32 and block_tables.stride(1) == 1
     else:
         _, Hk, Dk = k.shape
-        assert k.stride(1) == Dk and k.stride(2) == 1 and v.stride() == k.stride()
-        kv_row_stride = k.stride(0)
+        assert v.shape == k.shape
+        assert k.stride(1) == Dk and k.stride(2) == 1 and v.stride(1) == Dk and v.stride(2) == 1
+        k_row_stride, v_row_stride = k.stride(0), v.stride(0)
         n_rows = k.size(0)
         B = 0
         bt_ptr, bt_stride, max_blocks = None, 0, 0
@@ -117,7 +119,7 @@ def varlen_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     if out is None:
         out = torch.empty(N, Hq, D, dtype=_BF16, device=q.device)
     rc = _lib.lib().nkv_prefill_varlen(
-        q.data_ptr(), q.stride(0), k.data_ptr(), v.data_ptr(), kv_row_stride,
+        q.data_ptr(), q.stride(0), k.data_ptr(), v.data_ptr(), k_row_stride, v_row_stride,
         cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), bt_ptr, bt_stride, max_blocks, n_seqs,
         int(max_seqlen_q), Hq, Hk, D, B, n_rows, float(scale), out.data_ptr(), out.stride(0),
         _lib.stream_of(q))
@@ -157,10 +159,14 @@ class Attention(nn.Module):
             self._decode_ws = ws
         return ws
 
-    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, Layer):
+    def forward(self, q: torch.Tensor, k: torch.Tensor | None, v: torch.Tensor, Layer,
+                kv_stored: bool = False):
+        """``kv_stored=True``: k/v were already written to the cache (by
+        qk_norm_rope_store); k may then be None unless prefill reads it
+        contiguously (no block table)."""
         context = get_context()
         k_cache, v_cache = self.k_cache, self.v_cache
-        if k_cache.numel() and v_cache.numel():
+        if k_cache.numel() and v_cache.numel() and not kv_stored:
             store_kvcache(k, v, k_cache, v_cache, context.slot_mapping)
 
         if (context.use_decode_kernel and self.kv_compress_enabled and context.is_compress_step

@@ -161,7 +161,7 @@ def prefill_workload(n_seqs, Hq, Hk, len_lo, len_hi, seed, device="cpu", prefix_
         v_cache=_randn((n_blocks, BLOCK, Hk, D), seed * 7 + 2, device),
         block_tables=table, cu_seqlens_q=cu_q, cu_seqlens_k=cu_k, slot_mapping=slots,
         max_seqlen_q=max(Lq), max_seqlen_k=max(Lk), Lq=Lq, Lk=Lk, Hq=Hq, Hk=Hk,
-        scale=D ** -0.5)
+        scale=D ** -0.5, positions=positions.to(device))
 
 
 def prefill_qwen3_8b(seed=4, device="cpu", n_seqs=16):

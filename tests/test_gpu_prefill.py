@@ -164,3 +164,21 @@ def test_prefill_qwen3_8b_sample(nkv, dev):
     wl = wl_mod.prefill_workload(2, 32, 8, 512, 4096, seed=4)
     out, ref = _paged(nkv, dev, wl)
     assert _err(out, ref) <= TOL
+
+
+def test_prefill_contiguous_distinct_kv_strides(nkv, dev):
+    """Contiguous K next to V as a view of a wider qkv buffer (different row strides)."""
+    wl = wl_mod.prefill_workload(3, 32, 8, 1, 500, seed=22)
+    q, k, v = wl["q"], wl["key"], wl["value"]
+    N = k.size(0)
+    cu = wl["cu_seqlens_q"]
+    wide = torch.zeros(N, 48 * 128, dtype=torch.bfloat16)
+    wide[:, 40 * 128:] = v.reshape(N, -1)
+    vg = wide.to(dev)[:, 40 * 128:].view(N, 8, 128)
+    out = nkv.varlen_prefill(q.to(dev), k.to(dev), vg, cu.to(dev), cu.to(dev),
+                             wl["max_seqlen_q"], wl["scale"])
+    ref = varlen_prefill_ref(q.float(), k, v, cu, cu, wl["scale"])
+    assert _err(out, ref) <= TOL
+    same = nkv.varlen_prefill(q.to(dev), k.to(dev), v.to(dev), cu.to(dev), cu.to(dev),
+                              wl["max_seqlen_q"], wl["scale"])
+    assert torch.equal(out, same)

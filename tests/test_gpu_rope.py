@@ -1,0 +1,208 @@
+"""Fused q/k RMSNorm + RoPE + K/V store on the GPU vs the oracle.
+
+Bar: without the norm every output is bit-exact (the same fp32 products and
+roundings). With the norm, the kernel's sum of squares runs in another order
+and its rsqrt may differ by an ulp, so an element of bf16(x * r) that sits on
+a rounding boundary can land one bf16 ulp away; the test allows at most 0.1%
+of elements to differ, each by at most 2 bf16 ulps of the head row's largest
+magnitude (2^-6 * rowmax). V rows and cache rows not addressed are bit-exact.
+"""
+import importlib
+
+import pytest
+import torch
+
+from oracle.rope_ref import qk_norm_rope_store_ref, rotary_cos_sin_cache_ref
+
+pytestmark = pytest.mark.gpu
+D = 128
+MAX_DIFF_FRAC = 1e-3
+
+
+def _close(out, ref):
+    out, ref = out.float().cpu(), ref.float()
+    rowmax = ref.abs().amax(dim=-1, keepdim=True)
+    diff = (out - ref).abs()
+    assert torch.all(diff <= rowmax * 2.0 ** -6), f"max diff {diff.max().item()}"
+    frac = (diff > 0).float().mean().item()
+    assert frac <= MAX_DIFF_FRAC, f"{frac:.2e} of elements differ"
+
+
+def _case(N, Hq, Hk, seed, nb=8, B=256, max_pos=40960, pad=(), scale=3.0):
+    g = torch.Generator().manual_seed(seed)
+    qkv = (torch.randn(N, (Hq + 2 * Hk) * D, generator=g) * scale).to(torch.bfloat16)
+    qw = (1 + 0.3 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    kw = (1 + 0.3 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    pos = torch.randint(0, max_pos, (N,), generator=g)
+    cache = rotary_cos_sin_cache_ref(D, max_pos, 1e6)
+    kc = torch.randn(nb, B, Hk, D, generator=g).to(torch.bfloat16)
+    vc = torch.randn(nb, B, Hk, D, generator=g).to(torch.bfloat16)
+    slots = torch.randperm(nb * B, generator=g)[:N].to(torch.int32)
+    for i in pad:
+        slots[i] = -1
+    return qkv, qw, kw, pos, cache, kc, vc, slots
+
+
+def _split(qkv, Hq, Hk):
+    N = qkv.size(0)
+    q = qkv[:, :Hq * D].view(N, Hq, D)
+    k = qkv[:, Hq * D:(Hq + Hk) * D].view(N, Hk, D)
+    v = qkv[:, (Hq + Hk) * D:].view(N, Hk, D)
+    return q, k, v
+
+
+@pytest.mark.parametrize("Hq,Hk", [(32, 8), (16, 8), (64, 8), (8, 1)])
+def test_fused_norm_rope_store(nkv, dev, Hq, Hk):
+    N = 300
+    qkv, qw, kw, pos, cache, kc, vc, slots = _case(N, Hq, Hk, seed=Hq + Hk, pad=(0, 7, 299))
+    kg, vg = kc.to(dev), vc.to(dev)
+    q, k, v = _split(qkv.to(dev), Hq, Hk)
+    qo, ko, vo = nkv.qk_norm_rope_store(pos.to(dev), q, k, v, cache.to(dev), qw.to(dev),
+                                        kw.to(dev), 1e-6, k_cache=kg, v_cache=vg,
+                                        slot_mapping=slots.to(dev))
+    torch.cuda.synchronize()
+    qr, kr, vr = qk_norm_rope_store_ref(qkv, pos, qw, kw, 1e-6, cache, Hq, Hk, k_cache=kc,
+                                        v_cache=vc, slot_mapping=slots)
+    _close(qo, qr)
+    _close(ko, kr)
+    assert vo.data_ptr() == v.data_ptr()
+    # cache rows written from the same k' the test just checked; the rest untouched
+    _close(kg.cpu().view(-1, Hk, D), kc.view(-1, Hk, D))
+    assert torch.equal(vg.cpu(), vc)
+    stored = slots[slots >= 0].long()
+    assert torch.equal(kg.cpu().view(-1, Hk, D)[stored], ko.cpu()[slots >= 0])
+
+
+def test_rope_only_bit_exact(nkv, dev):
+    """No norm (qkv_bias models): identical fp32 products -> bitwise equal; via RotaryEmbedding."""
+    N, Hq, Hk = 257, 32, 8
+    qkv, _, _, pos, cache, _, _, _ = _case(N, Hq, Hk, seed=31)
+    rope = nkv.RotaryEmbedding(D, D, 40960, 1e6, device=dev)
+    rope.cos_sin_cache.copy_(cache.unsqueeze(1))  # same table as the oracle's
+    q, k, _ = _split(qkv.to(dev), Hq, Hk)
+    qo, ko = rope(pos.to(dev), q, k)
+    qr, kr, _ = qk_norm_rope_store_ref(qkv, pos, None, None, 0.0, cache, Hq, Hk)
+    assert torch.equal(qo.cpu(), qr) and torch.equal(ko.cpu(), kr)
+
+
+def test_device_table_matches_oracle_table(nkv, dev):
+    """The table RotaryEmbedding places on the GPU is bitwise the oracle's (built on the host)."""
+    rope = nkv.RotaryEmbedding(D, D, 40960, 1e6, device=dev)
+    ref = rotary_cos_sin_cache_ref(D, 40960, 1e6)
+    assert rope.cos_sin_cache.device.type == "cuda"
+    assert torch.equal(rope.cos_sin_cache.squeeze(1).cpu(), ref)
+
+
+def test_cache_only_and_edge_sizes(nkv, dev):
+    """need_k=False writes only q' and the caches; N = 0 and N = 1 work."""
+    Hq, Hk = 32, 8
+    for N in (0, 1, 17):
+        qkv, qw, kw, pos, cache, kc, vc, slots = _case(N, Hq, Hk, seed=40 + N, nb=2, B=16)
+        kg, vg = kc.to(dev), vc.to(dev)
+        q, k, v = _split(qkv.to(dev), Hq, Hk)
+        qo, ko, _ = nkv.qk_norm_rope_store(pos.to(dev), q, k, v, cache.to(dev), qw.to(dev),
+                                           kw.to(dev), 1e-6, k_cache=kg, v_cache=vg,
+                                           slot_mapping=slots.to(dev), need_k=False)
+        torch.cuda.synchronize()
+        assert ko is None and qo.shape == (N, Hq, D)
+        qr, kr, _ = qk_norm_rope_store_ref(qkv, pos, qw, kw, 1e-6, cache, Hq, Hk, k_cache=kc,
+                                           v_cache=vc, slot_mapping=slots)
+        if N:
+            _close(qo, qr)
+            _close(kg.cpu().view(-1, Hk, D), kc.view(-1, Hk, D))
+        assert torch.equal(vg.cpu(), vc)
+
+
+def test_positions_at_table_ends(nkv, dev):
+    """Positions 0 (identity rotation) and max_position - 1; q_out into a strided buffer."""
+    N, Hq, Hk, max_pos = 64, 16, 8, 4096
+    qkv, qw, kw, _, cache, _, _, _ = _case(N, Hq, Hk, seed=50, max_pos=max_pos)
+    pos = torch.tensor([0, max_pos - 1] * (N // 2), dtype=torch.int64)
+    q, k, _ = _split(qkv.to(dev), Hq, Hk)
+    wide = torch.zeros(N, (Hq + 4) * D, dtype=torch.bfloat16, device=dev)
+    q_out = wide[:, :Hq * D].view(N, Hq, D)
+    nkv.qk_norm_rope_store(pos.to(dev), q, k, None, cache.to(dev), qw.to(dev), kw.to(dev),
+                           1e-6, q_out=q_out)
+    torch.cuda.synchronize()
+    qr, _, _ = qk_norm_rope_store_ref(qkv, pos, qw, kw, 1e-6, cache, Hq, Hk)
+    _close(q_out, qr)
+    assert torch.all(wide[:, Hq * D:] == 0)
+
+
+def test_bad_arguments_raise(nkv, dev):
+    N, Hq, Hk = 4, 8, 2
+    qkv, qw, kw, pos, cache, kc, vc, slots = _case(N, Hq, Hk, seed=60, nb=1, B=16)
+    q, k, v = _split(qkv.to(dev), Hq, Hk)
+    with pytest.raises(ValueError):
+        nkv.qk_norm_rope_store(pos.to(dev), q, k, v, cache.to(dev), qw.to(dev), None)
+    # head_dim 64 is rejected by the library itself, before any launch
+    lib = importlib.import_module("nanokv-llm_amd._lib").lib()
+    pg, cg = pos.to(dev), cache.to(dev)
+    rc = lib.nkv_qk_norm_rope_store(q.data_ptr(), q.stride(0), k.data_ptr(), k.stride(0), None,
+                                    0, pg.data_ptr(), None, None, 1e-6, cg.data_ptr(), 4096,
+                                    q.data_ptr(), q.stride(0), k.data_ptr(), None, None, None,
+                                    0, N, Hq, Hk, 64, None)
+    assert rc != 0
+
+
+def test_decode_through_attention(nkv, dev):
+    """norm + rope + store, then Attention.forward(kv_stored=True) decode == oracle."""
+    from types import SimpleNamespace
+
+    from oracle.attention_ref import paged_decode_ref
+
+    bs, Hq, Hk, nb, B = 8, 32, 8, 32, 256
+    g = torch.Generator().manual_seed(70)
+    qkv, qw, kw, _, cache, kc, vc, _ = _case(bs, Hq, Hk, seed=71, nb=nb, B=B, scale=1.0)
+    ctx = torch.randint(1, 4 * B, (bs,), generator=g, dtype=torch.int32)
+    bt = torch.randperm(nb, generator=g).view(bs, 4).to(torch.int32)  # disjoint blocks
+    slots = torch.tensor([int(bt[b, (int(ctx[b]) - 1) // B]) * B + (int(ctx[b]) - 1) % B
+                          for b in range(bs)], dtype=torch.int32)
+    pos = (ctx - 1).long() + 1000  # rope positions can run ahead of the KV length
+    kg, vg = kc.to(dev), vc.to(dev)
+    attn = nkv.Attention(Hq, D, D ** -0.5, Hk, SimpleNamespace(kv_compress_enabled=False), 1)
+    attn.k_cache, attn.v_cache = kg, vg
+    nkv.set_context(True, slot_mapping=slots.to(dev), context_lens=ctx.to(dev),
+                    block_tables=bt.to(dev))
+    q, k, v = _split(qkv.to(dev), Hq, Hk)
+    qo, _, vo = nkv.qk_norm_rope_store(pos.to(dev), q, k, v, cache.to(dev), qw.to(dev),
+                                       kw.to(dev), 1e-6, k_cache=kg, v_cache=vg,
+                                       slot_mapping=slots.to(dev), need_k=False)
+    o = attn(qo, None, vo, 0, kv_stored=True)
+    torch.cuda.synchronize()
+    nkv.reset_context()
+    qr, _, _ = qk_norm_rope_store_ref(qkv, pos, qw, kw, 1e-6, cache, Hq, Hk, k_cache=kc,
+                                      v_cache=vc, slot_mapping=slots)
+    ref = paged_decode_ref(qr.float(), kc, vc, ctx, bt, D ** -0.5)
+    assert (o.squeeze(1).float().cpu() - ref).abs().max().item() <= 2e-2
+
+
+def test_prefill_through_attention(nkv, dev):
+    """Prefill without a block table reads the contiguous k' the fused op returns."""
+    from types import SimpleNamespace
+
+    from oracle.attention_ref import varlen_prefill_ref
+
+    Hq, Hk, lens = 32, 8, [70, 1, 200]
+    N = sum(lens)
+    # unit-scale values, as in the other attention tests (the 2e-2 bound is absolute)
+    qkv, qw, kw, _, cache, kc, vc, slots = _case(N, Hq, Hk, seed=80, nb=4, B=256, scale=1.0)
+    pos = torch.cat([torch.arange(n) for n in lens])
+    cu = torch.tensor([0, 70, 71, 271], dtype=torch.int32)
+    kg, vg = kc.to(dev), vc.to(dev)
+    attn = nkv.Attention(Hq, D, D ** -0.5, Hk, SimpleNamespace(kv_compress_enabled=False), 1)
+    attn.k_cache, attn.v_cache = kg, vg
+    nkv.set_context(False, cu_seqlens_q=cu.to(dev), cu_seqlens_k=cu.to(dev), max_seqlen_q=200,
+                    max_seqlen_k=200, slot_mapping=slots.to(dev))
+    q, k, v = _split(qkv.to(dev), Hq, Hk)
+    qo, ko, vo = nkv.qk_norm_rope_store(pos.to(dev), q, k, v, cache.to(dev), qw.to(dev),
+                                        kw.to(dev), 1e-6, k_cache=kg, v_cache=vg,
+                                        slot_mapping=slots.to(dev))
+    o = attn(qo, ko, vo, 0, kv_stored=True)
+    torch.cuda.synchronize()
+    nkv.reset_context()
+    qr, kr, vr = qk_norm_rope_store_ref(qkv, pos, qw, kw, 1e-6, cache, Hq, Hk, k_cache=kc,
+                                        v_cache=vc, slot_mapping=slots)
+    ref = varlen_prefill_ref(qr.float(), kr, vr, cu, cu, D ** -0.5)
+    assert (o.float().cpu() - ref).abs().max().item() <= 2e-2
+    _close(kg.cpu().view(-1, Hk, D), kc.view(-1, Hk, D))
