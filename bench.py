@@ -66,7 +66,7 @@ def parse():
     p.add_argument("--prefill-reps", type=int, default=20)
     p.add_argument("--longctx-steps", type=int, default=10)
     p.add_argument("--only", choices=["all", "decode", "compress", "prefill", "longctx",
-                                      "qkrope"],
+                                      "qkrope", "metadata"],
                    default="all",
                    help="run one part only (for profiling)")
     p.add_argument("--copy-calibration-mib", type=int, default=0,
@@ -453,6 +453,86 @@ def run_qkrope(args, dev):
     return res
 
 
+def run_metadata(args, dev):
+    """Per-step metadata (positions, slot_mapping, cu_seqlens, context_lens, padded block
+    tables) for the 16-prompt prefill batch (38,632 tokens) and a batch-500 decode step with
+    tables up to 64 blocks: the device builder (host packing + one copy + two kernels,
+    synchronised wall time) vs the reference's per-token Python loop (the oracle's
+    restatement, moved to the device the way prepare_step does)."""
+    from oracle.metadata_ref import prepare_step_ref
+    md = importlib.import_module("nanokv-llm_amd.engine.metadata")
+    gen = torch.Generator().manual_seed(11)
+    wl = wl_mod.prefill_qwen3_8b()  # CPU copy: only lengths and tables are used
+    tables_p = [[int(x) for x in row if x >= 0] for row in wl["block_tables"].tolist()]
+    cases = {
+        "prefill": ([0] * len(wl["Lq"]), list(wl["Lq"]), tables_p, None),
+    }
+    lens = torch.exp(torch.empty(500).uniform_(6.93, 9.70, generator=gen)).long().tolist()
+    perm = torch.randperm(40000, generator=gen).tolist()
+    tables_d, o = [], 0
+    for n in lens:
+        nb = (n + 255) // 256
+        tables_d.append(perm[o:o + nb])
+        o += nb
+    cases["decode"] = ([n - 1 for n in lens], [1] * len(lens), tables_d, [0] * len(lens))
+    res = {}
+    for name, (starts, num_new, tables, offs) in cases.items():
+        def dev_build():
+            return md.build_step_metadata(starts, num_new, tables, 256, dev, pos_offsets=offs)
+
+        def ref_build():
+            r = prepare_step_ref(starts, num_new, tables, 256, pos_offsets=offs)
+            return {k: (v.to(dev, non_blocking=True) if torch.is_tensor(v) else v)
+                    for k, v in r.items()}
+        t = {}
+        for tag, fn in (("device", dev_build), ("cpu_loop", ref_build)):
+            ts = []
+            for i in range(3 + 10):
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                out = fn()
+                torch.cuda.synchronize()
+                if i >= 3:
+                    ts.append(time.perf_counter() - t0)
+            t[tag] = statistics.median(ts)
+            if tag == "device":
+                got = {k: (v.cpu() if torch.is_tensor(v) else v) for k, v in out.items()}
+        ref = prepare_step_ref(starts, num_new, tables, 256, pos_offsets=offs)
+        ok = all(torch.equal(got[k], ref[k]) for k in ("positions", "slot_mapping",
+                                                     "cu_seqlens_q", "cu_seqlens_k",
+                                                     "context_lens", "block_tables"))
+        res[f"metadata_{name}_tokens"] = sum(num_new)
+        res[f"metadata_{name}_device_us"] = round(t["device"] * 1e6, 1)
+        res[f"metadata_{name}_cpu_loop_us"] = round(t["cpu_loop"] * 1e6, 1)
+        res[f"metadata_{name}_bit_exact"] = ok
+    # steady-state decode with the device-resident table store: per step ~2 of the 500
+    # tables gain a block (one block per 256 tokens per sequence)
+    starts, num_new, tables, offs = cases["decode"]
+    tables = [list(t) for t in tables]
+    store = md.BlockTableStore(512, 128, dev)
+    ids = list(range(len(tables)))
+    md.build_step_metadata(starts, num_new, tables, 256, dev, pos_offsets=offs, store=store,
+                           seq_ids=ids)
+    ts, nxt = [], 50000
+    for i in range(3 + 20):
+        for j in (i % 500, (i * 37 + 11) % 500):
+            tables[j].append(nxt)
+            nxt += 1
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        out = md.build_step_metadata(starts, num_new, tables, 256, dev, pos_offsets=offs,
+                                     store=store, seq_ids=ids)
+        torch.cuda.synchronize()
+        if i >= 3:
+            ts.append(time.perf_counter() - t0)
+    ref = prepare_step_ref(starts, num_new, tables, 256, pos_offsets=offs)
+    res["metadata_decode_store_us"] = round(statistics.median(ts) * 1e6, 1)
+    res["metadata_decode_store_bit_exact"] = all(
+        torch.equal(out[k].cpu(), ref[k]) for k in ("positions", "slot_mapping", "block_tables",
+                                                    "context_lens"))
+    return res
+
+
 def run_longctx(args, dev):
     """Qwen3-32B long-context decode at batch 500 on a pool filling most of HBM, and the
     compression step on that state (20 longest uncompressed sequences, window 4 blocks, keep
@@ -555,6 +635,9 @@ def main():
     if args.only == "qkrope":
         print(json.dumps(run_qkrope(args, dev)), flush=True)
         return
+    if args.only == "metadata":
+        print(json.dumps(run_metadata(args, dev)), flush=True)
+        return
     print(f"[bench] decode workload: bs 64, Hq 32, Hk 8, ctx U[2048,8192], pool 4096 blocks",
           file=sys.stderr, flush=True)
     wl, sets, r = run_decode(args, dev)
@@ -575,6 +658,9 @@ def main():
     qkrope = run_qkrope(args, dev)
     print(f"[bench] norm+rope+store done: {qkrope['qkrope_prefill_gbs']} GB/s",
           file=sys.stderr, flush=True)
+    meta = run_metadata(args, dev)
+    print(f"[bench] metadata done: prefill {meta['metadata_prefill_device_us']} us "
+          f"(loop {meta['metadata_prefill_cpu_loop_us']} us)", file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(wl, sets[0][0], wl["k_cache"], wl["v_cache"])
@@ -631,6 +717,7 @@ def main():
         **pre,
         **longctx,
         **qkrope,
+        **meta,
     }
     print(json.dumps(line), flush=True)
 

@@ -1,7 +1,9 @@
 /*
  * nkv.h -- C ABI of libnkv_amd.so, the MI355X (gfx950) attention hot path of
  * nano-kvllm: paged K/V store, paged decode attention, varlen causal prefill
- * over the paged cache, and the window-based periodic KV-compression step.
+ * over the paged cache, and the window-based periodic KV-compression step;
+ * beside it the steps either side of the path: the fused q/k RMSNorm + RoPE
+ * + K/V store, and the per-step metadata builders.
  *
  * Conventions (every entry point):
  *   - All tensor pointers are DEVICE pointers. Element types are fixed per
@@ -311,6 +313,48 @@ int nkv_compress_finalize(int32_t* block_tables, int64_t bt_row_stride,
                           int32_t m, int32_t keep_tokens, int32_t block_size,
                           int32_t window_blocks, int32_t rewrite_tables,
                           int32_t* slot_mapping, int32_t* events, void* stream);
+
+/*
+ * Per-step attention metadata built on the device from one packed int32
+ * buffer (device memory, n = n_seqs):
+ *   packed = [starts[n] | num_new[n] | pos_offsets[n] (if flags & NKV_META_POS_OFFSETS)
+ *             | tables]
+ *   tables, without a table store: [bt_offsets[n+1] | bt_flat[bt_offsets[n]]]
+ *     (sequence s's table is bt_flat[bt_offsets[s] .. bt_offsets[s+1]),
+ *     offsets nondecreasing from 0);
+ *   tables, with table_store [store_rows, store_row_stride] (device, kept by
+ *     the caller across steps): [rows[n] | counts[n] | updates[3*n_updates]]
+ *     -- first every update (row, col, id) is written to the store, then
+ *     sequence s's table is the first counts[s] entries of store row rows[s].
+ * Sequence s schedules num_new[s] tokens at KV positions starts[s] ..
+ * starts[s]+num_new[s]-1. Outputs:
+ *   cu_seqlens_q[n+1] = prefix sums of num_new; cu_seqlens_k[n+1] = prefix
+ *   sums of end = starts + num_new; context_lens[n] = end (optional);
+ *   logits_indices[n] = cu_seqlens_q[s+1] - 1 (int64, optional);
+ *   max_seqlens[2] = {max num_new, max end} (optional);
+ *   for token i of s at row r = cu_seqlens_q[s] + i (r < total_tokens):
+ *     positions[r] = starts[s] + i + pos_offsets[s] (int64; offset 0 if absent)
+ *     slot_mapping[r] = table[kv / block_size] * block_size + kv % block_size
+ *                       (kv = starts[s] + i; -1 if the table is too short or
+ *                       the entry is negative);
+ *   block_tables[s, 0:bt_width] = the table right-padded with -1 (optional).
+ * total_tokens = sum(num_new) sizes positions/slot_mapping; max_new_tokens
+ * sizes the launch only (any value gives the same result). Negative counts
+ * or starts are treated as 0; updates and rows outside the store are ignored.
+ * Replaces: ModelRunner.prepare_step's per-token loop and prepare_block_tables
+ *           (nanokvllm/engine/model_runner.py:154-219) and the decode builder
+ *           of prepare_decode (model_runner.py:265-285: RoPE position =
+ *           rope_pos, i.e. pos_offsets = rope_pos - (len - 1)).
+ */
+#define NKV_META_POS_OFFSETS 1
+int nkv_build_step_metadata(const int32_t* packed, int32_t n_seqs, int32_t block_size,
+                            int32_t max_new_tokens, int64_t total_tokens, int32_t flags,
+                            int32_t* table_store, int64_t store_row_stride, int32_t store_rows,
+                            int32_t n_updates, int32_t* cu_seqlens_q, int32_t* cu_seqlens_k,
+                            int32_t* context_lens, int64_t* positions, int32_t* slot_mapping,
+                            int64_t* logits_indices, int32_t* max_seqlens,
+                            int32_t* block_tables, int64_t bt_row_stride, int32_t bt_width,
+                            void* stream);
 
 #ifdef __cplusplus
 }

@@ -19,14 +19,13 @@
 * ``prepare_decode_metadata`` -- decode metadata as in prepare_decode
   (model_runner.py:265-285): positions = rope_pos, context_lens = physical
   length, slot = last block * B + last_block_num_tokens - 1, block tables
-  right-padded with -1.
+  right-padded with -1; built on the device (engine/metadata.py).
 * ``prepare_step_metadata`` -- the mixed prefill/decode builder of
-  prepare_step (model_runner.py:160-219).
+  prepare_step (model_runner.py:160-219), built on the device.
 """
 from __future__ import annotations
 
-import torch
-
+from .metadata import BlockTableStore, build_step_metadata
 from .sequence import ScheduledSeq, Sequence
 
 
@@ -36,47 +35,28 @@ def prepare_block_tables(seqs: list[Sequence], pad: int = -1) -> list[list[int]]
     return [s.block_table + [pad] * (max_len - len(s.block_table)) for s in seqs]
 
 
-def prepare_decode_metadata(seqs: list[Sequence], block_size: int, device="cuda"):
-    positions, slot_mapping, context_lens = [], [], []
-    for seq in seqs:
-        positions.append(seq.rope_pos)
-        context_lens.append(len(seq))
-        slot_mapping.append(seq.block_table[-1] * block_size + seq.last_block_num_tokens - 1)
-    to = dict(device=device)
-    return dict(
-        positions=torch.tensor(positions, dtype=torch.int64).to(**to),
-        slot_mapping=torch.tensor(slot_mapping, dtype=torch.int32).to(**to),
-        context_lens=torch.tensor(context_lens, dtype=torch.int32).to(**to),
-        block_tables=torch.tensor(prepare_block_tables(seqs), dtype=torch.int32).to(**to),
-    )
+def prepare_decode_metadata(seqs: list[Sequence], block_size: int, device="cuda",
+                            store: BlockTableStore | None = None):
+    """prepare_decode (model_runner.py:265-285) on the device: one token per sequence at KV
+    position len - 1 with RoPE position rope_pos; block tables padded with -1. With a
+    ``store`` only the table entries changed since the last step are sent."""
+    return build_step_metadata([len(s) - 1 for s in seqs], [1] * len(seqs),
+                               [s.block_table for s in seqs], block_size, device,
+                               pos_offsets=[s.rope_pos - (len(s) - 1) for s in seqs],
+                               store=store, seq_ids=[s.seq_id for s in seqs])
 
 
-def prepare_step_metadata(scheduled: list[ScheduledSeq], block_size: int, device="cuda"):
-    positions, slot_mapping, context_lens = [], [], []
-    cu_q, cu_k = [0], [0]
-    max_q = max_k = 0
-    for sched in scheduled:
-        seq, n = sched.seq, sched.num_new_tokens
-        start = seq.num_computed_tokens
-        end = start + n
-        positions.extend(range(start, end))
-        cu_q.append(cu_q[-1] + n)
-        cu_k.append(cu_k[-1] + end)
-        max_q, max_k = max(max_q, n), max(max_k, end)
-        for pos in range(start, end):
-            slot_mapping.append(seq.block_table[pos // block_size] * block_size + pos % block_size)
-        context_lens.append(end)
-    to = dict(device=device)
-    return dict(
-        positions=torch.tensor(positions, dtype=torch.int64).to(**to),
-        slot_mapping=torch.tensor(slot_mapping, dtype=torch.int32).to(**to),
-        context_lens=torch.tensor(context_lens, dtype=torch.int32).to(**to),
-        cu_seqlens_q=torch.tensor(cu_q, dtype=torch.int32).to(**to),
-        cu_seqlens_k=torch.tensor(cu_k, dtype=torch.int32).to(**to),
-        max_seqlen_q=max_q, max_seqlen_k=max_k,
-        block_tables=torch.tensor(prepare_block_tables([s.seq for s in scheduled]),
-                                  dtype=torch.int32).to(**to),
-    )
+def prepare_step_metadata(scheduled: list[ScheduledSeq], block_size: int, device="cuda",
+                          store: BlockTableStore | None = None):
+    """prepare_step (model_runner.py:160-219) on the device. Positions carry each sequence's
+    RoPE offset (rope_pos - (len - 1)), so a compressed sequence keeps its logical positions
+    in a mixed batch too; without compression this is the reference's range(start, end)."""
+    seqs = [s.seq for s in scheduled]
+    return build_step_metadata([s.num_computed_tokens for s in seqs],
+                               [s.num_new_tokens for s in scheduled],
+                               [s.block_table for s in seqs], block_size, device,
+                               pos_offsets=[s.rope_pos - (len(s) - 1) for s in seqs],
+                               store=store, seq_ids=[s.seq_id for s in seqs])
 
 
 class CompressionScheduler:

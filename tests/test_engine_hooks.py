@@ -10,6 +10,7 @@ from types import SimpleNamespace
 import pytest
 import torch
 
+from oracle import metadata_ref
 from oracle.compress_ref import compress_compact_ref
 
 hooks = importlib.import_module("nanokv-llm_amd.engine.compress_hooks")
@@ -134,6 +135,8 @@ def test_events_apply_and_decoding_continues(tail):
 
 
 def test_decode_and_step_metadata():
+    """The metadata oracle (model_runner.py:154-219, 265-285) on hand-built states; the
+    device builders are held to it in tests/test_gpu_metadata.py."""
     bm = BlockManager(32, B)
     a, b = _seq(300), _seq(2 * B)
     for s in (a, b):
@@ -141,7 +144,8 @@ def test_decode_and_step_metadata():
     a.num_computed_tokens, b.num_computed_tokens = 300, 2 * B
     b.append_token()
     bm.may_append(b)
-    md = hooks.prepare_decode_metadata([a, b], B, device="cpu")
+    md = metadata_ref.prepare_decode_ref([len(a), len(b)], [a.rope_pos, b.rope_pos],
+                                         [a.block_table, b.block_table], B)
     assert md["context_lens"].tolist() == [300, 2 * B + 1]
     assert md["slot_mapping"].tolist() == [a.block_table[1] * B + 300 - B - 1, b.block_table[2] * B]
     assert md["block_tables"].tolist() == [a.block_table + [-1], b.block_table]
@@ -150,10 +154,18 @@ def test_decode_and_step_metadata():
     c = _seq(3 * B + 5)
     bm.allocate(c)
     c.num_computed_tokens = 2 * B - 20
-    st = hooks.prepare_step_metadata([ScheduledSeq(c, 40), ScheduledSeq(a, 1)], B, device="cpu")
+    st = metadata_ref.prepare_step_ref([c.num_computed_tokens, a.num_computed_tokens], [40, 1],
+                                       [c.block_table, a.block_table], B)
     assert st["cu_seqlens_q"].tolist() == [0, 40, 41]
     assert st["cu_seqlens_k"].tolist() == [0, 2 * B + 20, 2 * B + 20 + 301]
     assert st["max_seqlen_q"] == 40 and st["max_seqlen_k"] == 2 * B + 20
+    assert st["logits_indices"].tolist() == [39, 40]
     pos = list(range(2 * B - 20, 2 * B + 20))
+    assert st["positions"].tolist() == pos + [300]
     exp = [c.block_table[p // B] * B + p % B for p in pos] + [a.block_table[300 // B] * B + 300 % B]
     assert st["slot_mapping"].tolist() == exp
+    # a compressed sequence keeps its RoPE position; a table too short gives slot -1
+    d = metadata_ref.prepare_decode_ref([10], [5000], [[7]], B)
+    assert d["positions"].tolist() == [5000] and d["slot_mapping"].tolist() == [7 * B + 9]
+    e = metadata_ref.prepare_step_ref([B - 1], [2], [[3]], B)
+    assert e["slot_mapping"].tolist() == [3 * B + B - 1, -1]
