@@ -315,6 +315,27 @@ int nkv_compress_finalize(int32_t* block_tables, int64_t bt_row_stride,
                           int32_t* slot_mapping, int32_t* events, void* stream);
 
 /*
+ * Device-side compression scheduling (graph-capturable): advances
+ * *step_counter by one; when the new value is a multiple of period, sequence
+ * i < batch is eligible iff context_lens[i] % block_size != block_size - 1,
+ * tail_uncompressed[i] >= window_blocks*block_size and
+ * context_lens[i] / block_size >= window_blocks; seq_idx[0:topk] receives the
+ * first topk eligible indices in batch order (policy 0) or the topk longest
+ * (policy 1, ties to the lower index), padded with -1; *n_selected the count;
+ * base_context_lens (optional) a copy of context_lens; batch <= 16384. Every compression
+ * entry point accepts such a -1 padded seq_idx (padding rows are skipped;
+ * their importance / keep_idx rows are left unwritten, their event rows read
+ * [-1, 0, 0, 0, -1...]), so a step can always be launched with m = topk.
+ * Replaces: the compression block of ModelRunner.prepare_decode
+ *           (nanokvllm/engine/model_runner.py:300-332).
+ */
+int nkv_compress_schedule(const int32_t* context_lens, const int32_t* tail_uncompressed,
+                          int32_t batch, int32_t block_size, int32_t window_blocks,
+                          int32_t topk, int32_t period, int32_t policy, int32_t* step_counter,
+                          int32_t* seq_idx, int32_t* n_selected, int32_t* base_context_lens,
+                          void* stream);
+
+/*
  * Per-step attention metadata built on the device from one packed int32
  * buffer (device memory, n = n_seqs):
  *   packed = [starts[n] | num_new[n] | pos_offsets[n] (if flags & NKV_META_POS_OFFSETS)

@@ -57,6 +57,8 @@ SIGNATURES = {
                                        _i32, _i32, _i32, _i32, _i64, _p]),
     "nkv_compress_finalize": (C.c_int, [_p, _i64, _i32, _p, _p, _i32, _i32, _i32, _i32, _i32, _p,
                                         _p, _p]),
+    "nkv_compress_schedule": (C.c_int, [_p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _p, _p, _p,
+                                        _p, _p]),
     "nkv_build_step_metadata": (C.c_int, [_p, _i32, _i32, _i32, _i64, _i32, _p, _i64, _i32, _i32,
                                           _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i32, _p]),
 }

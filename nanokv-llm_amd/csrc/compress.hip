@@ -60,7 +60,7 @@ __global__ __launch_bounds__(256) void compress_score_kernel(
   bool valid = true;
   if (block_tables) {
     const int seq = seq_idx[j];
-    const int len = base_context_lens[seq];
+    const int len = seq >= 0 ? base_context_lens[seq] : 0;  // seq -1: padding entry
     const int full = len / block_size;
     const int wblk = full - window_blocks + t0 / block_size;
     int64_t pb = -1;
@@ -384,7 +384,7 @@ __device__ __forceinline__ void group_importance(
   bool valid = t0 < Lw;
   if (block_tables) {
     const int seq = seq_idx[j];
-    const int len = base_context_lens[seq];
+    const int len = seq >= 0 ? base_context_lens[seq] : 0;  // seq -1: padding entry
     const int full = len / block_size;
     int64_t pb = -1;
     if (valid && full >= window_blocks && full <= max_blocks)
@@ -489,7 +489,7 @@ __device__ __forceinline__ void compact_unit(
     int window_blocks, int64_t n_blocks) {
   const int tid = threadIdx.x;
   const int seq = seq_idx[j];
-  const int len = base_context_lens[seq];
+  const int len = seq >= 0 ? base_context_lens[seq] : 0;  // seq -1: padding entry
   const int full = len / B;
   const int tail = len - full * B;
   // not compressible, or inconsistent with the table width: leave untouched
@@ -572,6 +572,7 @@ __global__ __launch_bounds__(kSelThreads) void compress_group_kernel(
   const int lane = tid & 63;
   const int kvh = blockIdx.x % Hk;
   const int j = blockIdx.x / Hk;
+  if (block_tables && seq_idx[j] < 0) return;  // padding entry (uniform): nothing written
   const int Lw = window_blocks * block_size;
   const int n_cand = Lw - 1;
   float gi[4];
@@ -606,6 +607,7 @@ __global__ __launch_bounds__(kSelThreads) void compress_partial_kernel(
   const int lane = threadIdx.x & 63;
   const int kvh = blockIdx.x % Hk;
   const int j = blockIdx.x / Hk;
+  if (block_tables && seq_idx[j] < 0) return;  // padding entry (uniform): nothing written
   const int Lw = window_blocks * block_size;
   float gi[4];
   group_importance<G>(L, q, q_row_stride, k, block_tables, bt_row_stride, max_blocks,
@@ -634,6 +636,7 @@ __global__ __launch_bounds__(kSelThreads) void compress_sum_kernel(
   const int tid = threadIdx.x;
   const int j = blockIdx.x / n_units_per_seq;
   const int kvh = blockIdx.x % n_units_per_seq;
+  if (block_tables && seq_idx[j] < 0) return;  // padding entry (uniform): nothing written
   const int Lw = window_blocks * block_size;
   const int n_cand = Lw - 1;
   const float* pj = partial + (int64_t)j * Hk * Lw;
@@ -676,7 +679,7 @@ __global__ __launch_bounds__(256) void compress_compact_kernel(
   const int kvh = (blockIdx.x >> 2) % Hk;
   const int j = (blockIdx.x >> 2) / Hk;
   const int seq = seq_idx[j];
-  const int len = base_context_lens[seq];
+  const int len = seq >= 0 ? base_context_lens[seq] : 0;  // seq -1: padding entry
   const int B = block_size;
   const int full = len / B;
   const int tail = len - full * B;
@@ -765,7 +768,7 @@ __global__ __launch_bounds__(64) void compress_finalize_kernel(
   const int ev_len = 4 + max_blocks;
   for (int j = threadIdx.x; j < m; j += blockDim.x) {
     const int seq = seq_idx[j];
-    const int len = base_context_lens[seq];
+    const int len = seq >= 0 ? base_context_lens[seq] : 0;  // seq -1: padding entry
     int32_t* ev = events + (int64_t)j * ev_len;
     int32_t* bt = block_tables + (int64_t)seq * bt_row_stride;
     const int full = len / B, tail = len - (len / B) * B;
@@ -789,6 +792,86 @@ __global__ __launch_bounds__(64) void compress_finalize_kernel(
     if (slot_mapping) {
       const int blk = new_len / B, off = new_len % B;
       slot_mapping[seq] = (off == 0 || blk >= max_blocks || bt[blk] < 0) ? -1 : bt[blk] * B + off;
+    }
+  }
+}
+
+// ----------------------------------------------------------------- schedule
+// The compression block of ModelRunner.prepare_decode (model_runner.py:300-332)
+// on the device, so a compression step needs no host data: the decode-step
+// counter advances; on every period-th step sequence i is eligible iff
+// len % B != B - 1, tail_uncompressed >= W*B and len / B >= W; the first topk
+// eligible in batch order (policy 0, the reference) or the topk longest
+// (policy 1, ties to the lower index) go to seq_idx, the rest is -1. One
+// workgroup; each sequence's eligibility key (its length, or -1) is staged in
+// LDS once; base_context_lens receives a copy of context_lens.
+constexpr int kSchedThreads = 1024;
+constexpr int kSchedMaxBatch = 16384;  // eligibility keys staged in LDS (64 KiB)
+
+__global__ __launch_bounds__(kSchedThreads) void compress_schedule_kernel(
+    const int32_t* __restrict__ context_lens, const int32_t* __restrict__ tail_uncompressed,
+    int32_t batch, int32_t block_size, int32_t window_blocks, int32_t topk, int32_t period,
+    int32_t policy, int32_t* __restrict__ step_counter, int32_t* __restrict__ seq_idx,
+    int32_t* __restrict__ n_selected, int32_t* __restrict__ base_context_lens) {
+  __shared__ __attribute__((aligned(16))) int32_t key[kSchedMaxBatch];  // length if eligible, else -1
+  __shared__ int32_t part[kSchedThreads];
+  __shared__ int32_t fire;
+  const int tid = threadIdx.x;
+  if (tid == 0) {
+    const int c = step_counter[0] + 1;
+    step_counter[0] = c;
+    fire = period > 0 && c % period == 0;
+  }
+  for (int r = tid; r < topk; r += kSchedThreads) seq_idx[r] = -1;
+  __syncthreads();
+  const int B = block_size;
+  for (int i = tid; i < batch; i += kSchedThreads) {
+    const int len = context_lens[i];
+    if (base_context_lens) base_context_lens[i] = len;
+    const bool ok = fire && len % B != B - 1 &&
+                    tail_uncompressed[i] >= window_blocks * B && len / B >= window_blocks;
+    key[i] = ok ? len : -1;
+  }
+  const int padded = (batch + 15) & ~15;  // the rank loop reads 16 keys at a time
+  for (int i = batch + tid; i < padded; i += kSchedThreads) key[i] = -1;
+  __syncthreads();
+  const int per = (batch + kSchedThreads - 1) / kSchedThreads;
+  const int i0 = min(batch, tid * per), i1 = min(batch, i0 + per);
+  int cnt = 0;
+  for (int i = i0; i < i1; ++i) cnt += key[i] >= 0;
+  part[tid] = cnt;
+  __syncthreads();
+  for (int o = 1; o < kSchedThreads; o <<= 1) {  // inclusive scan of the eligible counts
+    const int a = tid >= o ? part[tid - o] : 0;
+    __syncthreads();
+    part[tid] += a;
+    __syncthreads();
+  }
+  if (tid == 0) n_selected[0] = min(part[kSchedThreads - 1], topk);
+  if (policy == 0) {  // first topk in batch order
+    int rank = part[tid] - cnt;
+    for (int i = i0; i < i1 && rank < topk; ++i)
+      if (key[i] >= 0) seq_idx[rank++] = i;
+  } else {  // topk longest: rank = eligible sequences that are longer, or as long and earlier
+    typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
+    const i32x4_t* k4 = reinterpret_cast<const i32x4_t*>(key);
+    for (int i = tid; i < batch; i += kSchedThreads) {
+      const int li = key[i];
+      if (li < 0) continue;
+      int rank = 0;
+      for (int j0 = 0; j0 < padded && rank < topk; j0 += 16) {  // 4 LDS loads in flight
+        i32x4_t v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = k4[j0 / 4 + u];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int j2 = j0 + 4 * u + e;
+            rank += v[u][e] > li || (v[u][e] == li && j2 < i);
+          }
+      }
+      if (rank < topk) seq_idx[rank] = i;
     }
   }
 }
@@ -1130,4 +1213,25 @@ extern "C" int nkv_compress_step(const void* q, int64_t q_row_stride, void* k_ca
                               base_context_lens, context_lens, seq_idx, m, keep_idx, n_sets,
                               keep_tokens, n_kv_heads, head_dim, block_size, window_blocks,
                               n_blocks, stream);
+}
+
+extern "C" int nkv_compress_schedule(const int32_t* context_lens,
+                                     const int32_t* tail_uncompressed, int32_t batch,
+                                     int32_t block_size, int32_t window_blocks, int32_t topk,
+                                     int32_t period, int32_t policy, int32_t* step_counter,
+                                     int32_t* seq_idx, int32_t* n_selected,
+                                     int32_t* base_context_lens, void* stream) {
+  using namespace nkv;
+  clear_error();
+  NKV_REQUIRE(batch >= 0 && block_size > 0 && window_blocks > 0 && topk > 0 && period > 0 &&
+                  (policy == 0 || policy == 1),
+              NKV_EINVAL, "compress_schedule: bad arguments");
+  NKV_REQUIRE(batch <= kSchedMaxBatch, NKV_EUNSUPPORTED, "compress_schedule: batch above %d",
+              kSchedMaxBatch);
+  NKV_REQUIRE(context_lens && tail_uncompressed && step_counter && seq_idx && n_selected,
+              NKV_EINVAL, "compress_schedule: null pointer");
+  hipLaunchKernelGGL(compress_schedule_kernel, dim3(1), dim3(kSchedThreads), 0, as_stream(stream),
+                     context_lens, tail_uncompressed, batch, block_size, window_blocks, topk,
+                     period, policy, step_counter, seq_idx, n_selected, base_context_lens);
+  return check_launch("nkv_compress_schedule");
 }

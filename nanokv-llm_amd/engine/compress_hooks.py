@@ -25,6 +25,8 @@
 """
 from __future__ import annotations
 
+import torch
+
 from .metadata import BlockTableStore, build_step_metadata
 from .sequence import ScheduledSeq, Sequence
 
@@ -100,6 +102,66 @@ class CompressionScheduler:
         context.compress_selected_seq_ids = ids
         context.compress_base_context_lens = (context.context_lens.clone()
                                               if is_step and idx else None)
+
+
+class DeviceCompressionScheduler:
+    """The same selection as ``CompressionScheduler`` made on the device
+    (nkv_compress_schedule), so a compression step reads no host data and can be captured
+    in a HIP graph. The host keeps the step counter (it decides which steps compress, i.e.
+    which graph to replay); on a compression step the kernel picks the sequences from the
+    device ``context_lens`` and ``tail_uncompressed`` into a -1 padded ``seq_idx`` of
+    length topk, which every compression kernel accepts. After the step the last layer's
+    events are in ``context.compression_events_device``: pass them to
+    ``apply_compression_events_device``."""
+
+    def __init__(self, config, max_batch: int, device, policy: str = "first"):
+        self.block_size = config.kvcache_block_size
+        self.window_blocks = config.kv_compress_window_blocks
+        self.topk = config.kv_compress_topk
+        self.period = config.kv_compress_period
+        self.policy = policy
+        self.step_counter = 0
+        i32 = dict(dtype=torch.int32, device=device)
+        self.device_counter = torch.zeros(1, **i32)
+        self.seq_idx = torch.full((self.topk,), -1, **i32)
+        self.n_selected = torch.zeros(1, **i32)
+        self.base_context_lens = torch.zeros(max_batch, **i32)
+
+    def prepare(self, context, tail_uncompressed: torch.Tensor) -> bool:
+        """Fill the compression fields of ``context``; ``tail_uncompressed`` is a device int32
+        [batch] (tokens since each sequence's last compression). Returns is_compress_step."""
+        from ..layers.compress_utils import compress_schedule
+        context.compress_need_mask = None
+        context.compress_any = False
+        self.step_counter += 1
+        fire = self.step_counter % self.period == 0
+        context.is_compress_step = fire
+        context.compress_selected_batch_indices = None
+        context.compress_selected_seq_ids = None
+        context.compression_events_device = None
+        if not fire:
+            context.compress_seq_idx = None
+            context.compress_base_context_lens = None
+            return False
+        bs = context.context_lens.numel()
+        base = self.base_context_lens[:bs]
+        compress_schedule(context.context_lens, tail_uncompressed, self.block_size,
+                          self.window_blocks, self.topk, 1, self.device_counter, self.seq_idx,
+                          self.n_selected, base, policy=self.policy)
+        context.compress_seq_idx = self.seq_idx
+        context.compress_base_context_lens = base
+        return True
+
+
+def apply_compression_events_device(scheduled: list, events: torch.Tensor | None,
+                                    block_manager) -> None:
+    """Read the event rows a device-selected step left on the device (one copy) and apply
+    them like ``apply_compression_events``; padding rows (batch index -1) are skipped."""
+    if events is None:
+        return
+    from ..layers.compress_utils import events_to_dicts
+    evs = [e for e in events_to_dicts(events, -1) if e["batch_index"] >= 0]
+    apply_compression_events(scheduled, evs, block_manager)
 
 
 def apply_compression_events(scheduled: list, events: list[dict] | None, block_manager) -> None:

@@ -170,7 +170,8 @@ class Attention(nn.Module):
             store_kvcache(k, v, k_cache, v_cache, context.slot_mapping)
 
         if (context.use_decode_kernel and self.kv_compress_enabled and context.is_compress_step
-                and context.compress_selected_batch_indices):
+                and (context.compress_selected_batch_indices
+                     or context.compress_seq_idx is not None)):
             MyCompressCompact(
                 q_current=q, k_cache=k_cache, v_cache=v_cache, layer_id=Layer,
                 block_size=k_cache.size(1), window_blocks=self.kv_compress_window_blocks,

@@ -25,19 +25,30 @@ AGG_MODES = {"all": _lib.NKV_AGG_ALL, "group": _lib.NKV_AGG_GROUP}
 
 
 class _StepBuffers:
-    """Device buffers of one compression step, shared by all layers."""
+    """Device buffers of one compression step, shared by all layers. ``selected`` is the
+    host list of batch indices, or a device int32 tensor (-1 padded) selected on the
+    device; then no host data enters the step and it can be captured in a HIP graph."""
 
     def __init__(self, selected, device, m, n_sets, n_cand, keep_tokens, ws_bytes, ev_len):
-        self.key = (tuple(selected), device, n_sets, n_cand, keep_tokens, ws_bytes, ev_len)
-        self.seq_idx = torch.tensor(selected, dtype=torch.int32).to(device, non_blocking=True)
+        self.key = _key(selected, device, n_sets, n_cand, keep_tokens, ws_bytes, ev_len)
+        if torch.is_tensor(selected):
+            self.seq_idx = selected
+        else:
+            self.seq_idx = torch.tensor(selected, dtype=torch.int32).to(device, non_blocking=True)
         self.importance = torch.empty(m, n_sets, n_cand, dtype=torch.float32, device=device)
         self.keep_idx = torch.empty(m, n_sets, keep_tokens, dtype=torch.int32, device=device)
         self.workspace = torch.empty(max(ws_bytes, 4), dtype=torch.uint8, device=device)
         self.events = torch.empty(m, ev_len, dtype=torch.int32, device=device)
 
 
+def _key(selected, device, n_sets, n_cand, keep_tokens, ws_bytes, ev_len):
+    sel = ("device", selected.data_ptr(), selected.numel()) if torch.is_tensor(selected) \
+        else tuple(selected)
+    return (sel, device, n_sets, n_cand, keep_tokens, ws_bytes, ev_len)
+
+
 def _buffers(context, selected, device, m, n_sets, n_cand, keep_tokens, ws_bytes, ev_len):
-    key = (tuple(selected), device, n_sets, n_cand, keep_tokens, ws_bytes, ev_len)
+    key = _key(selected, device, n_sets, n_cand, keep_tokens, ws_bytes, ev_len)
     buf = getattr(context, "_nkv_compress_buffers", None)
     if buf is None or buf.key != key:
         buf = _StepBuffers(selected, device, m, n_sets, n_cand, keep_tokens, ws_bytes, ev_len)
@@ -168,13 +179,18 @@ def MyCompressCompact(q_current: torch.Tensor, k_cache: torch.Tensor, v_cache: t
     if (not context.use_decode_kernel) or context.context_lens is None \
             or context.block_tables is None:
         return False
-    selected = context.compress_selected_batch_indices
-    if not selected:
-        return False
-    m = len(selected)
-    bs = context.context_lens.numel()
-    assert all(0 <= i < bs for i in selected) and len(set(selected)) == m, \
-        f"selected batch indices must be distinct and < {bs}: {selected}"
+    device_sel = getattr(context, "compress_seq_idx", None)
+    if device_sel is not None:  # selected on the device (nkv_compress_schedule), -1 padded
+        selected = device_sel
+        m = selected.numel()
+    else:
+        selected = context.compress_selected_batch_indices
+        if not selected:
+            return False
+        m = len(selected)
+        bs = context.context_lens.numel()
+        assert all(0 <= i < bs for i in selected) and len(set(selected)) == m, \
+            f"selected batch indices must be distinct and < {bs}: {selected}"
     B = block_size
     window_tokens = window_blocks * B
     keep_tokens = keep_blocks * B + keep_extra_tokens
@@ -198,7 +214,26 @@ def MyCompressCompact(q_current: torch.Tensor, k_cache: torch.Tensor, v_cache: t
         compress_finalize(context.block_tables, base, buf.seq_idx, keep_tokens, B, window_blocks,
                           buf.events, rewrite_tables=rewrite_tables,
                           slot_mapping=context.slot_mapping if rewrite_tables else None)
-        if context.compression_events is None:
-            context.compression_events = []
-        context.compression_events.extend(events_to_dicts(buf.events, layer_id))
+        if device_sel is not None:  # read by the host after the step, no sync here
+            context.compression_events_device = buf.events
+        else:
+            if context.compression_events is None:
+                context.compression_events = []
+            context.compression_events.extend(events_to_dicts(buf.events, layer_id))
     return True
+
+
+def compress_schedule(context_lens, tail_uncompressed, block_size, window_blocks, topk, period,
+                      step_counter, seq_idx, n_selected, base_context_lens=None,
+                      policy="first"):
+    """The compression selection of prepare_decode (model_runner.py:300-332) on the device:
+    advances ``step_counter`` and fills ``seq_idx`` (int32 [topk], -1 padded),
+    ``n_selected`` and ``base_context_lens`` without reading anything on the host."""
+    bs = context_lens.numel()
+    assert tail_uncompressed.numel() >= bs and seq_idx.numel() == topk
+    rc = _lib.lib().nkv_compress_schedule(
+        context_lens.data_ptr(), tail_uncompressed.data_ptr(), bs, block_size, window_blocks,
+        topk, period, {"first": 0, "longest": 1}[policy], step_counter.data_ptr(),
+        seq_idx.data_ptr(), n_selected.data_ptr(), _lib.ptr(base_context_lens),
+        _lib.stream_of(context_lens))
+    _lib.check(rc, "compress_schedule")

@@ -1,7 +1,8 @@
 """Per-step attention metadata shared by every Attention layer.
 
 Same fields, defaults and functions as nanokvllm/utils/context.py:3-40, so a
-model runner written for the reference fills it unchanged.
+model runner written for the reference fills it unchanged; two more fields
+carry the device-side compression selection and its events.
 """
 from __future__ import annotations
 
@@ -29,6 +30,12 @@ class Context:
     compress_selected_batch_indices: list | None = None
     compress_selected_seq_ids: list[int] | None = None
     compress_base_context_lens: torch.Tensor | None = None
+
+    # device-side selection (graph-capturable compression step): int32 [topk], -1 padded,
+    # filled on the device by nkv_compress_schedule; the last layer then leaves its event
+    # rows in compression_events_device for the host to apply after the step
+    compress_seq_idx: torch.Tensor | None = None
+    compression_events_device: torch.Tensor | None = None
 
 
 _CONTEXT = Context()

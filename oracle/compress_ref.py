@@ -180,3 +180,21 @@ def compress_compact_ref(q_current, k_cache, v_cache, block_tables, base_context
                 "freed_block_ids": freed, "tail_uncompressed_len_after": 0,
             })
     return True, keep_idx, events
+
+
+def compress_schedule_ref(context_lens, tail_uncompressed, block_size, window_blocks, topk,
+                          counter, period, policy="first"):
+    """model_runner.py:300-332: counter += 1; on every period-th step sequence i is eligible
+    iff len % B != B - 1, tail_uncompressed >= W*B and len // B >= W; the first topk
+    eligible in batch order ("first", the reference) or the topk longest ("longest", ties
+    to the lower index). Returns (new counter, selected indices, fired)."""
+    counter += 1
+    fired = counter % period == 0
+    if not fired:
+        return counter, [], False
+    B = block_size
+    cand = [i for i, (n, t) in enumerate(zip(context_lens, tail_uncompressed))
+            if n % B != B - 1 and t >= window_blocks * B and n // B >= window_blocks]
+    if policy == "longest":
+        cand.sort(key=lambda i: (-context_lens[i], i))
+    return counter, cand[:topk], True

@@ -11,7 +11,7 @@ import pytest
 import torch
 
 from oracle import metadata_ref
-from oracle.compress_ref import compress_compact_ref
+from oracle.compress_ref import compress_compact_ref, compress_schedule_ref
 
 hooks = importlib.import_module("nanokv-llm_amd.engine.compress_hooks")
 seqmod = importlib.import_module("nanokv-llm_amd.engine.sequence")
@@ -169,3 +169,42 @@ def test_decode_and_step_metadata():
     assert d["positions"].tolist() == [5000] and d["slot_mapping"].tolist() == [7 * B + 9]
     e = metadata_ref.prepare_step_ref([B - 1], [2], [[3]], B)
     assert e["slot_mapping"].tolist() == [3 * B + B - 1, -1]
+
+
+@pytest.mark.parametrize("policy", ["first", "longest"])
+def test_schedule_oracle_matches_host_scheduler(policy):
+    """The schedule oracle (the device kernel's checker) and the host CompressionScheduler
+    make the same choice on random states, firing on the same steps."""
+    gen = torch.Generator().manual_seed(3 if policy == "first" else 4)
+    sched = hooks.CompressionScheduler(_cfg(period=2, topk=5), policy=policy)
+    counter = 0
+    for _ in range(6):
+        lens = torch.randint(B, 20 * B, (60,), generator=gen).tolist()
+        lens[::7] = [(x // B) * B + B - 1 for x in lens[::7]]  # tail == B-1 rows
+        tails = torch.randint(0, 2 * W * B, (60,), generator=gen).tolist()
+        seqs = [_seq(n, tail_uncompressed=t) for n, t in zip(lens, tails)]
+        fired, idx, _ = sched.select(seqs)
+        counter, sel, fired_ref = compress_schedule_ref(lens, tails, B, W, 5, counter, 2, policy)
+        assert fired == fired_ref and idx == sel
+    # a hand-built case: only rows 0 and 2 qualify
+    assert compress_schedule_ref([1024, 1279, 2000, 1023, 5000], [1024, 2000, 1024, 5000, 100],
+                                 B, W, 2, 2, 3) == (3, [0, 2], True)
+
+
+def test_device_events_skip_padding_rows():
+    """apply_compression_events_device: padding rows (batch index -1) are ignored, real rows
+    are applied like the host path's event dicts."""
+    bm = BlockManager(32, B)
+    a = _seq(6 * B + 10)
+    bm.allocate(a)
+    n_before = len(bm.free_block_ids)
+    ev = torch.full((2, 4 + 8), -1, dtype=torch.int32)
+    ev[0, :4] = torch.tensor([-1, 0, 0, 0])
+    new_len = 6 * B + 10 - W * B + 513
+    keep_blocks = (new_len + B - 1) // B
+    freed = a.block_table[keep_blocks:]
+    ev[1, :4] = torch.tensor([0, new_len, keep_blocks, len(freed)])
+    ev[1, 4:4 + len(freed)] = torch.tensor(freed)
+    hooks.apply_compression_events_device([ScheduledSeq(a, 1)], ev, bm)
+    assert len(a) == new_len and len(a.block_table) == keep_blocks
+    assert a.tail_uncompressed_len == 0 and len(bm.free_block_ids) == n_before + len(freed)
