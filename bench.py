@@ -163,6 +163,50 @@ def run_decode(args, dev):
     return wl, sets, res
 
 
+def run_decode_fp8(args, dev, wl, sets):
+    """The same decode workload over an fp8 (E4M3FN, scales 1) copy of the pool: store_fp8 +
+    decode_fp8 per step on the rotated tables; half the cache bytes per decoded token."""
+    kvc = importlib.import_module("nanokv-llm_amd.layers.kv_cache")
+    q, key, value = wl["q"].to(dev), wl["key"].to(dev), wl["value"].to(dev)
+    kq, vq = kvc.fp8_quantize(wl["k_cache"]), kvc.fp8_quantize(wl["v_cache"])
+    ctx = wl["context_lens"].to(dev)
+    bs, Hq, D = q.shape
+    NB, B, Hk, _ = kq.shape
+    width = sets[0][0].size(1)
+    ws = torch.empty(_lib.lib().nkv_paged_decode_workspace_bytes(bs, Hq, D, width, B),
+                     dtype=torch.uint8, device=dev)
+    out = torch.empty(bs, Hq, D, dtype=torch.bfloat16, device=dev)
+    stream = torch.cuda.current_stream()
+
+    def step(i, ev=None):
+        bt, slots = sets[i % len(sets)]
+        nkv.store_kvcache(key, value, kq, vq, slots)
+        if ev:
+            ev[0].record(stream)
+        nkv.paged_decode(q, kq, vq, ctx, bt, wl["scale"], out=out, workspace=ws)
+        if ev:
+            ev[1].record(stream)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(args.steps)]
+    for i in range(args.steps):
+        step(i, evs[i])
+    torch.cuda.synchronize()
+    dec_ms = statistics.mean(e[0].elapsed_time(e[1]) for e in evs)
+    n_tok = int(wl["context_lens"].sum())
+    nbytes = n_tok * Hk * D * 2 + bs * Hq * D * 2 * 2 + bs * 4 * (width + 1)
+    kd, vd = kvc.fp8_dequantize(kq), kvc.fp8_dequantize(vq)
+    err = parity_sample(wl, sets[(args.steps - 1) % len(sets)][0], out, kd, vd, n=4)
+    del kq, vq, kd, vd, ws
+    torch.cuda.empty_cache()
+    return {"decode_fp8_us": round(dec_ms * 1e3, 2),
+            "decode_fp8_gbs": round(nbytes / (dec_ms * 1e-3) / 1e9, 1),
+            "decode_fp8_bytes": nbytes,
+            "decode_fp8_parity_max_abs_err": err}
+
+
 def _gather_sample(wl, bt, kc, vc, n):
     """Copy the blocks of the first n sequences to host: compact pool + remapped table."""
     return _gather_sample_rows(bt[:n].cpu(), kc, vc)
@@ -683,8 +727,11 @@ def main():
     print(f"[bench] decode done: {r['decode_ms'] * 1e3:.1f} us/decode, "
           f"split {r['split_ms'] * 1e3:.1f} us, parity err {r['parity_max_abs_err']:.3e}",
           file=sys.stderr, flush=True)
+    fp8 = run_decode_fp8(args, dev, wl, sets)
+    print(f"[bench] fp8 decode done: {fp8['decode_fp8_us']} us/decode "
+          f"({fp8['decode_fp8_gbs']} GB/s)", file=sys.stderr, flush=True)
     if args.only == "decode":
-        print(json.dumps(r), flush=True)
+        print(json.dumps({**r, **fp8}), flush=True)
         return
     comp = run_compress(args, dev)
     print(f"[bench] compress done: {comp['compress_step_us']} us", file=sys.stderr, flush=True)
@@ -757,6 +804,8 @@ def main():
         **longctx,
         **qkrope,
         **meta,
+        **fp8,
+        "decode_fp8_speedup": round(r["decode_ms"] * 1e3 / fp8["decode_fp8_us"], 2),
     }
     print(json.dumps(line), flush=True)
 

@@ -61,6 +61,26 @@ int nkv_store_kvcache(const void* key, int64_t key_row_stride,
                       void* stream);
 
 /*
+ * fp8 K/V (OCP E4M3FN: bias 7, largest finite 448, round to nearest even).
+ * An fp8 pool stores code = E4M3FN(clamp(x * (1/scale), -448, 448)) (NaN kept)
+ * with one scale per K or V cache, and reads code * scale.
+ *   nkv_fp8_quantize:   dst[i] = code of src[i] (bf16 in, 1 byte out)
+ *   nkv_fp8_dequantize: dst[i] = bf16(value(src[i]) * scale)
+ *   nkv_store_kvcache_fp8: store_kvcache into fp8 caches (same slot rules as
+ *     nkv_store_kvcache; rows of n_kv_heads*head_dim codes).
+ * n and rows are multiples of 16 elements, pointers 16-byte aligned.
+ * Replaces: the store of an fp8 pool (store_kvcache, nanokvllm/layers/attention.py:10-40;
+ *           pool of ModelRunner.allocate_kv_cache, nanokvllm/engine/model_runner.py:133-152).
+ */
+int nkv_fp8_quantize(const void* src, int64_t n, float scale, void* dst, void* stream);
+int nkv_fp8_dequantize(const void* src, int64_t n, float scale, void* dst, void* stream);
+int nkv_store_kvcache_fp8(const void* key, int64_t key_row_stride, const void* value,
+                          int64_t value_row_stride, void* k_cache, void* v_cache,
+                          const int32_t* slot_mapping, int64_t n_tokens, int32_t n_kv_heads,
+                          int32_t head_dim, int64_t n_slots, float k_scale, float v_scale,
+                          void* stream);
+
+/*
  * Fused q/k RMSNorm + rotary embedding + K/V store, the step between the qkv
  * projection and attention. q, k, v are row-strided bf16 views: element
  * (i, h, d) of q at q[i*q_row_stride + h*head_dim + d], likewise k and v
@@ -127,6 +147,21 @@ int nkv_paged_decode(const void* q, int64_t q_row_stride,
                      int64_t n_blocks, float scale,
                      void* out, int64_t out_row_stride,
                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* Paged decode over fp8 (OCP E4M3FN) caches: same arguments and result as
+ * nkv_paged_decode with K = code * k_scale and V = code * v_scale (codes of
+ * nkv_store_kvcache_fp8); half the cache bytes per decoded token. Same
+ * workspace size. Replaces: the same flash_attn_with_kvcache call
+ * (attention.py:104-107) over an fp8 pool. */
+int nkv_paged_decode_fp8(const void* q, int64_t q_row_stride,
+                         const void* k_cache, const void* v_cache,
+                         const int32_t* block_tables, int64_t bt_row_stride,
+                         const int32_t* context_lens, int32_t batch,
+                         int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                         int32_t block_size, int32_t max_blocks_per_seq,
+                         int64_t n_blocks, float scale, float k_scale, float v_scale,
+                         void* out, int64_t out_row_stride,
+                         void* workspace, size_t workspace_bytes, void* stream);
 
 /* The two stages nkv_paged_decode launches, exported so a caller can time or
  * schedule them separately. Same arguments as nkv_paged_decode.

@@ -30,12 +30,19 @@ SIGNATURES = {
     "nkv_last_error": (C.c_char_p, []),
     "nkv_version": (C.c_char_p, []),
     "nkv_store_kvcache": (C.c_int, [_p, _i64, _p, _i64, _p, _p, _p, _i64, _i32, _i32, _i64, _p]),
+    "nkv_fp8_quantize": (C.c_int, [_p, _i64, _f32, _p, _p]),
+    "nkv_fp8_dequantize": (C.c_int, [_p, _i64, _f32, _p, _p]),
+    "nkv_store_kvcache_fp8": (C.c_int, [_p, _i64, _p, _i64, _p, _p, _p, _i64, _i32, _i32, _i64,
+                                        _f32, _f32, _p]),
     "nkv_qk_norm_rope_store": (C.c_int, [_p, _i64, _p, _i64, _p, _i64, _p, _p, _p, _f32, _p,
                                          _i64, _p, _i64, _p, _p, _p, _p, _i64, _i64, _i32,
                                          _i32, _i32, _p]),
     "nkv_paged_decode_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
     "nkv_paged_decode": (C.c_int, [_p, _i64, _p, _p, _p, _i64, _p, _i32, _i32, _i32, _i32, _i32,
                                    _i32, _i64, _f32, _p, _i64, _p, _sz, _p]),
+    "nkv_paged_decode_fp8": (C.c_int, [_p, _i64, _p, _p, _p, _i64, _p, _i32, _i32, _i32, _i32,
+                                       _i32, _i32, _i64, _f32, _f32, _f32, _p, _i64, _p, _sz,
+                                       _p]),
     "nkv_paged_decode_split": (C.c_int, [_p, _i64, _p, _p, _p, _i64, _p, _i32, _i32, _i32, _i32,
                                          _i32, _i32, _i64, _f32, _p, _sz, _p]),
     "nkv_paged_decode_combine": (C.c_int, [_p, _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64, _p,

@@ -99,4 +99,41 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// ---------------------------------------------------------------- fp8 KV (OCP E4M3FN)
+// gfx950's v_cvt_pk_f32_fp8 / v_cvt_pk_fp8_f32 convert between fp32 and the OCP
+// E4M3FN format (bias 7, largest finite 448, NaN = S.1111.111), round to
+// nearest even. An E4M3FN value has at most 4 significant bits and an
+// exponent in [-9, 8], so it is exact in bf16: the fp32 result's upper half.
+constexpr float kFp8Max = 448.f;
+
+// 16 codes (one 16-byte word) -> 16 bf16 (two 16-byte words), exact.
+__device__ __forceinline__ void fp8x16_to_bf16(u32x4_t in, u32x4_t& lo, u32x4_t& hi) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const auto a = __builtin_amdgcn_cvt_pk_f32_fp8((int)in[w], false);  // bytes 0, 1
+    const auto b = __builtin_amdgcn_cvt_pk_f32_fp8((int)in[w], true);   // bytes 2, 3
+    const uint32_t p0 = __builtin_amdgcn_perm(__float_as_uint(a[1]), __float_as_uint(a[0]),
+                                              0x07060302u);
+    const uint32_t p1 = __builtin_amdgcn_perm(__float_as_uint(b[1]), __float_as_uint(b[0]),
+                                              0x07060302u);
+    if (w < 2) {
+      lo[2 * w] = p0;
+      lo[2 * w + 1] = p1;
+    } else {
+      hi[2 * (w - 2)] = p0;
+      hi[2 * (w - 2) + 1] = p1;
+    }
+  }
+}
+
+// x -> E4M3FN after clamping to +-448 (NaN stays NaN), round to nearest even.
+__device__ __forceinline__ float fp8_clamp(float x) {
+  return __builtin_isnan(x) ? x : fminf(fmaxf(x, -kFp8Max), kFp8Max);
+}
+__device__ __forceinline__ uint32_t f32x4_to_fp8x4(float x0, float x1, float x2, float x3) {
+  int r = __builtin_amdgcn_cvt_pk_fp8_f32(fp8_clamp(x0), fp8_clamp(x1), 0, false);
+  r = __builtin_amdgcn_cvt_pk_fp8_f32(fp8_clamp(x2), fp8_clamp(x3), r, true);
+  return (uint32_t)r;
+}
+
 }  // namespace nkv

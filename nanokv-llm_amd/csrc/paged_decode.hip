@@ -88,15 +88,22 @@ __device__ __forceinline__ void seq_load(SeqCursor& c, const int32_t* __restrict
   c.tot = __builtin_amdgcn_readlane(c.incl, 63);
 }
 
-template <int G>
+// F8: the caches hold fp8 (OCP E4M3FN) codes; a chunk's rows are half as many
+// bytes (two loads per lane per K or V chunk instead of four) and are widened
+// to bf16 (exact) when staged in LDS; the K scale is folded into scale_log2 and
+// the V scale multiplies the partial O.
+template <int G, bool F8>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2)))
 void paged_decode_split_kernel(
     const bf16_t* __restrict__ q, int64_t q_row_stride,
-    const bf16_t* __restrict__ k_cache, const bf16_t* __restrict__ v_cache,
+    const void* __restrict__ k_cache, const void* __restrict__ v_cache,
     const int32_t* __restrict__ block_tables, int64_t bt_row_stride,
     const int32_t* __restrict__ context_lens, int32_t batch, int32_t Hk,
     int32_t block_size, int32_t max_blocks, int64_t n_blocks, int32_t slots, float scale_log2,
-    float* __restrict__ part_o, float* __restrict__ part_ml, int32_t* __restrict__ nslots) {
+    float v_scale, float* __restrict__ part_o, float* __restrict__ part_ml,
+    int32_t* __restrict__ nslots) {
+  constexpr int kEl = F8 ? 1 : 2;    // bytes per cache element
+  constexpr int kLoads = F8 ? 2 : 4; // 16-byte loads per lane per K (or V) chunk
   __shared__ __attribute__((aligned(16))) bf16_t kbuf[kChunk * kVRow];
   __shared__ __attribute__((aligned(16))) bf16_t vbuf[kChunk * kVRow];
 
@@ -104,8 +111,7 @@ void paged_decode_split_kernel(
   const int g4 = lane >> 4;   // key group: keys 4*g4 .. 4*g4+3 of a chunk
   const int col = lane & 15;  // MFMA column: query head (S^T, O^T) / key row (K)
   const int Hq = Hk * G;
-  const int64_t row = (int64_t)Hk * kD;
-  const int row_b = (int)(row * 2);
+  const int row_b = Hk * kD * kEl;  // bytes of one cache row (token)
   const int max_tokens = max_blocks * block_size;
 
   // ---- this wave's KV head and chunk range. Every KV head has the same
@@ -130,10 +136,12 @@ void paged_decode_split_kernel(
   cur.base = 0;
   seq_load(cur, context_lens, batch, max_tokens);
 
-  // per-lane constant load offset: K and V are both read as 4 whole 256-byte
-  // rows per load instruction (lane l: key 4r + l/16, dims 8*(l%16)) and
+  // per-lane constant load offset: K and V are both read as whole head rows,
+  // bf16: 4 rows of 256 B per load (lane l: key 4r + l/16, dims 8*(l%16));
+  // fp8: 8 rows of 128 B per load (lane l: key 8r + l/8, dims 16*(l%8));
   // staged row-major in LDS; K is re-read from there in the MFMA A layout.
-  const int roff = g4 * row_b + col * 16;
+  const int roff = F8 ? (lane >> 3) * row_b + (lane & 7) * 16 : g4 * row_b + col * 16;
+  const int rstep = (F8 ? 8 : 4) * row_b;  // bytes between a lane's consecutive loads
   const int tr_row = 4 * g4 + (col >> 2);  // ds_read_b64_tr_b16 source row / column
   const int tr_col = (col & 3) * 4;
 
@@ -163,8 +171,8 @@ void paged_decode_split_kernel(
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) qreg[ks] = qp[ks * 4];
     }
-    const bf16_t* kbase = k_cache + (int64_t)kvh * kD;
-    const bf16_t* vbase = v_cache + (int64_t)kvh * kD;
+    const char* kbase = static_cast<const char*>(k_cache) + (int64_t)kvh * kD * kEl;
+    const char* vbase = static_cast<const char*>(v_cache) + (int64_t)kvh * kD * kEl;
     const int32_t* bt_row = block_tables + (int64_t)b * bt_row_stride;
 
     f32x4_t acc[8];  // O^T: lane l -> head l%16, dims 16*db + 4*(l/16) .. +3
@@ -187,8 +195,8 @@ void paged_decode_split_kernel(
         }
       }
 
-      u32x4_t kreg[kDepth][4];
-      u32x4_t vreg[kDepth][4];
+      u32x4_t kreg[kDepth][kLoads];
+      u32x4_t vreg[kDepth][kLoads];
       int nv[kDepth];  // valid keys of the chunk in each ring slot (0: masked)
       auto issue = [&](int j, int s) {
         const int t0 = (wlo + j) * kChunk;
@@ -198,27 +206,41 @@ void paged_decode_split_kernel(
         const int64_t r0 = (int64_t)(pb < 0 ? 0 : pb) * block_size + t0 % block_size;
         const uint32_t bytes = (uint32_t)(n * row_b);
         const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-            (void*)(kbase + r0 * row), (short)0, bytes, kBufferFlags);
+            (void*)(kbase + r0 * row_b), (short)0, bytes, kBufferFlags);
         const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-            (void*)(vbase + r0 * row), (short)0, bytes, kBufferFlags);
+            (void*)(vbase + r0 * row_b), (short)0, bytes, kBufferFlags);
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
+        for (int r = 0; r < kLoads; ++r)
           kreg[s][r] = __builtin_bit_cast(
-              u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rk, roff + r * 4 * row_b, 0,
+              u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rk, roff + r * rstep, 0,
                                                              kStreamPolicy));
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
+        for (int r = 0; r < kLoads; ++r)
           vreg[s][r] = __builtin_bit_cast(
-              u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rv, roff + r * 4 * row_b, 0,
+              u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rv, roff + r * rstep, 0,
                                                              kStreamPolicy));
       };
 
       auto consume = [&](int s) {
-        // stage the chunk's K and V rows (row-major) in LDS
+        // stage the chunk's K and V rows (row-major, bf16) in LDS
+        if constexpr (F8) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          *reinterpret_cast<u32x4_t*>(&kbuf[(4 * r + g4) * kVRow + col * 8]) = kreg[s][r];
-          *reinterpret_cast<u32x4_t*>(&vbuf[(4 * r + g4) * kVRow + col * 8]) = vreg[s][r];
+          for (int r = 0; r < kLoads; ++r) {
+            const int e = (8 * r + (lane >> 3)) * kVRow + (lane & 7) * 16;
+            u32x4_t lo, hi;
+            fp8x16_to_bf16(kreg[s][r], lo, hi);
+            *reinterpret_cast<u32x4_t*>(&kbuf[e]) = lo;
+            *reinterpret_cast<u32x4_t*>(&kbuf[e + 8]) = hi;
+            fp8x16_to_bf16(vreg[s][r], lo, hi);
+            *reinterpret_cast<u32x4_t*>(&vbuf[e]) = lo;
+            *reinterpret_cast<u32x4_t*>(&vbuf[e + 8]) = hi;
+          }
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            *reinterpret_cast<u32x4_t*>(&kbuf[(4 * r + g4) * kVRow + col * 8]) = kreg[s][r];
+            *reinterpret_cast<u32x4_t*>(&vbuf[(4 * r + g4) * kVRow + col * 8]) = vreg[s][r];
+          }
         }
         // S^T for 16 keys x 16 heads; A operand: lane l -> key l%16, dims 8*(l/16) + 32*ks
         f32x4_t st = {0.f, 0.f, 0.f, 0.f};
@@ -284,6 +306,10 @@ void paged_decode_split_kernel(
     // ---- segment epilogue: l over the four key groups, then the partial
     l_run += __shfl_xor(l_run, 16, 64);
     l_run += __shfl_xor(l_run, 32, 64);
+    if constexpr (F8) {
+#pragma unroll
+      for (int db = 0; db < 8; ++db) acc[db] *= v_scale;
+    }
     const int64_t obase = ((int64_t)b * Hq + (int64_t)kvh * G) * slots + slot;
     if (col < G) {
       const int64_t prow = obase + (int64_t)col * slots;
@@ -401,7 +427,7 @@ static int decode_check(const void* q, const void* k_cache, const void* v_cache,
 }
 
 // Persistent grid: as many one-wave workgroups as are resident at once.
-template <int G>
+template <int G, bool F8>
 static int decode_grid() {
   static int cached[64] = {0};
   int dev = 0;
@@ -412,7 +438,7 @@ static int decode_grid() {
         n_cu <= 0)
       n_cu = 256;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, reinterpret_cast<const void*>(paged_decode_split_kernel<G>), 64, 0) !=
+            &per_cu, reinterpret_cast<const void*>(paged_decode_split_kernel<G, F8>), 64, 0) !=
             hipSuccess ||
         per_cu <= 0)
       per_cu = 8;
@@ -449,20 +475,20 @@ extern "C" size_t nkv_paged_decode_workspace_bytes(int32_t batch, int32_t n_q_he
          (size_t)batch * n_q_heads * sizeof(int32_t);
 }
 
-extern "C" int nkv_paged_decode_split(const void* q, int64_t q_row_stride, const void* k_cache,
-                                      const void* v_cache, const int32_t* block_tables,
-                                      int64_t bt_row_stride, const int32_t* context_lens,
-                                      int32_t batch, int32_t n_q_heads, int32_t n_kv_heads,
-                                      int32_t head_dim, int32_t block_size,
-                                      int32_t max_blocks_per_seq, int64_t n_blocks, float scale,
-                                      void* workspace, size_t workspace_bytes, void* stream) {
-  using namespace nkv;
-  clear_error();
+namespace nkv {
+template <bool F8>
+static int decode_split(const void* q, int64_t q_row_stride, const void* k_cache,
+                        const void* v_cache, const int32_t* block_tables, int64_t bt_row_stride,
+                        const int32_t* context_lens, int32_t batch, int32_t n_q_heads,
+                        int32_t n_kv_heads, int32_t head_dim, int32_t block_size,
+                        int32_t max_blocks_per_seq, int64_t n_blocks, float scale, float k_scale,
+                        float v_scale, void* workspace, size_t workspace_bytes, void* stream) {
   int rc = decode_check(q, k_cache, v_cache, block_tables, context_lens, batch, n_q_heads,
                         n_kv_heads, head_dim, block_size, max_blocks_per_seq, q_row_stride,
                         bt_row_stride);
   if (rc) return rc;
   if (batch == 0) return NKV_OK;
+  NKV_REQUIRE(k_scale > 0.f && v_scale > 0.f, NKV_EINVAL, "paged_decode: scales must be > 0");
   const size_t need = nkv_paged_decode_workspace_bytes(batch, n_q_heads, head_dim,
                                                        max_blocks_per_seq, block_size);
   NKV_REQUIRE(workspace && workspace_bytes >= need, NKV_EWORKSPACE,
@@ -472,17 +498,17 @@ extern "C" int nkv_paged_decode_split(const void* q, int64_t q_row_stride, const
   NKV_REQUIRE(max_chunks * batch * n_kv_heads < (1ll << 31), NKV_EUNSUPPORTED,
               "paged_decode: too many chunks in one call");
   DecodeWorkspace w = decode_workspace(workspace, batch, n_q_heads, n_kv_heads, slots);
-  const float scale_log2 = scale * kLog2e;
+  const float scale_log2 = scale * k_scale * kLog2e;
   const int g = n_q_heads / n_kv_heads;
   hipStream_t s = as_stream(stream);
 #define NKV_DECODE_LAUNCH(G)                                                                  \
-  hipLaunchKernelGGL((paged_decode_split_kernel<G>),                                          \
-                     dim3((unsigned)std::max(n_kv_heads, decode_grid<G>() / n_kv_heads *      \
+  hipLaunchKernelGGL((paged_decode_split_kernel<G, F8>),                                      \
+                     dim3((unsigned)std::max(n_kv_heads, decode_grid<G, F8>() / n_kv_heads *  \
                                                              n_kv_heads)),                    \
-                     dim3(64), 0, s, (const bf16_t*)q, q_row_stride, (const bf16_t*)k_cache,  \
-                     (const bf16_t*)v_cache, block_tables, bt_row_stride, context_lens, batch, \
-                     n_kv_heads, block_size, max_blocks_per_seq, n_blocks, (int32_t)slots,    \
-                     scale_log2, w.part_o, w.part_ml, w.nslots)
+                     dim3(64), 0, s, (const bf16_t*)q, q_row_stride, k_cache, v_cache,        \
+                     block_tables, bt_row_stride, context_lens, batch, n_kv_heads, block_size, \
+                     max_blocks_per_seq, n_blocks, (int32_t)slots, scale_log2, v_scale,       \
+                     w.part_o, w.part_ml, w.nslots)
   switch (g) {
     case 1: NKV_DECODE_LAUNCH(1); break;
     case 2: NKV_DECODE_LAUNCH(2); break;
@@ -492,6 +518,21 @@ extern "C" int nkv_paged_decode_split(const void* q, int64_t q_row_stride, const
   }
 #undef NKV_DECODE_LAUNCH
   return check_launch("nkv_paged_decode_split");
+}
+}  // namespace nkv
+
+extern "C" int nkv_paged_decode_split(const void* q, int64_t q_row_stride, const void* k_cache,
+                                      const void* v_cache, const int32_t* block_tables,
+                                      int64_t bt_row_stride, const int32_t* context_lens,
+                                      int32_t batch, int32_t n_q_heads, int32_t n_kv_heads,
+                                      int32_t head_dim, int32_t block_size,
+                                      int32_t max_blocks_per_seq, int64_t n_blocks, float scale,
+                                      void* workspace, size_t workspace_bytes, void* stream) {
+  nkv::clear_error();
+  return nkv::decode_split<false>(q, q_row_stride, k_cache, v_cache, block_tables,
+                                  bt_row_stride, context_lens, batch, n_q_heads, n_kv_heads,
+                                  head_dim, block_size, max_blocks_per_seq, n_blocks, scale, 1.f,
+                                  1.f, workspace, workspace_bytes, stream);
 }
 
 extern "C" int nkv_paged_decode_combine(const int32_t* context_lens, int32_t batch,
@@ -536,6 +577,26 @@ extern "C" int nkv_paged_decode(const void* q, int64_t q_row_stride, const void*
                                   context_lens, batch, n_q_heads, n_kv_heads, head_dim,
                                   block_size, max_blocks_per_seq, n_blocks, scale, workspace,
                                   workspace_bytes, stream);
+  if (rc) return rc;
+  return nkv_paged_decode_combine(context_lens, batch, n_q_heads, n_kv_heads, head_dim,
+                                  block_size, max_blocks_per_seq, out, out_row_stride, workspace,
+                                  workspace_bytes, stream);
+}
+
+extern "C" int nkv_paged_decode_fp8(const void* q, int64_t q_row_stride, const void* k_cache,
+                                    const void* v_cache, const int32_t* block_tables,
+                                    int64_t bt_row_stride, const int32_t* context_lens,
+                                    int32_t batch, int32_t n_q_heads, int32_t n_kv_heads,
+                                    int32_t head_dim, int32_t block_size,
+                                    int32_t max_blocks_per_seq, int64_t n_blocks, float scale,
+                                    float k_scale, float v_scale, void* out,
+                                    int64_t out_row_stride, void* workspace,
+                                    size_t workspace_bytes, void* stream) {
+  nkv::clear_error();
+  int rc = nkv::decode_split<true>(q, q_row_stride, k_cache, v_cache, block_tables,
+                                   bt_row_stride, context_lens, batch, n_q_heads, n_kv_heads,
+                                   head_dim, block_size, max_blocks_per_seq, n_blocks, scale,
+                                   k_scale, v_scale, workspace, workspace_bytes, stream);
   if (rc) return rc;
   return nkv_paged_decode_combine(context_lens, batch, n_q_heads, n_kv_heads, head_dim,
                                   block_size, max_blocks_per_seq, out, out_row_stride, workspace,

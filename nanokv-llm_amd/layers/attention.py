@@ -19,11 +19,13 @@ _BF16 = torch.bfloat16
 
 
 def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
-                  v_cache: torch.Tensor, slot_mapping: torch.Tensor) -> None:
+                  v_cache: torch.Tensor, slot_mapping: torch.Tensor, k_scale: float = 1.0,
+                  v_scale: float = 1.0) -> None:
     """k_cache/v_cache row slot_mapping[i] <- key[i]/value[i]; -1 slots skipped.
 
     Same checks as the reference (attention.py:33-40): last dim contiguous,
     head stride == head_dim, cache token stride == Hk*D, one slot per token.
+    An fp8 (float8_e4m3fn) cache stores E4M3FN(clamp(x / scale)).
     """
     N, num_heads, head_dim = key.shape
     D = num_heads * head_dim
@@ -31,9 +33,17 @@ def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
     assert key.stride(1) == head_dim and value.stride(1) == head_dim
     assert k_cache.stride(1) == D and v_cache.stride(1) == D
     assert slot_mapping.numel() == N
-    assert key.dtype == _BF16 and value.dtype == _BF16 and k_cache.dtype == _BF16
     assert slot_mapping.dtype == torch.int32 and slot_mapping.is_contiguous()
     n_slots = k_cache.numel() // D
+    if k_cache.dtype == torch.float8_e4m3fn:
+        assert v_cache.dtype == k_cache.dtype and key.dtype == _BF16 and value.dtype == _BF16
+        rc = _lib.lib().nkv_store_kvcache_fp8(
+            key.data_ptr(), key.stride(0), value.data_ptr(), value.stride(0),
+            k_cache.data_ptr(), v_cache.data_ptr(), slot_mapping.data_ptr(), N, num_heads,
+            head_dim, n_slots, float(k_scale), float(v_scale), _lib.stream_of(key))
+        _lib.check(rc, "store_kvcache_fp8")
+        return
+    assert key.dtype == _BF16 and value.dtype == _BF16 and k_cache.dtype == _BF16
     rc = _lib.lib().nkv_store_kvcache(
         key.data_ptr(), key.stride(0), value.data_ptr(), value.stride(0),
         k_cache.data_ptr(), v_cache.data_ptr(), slot_mapping.data_ptr(), N,
@@ -63,18 +73,30 @@ def paged_decode_workspace(q: torch.Tensor, k_cache: torch.Tensor,
 def paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                  context_lens: torch.Tensor, block_tables: torch.Tensor, scale: float,
                  out: torch.Tensor | None = None,
-                 workspace: torch.Tensor | None = None) -> torch.Tensor:
+                 workspace: torch.Tensor | None = None, k_scale: float = 1.0,
+                 v_scale: float = 1.0) -> torch.Tensor:
     """Paged GQA decode: q [bs, Hq, D] -> out [bs, Hq, D] (bf16).
 
     Same math as flash_attn_with_kvcache(q.unsqueeze(1), k_cache, v_cache,
     cache_seqlens=context_lens, block_table=block_tables, softmax_scale=scale,
-    causal=True) at attention.py:104-107.
+    causal=True) at attention.py:104-107. fp8 (float8_e4m3fn) caches are read
+    as code * k_scale / code * v_scale.
     """
     bs, Hq, D, NB, B, Hk = _decode_args(q, k_cache, block_tables, context_lens)
     if out is None:
         out = torch.empty(bs, Hq, D, dtype=_BF16, device=q.device)
     if workspace is None:
         workspace = paged_decode_workspace(q, k_cache, block_tables)
+    if k_cache.dtype == torch.float8_e4m3fn:
+        assert v_cache.dtype == k_cache.dtype and v_cache.is_contiguous()
+        rc = _lib.lib().nkv_paged_decode_fp8(
+            q.data_ptr(), q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(),
+            block_tables.data_ptr(), block_tables.stride(0), context_lens.data_ptr(), bs, Hq,
+            Hk, D, B, block_tables.size(1), NB, float(scale), float(k_scale), float(v_scale),
+            out.data_ptr(), out.stride(0), workspace.data_ptr(), workspace.numel(),
+            _lib.stream_of(q))
+        _lib.check(rc, "paged_decode_fp8")
+        return out
     rc = _lib.lib().nkv_paged_decode(
         q.data_ptr(), q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(),
         block_tables.data_ptr(), block_tables.stride(0), context_lens.data_ptr(), bs, Hq, Hk, D,
@@ -140,6 +162,7 @@ class Attention(nn.Module):
         self.scale = scale
         self.num_kv_heads = num_kv_heads
         self.k_cache = self.v_cache = torch.tensor([])
+        self.k_scale = self.v_scale = 1.0  # fp8 pools (KVCachePool.bind sets them)
 
         self.kv_compress_enabled = vllm_config.kv_compress_enabled
         if self.kv_compress_enabled:
@@ -167,7 +190,13 @@ class Attention(nn.Module):
         context = get_context()
         k_cache, v_cache = self.k_cache, self.v_cache
         if k_cache.numel() and v_cache.numel() and not kv_stored:
-            store_kvcache(k, v, k_cache, v_cache, context.slot_mapping)
+            store_kvcache(k, v, k_cache, v_cache, context.slot_mapping, self.k_scale,
+                          self.v_scale)
+        fp8 = k_cache.dtype == torch.float8_e4m3fn
+        if fp8 and (not context.use_decode_kernel or context.is_compress_step):
+            raise NotImplementedError(
+                "an fp8 K/V pool supports store and decode only: prefill over the cache and "
+                "the compression step need a bf16 pool")
 
         if (context.use_decode_kernel and self.kv_compress_enabled and context.is_compress_step
                 and (context.compress_selected_batch_indices
@@ -187,5 +216,6 @@ class Attention(nn.Module):
             return varlen_prefill(q, k, v, context.cu_seqlens_q, context.cu_seqlens_k,
                                   context.max_seqlen_q, self.scale)
         o = paged_decode(q, k_cache, v_cache, context.context_lens, context.block_tables,
-                         self.scale, workspace=self._workspace(q, context.block_tables))
+                         self.scale, workspace=self._workspace(q, context.block_tables),
+                         k_scale=self.k_scale, v_scale=self.v_scale)
         return o.unsqueeze(1)
