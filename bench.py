@@ -292,9 +292,29 @@ def run_compress(args, dev):
         key = "compress_step_us" if agg == "group" else "compress_step_all_us"
         res[key] = round(med, 2)
         res[key.replace("_us", "_gbs")] = round(nbytes / (med * 1e-6) / 1e9, 1)
+    # the same step over an fp8 (E4M3FN) copy of the pool (agg "group")
+    kvc = importlib.import_module("nanokv-llm_amd.layers.kv_cache")
+    kq, vq = kvc.fp8_quantize(kg), kvc.fp8_quantize(vg)
+    imp = torch.empty(m, Hk, 1023, dtype=torch.float32, device=dev)
+    keep = torch.empty(m, Hk, 513, dtype=torch.int32, device=dev)
+    times = []
+    for i in range(3 + args.compress_reps):
+        flush.sum()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        cu.compress_step(q, kq, vq, btg, base, ctx, sel, 4, 513, 128 ** -0.5, "group",
+                         importance=imp, keep_idx=keep, workspace=ws)
+        b.record(stream)
+        torch.cuda.synchronize()
+        if i >= 3:
+            times.append(a.elapsed_time(b) * 1000.0)
+    res["compress_step_fp8_us"] = round(statistics.median(times), 2)
+    del kq, vq
     res.update({"compress_bytes": nbytes, "compress_sequences": m,
                 "compress_config": "agg group (importance summed over each GQA group, kept "
-                                   "set per KV head); compress_step_all_*: all-head importance"})
+                                   "set per KV head); compress_step_all_*: all-head importance; "
+                                   "compress_step_fp8_us: agg group over an fp8 pool"})
     return res
 
 
@@ -371,6 +391,36 @@ def _gather_sample_rows(btr, kc, vc):
     return kh, vh, bt2
 
 
+def run_prefill_fp8(args, dev):
+    """Chunked prefill reading an fp8 (E4M3FN) pool: each sequence's rows widened into
+    contiguous bf16, then the contiguous prefill (timed together)."""
+    kvc = importlib.import_module("nanokv-llm_amd.layers.kv_cache")
+    wl = wl_mod.prefill_chunked_qwen3_8b(device=dev)
+    kq, vq = kvc.fp8_quantize(wl["k_cache"]), kvc.fp8_quantize(wl["v_cache"])
+    del wl["k_cache"], wl["v_cache"]
+    q = wl["q"]
+    cq, ck = wl["cu_seqlens_q"].to(dev), wl["cu_seqlens_k"].to(dev)
+    bt = wl["block_tables"].to(dev)
+    out = torch.empty_like(q)
+    stream = torch.cuda.current_stream()
+    t = []
+    for i in range(3 + args.prefill_reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        nkv.varlen_prefill(q, kq, vq, cq, ck, wl["max_seqlen_q"], wl["scale"], block_tables=bt,
+                           out=out, max_seqlen_k=wl["max_seqlen_k"])
+        b.record(stream)
+        torch.cuda.synchronize()
+        if i >= 3:
+            t.append(a.elapsed_time(b))
+    ms = statistics.median(t)
+    flops = prefill_flops(wl["Lq"], wl["Lk"], wl["Hq"])
+    del kq, vq, out
+    torch.cuda.empty_cache()
+    return {"prefill_chunked_fp8_us": round(ms * 1e3, 1),
+            "prefill_chunked_fp8_tflops": round(flops / (ms * 1e-3) / 1e12, 1)}
+
+
 def run_prefill(args, dev):
     res = {}
     for name, fn in (("prefill", wl_mod.prefill_qwen3_8b),
@@ -379,6 +429,7 @@ def run_prefill(args, dev):
         res.update(run_prefill_one(args, dev, name, wl))
         del wl
         torch.cuda.empty_cache()
+    res.update(run_prefill_fp8(args, dev))
     return res
 
 

@@ -74,6 +74,19 @@ int nkv_store_kvcache(const void* key, int64_t key_row_stride,
  */
 int nkv_fp8_quantize(const void* src, int64_t n, float scale, void* dst, void* stream);
 int nkv_fp8_dequantize(const void* src, int64_t n, float scale, void* dst, void* stream);
+/* Rows of each sequence gathered from fp8 caches into contiguous bf16:
+ * k_out[cu_seqlens_k[s] + t] = code(k_cache row of token t of s) * k_scale
+ * (likewise v), t < Lk_s; missing or out-of-range table entries give zero
+ * rows. k_out/v_out are [cu_seqlens_k[n_seqs], Hk, D]; max_seqlen_k sizes
+ * the launch. Feeds nkv_prefill_varlen's contiguous mode over an fp8 pool.
+ * Replaces: the paged K/V read of flash_attn_varlen_func(..., block_table)
+ *           (nanokvllm/layers/attention.py:96-102) for an fp8 pool. */
+int nkv_fp8_gather_rows(const void* k_cache, const void* v_cache,
+                        const int32_t* block_tables, int64_t bt_row_stride,
+                        int32_t max_blocks_per_seq, const int32_t* cu_seqlens_k,
+                        int32_t n_seqs, int32_t max_seqlen_k, int32_t n_kv_heads,
+                        int32_t head_dim, int32_t block_size, int64_t n_blocks,
+                        float k_scale, float v_scale, void* k_out, void* v_out, void* stream);
 int nkv_store_kvcache_fp8(const void* key, int64_t key_row_stride, const void* value,
                           int64_t value_row_stride, void* k_cache, void* v_cache,
                           const int32_t* slot_mapping, int64_t n_tokens, int32_t n_kv_heads,
@@ -369,6 +382,22 @@ int nkv_compress_schedule(const int32_t* context_lens, const int32_t* tail_uncom
                           int32_t topk, int32_t period, int32_t policy, int32_t* step_counter,
                           int32_t* seq_idx, int32_t* n_selected, int32_t* base_context_lens,
                           void* stream);
+
+/* The compression step over fp8 (OCP E4M3FN) caches (nkv_store_kvcache_fp8 codes):
+ * same arguments and effects as nkv_compress_step with K = code * k_scale;
+ * scoring widens K to bf16, compaction moves the 1-byte rows. Needs the
+ * workspace of nkv_compress_workspace_bytes (or more); block_size a power of
+ * two multiple of 256. -1 padded seq_idx accepted.
+ * Replaces: MyCompressCompact (compress_utils.py:100-290) over an fp8 pool. */
+int nkv_compress_step_fp8(const void* q, int64_t q_row_stride, void* k_cache, void* v_cache,
+                          const int32_t* block_tables, int64_t bt_row_stride,
+                          int32_t max_blocks_per_seq, const int32_t* base_context_lens,
+                          int32_t* context_lens, const int32_t* seq_idx, int32_t m,
+                          int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                          int32_t block_size, int32_t window_blocks, int64_t n_blocks,
+                          float scale, float k_scale, int32_t agg_mode, int32_t keep_tokens,
+                          float* importance_out, int32_t* keep_idx, void* workspace,
+                          size_t workspace_bytes, void* stream);
 
 /*
  * Per-step attention metadata built on the device from one packed int32

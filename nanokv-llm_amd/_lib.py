@@ -32,6 +32,8 @@ SIGNATURES = {
     "nkv_store_kvcache": (C.c_int, [_p, _i64, _p, _i64, _p, _p, _p, _i64, _i32, _i32, _i64, _p]),
     "nkv_fp8_quantize": (C.c_int, [_p, _i64, _f32, _p, _p]),
     "nkv_fp8_dequantize": (C.c_int, [_p, _i64, _f32, _p, _p]),
+    "nkv_fp8_gather_rows": (C.c_int, [_p, _p, _p, _i64, _i32, _p, _i32, _i32, _i32, _i32, _i32,
+                                      _i64, _f32, _f32, _p, _p, _p]),
     "nkv_store_kvcache_fp8": (C.c_int, [_p, _i64, _p, _i64, _p, _p, _p, _i64, _i32, _i32, _i64,
                                         _f32, _f32, _p]),
     "nkv_qk_norm_rope_store": (C.c_int, [_p, _i64, _p, _i64, _p, _i64, _p, _p, _p, _f32, _p,
@@ -60,6 +62,9 @@ SIGNATURES = {
     "nkv_compress_step": (C.c_int, [_p, _i64, _p, _p, _p, _i64, _i32, _p, _p, _p, _i32, _i32, _i32,
                                     _i32, _i32, _i32, _i64, _f32, _i32, _i32, _p, _p, _p, _sz,
                                     _p]),
+    "nkv_compress_step_fp8": (C.c_int, [_p, _i64, _p, _p, _p, _i64, _i32, _p, _p, _p, _i32, _i32,
+                                        _i32, _i32, _i32, _i32, _i64, _f32, _f32, _i32, _i32, _p,
+                                        _p, _p, _sz, _p]),
     "nkv_compress_compact": (C.c_int, [_p, _p, _p, _i64, _i32, _p, _p, _p, _i32, _p, _i32, _i32,
                                        _i32, _i32, _i32, _i32, _i64, _p]),
     "nkv_compress_finalize": (C.c_int, [_p, _i64, _i32, _p, _p, _i32, _i32, _i32, _i32, _i32, _p,

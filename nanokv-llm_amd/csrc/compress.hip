@@ -37,9 +37,11 @@ constexpr int kMaxRows = 1024;  // kept tokens + tail rows per compaction unit
 // ------------------------------------------------------------------ score
 // scores[j][h][t] for t < Lw (window tokens); t == 0 and t == Lw-1 are -inf
 // (sink mask; the last window token is not scored).
-template <int G>
+// F8: K is fp8 (OCP E4M3FN) codes, widened to bf16 (exact) on load; the K scale is
+// folded into scale_log2 by the caller.
+template <int G, bool F8>
 __global__ __launch_bounds__(256) void compress_score_kernel(
-    const bf16_t* __restrict__ q, int64_t q_row_stride, const bf16_t* __restrict__ k,
+    const bf16_t* __restrict__ q, int64_t q_row_stride, const void* __restrict__ k,
     const int32_t* __restrict__ block_tables, int64_t bt_row_stride, int32_t max_blocks,
     const int32_t* __restrict__ base_context_lens, const int32_t* __restrict__ seq_idx,
     int32_t Hk, int32_t block_size, int32_t window_blocks, int64_t n_blocks, float scale_log2,
@@ -85,9 +87,20 @@ __global__ __launch_bounds__(256) void compress_score_kernel(
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
     const int tw = wave * 64 + g * 16 + (lane & 15);
-    const bf16_t* kp = k + base + tw * tok_stride + (lane >> 4) * 8;
+    const int64_t e0 = base + tw * tok_stride + (lane >> 4) * 8;  // element offset
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) kreg[g][ks] = *reinterpret_cast<const uint4*>(kp + ks * 32);
+    for (int ks = 0; ks < 4; ++ks) {
+      if constexpr (F8) {
+        const uint2 c = *reinterpret_cast<const uint2*>(static_cast<const uint8_t*>(k) + e0 +
+                                                        ks * 32);
+        u32x4_t lo, hi;
+        fp8x16_to_bf16(u32x4_t{c.x, c.y, 0u, 0u}, lo, hi);
+        kreg[g][ks] = uint4{lo[0], lo[1], lo[2], lo[3]};
+      } else {
+        kreg[g][ks] = *reinterpret_cast<const uint4*>(static_cast<const bf16_t*>(k) + e0 +
+                                                      ks * 32);
+      }
+    }
   }
   __builtin_amdgcn_sched_barrier(0);  // all loads issued before the first MFMA
   uint4 qreg[4];
@@ -666,9 +679,11 @@ __global__ __launch_bounds__(kSelThreads) void compress_sum_kernel(
 // Unit = (selected j, KV head, K|V, half row). Rows i < keep_tokens move from
 // window position keep_idx[i] to window position i; rows keep_tokens + u
 // (u < tail) move from the tail block offset u to slot(window pos keep-1)+1+u.
-template <int ROUNDS>
+// F8: 1-byte (fp8) cache rows: half a head row is 64 bytes, moved by 4 lanes, so a
+// round covers 64 rows instead of 32.
+template <int ROUNDS, bool F8>
 __global__ __launch_bounds__(256) void compress_compact_kernel(
-    bf16_t* __restrict__ k_cache, bf16_t* __restrict__ v_cache,
+    void* __restrict__ k_cache, void* __restrict__ v_cache,
     const int32_t* __restrict__ block_tables, int64_t bt_row_stride, int32_t max_blocks,
     const int32_t* __restrict__ base_context_lens, int32_t* __restrict__ context_lens,
     const int32_t* __restrict__ seq_idx, const int32_t* __restrict__ keep_idx, int32_t n_sets,
@@ -710,7 +725,11 @@ __global__ __launch_bounds__(256) void compress_compact_kernel(
   const int32_t last_dst = last_pb >= 0 ? last_pb * B + ((keep_tokens - 1) & (B - 1)) : -1;
   const int nrows = keep_tokens + tail;
   const int64_t n_slots = n_blocks * B;
-  for (int i = threadIdx.x; i < ROUNDS * 32; i += blockDim.x) {
+  constexpr int kEl = F8 ? 1 : 2;
+  constexpr int kLanesPerRow = 4 * kEl;             // 16-byte lanes per half head row
+  constexpr int kRowsPerRound = 256 / kLanesPerRow;  // 32 (bf16) or 64 (fp8)
+  static_assert(ROUNDS * kRowsPerRound <= kMaxRows, "compaction table too small");
+  for (int i = threadIdx.x; i < ROUNDS * kRowsPerRound; i += blockDim.x) {
     int32_t sv = -1, d = -1;
     if (i < keep_tokens) {
       const int p = kidx[i];
@@ -733,14 +752,14 @@ __global__ __launch_bounds__(256) void compress_compact_kernel(
 
   // phase 2: every source row of the unit, as unconditional 128-bit loads
   // (rows that are not moved re-read slot 0, always valid)
-  bf16_t* cache = is_v ? v_cache : k_cache;
-  const int64_t row = (int64_t)Hk * kCD;
-  const int64_t col = (int64_t)kvh * kCD + half * 64 + (threadIdx.x & 7) * 8;
-  const int rsub = threadIdx.x >> 3;  // 0..31: row within a round
+  char* cache = static_cast<char*>(is_v ? v_cache : k_cache);
+  const int64_t row = (int64_t)Hk * kCD * kEl;  // bytes
+  const int64_t col = ((int64_t)kvh * kCD + half * 64) * kEl + (threadIdx.x % kLanesPerRow) * 16;
+  const int rsub = threadIdx.x / kLanesPerRow;  // row within a round
   u32x4_t reg[ROUNDS];
 #pragma unroll
   for (int rr = 0; rr < ROUNDS; ++rr) {
-    const int32_t sv = max(src_lds[rr * 32 + rsub], 0);
+    const int32_t sv = max(src_lds[rr * kRowsPerRound + rsub], 0);
     reg[rr] = *reinterpret_cast<const u32x4_t*>(cache + (int64_t)sv * row + col);
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -750,7 +769,7 @@ __global__ __launch_bounds__(256) void compress_compact_kernel(
   // phase 3: writes
 #pragma unroll
   for (int rr = 0; rr < ROUNDS; ++rr) {
-    const int32_t d = dst_lds[rr * 32 + rsub];
+    const int32_t d = dst_lds[rr * kRowsPerRound + rsub];
     if (d >= 0) *reinterpret_cast<u32x4_t*>(cache + (int64_t)d * row + col) = reg[rr];
   }
 
@@ -926,8 +945,8 @@ extern "C" int nkv_compress_score(const void* q, int64_t q_row_stride, const voi
   const unsigned grid = (unsigned)(m * n_kv_heads * (Lw / kChunk));
   const float sl2 = scale * kLog2e;
 #define NKV_SCORE_LAUNCH(G)                                                                    \
-  hipLaunchKernelGGL(compress_score_kernel<G>, dim3(grid), dim3(256), 0, s, (const bf16_t*)q,   \
-                     q_row_stride, (const bf16_t*)k_cache, block_tables, bt_row_stride,         \
+  hipLaunchKernelGGL((compress_score_kernel<G, false>), dim3(grid), dim3(256), 0, s,             \
+                     (const bf16_t*)q, q_row_stride, k_cache, block_tables, bt_row_stride,      \
                      max_blocks_per_seq, base_context_lens, seq_idx, n_kv_heads, block_size, window_blocks,         \
                      n_blocks, sl2, scores)
   switch (g) {
@@ -1125,8 +1144,8 @@ extern "C" int nkv_compress_compact(void* k_cache, void* v_cache, const int32_t*
   hipStream_t s = as_stream(stream);
   const unsigned grid = (unsigned)(m * n_kv_heads * 4);
 #define NKV_COMPACT_LAUNCH(R)                                                                  \
-  hipLaunchKernelGGL(compress_compact_kernel<R>, dim3(grid), dim3(256), 0, s, (bf16_t*)k_cache, \
-                     (bf16_t*)v_cache, block_tables, bt_row_stride, max_blocks_per_seq,         \
+  hipLaunchKernelGGL((compress_compact_kernel<R, false>), dim3(grid), dim3(256), 0, s, k_cache, \
+                     v_cache, block_tables, bt_row_stride, max_blocks_per_seq,                  \
                      base_context_lens,                                                         \
                      context_lens, seq_idx, keep_idx, n_sets, keep_tokens, n_kv_heads,          \
                      block_size, window_blocks, n_blocks)
@@ -1234,4 +1253,98 @@ extern "C" int nkv_compress_schedule(const int32_t* context_lens,
                      context_lens, tail_uncompressed, batch, block_size, window_blocks, topk,
                      period, policy, step_counter, seq_idx, n_selected, base_context_lens);
   return check_launch("nkv_compress_schedule");
+}
+
+// Compression step over fp8 (OCP E4M3FN) caches: K codes are widened to bf16 for
+// scoring (k_scale folded into the score scale), then importance, top-k, and the
+// compaction of the 1-byte rows; same results contract as nkv_compress_step's
+// general path.
+extern "C" int nkv_compress_step_fp8(const void* q, int64_t q_row_stride, void* k_cache,
+                                     void* v_cache, const int32_t* block_tables,
+                                     int64_t bt_row_stride, int32_t max_blocks_per_seq,
+                                     const int32_t* base_context_lens, int32_t* context_lens,
+                                     const int32_t* seq_idx, int32_t m, int32_t n_q_heads,
+                                     int32_t n_kv_heads, int32_t head_dim, int32_t block_size,
+                                     int32_t window_blocks, int64_t n_blocks, float scale,
+                                     float k_scale, int32_t agg_mode, int32_t keep_tokens,
+                                     float* importance_out, int32_t* keep_idx, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  using namespace nkv;
+  clear_error();
+  NKV_REQUIRE(m >= 0 && n_q_heads > 0 && n_kv_heads > 0 && window_blocks > 0 &&
+                  block_size > 0 && k_scale > 0.f,
+              NKV_EINVAL, "compress_step_fp8: bad sizes");
+  if (m == 0) return NKV_OK;
+  NKV_REQUIRE(head_dim == kCD, NKV_EUNSUPPORTED, "compress_step_fp8: head_dim must be 128");
+  NKV_REQUIRE(n_q_heads % n_kv_heads == 0, NKV_EINVAL, "compress_step_fp8: Hq %% Hk != 0");
+  const int g = n_q_heads / n_kv_heads;
+  NKV_REQUIRE(g == 1 || g == 2 || g == 4 || g == 8 || g == 16, NKV_EUNSUPPORTED,
+              "compress_step_fp8: GQA group %d not in {1,2,4,8,16}", g);
+  NKV_REQUIRE(block_size % kChunk == 0 && (block_size & (block_size - 1)) == 0,
+              NKV_EUNSUPPORTED, "compress_step_fp8: block_size must be a power-of-two "
+              "multiple of 256");
+  NKV_REQUIRE(agg_mode == NKV_AGG_ALL || agg_mode == NKV_AGG_GROUP, NKV_EINVAL,
+              "compress_step_fp8: bad agg_mode %d", agg_mode);
+  NKV_REQUIRE(q && k_cache && v_cache && block_tables && base_context_lens && context_lens &&
+                  seq_idx && importance_out && keep_idx,
+              NKV_EINVAL, "compress_step_fp8: null pointer");
+  NKV_REQUIRE(aligned16(q) && aligned16(k_cache) && aligned16(v_cache) && q_row_stride % 8 == 0,
+              NKV_EINVAL, "compress_step_fp8: q/k/v must be 16-byte aligned");
+  NKV_REQUIRE(max_blocks_per_seq > 0 && bt_row_stride >= max_blocks_per_seq, NKV_EINVAL,
+              "compress_step_fp8: bad block table width/stride");
+  NKV_REQUIRE(window_blocks <= kMaxWindowBlocks, NKV_EUNSUPPORTED,
+              "compress_step_fp8: window_blocks > %d", kMaxWindowBlocks);
+  NKV_REQUIRE(n_blocks * block_size < (1ll << 31), NKV_EUNSUPPORTED,
+              "compress_step_fp8: pool exceeds 2^31 slots");
+  const int Lw = window_blocks * block_size;
+  const int num_keep = keep_tokens - 2;
+  NKV_REQUIRE(num_keep > 0 && num_keep < Lw - 1 && Lw - 1 <= 4096, NKV_EINVAL,
+              "compress_step_fp8: need 0 < keep_tokens - 2 < W*B - 1 <= 4096");
+  const int max_rows = keep_tokens + block_size - 1;
+  NKV_REQUIRE(max_rows <= kMaxRows, NKV_EUNSUPPORTED,
+              "compress_step_fp8: keep_tokens + block_size - 1 = %d exceeds %d", max_rows,
+              kMaxRows);
+  const size_t need = nkv_compress_workspace_bytes(m, n_q_heads, window_blocks, block_size);
+  NKV_REQUIRE(workspace && workspace_bytes >= need, NKV_EWORKSPACE,
+              "compress_step_fp8: workspace needs %zu bytes (got %zu)", need, workspace_bytes);
+  float* scores = (float*)workspace;
+  hipStream_t s = as_stream(stream);
+  const unsigned sgrid = (unsigned)(m * n_kv_heads * (Lw / kChunk));
+  const float sl2 = scale * k_scale * kLog2e;
+#define NKV_SCORE8_LAUNCH(G)                                                                   \
+  hipLaunchKernelGGL((compress_score_kernel<G, true>), dim3(sgrid), dim3(256), 0, s,            \
+                     (const bf16_t*)q, q_row_stride, k_cache, block_tables, bt_row_stride,      \
+                     max_blocks_per_seq, base_context_lens, seq_idx, n_kv_heads, block_size,    \
+                     window_blocks, n_blocks, sl2, scores)
+  switch (g) {
+    case 1: NKV_SCORE8_LAUNCH(1); break;
+    case 2: NKV_SCORE8_LAUNCH(2); break;
+    case 4: NKV_SCORE8_LAUNCH(4); break;
+    case 8: NKV_SCORE8_LAUNCH(8); break;
+    default: NKV_SCORE8_LAUNCH(16); break;
+  }
+#undef NKV_SCORE8_LAUNCH
+  int rc = check_launch("nkv_compress_step_fp8 (score)");
+  if (rc) return rc;
+  const int n_sets = agg_mode == NKV_AGG_ALL ? 1 : n_kv_heads;
+  const int hps = n_q_heads / n_sets;
+  hipLaunchKernelGGL(compress_importance_kernel, dim3((unsigned)(m * n_sets)), dim3(256),
+                     (size_t)hps * 2 * sizeof(float), s, scores, n_q_heads, n_sets, Lw,
+                     importance_out);
+  rc = check_launch("nkv_compress_step_fp8 (importance)");
+  if (rc) return rc;
+  rc = nkv_compress_topk(importance_out, m * n_sets, Lw - 1, num_keep, keep_idx, stream);
+  if (rc) return rc;
+  const unsigned cgrid = (unsigned)(m * n_kv_heads * 4);
+#define NKV_COMPACT8_LAUNCH(R)                                                                 \
+  hipLaunchKernelGGL((compress_compact_kernel<R, true>), dim3(cgrid), dim3(256), 0, s, k_cache, \
+                     v_cache, block_tables, bt_row_stride, max_blocks_per_seq,                  \
+                     base_context_lens, context_lens, seq_idx, keep_idx, n_sets, keep_tokens,   \
+                     n_kv_heads, block_size, window_blocks, n_blocks)
+  if (max_rows <= 256) NKV_COMPACT8_LAUNCH(4);
+  else if (max_rows <= 512) NKV_COMPACT8_LAUNCH(8);
+  else if (max_rows <= 768) NKV_COMPACT8_LAUNCH(12);
+  else NKV_COMPACT8_LAUNCH(16);
+#undef NKV_COMPACT8_LAUNCH
+  return check_launch("nkv_compress_step_fp8 (compact)");
 }

@@ -109,7 +109,8 @@ def paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
 def varlen_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                    cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor, max_seqlen_q: int,
                    scale: float, block_tables: torch.Tensor | None = None,
-                   out: torch.Tensor | None = None) -> torch.Tensor:
+                   out: torch.Tensor | None = None, max_seqlen_k: int | None = None,
+                   k_scale: float = 1.0, v_scale: float = 1.0) -> torch.Tensor:
     """Varlen causal (bottom-right) attention: q [sum Lq, Hq, D] -> [sum Lq, Hq, D].
 
     With ``block_tables`` k/v are the paged caches [NB, B, Hk, D]; without,
@@ -121,6 +122,23 @@ def varlen_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     assert q.stride(-1) == 1 and q.stride(1) == D
     assert cu_seqlens_q.dtype == torch.int32 and cu_seqlens_k.dtype == torch.int32
     n_seqs = cu_seqlens_q.numel() - 1
+    if block_tables is not None and k.dtype == torch.float8_e4m3fn:
+        # fp8 pool: each sequence's rows widened into contiguous bf16, then the contiguous path
+        if max_seqlen_k is None:
+            raise ValueError("prefill over an fp8 pool needs max_seqlen_k")
+        NB, B, Hk, Dk = k.shape
+        rows = max(n_seqs * int(max_seqlen_k), 1)
+        kw = torch.empty(rows, Hk, Dk, dtype=_BF16, device=q.device)
+        vw = torch.empty_like(kw)
+        assert block_tables.dtype == torch.int32 and block_tables.stride(1) == 1
+        rc = _lib.lib().nkv_fp8_gather_rows(
+            k.data_ptr(), v.data_ptr(), block_tables.data_ptr(), block_tables.stride(0),
+            block_tables.size(1), cu_seqlens_k.data_ptr(), n_seqs, int(max_seqlen_k), Hk, Dk,
+            B, NB, float(k_scale), float(v_scale), kw.data_ptr(), vw.data_ptr(),
+            _lib.stream_of(q))
+        _lib.check(rc, "fp8_gather_rows")
+        return varlen_prefill(q, kw, vw, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, scale,
+                              out=out)
     if block_tables is not None:
         NB, B, Hk, Dk = k.shape
         assert k.is_contiguous() and v.is_contiguous() and v.shape == k.shape
@@ -192,11 +210,6 @@ class Attention(nn.Module):
         if k_cache.numel() and v_cache.numel() and not kv_stored:
             store_kvcache(k, v, k_cache, v_cache, context.slot_mapping, self.k_scale,
                           self.v_scale)
-        fp8 = k_cache.dtype == torch.float8_e4m3fn
-        if fp8 and (not context.use_decode_kernel or context.is_compress_step):
-            raise NotImplementedError(
-                "an fp8 K/V pool supports store and decode only: prefill over the cache and "
-                "the compression step need a bf16 pool")
 
         if (context.use_decode_kernel and self.kv_compress_enabled and context.is_compress_step
                 and (context.compress_selected_batch_indices
@@ -206,13 +219,16 @@ class Attention(nn.Module):
                 block_size=k_cache.size(1), window_blocks=self.kv_compress_window_blocks,
                 keep_blocks=self.kv_compress_keep_blocks,
                 keep_extra_tokens=self.kv_compress_keep_extra_tokens,
-                num_layers=self.num_layers, context=context, agg=self.kv_compress_agg)
+                num_layers=self.num_layers, context=context, agg=self.kv_compress_agg,
+                k_scale=self.k_scale)
 
         if not context.use_decode_kernel:
             if context.block_tables is not None:  # K/V read back from the paged cache
                 return varlen_prefill(q, k_cache, v_cache, context.cu_seqlens_q,
                                       context.cu_seqlens_k, context.max_seqlen_q, self.scale,
-                                      block_tables=context.block_tables)
+                                      block_tables=context.block_tables,
+                                      max_seqlen_k=context.max_seqlen_k, k_scale=self.k_scale,
+                                      v_scale=self.v_scale)
             return varlen_prefill(q, k, v, context.cu_seqlens_q, context.cu_seqlens_k,
                                   context.max_seqlen_q, self.scale)
         o = paged_decode(q, k_cache, v_cache, context.context_lens, context.block_tables,

@@ -108,7 +108,7 @@ def compress_compact(k_cache, v_cache, block_tables, base_context_lens, context_
 
 def compress_step(q, k_cache, v_cache, block_tables, base_context_lens, context_lens, seq_idx,
                   window_blocks, keep_tokens, scale, agg="all", importance=None, keep_idx=None,
-                  workspace=None):
+                  workspace=None, k_scale=1.0):
     """compress_select + compress_compact in one call (fused on the GPU).
 
     Returns (keep_idx, importance) like compress_select; the caches and
@@ -126,6 +126,16 @@ def compress_step(q, k_cache, v_cache, block_tables, base_context_lens, context_
     ws_bytes = select_workspace_bytes(m, Hq, Hk, window_blocks, B)
     if workspace is None:
         workspace = torch.empty(max(ws_bytes, 4), dtype=torch.uint8, device=q.device)
+    if k_cache.dtype == torch.float8_e4m3fn:  # fp8 pool (K read as code * k_scale)
+        rc = _lib.lib().nkv_compress_step_fp8(
+            q.data_ptr(), q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(),
+            block_tables.data_ptr(), block_tables.stride(0), block_tables.size(1),
+            base_context_lens.data_ptr(), context_lens.data_ptr(), seq_idx.data_ptr(), m, Hq, Hk,
+            D, B, window_blocks, NB, float(scale), float(k_scale), AGG_MODES[agg], keep_tokens,
+            importance.data_ptr(), keep_idx.data_ptr(), workspace.data_ptr(), workspace.numel(),
+            _lib.stream_of(q))
+        _lib.check(rc, "compress_step_fp8")
+        return keep_idx, importance
     rc = _lib.lib().nkv_compress_step(
         q.data_ptr(), q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(), block_tables.data_ptr(),
         block_tables.stride(0), block_tables.size(1), base_context_lens.data_ptr(),
@@ -165,7 +175,7 @@ def events_to_dicts(events: torch.Tensor, layer_id: int) -> list[dict]:
 def MyCompressCompact(q_current: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                       layer_id: int, block_size: int, window_blocks: int, keep_blocks: int,
                       keep_extra_tokens: int, num_layers: int, context=None, agg: str = "all",
-                      rewrite_tables: bool = True) -> bool:
+                      rewrite_tables: bool = True, k_scale: float = 1.0) -> bool:
     """Compress the last ``window_blocks`` full blocks of each selected sequence.
 
     agg="all" sums key importance over every query head (the reference,
@@ -209,7 +219,8 @@ def MyCompressCompact(q_current: torch.Tensor, k_cache: torch.Tensor, v_cache: t
                    ws_bytes, 4 + context.block_tables.size(1))
     compress_step(q_current, k_cache, v_cache, context.block_tables, base, context.context_lens,
                   buf.seq_idx, window_blocks, keep_tokens, D ** -0.5, agg,
-                  importance=buf.importance, keep_idx=buf.keep_idx, workspace=buf.workspace)
+                  importance=buf.importance, keep_idx=buf.keep_idx, workspace=buf.workspace,
+                  k_scale=k_scale)
     if layer_id + 1 >= num_layers:
         compress_finalize(context.block_tables, base, buf.seq_idx, keep_tokens, B, window_blocks,
                           buf.events, rewrite_tables=rewrite_tables,

@@ -9,6 +9,7 @@ from oracle import fp8_ref
 
 pytestmark = pytest.mark.gpu
 kvc = importlib.import_module("nanokv-llm_amd.layers.kv_cache")
+cu = importlib.import_module("nanokv-llm_amd.layers.compress_utils")
 
 
 def test_dequantize_every_code(nkv, dev):
@@ -92,7 +93,7 @@ def test_decode_fp8_vs_oracle(nkv, dev, k_scale, v_scale):
 
 def test_attention_with_fp8_pool(nkv, dev):
     """KVCachePool(fp8) bound to two layers: store + decode through Attention.forward vs the
-    oracle on the dequantized cache; prefill over an fp8 pool raises."""
+    oracle on the dequantized cache."""
     from types import SimpleNamespace
 
     from oracle.attention_ref import paged_decode_ref
@@ -119,12 +120,26 @@ def test_attention_with_fp8_pool(nkv, dev):
     ref = paged_decode_ref(wl["q"].float(), kq.view(torch.float8_e4m3fn).float() * 0.25,
                            vq.view(torch.float8_e4m3fn).float() * 0.5, ctx, bt, wl["scale"])
     assert (o.squeeze(1).float().cpu() - ref).abs().max().item() <= 2e-2
-    cu = torch.tensor([0, 1], dtype=torch.int32, device=dev)
-    nkv.set_context(False, cu_seqlens_q=cu, cu_seqlens_k=cu, max_seqlen_q=1, max_seqlen_k=1,
-                    slot_mapping=slots[:1].to(dev), block_tables=bt[:1].to(dev))
-    with pytest.raises(NotImplementedError):
-        layers[1](wl["q"][:1].to(dev), wl["key"][:1].to(dev), wl["value"][:1].to(dev), 1)
-    nkv.reset_context()
+
+
+def test_prefill_over_fp8_pool(nkv, dev):
+    """Chunked prefill reading a paged fp8 cache (gathered and widened on the GPU) vs the
+    oracle on the fp32-dequantized cache."""
+    from oracle.attention_ref import varlen_prefill_ref
+    wl = wl_mod.prefill_workload(3, 32, 8, 0, 0, seed=12, prefix_lo=0, prefix_hi=900, chunk=200)
+    kq = fp8_ref.fp8_quantize_ref(wl["k_cache"], 0.5)
+    vq = fp8_ref.fp8_quantize_ref(wl["v_cache"], 2.0)
+    fp8_ref.store_kvcache_fp8_ref(wl["key"], wl["value"], kq, vq, wl["slot_mapping"], 0.5, 2.0)
+    out = nkv.varlen_prefill(wl["q"].to(dev), kq.to(dev).view(torch.float8_e4m3fn),
+                             vq.to(dev).view(torch.float8_e4m3fn), wl["cu_seqlens_q"].to(dev),
+                             wl["cu_seqlens_k"].to(dev), wl["max_seqlen_q"], wl["scale"],
+                             block_tables=wl["block_tables"].to(dev),
+                             max_seqlen_k=wl["max_seqlen_k"], k_scale=0.5, v_scale=2.0)
+    kf = kq.view(torch.float8_e4m3fn).float() * 0.5
+    vf = vq.view(torch.float8_e4m3fn).float() * 2.0
+    ref = varlen_prefill_ref(wl["q"].float(), kf, vf, wl["cu_seqlens_q"], wl["cu_seqlens_k"],
+                             wl["scale"], block_tables=wl["block_tables"])
+    assert (out.float().cpu() - ref).abs().max().item() <= 2e-2
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float8_e4m3fn])
@@ -146,3 +161,44 @@ def test_pool_sizing_follows_the_reference_formula(nkv, dev, dtype):
     assert pool.kv_cache.shape == (2, L, pool.num_blocks, B, Hk, D)
     del pool
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("agg", ["all", "group"])
+def test_compress_step_over_fp8_pool(nkv, dev, agg):
+    """Compression on an fp8 pool: importance within rtol 1e-4 of the oracle's fp32 SnapKV on
+    the fp32-dequantized window, kept sets bit-exact given those scores, and the 1-byte rows
+    compacted bit-exactly; -1 padding in seq_idx skipped."""
+    from oracle.compress_ref import (compress_compact_ref, gather_kv_by_slots_ref,
+                                     get_tail_window_and_tail_slots_ref, select_topk_ref,
+                                     snapkv_importance_ref)
+    W, KEEP, ks = 4, 2 * 256 + 1, 0.5
+    wl = wl_mod.compress_workload(32, 32, 8, 1500, 4096, 6, 4, selected_only=True)
+    kq = fp8_ref.fp8_quantize_ref(wl["k_cache"], ks)
+    vq = fp8_ref.fp8_quantize_ref(wl["v_cache"], 2.0)
+    kg = kq.to(dev).view(torch.float8_e4m3fn)
+    vg = vq.to(dev).view(torch.float8_e4m3fn)
+    sel = wl["seq_idx"]
+    seq_idx = torch.tensor(sel[:3] + [-1] + sel[3:], dtype=torch.int32, device=dev)
+    base = wl["context_lens"].to(dev)
+    ctx = base.clone()
+    keep, imp = cu.compress_step(wl["q"].to(dev), kg, vg, wl["block_tables"].to(dev), base, ctx,
+                                 seq_idx, W, KEEP, 128 ** -0.5, agg, k_scale=ks)
+    torch.cuda.synchronize()
+    real = [i for i in range(seq_idx.numel()) if i != 3]
+    imp, keep = imp.cpu()[real], keep.cpu()[real]
+    # importance against the oracle on the fp32-dequantized K
+    st = torch.tensor(sel)
+    slots, *_ = get_tail_window_and_tail_slots_ref(wl["block_tables"], wl["context_lens"], st,
+                                                   256, W)
+    kf = kq.view(torch.float8_e4m3fn).float() * ks
+    k_sub, _ = gather_kv_by_slots_ref(kf, kf, slots)
+    ref_imp = snapkv_importance_ref(wl["q"].index_select(0, st).unsqueeze(2), k_sub, 1, "fp32",
+                                    agg)
+    assert torch.allclose(imp, ref_imp, rtol=1e-4, atol=1e-7)
+    assert torch.equal(keep[..., 1:-1].long(), select_topk_ref(imp, KEEP - 2))
+    # compaction of the codes, given the GPU's kept positions
+    kc, vc, ctx_ref = kq.clone(), vq.clone(), wl["context_lens"].clone()
+    compress_compact_ref(None, kc, vc, wl["block_tables"], wl["context_lens"], ctx_ref, sel, 256,
+                         W, 2, 1, 0, 2, keep_idx=keep.long())
+    assert torch.equal(kg.view(torch.uint8).cpu(), kc) and torch.equal(vg.view(torch.uint8).cpu(), vc)
+    assert torch.equal(ctx.cpu(), ctx_ref)
