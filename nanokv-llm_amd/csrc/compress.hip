@@ -83,22 +83,25 @@ __global__ __launch_bounds__(256) void compress_score_kernel(
       srow[(int64_t)(i / kChunk) * Lw + i % kChunk] = -INFINITY;
     return;
   }
-  uint4 kreg[4][4];
+  // K rows are read whole (bf16: one 256-byte head row per 16 lanes, 4 rows per load;
+  // fp8: one 128-byte row per 8 lanes, 8 rows per load), staged row-major in LDS as bf16
+  // and re-read in the MFMA operand layout (lane l: key l%16, dims 8*(l/16) + 32ks).
+  __shared__ __attribute__((aligned(16))) bf16_t stage_all[4][16 * (kCD + 8)];
+  bf16_t* stage = stage_all[wave];
+  constexpr int kSR = kCD + 8;
+  u32x4_t kraw[4][F8 ? 2 : 4];
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
-    const int tw = wave * 64 + g * 16 + (lane & 15);
-    const int64_t e0 = base + tw * tok_stride + (lane >> 4) * 8;  // element offset
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
+    for (int r = 0; r < (F8 ? 2 : 4); ++r) {
       if constexpr (F8) {
-        const uint2 c = *reinterpret_cast<const uint2*>(static_cast<const uint8_t*>(k) + e0 +
-                                                        ks * 32);
-        u32x4_t lo, hi;
-        fp8x16_to_bf16(u32x4_t{c.x, c.y, 0u, 0u}, lo, hi);
-        kreg[g][ks] = uint4{lo[0], lo[1], lo[2], lo[3]};
+        const int key = wave * 64 + g * 16 + 8 * r + (lane >> 3);
+        kraw[g][r] = *reinterpret_cast<const u32x4_t*>(static_cast<const uint8_t*>(k) + base +
+                                                      key * tok_stride + (lane & 7) * 16);
       } else {
-        kreg[g][ks] = *reinterpret_cast<const uint4*>(static_cast<const bf16_t*>(k) + e0 +
-                                                      ks * 32);
+        const int key = wave * 64 + g * 16 + 4 * r + (lane >> 4);
+        kraw[g][r] = *reinterpret_cast<const u32x4_t*>(static_cast<const bf16_t*>(k) + base +
+                                                      key * tok_stride + (lane & 15) * 8);
       }
     }
   }
@@ -113,11 +116,29 @@ __global__ __launch_bounds__(256) void compress_score_kernel(
   }
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
+    if constexpr (F8) {
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        u32x4_t lo, hi;
+        fp8x16_to_bf16(kraw[g][r], lo, hi);
+        bf16_t* d = &stage[(8 * r + (lane >> 3)) * kSR + (lane & 7) * 16];
+        *reinterpret_cast<u32x4_t*>(d) = lo;
+        *reinterpret_cast<u32x4_t*>(d + 8) = hi;
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        *reinterpret_cast<u32x4_t*>(&stage[(4 * r + (lane >> 4)) * kSR + (lane & 15) * 8]) =
+            kraw[g][r];
+    }
     f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(qreg[ks]), as_bf16x8(kreg[g][ks]),
-                                                     acc, 0, 0, 0);
+    for (int ks = 0; ks < 4; ++ks) {
+      const uint4 kb = *reinterpret_cast<const uint4*>(
+          &stage[(lane & 15) * kSR + (lane >> 4) * 8 + ks * 32]);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(qreg[ks]), as_bf16x8(kb), acc, 0,
+                                                     0, 0);
+    }
     const int tw = wave * 64 + g * 16 + (lane & 15);
     const int t = t0 + tw;
 #pragma unroll
@@ -274,7 +295,11 @@ constexpr int kSelMaxWindow = kSelWaves * kSelKeysPerWave;  // 1024
 constexpr int kStepRounds = 12;                             // 64 rows per round
 constexpr int kStepMaxRows = 64 * kStepRounds;              // kept + tail rows
 
+constexpr int kStageRow = kCD + 8;  // LDS row stride (elements) of a staged 16-key group
+
 struct SelectLds {
+  // per wave: one 16-key group of K rows, row-major (bf16), re-read as MFMA operands
+  __attribute__((aligned(16))) bf16_t kstage[kSelWaves][16 * kStageRow];
   float red[kSelWaves][16];
   __attribute__((aligned(16))) float imp[kSelMaxWindow];
   __attribute__((aligned(16))) int cnt[2][16][kSelWaves];  // [pass parity][digit][wave]
@@ -413,25 +438,38 @@ __device__ __forceinline__ void group_importance(
   }
   f32x4_t acc[4] = {};
   if (valid) {  // wave-uniform
+    // K rows are read whole: load r of group g brings keys 16g + 4r .. +3, one 256-byte
+    // head row per 16 lanes (lane l: key 16g + 4r + l/16, dims 8*(l%16)), so every load
+    // instruction is 4 row-sized requests; each group is staged row-major in LDS and
+    // re-read in the MFMA operand layout (lane l: key l%16, dims 8*(l/16) + 32ks).
     u32x4_t kreg[4][4];
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      const bf16_t* kp = k + base + (g * 16 + col) * tok_stride + hg * 8;
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) kreg[g][ks] = *reinterpret_cast<const u32x4_t*>(kp + ks * 32);
+      for (int r = 0; r < 4; ++r) {
+        const bf16_t* kp = k + base + (g * 16 + 4 * r + hg) * tok_stride + col * 8;
+        kreg[g][r] = *reinterpret_cast<const u32x4_t*>(kp);
+      }
     }
     u32x4_t qreg[4];
     const int hc = col < G ? col : 0;  // MFMA rows >= G are computed and discarded
     const bf16_t* qp = q + qrow * q_row_stride + (int64_t)(kvh * G + hc) * kCD + hg * 8;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) qreg[ks] = *reinterpret_cast<const u32x4_t*>(qp + ks * 32);
+    bf16_t* stage = L.kstage[wave];
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        *reinterpret_cast<u32x4_t*>(&stage[(4 * r + hg) * kStageRow + col * 8]) = kreg[g][r];
       f32x4_t a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-        a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8_v(qreg[ks]), as_bf16x8_v(kreg[g][ks]),
-                                                     a, 0, 0, 0);
+      for (int ks = 0; ks < 4; ++ks) {
+        const u32x4_t kb =
+            *reinterpret_cast<const u32x4_t*>(&stage[col * kStageRow + hg * 8 + ks * 32]);
+        a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8_v(qreg[ks]), as_bf16x8_v(kb), a,
+                                                     0, 0, 0);
+      }
       acc[g] = a;
     }
   }
