@@ -403,10 +403,12 @@ __device__ __forceinline__ void block_select(SelectLds& L, int n_cand, int num_k
 // Window of (sequence j, KV head kvh): the importance of each key summed over
 // the G query heads of the group, for this thread's keys t0 + 16g + col
 // (valid in lanes of row group 0). Uses L.red.
-template <int G>
+// F8: the cache holds fp8 (OCP E4M3FN) codes, 128-byte head rows read by 8 lanes (8 rows
+// per load) and widened to bf16 when staged; the K scale is folded into scale_log2.
+template <int G, bool F8>
 __device__ __forceinline__ void group_importance(
     SelectLds& L, const bf16_t* __restrict__ q, int64_t q_row_stride,
-    const bf16_t* __restrict__ k, const int32_t* __restrict__ block_tables,
+    const void* __restrict__ k, const int32_t* __restrict__ block_tables,
     int64_t bt_row_stride, int32_t max_blocks, const int32_t* __restrict__ base_context_lens,
     const int32_t* __restrict__ seq_idx, int j, int kvh, int Hk, int block_size,
     int window_blocks, int64_t n_blocks, float scale_log2, float gi[4]) {
@@ -442,13 +444,21 @@ __device__ __forceinline__ void group_importance(
     // head row per 16 lanes (lane l: key 16g + 4r + l/16, dims 8*(l%16)), so every load
     // instruction is 4 row-sized requests; each group is staged row-major in LDS and
     // re-read in the MFMA operand layout (lane l: key l%16, dims 8*(l/16) + 32ks).
-    u32x4_t kreg[4][4];
+    constexpr int kLd = F8 ? 2 : 4;  // loads per 16-key group
+    u32x4_t kreg[4][kLd];
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const bf16_t* kp = k + base + (g * 16 + 4 * r + hg) * tok_stride + col * 8;
-        kreg[g][r] = *reinterpret_cast<const u32x4_t*>(kp);
+      for (int r = 0; r < kLd; ++r) {
+        if constexpr (F8) {
+          const uint8_t* kp = static_cast<const uint8_t*>(k) + base +
+                              (g * 16 + 8 * r + (lane >> 3)) * tok_stride + (lane & 7) * 16;
+          kreg[g][r] = *reinterpret_cast<const u32x4_t*>(kp);
+        } else {
+          const bf16_t* kp = static_cast<const bf16_t*>(k) + base +
+                             (g * 16 + 4 * r + hg) * tok_stride + col * 8;
+          kreg[g][r] = *reinterpret_cast<const u32x4_t*>(kp);
+        }
       }
     }
     u32x4_t qreg[4];
@@ -459,9 +469,20 @@ __device__ __forceinline__ void group_importance(
     bf16_t* stage = L.kstage[wave];
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
+      if constexpr (F8) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        *reinterpret_cast<u32x4_t*>(&stage[(4 * r + hg) * kStageRow + col * 8]) = kreg[g][r];
+        for (int r = 0; r < kLd; ++r) {
+          u32x4_t lo, hi;
+          fp8x16_to_bf16(kreg[g][r], lo, hi);
+          bf16_t* d = &stage[(8 * r + (lane >> 3)) * kStageRow + (lane & 7) * 16];
+          *reinterpret_cast<u32x4_t*>(d) = lo;
+          *reinterpret_cast<u32x4_t*>(d + 8) = hi;
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < kLd; ++r)
+          *reinterpret_cast<u32x4_t*>(&stage[(4 * r + hg) * kStageRow + col * 8]) = kreg[g][r];
+      }
       f32x4_t a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
@@ -531,9 +552,11 @@ __device__ __forceinline__ void group_importance(
 }
 
 // In-place compaction of KV head kvh of sequence seq_idx[j], K and V, with the
-// kept window positions in L.keep; kvh 0 also sets the new context length.
+// kept window positions in L.keep; kvh 0 also sets the new context length. F8:
+// 1-byte rows (a 128-byte head row per 8 lanes, 128 rows per round).
+template <bool F8>
 __device__ __forceinline__ void compact_unit(
-    SelectLds& L, bf16_t* __restrict__ k_cache, bf16_t* __restrict__ v_cache,
+    SelectLds& L, void* __restrict__ k_cache, void* __restrict__ v_cache,
     const int32_t* __restrict__ block_tables, int64_t bt_row_stride, int32_t max_blocks,
     const int32_t* __restrict__ base_context_lens, int32_t* __restrict__ context_lens,
     const int32_t* __restrict__ seq_idx, int j, int kvh, int keep_tokens, int Hk, int B,
@@ -584,39 +607,45 @@ __device__ __forceinline__ void compact_unit(
   __syncthreads();
   // all source rows (K and V) as unconditional 16-byte loads (rows that are
   // not moved re-read slot 0, always valid), then the writes
-  const int64_t row = (int64_t)Hk * kCD;
-  const int64_t col = (int64_t)kvh * kCD + (tid & 15) * 8;
-  const int rsub = tid >> 4;  // 0..63: row within a round
-  u32x4_t kr[kStepRounds], vr[kStepRounds];
+  constexpr int kEl = F8 ? 1 : 2;
+  constexpr int kLanes = 8 * kEl;                  // 16-byte lanes per head row
+  constexpr int kRpr = kSelThreads / kLanes;       // rows per round: 64 (bf16), 128 (fp8)
+  constexpr int kRounds = kStepMaxRows / kRpr;     // 12 (bf16), 6 (fp8)
+  char* kc = static_cast<char*>(k_cache);
+  char* vc = static_cast<char*>(v_cache);
+  const int64_t row = (int64_t)Hk * kCD * kEl;    // bytes
+  const int64_t col = (int64_t)kvh * kCD * kEl + (tid % kLanes) * 16;
+  const int rsub = tid / kLanes;  // row within a round
+  u32x4_t kr[kRounds], vr[kRounds];
 #pragma unroll
-  for (int rr = 0; rr < kStepRounds; ++rr) {
-    const int64_t sv = max(L.src[rr * 64 + rsub], 0);
-    kr[rr] = *reinterpret_cast<const u32x4_t*>(k_cache + sv * row + col);
-    vr[rr] = *reinterpret_cast<const u32x4_t*>(v_cache + sv * row + col);
+  for (int rr = 0; rr < kRounds; ++rr) {
+    const int64_t sv = max(L.src[rr * kRpr + rsub], 0);
+    kr[rr] = *reinterpret_cast<const u32x4_t*>(kc + sv * row + col);
+    vr[rr] = *reinterpret_cast<const u32x4_t*>(vc + sv * row + col);
   }
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_waitcnt(0);  // all reads of the unit land before any write
   __syncthreads();
 #pragma unroll
-  for (int rr = 0; rr < kStepRounds; ++rr) {
-    const int64_t d = L.dst[rr * 64 + rsub];
+  for (int rr = 0; rr < kRounds; ++rr) {
+    const int64_t d = L.dst[rr * kRpr + rsub];
     if (d >= 0) {
-      *reinterpret_cast<u32x4_t*>(k_cache + d * row + col) = kr[rr];
-      *reinterpret_cast<u32x4_t*>(v_cache + d * row + col) = vr[rr];
+      *reinterpret_cast<u32x4_t*>(kc + d * row + col) = kr[rr];
+      *reinterpret_cast<u32x4_t*>(vc + d * row + col) = vr[rr];
     }
   }
   if (kvh == 0 && tid == 0) context_lens[seq] = len - Lw + keep_tokens;
 }
 
 // agg "group": score -> select -> (if k_cache_w) compact. Grid m * Hk.
-template <int G>
+template <int G, bool F8>
 __global__ __launch_bounds__(kSelThreads) void compress_group_kernel(
-    const bf16_t* __restrict__ q, int64_t q_row_stride, const bf16_t* __restrict__ k,
+    const bf16_t* __restrict__ q, int64_t q_row_stride, const void* __restrict__ k,
     const int32_t* __restrict__ block_tables, int64_t bt_row_stride, int32_t max_blocks,
     const int32_t* __restrict__ base_context_lens, const int32_t* __restrict__ seq_idx,
     int32_t Hk, int32_t block_size, int32_t window_blocks, int64_t n_blocks, float scale_log2,
     int32_t num_keep, float* __restrict__ importance_out, int32_t* __restrict__ keep_idx,
-    bf16_t* __restrict__ k_cache_w, bf16_t* __restrict__ v_cache_w,
+    void* __restrict__ k_cache_w, void* __restrict__ v_cache_w,
     int32_t* __restrict__ context_lens) {
   __shared__ SelectLds L;
   const int tid = threadIdx.x;
@@ -627,9 +656,9 @@ __global__ __launch_bounds__(kSelThreads) void compress_group_kernel(
   const int Lw = window_blocks * block_size;
   const int n_cand = Lw - 1;
   float gi[4];
-  group_importance<G>(L, q, q_row_stride, k, block_tables, bt_row_stride, max_blocks,
-                      base_context_lens, seq_idx, j, kvh, Hk, block_size, window_blocks,
-                      n_blocks, scale_log2, gi);
+  group_importance<G, F8>(L, q, q_row_stride, k, block_tables, bt_row_stride, max_blocks,
+                          base_context_lens, seq_idx, j, kvh, Hk, block_size, window_blocks,
+                          n_blocks, scale_log2, gi);
   const int t0 = (tid >> 6) * kSelKeysPerWave;
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
@@ -641,15 +670,15 @@ __global__ __launch_bounds__(kSelThreads) void compress_group_kernel(
   for (int t = tid; t < n_cand; t += kSelThreads) irow[t] = L.imp[t];
   block_select(L, n_cand, num_keep, keep_idx + ((int64_t)j * Hk + kvh) * (num_keep + 2));
   if (k_cache_w)
-    compact_unit(L, k_cache_w, v_cache_w, block_tables, bt_row_stride, max_blocks,
+    compact_unit<F8>(L, k_cache_w, v_cache_w, block_tables, bt_row_stride, max_blocks,
                  base_context_lens, context_lens, seq_idx, j, kvh, num_keep + 2, Hk, block_size,
                  window_blocks, n_blocks);
 }
 
 // agg "all", first kernel: each group's importance -> partial[j][kvh][Lw]. Grid m * Hk.
-template <int G>
+template <int G, bool F8>
 __global__ __launch_bounds__(kSelThreads) void compress_partial_kernel(
-    const bf16_t* __restrict__ q, int64_t q_row_stride, const bf16_t* __restrict__ k,
+    const bf16_t* __restrict__ q, int64_t q_row_stride, const void* __restrict__ k,
     const int32_t* __restrict__ block_tables, int64_t bt_row_stride, int32_t max_blocks,
     const int32_t* __restrict__ base_context_lens, const int32_t* __restrict__ seq_idx,
     int32_t Hk, int32_t block_size, int32_t window_blocks, int64_t n_blocks, float scale_log2,
@@ -661,9 +690,9 @@ __global__ __launch_bounds__(kSelThreads) void compress_partial_kernel(
   if (block_tables && seq_idx[j] < 0) return;  // padding entry (uniform): nothing written
   const int Lw = window_blocks * block_size;
   float gi[4];
-  group_importance<G>(L, q, q_row_stride, k, block_tables, bt_row_stride, max_blocks,
-                      base_context_lens, seq_idx, j, kvh, Hk, block_size, window_blocks,
-                      n_blocks, scale_log2, gi);
+  group_importance<G, F8>(L, q, q_row_stride, k, block_tables, bt_row_stride, max_blocks,
+                          base_context_lens, seq_idx, j, kvh, Hk, block_size, window_blocks,
+                          n_blocks, scale_log2, gi);
   float* prow = partial + ((int64_t)j * Hk + kvh) * Lw;
   const int t0 = (threadIdx.x >> 6) * kSelKeysPerWave;
 #pragma unroll
@@ -676,11 +705,12 @@ __global__ __launch_bounds__(kSelThreads) void compress_partial_kernel(
 // agg "all", second kernel: importance[j] = sum over KV heads (in order) of the
 // partials, the selection, and (if k_cache_w) the compaction of KV head kvh.
 // Grid m (selection only) or m * Hk (step: every KV head derives the same set).
+template <bool F8>
 __global__ __launch_bounds__(kSelThreads) void compress_sum_kernel(
     const float* __restrict__ partial, int32_t Hk, int32_t n_units_per_seq, int32_t block_size,
     int32_t window_blocks, int32_t num_keep, float* __restrict__ importance_out,
-    int32_t* __restrict__ keep_idx, bf16_t* __restrict__ k_cache_w,
-    bf16_t* __restrict__ v_cache_w, const int32_t* __restrict__ block_tables,
+    int32_t* __restrict__ keep_idx, void* __restrict__ k_cache_w,
+    void* __restrict__ v_cache_w, const int32_t* __restrict__ block_tables,
     int64_t bt_row_stride, int32_t max_blocks, const int32_t* __restrict__ base_context_lens,
     int32_t* __restrict__ context_lens, const int32_t* __restrict__ seq_idx, int64_t n_blocks) {
   __shared__ SelectLds L;
@@ -708,7 +738,7 @@ __global__ __launch_bounds__(kSelThreads) void compress_sum_kernel(
   __syncthreads();
   block_select(L, n_cand, num_keep, writer ? keep_idx + (int64_t)j * (num_keep + 2) : nullptr);
   if (k_cache_w)
-    compact_unit(L, k_cache_w, v_cache_w, block_tables, bt_row_stride, max_blocks,
+    compact_unit<F8>(L, k_cache_w, v_cache_w, block_tables, bt_row_stride, max_blocks,
                  base_context_lens, context_lens, seq_idx, j, kvh, num_keep + 2, Hk, block_size,
                  window_blocks, n_blocks);
 }
@@ -1039,6 +1069,7 @@ extern "C" size_t nkv_compress_select_workspace_bytes(int32_t m, int32_t n_q_hea
 namespace nkv {
 // Launches the fused selection (and, with k_cache_w, the compaction) when the
 // shape allows it; returns 1 if the caller must take the general path.
+template <bool F8>
 static int launch_fused(const void* q, int64_t q_row_stride, const void* k_cache,
                         const int32_t* block_tables, int64_t bt_row_stride,
                         int32_t max_blocks_per_seq, const int32_t* base_context_lens,
@@ -1059,8 +1090,6 @@ static int launch_fused(const void* q, int64_t q_row_stride, const void* k_cache
   const float sl2 = scale * kLog2e;
   const unsigned units = (unsigned)(m * n_kv_heads);
   float* partial = (float*)workspace;
-  bf16_t* kw = (bf16_t*)k_cache_w;
-  bf16_t* vw = (bf16_t*)v_cache_w;
 #define NKV_G_SWITCH(MACRO) \
   switch (g) {              \
     case 1: MACRO(1); break; \
@@ -1071,29 +1100,30 @@ static int launch_fused(const void* q, int64_t q_row_stride, const void* k_cache
   }
   if (agg_mode == NKV_AGG_GROUP) {
 #define NKV_GROUP(G)                                                                          \
-  hipLaunchKernelGGL(compress_group_kernel<G>, dim3(units), dim3(kSelThreads), 0, s,           \
-                     (const bf16_t*)q, q_row_stride, (const bf16_t*)k_cache, block_tables,     \
-                     bt_row_stride, max_blocks_per_seq, base_context_lens, seq_idx, n_kv_heads, \
-                     block_size, window_blocks, n_blocks, sl2, num_keep, importance_out,       \
-                     keep_idx, kw, vw, context_lens)
+  hipLaunchKernelGGL((compress_group_kernel<G, F8>), dim3(units), dim3(kSelThreads), 0, s,     \
+                     (const bf16_t*)q, q_row_stride, k_cache, block_tables, bt_row_stride,     \
+                     max_blocks_per_seq, base_context_lens, seq_idx, n_kv_heads, block_size,   \
+                     window_blocks, n_blocks, sl2, num_keep, importance_out, keep_idx,         \
+                     k_cache_w, v_cache_w, context_lens)
     NKV_G_SWITCH(NKV_GROUP)
 #undef NKV_GROUP
     return check_launch("compress (group)") ? -1 : 0;
   }
 #define NKV_PARTIAL(G)                                                                        \
-  hipLaunchKernelGGL(compress_partial_kernel<G>, dim3(units), dim3(kSelThreads), 0, s,         \
-                     (const bf16_t*)q, q_row_stride, (const bf16_t*)k_cache, block_tables,     \
-                     bt_row_stride, max_blocks_per_seq, base_context_lens, seq_idx, n_kv_heads, \
-                     block_size, window_blocks, n_blocks, sl2, partial)
+  hipLaunchKernelGGL((compress_partial_kernel<G, F8>), dim3(units), dim3(kSelThreads), 0, s,   \
+                     (const bf16_t*)q, q_row_stride, k_cache, block_tables, bt_row_stride,     \
+                     max_blocks_per_seq, base_context_lens, seq_idx, n_kv_heads, block_size,   \
+                     window_blocks, n_blocks, sl2, partial)
   NKV_G_SWITCH(NKV_PARTIAL)
 #undef NKV_PARTIAL
 #undef NKV_G_SWITCH
   if (check_launch("compress (partial)")) return -1;
   const int per_seq = step ? n_kv_heads : 1;
-  hipLaunchKernelGGL(compress_sum_kernel, dim3((unsigned)(m * per_seq)), dim3(kSelThreads), 0, s,
-                     (const float*)partial, n_kv_heads, per_seq, block_size, window_blocks,
-                     num_keep, importance_out, keep_idx, kw, vw, block_tables, bt_row_stride,
-                     max_blocks_per_seq, base_context_lens, context_lens, seq_idx, n_blocks);
+  hipLaunchKernelGGL((compress_sum_kernel<F8>), dim3((unsigned)(m * per_seq)), dim3(kSelThreads),
+                     0, s, (const float*)partial, n_kv_heads, per_seq, block_size,
+                     window_blocks, num_keep, importance_out, keep_idx, k_cache_w, v_cache_w,
+                     block_tables, bt_row_stride, max_blocks_per_seq, base_context_lens,
+                     context_lens, seq_idx, n_blocks);
   return check_launch("compress (sum)") ? -1 : 0;
 }
 }  // namespace nkv
@@ -1130,7 +1160,7 @@ extern "C" int nkv_compress_select(const void* q, int64_t q_row_stride, const vo
   NKV_REQUIRE(workspace && workspace_bytes >= need, NKV_EWORKSPACE,
               "compress_select: workspace needs %zu bytes (got %zu)", need, workspace_bytes);
   hipStream_t s = as_stream(stream);
-  const int rc = launch_fused(q, q_row_stride, k_cache, block_tables, bt_row_stride,
+  const int rc = launch_fused<false>(q, q_row_stride, k_cache, block_tables, bt_row_stride,
                               max_blocks_per_seq, base_context_lens, seq_idx, m, n_q_heads,
                               n_kv_heads, head_dim, block_size, window_blocks, n_blocks, scale,
                               agg_mode, num_keep, importance_out, keep_idx, workspace, nullptr,
@@ -1253,10 +1283,11 @@ extern "C" int nkv_compress_step(const void* q, int64_t q_row_stride, void* k_ca
   NKV_REQUIRE(workspace && workspace_bytes >= need, NKV_EWORKSPACE,
               "compress_step: workspace needs %zu bytes (got %zu)", need, workspace_bytes);
   hipStream_t s = as_stream(stream);
-  int rc = launch_fused(q, q_row_stride, k_cache, block_tables, bt_row_stride, max_blocks_per_seq,
-                    base_context_lens, seq_idx, m, n_q_heads, n_kv_heads, head_dim, block_size,
-                    window_blocks, n_blocks, scale, agg_mode, num_keep, importance_out, keep_idx,
-                    workspace, k_cache, v_cache, context_lens, s);
+  int rc = launch_fused<false>(q, q_row_stride, k_cache, block_tables, bt_row_stride,
+                               max_blocks_per_seq, base_context_lens, seq_idx, m, n_q_heads,
+                               n_kv_heads, head_dim, block_size, window_blocks, n_blocks, scale,
+                               agg_mode, num_keep, importance_out, keep_idx, workspace, k_cache,
+                               v_cache, context_lens, s);
   if (rc < 0) return NKV_ELAUNCH;
   if (rc == 0) return NKV_OK;
   // general path: selection, then the compaction kernel
@@ -1295,8 +1326,8 @@ extern "C" int nkv_compress_schedule(const int32_t* context_lens,
 
 // Compression step over fp8 (OCP E4M3FN) caches: K codes are widened to bf16 for
 // scoring (k_scale folded into the score scale), then importance, top-k, and the
-// compaction of the 1-byte rows; same results contract as nkv_compress_step's
-// general path.
+// compaction of the 1-byte rows. Windows of up to 1024 tokens take the fused kernels
+// (as nkv_compress_step), longer ones the four-kernel general path; same results.
 extern "C" int nkv_compress_step_fp8(const void* q, int64_t q_row_stride, void* k_cache,
                                      void* v_cache, const int32_t* block_tables,
                                      int64_t bt_row_stride, int32_t max_blocks_per_seq,
@@ -1345,8 +1376,16 @@ extern "C" int nkv_compress_step_fp8(const void* q, int64_t q_row_stride, void* 
   const size_t need = nkv_compress_workspace_bytes(m, n_q_heads, window_blocks, block_size);
   NKV_REQUIRE(workspace && workspace_bytes >= need, NKV_EWORKSPACE,
               "compress_step_fp8: workspace needs %zu bytes (got %zu)", need, workspace_bytes);
-  float* scores = (float*)workspace;
   hipStream_t s = as_stream(stream);
+  int rc = launch_fused<true>(q, q_row_stride, k_cache, block_tables, bt_row_stride,
+                              max_blocks_per_seq, base_context_lens, seq_idx, m, n_q_heads,
+                              n_kv_heads, head_dim, block_size, window_blocks, n_blocks,
+                              scale * k_scale, agg_mode, num_keep, importance_out, keep_idx,
+                              workspace, k_cache, v_cache, context_lens, s);
+  if (rc < 0) return NKV_ELAUNCH;
+  if (rc == 0) return NKV_OK;
+  // general path: score, importance, top-k, compaction
+  float* scores = (float*)workspace;
   const unsigned sgrid = (unsigned)(m * n_kv_heads * (Lw / kChunk));
   const float sl2 = scale * k_scale * kLog2e;
 #define NKV_SCORE8_LAUNCH(G)                                                                   \
@@ -1362,7 +1401,7 @@ extern "C" int nkv_compress_step_fp8(const void* q, int64_t q_row_stride, void* 
     default: NKV_SCORE8_LAUNCH(16); break;
   }
 #undef NKV_SCORE8_LAUNCH
-  int rc = check_launch("nkv_compress_step_fp8 (score)");
+  rc = check_launch("nkv_compress_step_fp8 (score)");
   if (rc) return rc;
   const int n_sets = agg_mode == NKV_AGG_ALL ? 1 : n_kv_heads;
   const int hps = n_q_heads / n_sets;
