@@ -182,3 +182,48 @@ def test_prefill_contiguous_distinct_kv_strides(nkv, dev):
     same = nkv.varlen_prefill(q.to(dev), k.to(dev), v.to(dev), cu.to(dev), cu.to(dev),
                               wl["max_seqlen_q"], wl["scale"])
     assert torch.equal(out, same)
+
+
+def test_prefill_chunked_equals_one_shot_full_size(nkv, dev):
+    """The full chunked workload (16 sequences, 2048-token chunks after paged prefixes
+    U[0,8192]) equals, bit for bit, the same rows of a one-shot prefill over the whole
+    sequences: a row's keys, steps and lazy-max decisions do not depend on how the queries
+    are tiled, and masked or fully invisible keys add exact zeros."""
+    wl = wl_mod.prefill_chunked_qwen3_8b(device=dev)
+    kc, vc = wl["k_cache"], wl["v_cache"]
+    nkv.store_kvcache(wl["key"], wl["value"], kc, vc, wl["slot_mapping"].to(dev))
+    cq, ck = wl["cu_seqlens_q"].tolist(), wl["cu_seqlens_k"].tolist()
+    bt = wl["block_tables"].to(dev)
+    out_c = nkv.varlen_prefill(wl["q"], kc, vc, wl["cu_seqlens_q"].to(dev),
+                               wl["cu_seqlens_k"].to(dev), wl["max_seqlen_q"], wl["scale"],
+                               block_tables=bt)
+    g = torch.Generator().manual_seed(11)
+    q_full = torch.randn(ck[-1], wl["Hq"], 128, generator=g).to(torch.bfloat16).to(dev)
+    sel = []
+    for i, (lq, lk) in enumerate(zip(wl["Lq"], wl["Lk"])):
+        r0 = ck[i] + lk - lq
+        q_full[r0:r0 + lq] = wl["q"][cq[i]:cq[i + 1]]
+        sel.append(torch.arange(r0, r0 + lq))
+    ckd = wl["cu_seqlens_k"].to(dev)
+    out_f = nkv.varlen_prefill(q_full, kc, vc, ckd, ckd, max(wl["Lk"]), wl["scale"],
+                               block_tables=bt)
+    torch.cuda.synchronize()
+    assert torch.equal(out_f[torch.cat(sel).to(dev)], out_c)
+
+
+def test_prefill_last_rows_match_decode_full_size(nkv, dev):
+    """One-shot prefill of the full workload (16 sequences, prompts U[512,4096]): each
+    sequence's last query row equals paged decode of that query over the same context
+    (two kernels, two summation orders: within the bf16 tolerance)."""
+    wl = wl_mod.prefill_qwen3_8b(device=dev)
+    kc, vc = wl["k_cache"], wl["v_cache"]
+    nkv.store_kvcache(wl["key"], wl["value"], kc, vc, wl["slot_mapping"].to(dev))
+    bt = wl["block_tables"].to(dev)
+    out = nkv.varlen_prefill(wl["q"], kc, vc, wl["cu_seqlens_q"].to(dev),
+                             wl["cu_seqlens_k"].to(dev), wl["max_seqlen_q"], wl["scale"],
+                             block_tables=bt)
+    last = (wl["cu_seqlens_q"][1:] - 1).to(torch.int64).to(dev)
+    ctx = torch.tensor(wl["Lk"], dtype=torch.int32, device=dev)
+    dec = nkv.paged_decode(wl["q"][last].contiguous(), kc, vc, ctx, bt, wl["scale"])
+    torch.cuda.synchronize()
+    assert (dec.float() - out[last].float()).abs().max().item() <= TOL
