@@ -17,7 +17,9 @@ compression truncates). Host work is then O(sequences + changed blocks).
 """
 from __future__ import annotations
 
-import numpy as np
+import itertools
+import struct
+
 import torch
 
 from .. import _lib
@@ -48,29 +50,34 @@ class BlockTableStore:
 
     def sync(self, seq_ids: list[int], tables: list[list[int]]):
         """-> (rows, counts, flat updates [row, col, id, ...])."""
-        rows, counts, updates = [], [], []
-        for sid, t in zip(seq_ids, tables):
-            if len(t) > self.max_blocks:
-                raise ValueError(f"block table of {len(t)} entries exceeds the store's "
-                                 f"{self.max_blocks}")
-            row = self._row.get(sid)
-            if row is None:
+        counts = list(map(len, tables))
+        if counts and max(counts) > self.max_blocks:
+            raise ValueError(f"block table of {max(counts)} entries exceeds the store's "
+                             f"{self.max_blocks}")
+        row_of, sent_of = self._row, self._sent
+        rows = [row_of.get(sid, -1) for sid in seq_ids]
+        # decode steps leave almost every table as it was: find the others first
+        changed = [i for i, (r, sid, t) in enumerate(zip(rows, seq_ids, tables))
+                   if r < 0 or sent_of[sid] != t]
+        updates = []
+        for i in changed:
+            sid, t = seq_ids[i], tables[i]
+            row = row_of.get(sid, -1)  # set earlier in this call if sid repeats
+            if row < 0:
                 if not self._free:
                     raise RuntimeError("BlockTableStore is full: release finished sequences")
                 row = self._free.pop()
-                self._row[sid] = row
+                row_of[sid] = row
                 sent = []
             else:
-                sent = self._sent[sid]
-            if t != sent:
-                k, lim = 0, min(len(t), len(sent))
-                while k < lim and t[k] == sent[k]:
-                    k += 1
-                for c in range(k, len(t)):
-                    updates += (row, c, t[c])
-                self._sent[sid] = list(t)
-            rows.append(row)
-            counts.append(len(t))
+                sent = sent_of[sid]
+            rows[i] = row
+            k, lim = 0, min(len(t), len(sent))
+            while k < lim and t[k] == sent[k]:
+                k += 1
+            for c in range(k, len(t)):
+                updates += (row, c, t[c])
+            sent_of[sid] = list(t)
         return rows, counts, updates
 
 
@@ -90,22 +97,29 @@ def build_step_metadata(starts: list[int], num_new: list[int], tables: list[list
     max_q = max(num_new, default=0)
     max_k = max((s + k for s, k in zip(starts, num_new)), default=0)
     width = max((len(t) for t in tables), default=0) if bt_width is None else bt_width
-    head = list(starts) + list(num_new) + (list(pos_offsets) if pos_offsets is not None else [])
+    vals = list(starts)
+    vals += num_new
+    if pos_offsets is not None:
+        vals += pos_offsets
     n_updates = 0
     if store is not None:
         if seq_ids is None or len(seq_ids) != n:
             raise ValueError("a BlockTableStore needs one seq_id per sequence")
         rows, counts, updates = store.sync(seq_ids, tables)
         n_updates = len(updates) // 3
-        packed_np = np.array(head + rows + counts + updates, dtype=np.int32)
+        vals += rows
+        vals += counts
+        vals += updates
     else:
-        lens = [len(t) for t in tables]
-        packed_np = np.empty(len(head) + n + 1 + sum(lens), dtype=np.int32)
-        packed_np[:len(head)] = head
-        off = packed_np[len(head):len(head) + n + 1]
-        off[0] = 0
-        np.cumsum(lens, out=off[1:])
-        packed_np[len(head) + n + 1:] = [b for t in tables for b in t]
+        vals.append(0)
+        vals += itertools.accumulate(map(len, tables))
+        vals += itertools.chain.from_iterable(tables)
+    # struct converts the Python ints in C (several times faster than numpy or torch from
+    # a list); it raises on values outside int32
+    try:
+        packed_buf = bytearray(struct.pack(f"{len(vals)}i", *vals))
+    except struct.error as e:
+        raise ValueError(f"step metadata value outside int32: {e}") from None
     i32 = dict(dtype=torch.int32, device=device)
     out = dict(
         positions=torch.empty(total, dtype=torch.int64, device=device),
@@ -122,7 +136,8 @@ def build_step_metadata(starts: list[int], num_new: list[int], tables: list[list
         out["cu_seqlens_k"].zero_()
         return out
     # pinned staging (torch's host allocator keeps it until the copy has run)
-    packed = torch.from_numpy(packed_np).pin_memory().to(device, non_blocking=True)
+    packed = torch.frombuffer(packed_buf, dtype=torch.int32).pin_memory().to(device,
+                                                                             non_blocking=True)
     bt = out["block_tables"]
     st = store.table if store is not None else None
     rc = _lib.lib().nkv_build_step_metadata(
