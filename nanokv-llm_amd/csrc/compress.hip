@@ -895,19 +895,53 @@ __global__ __launch_bounds__(64) void compress_finalize_kernel(
 constexpr int kSchedThreads = 1024;
 constexpr int kSchedMaxBatch = 16384;  // eligibility keys staged in LDS (64 KiB)
 
+// Exclusive prefix sum of v over the workgroup in thread order; *total gets the sum.
+// Wave scans with shuffles, then the 16 wave totals through LDS (two barriers).
+__device__ __forceinline__ int sched_scan(int v, int* wsum, int* total) {
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  int incl = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += y;
+  }
+  if (lane == 63) wsum[w] = incl;
+  __syncthreads();
+  int off = 0, tot = 0;
+#pragma unroll
+  for (int k = 0; k < kSchedThreads / 64; ++k) {
+    const int t = wsum[k];
+    off += k < w ? t : 0;
+    tot += t;
+  }
+  *total = tot;
+  __syncthreads();  // wsum is reused by the next scan
+  return off + incl - v;
+}
+
+// Each thread owns a contiguous range of sequences. Policy 1 finds the topk-th largest
+// length with a 4-bit radix select, takes the sequences above it and the lowest-indexed
+// ones equal to it, and ranks only those (written longest first).
 __global__ __launch_bounds__(kSchedThreads) void compress_schedule_kernel(
     const int32_t* __restrict__ context_lens, const int32_t* __restrict__ tail_uncompressed,
     int32_t batch, int32_t block_size, int32_t window_blocks, int32_t topk, int32_t period,
     int32_t policy, int32_t* __restrict__ step_counter, int32_t* __restrict__ seq_idx,
     int32_t* __restrict__ n_selected, int32_t* __restrict__ base_context_lens) {
-  __shared__ __attribute__((aligned(16))) int32_t key[kSchedMaxBatch];  // length if eligible, else -1
-  __shared__ int32_t part[kSchedThreads];
+  __shared__ int32_t key[kSchedMaxBatch];   // length if eligible, else -1
+  __shared__ int32_t cand[kSchedMaxBatch];  // policy 1: the selected sequences, index order
+  __shared__ int32_t wsum[kSchedThreads / 64];
+  __shared__ int32_t hist[16];
+  __shared__ uint32_t sh_prefix;
+  __shared__ int32_t sh_need;
+  __shared__ int32_t sh_max;  // longest eligible length
   __shared__ int32_t fire;
   const int tid = threadIdx.x;
   if (tid == 0) {
     const int c = step_counter[0] + 1;
     step_counter[0] = c;
     fire = period > 0 && c % period == 0;
+    sh_max = 0;
   }
   for (int r = tid; r < topk; r += kSchedThreads) seq_idx[r] = -1;
   __syncthreads();
@@ -918,48 +952,93 @@ __global__ __launch_bounds__(kSchedThreads) void compress_schedule_kernel(
     const bool ok = fire && len % B != B - 1 &&
                     tail_uncompressed[i] >= window_blocks * B && len / B >= window_blocks;
     key[i] = ok ? len : -1;
+    if (ok && policy == 1) atomicMax(&sh_max, len);
   }
-  const int padded = (batch + 15) & ~15;  // the rank loop reads 16 keys at a time
-  for (int i = batch + tid; i < padded; i += kSchedThreads) key[i] = -1;
   __syncthreads();
   const int per = (batch + kSchedThreads - 1) / kSchedThreads;
   const int i0 = min(batch, tid * per), i1 = min(batch, i0 + per);
   int cnt = 0;
   for (int i = i0; i < i1; ++i) cnt += key[i] >= 0;
-  part[tid] = cnt;
-  __syncthreads();
-  for (int o = 1; o < kSchedThreads; o <<= 1) {  // inclusive scan of the eligible counts
-    const int a = tid >= o ? part[tid - o] : 0;
-    __syncthreads();
-    part[tid] += a;
-    __syncthreads();
-  }
-  if (tid == 0) n_selected[0] = min(part[kSchedThreads - 1], topk);
+  int n_elig;
+  const int before = sched_scan(cnt, wsum, &n_elig);
+  const int take = min(n_elig, topk);
+  if (tid == 0) n_selected[0] = take;
   if (policy == 0) {  // first topk in batch order
-    int rank = part[tid] - cnt;
+    int rank = before;
     for (int i = i0; i < i1 && rank < topk; ++i)
       if (key[i] >= 0) seq_idx[rank++] = i;
-  } else {  // topk longest: rank = eligible sequences that are longer, or as long and earlier
-    typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
-    const i32x4_t* k4 = reinterpret_cast<const i32x4_t*>(key);
+    return;
+  }
+  if (take == 0) return;  // uniform
+  // topk longest. T = the take-th largest eligible length, 4 bits a pass from the highest
+  // nibble any eligible length uses; need = how many sequences of length T are taken (the
+  // lowest indices).
+  uint32_t prefix = 0;
+  int need = take;
+  const int top_bit = 31 - __builtin_clz((uint32_t)sh_max | 1u);
+  for (int shift = top_bit & ~3; shift >= 0; shift -= 4) {
+    if (tid < 16) hist[tid] = 0;
+    __syncthreads();
+    const uint32_t hi = shift >= 28 ? 0u : ~((1u << (shift + 4)) - 1u);  // digits already fixed
     for (int i = tid; i < batch; i += kSchedThreads) {
-      const int li = key[i];
-      if (li < 0) continue;
-      int rank = 0;
-      for (int j0 = 0; j0 < padded && rank < topk; j0 += 16) {  // 4 LDS loads in flight
-        i32x4_t v[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] = k4[j0 / 4 + u];
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int j2 = j0 + 4 * u + e;
-            rank += v[u][e] > li || (v[u][e] == li && j2 < i);
-          }
-      }
-      if (rank < topk) seq_idx[rank] = i;
+      const int k = key[i];
+      if (k >= 0 && ((uint32_t)k & hi) == prefix) atomicAdd(&hist[((uint32_t)k >> shift) & 15u], 1);
     }
+    __syncthreads();
+    if (tid < 64) {  // the digit whose bucket holds the need-th largest: suffix sums over 16 lanes
+      const int h = tid < 16 ? hist[tid] : 0;
+      int incl = h;  // sum of hist[tid .. 15]
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) {
+        const int y = __shfl_down(incl, o, 64);
+        if (tid + o < 16) incl += y;
+      }
+      const int above = incl - h;
+      if (tid < 16 && above < need && incl >= need) {
+        sh_prefix = prefix | ((uint32_t)tid << shift);
+        sh_need = need - above;
+      }
+    }
+    __syncthreads();
+    prefix = sh_prefix;
+    need = sh_need;
+  }
+  const int T = (int)prefix;
+  int ties = 0;
+  for (int i = i0; i < i1; ++i) ties += key[i] == T;
+  int tie_total;
+  const int tie_before = sched_scan(ties, wsum, &tie_total);
+  int nsel = 0;
+  {
+    int tr = tie_before;
+    for (int i = i0; i < i1; ++i) {
+      const int k = key[i];
+      nsel += k > T || (k == T && tr < need);
+      tr += k == T;
+    }
+  }
+  int sel_total;
+  int pos = sched_scan(nsel, wsum, &sel_total);  // sel_total == take
+  {
+    int tr = tie_before;
+    for (int i = i0; i < i1; ++i) {
+      const int k = key[i];
+      if (k > T || (k == T && tr < need)) cand[pos++] = i;
+      tr += k == T;
+    }
+  }
+  __syncthreads();
+  // longest first, ties to the lower index
+  for (int r = tid; r < take; r += kSchedThreads) {
+    const int i = cand[r];
+    const int li = key[i];
+    int rank = 0;
+    for (int t = 0; t < take; ++t) {
+      const int j = cand[t];
+      const int lj = key[j];
+      rank += lj > li || (lj == li && j < i);
+    }
+    seq_idx[rank] = i;
   }
 }
 
