@@ -103,19 +103,20 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 // gfx950's v_cvt_pk_f32_fp8 / v_cvt_pk_fp8_f32 convert between fp32 and the OCP
 // E4M3FN format (bias 7, largest finite 448, NaN = S.1111.111), round to
 // nearest even. An E4M3FN value has at most 4 significant bits and an
-// exponent in [-9, 8], so it is exact in bf16: the fp32 result's upper half.
+// exponent in [-9, 8], so it is exact in bf16, and v_cvt_scalef32_pk_bf16_fp8
+// (scale 1) produces it directly.
 constexpr float kFp8Max = 448.f;
 
 // 16 codes (one 16-byte word) -> 16 bf16 (two 16-byte words), exact.
 __device__ __forceinline__ void fp8x16_to_bf16(u32x4_t in, u32x4_t& lo, u32x4_t& hi) {
+  // v_cvt_scalef32_pk_bf16_fp8 with scale 1: two codes to a packed bf16 pair, exact
+  typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
-    const auto a = __builtin_amdgcn_cvt_pk_f32_fp8((int)in[w], false);  // bytes 0, 1
-    const auto b = __builtin_amdgcn_cvt_pk_f32_fp8((int)in[w], true);   // bytes 2, 3
-    const uint32_t p0 = __builtin_amdgcn_perm(__float_as_uint(a[1]), __float_as_uint(a[0]),
-                                              0x07060302u);
-    const uint32_t p1 = __builtin_amdgcn_perm(__float_as_uint(b[1]), __float_as_uint(b[0]),
-                                              0x07060302u);
+    const bf16x2v a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(in[w], 1.0f, false);  // bytes 0, 1
+    const bf16x2v b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(in[w], 1.0f, true);   // bytes 2, 3
+    const uint32_t p0 = __builtin_bit_cast(uint32_t, a);
+    const uint32_t p1 = __builtin_bit_cast(uint32_t, b);
     if (w < 2) {
       lo[2 * w] = p0;
       lo[2 * w + 1] = p1;
