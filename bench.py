@@ -829,14 +829,14 @@ def main():
         "store_us": round(r["store_ms"] * 1e3, 2),
         "parity_max_abs_err": r["parity_max_abs_err"],
         "roofline": {
-            "kernel": "paged_decode_split_kernel<4>",
+            "kernel": "paged_decode_split_kernel<4, false, 2>",
             "bound": "hbm",
             "achieved": round(split_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(split_gbs / HBM_PEAK_GBS, 4),
             "traffic": measured_traffic("paged_decode_qwen3_8b_bs64.txt",
-                                        "paged_decode_split_kernel<4>"),
+                                        "paged_decode_split_kernel<4, false, 2>"),
             "avg_us": round(r["split_ms"] * 1e3, 2),
             "algorithmic_bytes": r["split_bytes"],
         },

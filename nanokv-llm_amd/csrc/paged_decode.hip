@@ -45,7 +45,6 @@ constexpr int kWinBlocks = 64;           // block ids held per window (one per l
 constexpr int kVRow = kD + 16;           // LDS row stride of a staged V chunk (elements)
 constexpr int kBufferFlags = 0x00020000; // raw buffer resource word 3 (dword data)
 constexpr int kStreamPolicy = 2;         // cache policy "nt": K/V are read exactly once
-constexpr int kDepth = 4;                // ring depth (chunks in flight per wave)
 
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
@@ -89,10 +88,16 @@ __device__ __forceinline__ void seq_load(SeqCursor& c, const int32_t* __restrict
 }
 
 // F8: the caches hold fp8 (OCP E4M3FN) codes; a chunk's rows are half as many
-// bytes (two loads per lane per K or V chunk instead of four) and are widened
-// to bf16 (exact) when staged in LDS; the K scale is folded into scale_log2 and
-// the V scale multiplies the partial O.
-template <int G, bool F8>
+// bytes and are widened to bf16 (exact) when staged in LDS; the K scale is
+// folded into scale_log2 and the V scale multiplies the partial O.
+// HP: KV heads per wave. With HP = 2 a wave reads both heads' halves of every
+// token row as one contiguous piece (512 B bf16, 256 B fp8) instead of one
+// head's 256 B: on this part a stream of 256-byte pieces at 2 KiB stride runs
+// unevenly (pieces at odd 256-byte offsets come back later), and the waves of
+// the slow heads set the kernel's length. The 2G query heads fill MFMA columns
+// 0..2G-1; each head's scores use its own K, the softmax weights of a column
+// are zero for the other head, so both heads' PV products add into one O^T.
+template <int G, bool F8, int HP>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2)))
 void paged_decode_split_kernel(
     const bf16_t* __restrict__ q, int64_t q_row_stride,
@@ -102,10 +107,16 @@ void paged_decode_split_kernel(
     int32_t block_size, int32_t max_blocks, int64_t n_blocks, int32_t slots, float scale_log2,
     float v_scale, float* __restrict__ part_o, float* __restrict__ part_ml,
     int32_t* __restrict__ nslots) {
-  constexpr int kEl = F8 ? 1 : 2;    // bytes per cache element
-  constexpr int kLoads = F8 ? 2 : 4; // 16-byte loads per lane per K (or V) chunk
-  __shared__ __attribute__((aligned(16))) bf16_t kbuf[kChunk * kVRow];
-  __shared__ __attribute__((aligned(16))) bf16_t vbuf[kChunk * kVRow];
+  static_assert(HP == 1 || HP * G <= 16, "HP heads of G query heads must fit 16 columns");
+  constexpr int kEl = F8 ? 1 : 2;              // bytes per cache element
+  constexpr int kSeg = HP * kD * kEl;          // bytes a wave reads of each token row
+  constexpr int kLpr = kSeg / 16;              // lanes per row (16-byte loads)
+  constexpr int kRpl = 64 / kLpr;              // rows per load instruction
+  constexpr int kLoads = kChunk / kRpl;        // loads per lane per K (or V) chunk
+  constexpr int kRing = kLoads >= 8 ? 2 : 4;   // ring depth: at most 16 loads per lane in flight
+  constexpr int kLph = kLpr / HP;              // lanes per head within a row
+  __shared__ __attribute__((aligned(16))) bf16_t kbuf[HP][kChunk * kVRow];
+  __shared__ __attribute__((aligned(16))) bf16_t vbuf[HP][kChunk * kVRow];
 
   const int lane = threadIdx.x;
   const int g4 = lane >> 4;   // key group: keys 4*g4 .. 4*g4+3 of a chunk
@@ -114,13 +125,14 @@ void paged_decode_split_kernel(
   const int row_b = Hk * kD * kEl;  // bytes of one cache row (token)
   const int max_tokens = max_blocks * block_size;
 
-  // ---- this wave's KV head and chunk range. Every KV head has the same
-  // chunk stream (sequence-major); waves kvh, kvh+Hk, kvh+2Hk, ... split it
-  // into equal ranges, so the Hk waves i*Hk .. i*Hk+Hk-1 read the same cache
-  // blocks (the Hk heads of a block) at the same time.
-  const int kvh = blockIdx.x % Hk;
-  const int wi = blockIdx.x / Hk;
-  const int Wh = gridDim.x / Hk;
+  // ---- this wave's KV heads and chunk range. Every head group has the same
+  // chunk stream (sequence-major); waves p, p+NP, p+2NP, ... split it into
+  // equal ranges, so the NP waves i*NP .. i*NP+NP-1 read the Hk heads of the
+  // same cache blocks at the same time.
+  const int NP = Hk / HP;
+  const int kvh0 = (blockIdx.x % NP) * HP;
+  const int wi = blockIdx.x / NP;
+  const int Wh = gridDim.x / NP;
   if (wi >= Wh) return;
   SeqCursor cur;
   int T = 0;
@@ -136,14 +148,17 @@ void paged_decode_split_kernel(
   cur.base = 0;
   seq_load(cur, context_lens, batch, max_tokens);
 
-  // per-lane constant load offset: K and V are both read as whole head rows,
-  // bf16: 4 rows of 256 B per load (lane l: key 4r + l/16, dims 8*(l%16));
-  // fp8: 8 rows of 128 B per load (lane l: key 8r + l/8, dims 16*(l%8));
-  // staged row-major in LDS; K is re-read from there in the MFMA A layout.
-  const int roff = F8 ? (lane >> 3) * row_b + (lane & 7) * 16 : g4 * row_b + col * 16;
-  const int rstep = (F8 ? 8 : 4) * row_b;  // bytes between a lane's consecutive loads
+  // per-lane load offset: lane l reads 16 bytes of row l / kLpr (+ kRpl per
+  // load), byte 16 * (l % kLpr) of the wave's piece of the row; it stages them
+  // in head sh's LDS rows at dim sd (fp8 codes widen to 16 bf16 there). K is
+  // re-read from LDS in the MFMA A layout.
+  const int roff = (lane / kLpr) * row_b + (lane % kLpr) * 16;
+  const int rstep = kRpl * row_b;  // bytes between a lane's consecutive loads
+  const int sh = (lane % kLpr) / kLph;
+  const int sd = (lane % kLph) * (16 / kEl);
   const int tr_row = 4 * g4 + (col >> 2);  // ds_read_b64_tr_b16 source row / column
   const int tr_col = (col & 3) * 4;
+  const int hsel = col / G;                // head (of the HP) of this lane's column
 
   for (int k = k_begin; k < k_end;) {
     // ---- locate the sequence holding stream chunk k (wave-uniform)
@@ -161,21 +176,21 @@ void paged_decode_split_kernel(
     const int n_seg = min(nc - c_lo, k_end - k);
     const int slot = wi - g0 / C;
 
-    // q^T as the MFMA B operand: lane l -> head l%16 (columns >= g re-read
-    // head 0 and are discarded), dims 8*(l/16) + 32*ks .. +8
+    // q^T as the MFMA B operand: lane l -> query head kvh0*G + l%16 (columns
+    // >= HP*G re-read the first head and are discarded), dims 8*(l/16) + 32*ks
     u32x4_t qreg[4];
     {
-      const int hc = col < G ? col : 0;
+      const int hc = col < HP * G ? col : 0;
       const u32x4_t* qp = reinterpret_cast<const u32x4_t*>(
-          q + (int64_t)b * q_row_stride + (int64_t)(kvh * G + hc) * kD + g4 * 8);
+          q + (int64_t)b * q_row_stride + (int64_t)(kvh0 * G + hc) * kD + g4 * 8);
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) qreg[ks] = qp[ks * 4];
     }
-    const char* kbase = static_cast<const char*>(k_cache) + (int64_t)kvh * kD * kEl;
-    const char* vbase = static_cast<const char*>(v_cache) + (int64_t)kvh * kD * kEl;
+    const char* kbase = static_cast<const char*>(k_cache) + (int64_t)kvh0 * kD * kEl;
+    const char* vbase = static_cast<const char*>(v_cache) + (int64_t)kvh0 * kD * kEl;
     const int32_t* bt_row = block_tables + (int64_t)b * bt_row_stride;
 
-    f32x4_t acc[8];  // O^T: lane l -> head l%16, dims 16*db + 4*(l/16) .. +3
+    f32x4_t acc[8];  // O^T: lane l -> column l%16, dims 16*db + 4*(l/16) .. +3
 #pragma unroll
     for (int db = 0; db < 8; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     float m_run = -INFINITY, l_run = 0.f;
@@ -195,9 +210,9 @@ void paged_decode_split_kernel(
         }
       }
 
-      u32x4_t kreg[kDepth][kLoads];
-      u32x4_t vreg[kDepth][kLoads];
-      int nv[kDepth];  // valid keys of the chunk in each ring slot (0: masked)
+      u32x4_t kreg[kRing][kLoads];
+      u32x4_t vreg[kRing][kLoads];
+      int nv[kRing];  // valid keys of the chunk in each ring slot (0: masked)
       auto issue = [&](int j, int s) {
         const int t0 = (wlo + j) * kChunk;
         const int pb = __builtin_amdgcn_readlane(blk_id, min(t0 / block_size - blk0, 63));
@@ -222,40 +237,46 @@ void paged_decode_split_kernel(
       };
 
       auto consume = [&](int s) {
-        // stage the chunk's K and V rows (row-major, bf16) in LDS
-        if constexpr (F8) {
+        // stage the chunk's K and V rows (row-major per head, bf16) in LDS
 #pragma unroll
-          for (int r = 0; r < kLoads; ++r) {
-            const int e = (8 * r + (lane >> 3)) * kVRow + (lane & 7) * 16;
+        for (int r = 0; r < kLoads; ++r) {
+          const int e = (kRpl * r + lane / kLpr) * kVRow + sd;
+          if constexpr (F8) {
             u32x4_t lo, hi;
             fp8x16_to_bf16(kreg[s][r], lo, hi);
-            *reinterpret_cast<u32x4_t*>(&kbuf[e]) = lo;
-            *reinterpret_cast<u32x4_t*>(&kbuf[e + 8]) = hi;
+            *reinterpret_cast<u32x4_t*>(&kbuf[sh][e]) = lo;
+            *reinterpret_cast<u32x4_t*>(&kbuf[sh][e + 8]) = hi;
             fp8x16_to_bf16(vreg[s][r], lo, hi);
-            *reinterpret_cast<u32x4_t*>(&vbuf[e]) = lo;
-            *reinterpret_cast<u32x4_t*>(&vbuf[e + 8]) = hi;
-          }
-        } else {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            *reinterpret_cast<u32x4_t*>(&kbuf[(4 * r + g4) * kVRow + col * 8]) = kreg[s][r];
-            *reinterpret_cast<u32x4_t*>(&vbuf[(4 * r + g4) * kVRow + col * 8]) = vreg[s][r];
+            *reinterpret_cast<u32x4_t*>(&vbuf[sh][e]) = lo;
+            *reinterpret_cast<u32x4_t*>(&vbuf[sh][e + 8]) = hi;
+          } else {
+            *reinterpret_cast<u32x4_t*>(&kbuf[sh][e]) = kreg[s][r];
+            *reinterpret_cast<u32x4_t*>(&vbuf[sh][e]) = vreg[s][r];
           }
         }
-        // S^T for 16 keys x 16 heads; A operand: lane l -> key l%16, dims 8*(l/16) + 32*ks
-        f32x4_t st = {0.f, 0.f, 0.f, 0.f};
+        // S^T for 16 keys x 16 columns per head; A operand: lane l -> key l%16,
+        // dims 8*(l/16) + 32*ks
+        f32x4_t st[HP];
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          const u32x4_t ka = *reinterpret_cast<const u32x4_t*>(&kbuf[col * kVRow + g4 * 8 + ks * 32]);
-          st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8_v(ka), as_bf16x8_v(qreg[ks]), st,
-                                                        0, 0, 0);
+        for (int hh = 0; hh < HP; ++hh) {
+          f32x4_t a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks) {
+            const u32x4_t ka =
+                *reinterpret_cast<const u32x4_t*>(&kbuf[hh][col * kVRow + g4 * 8 + ks * 32]);
+            a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8_v(ka), as_bf16x8_v(qreg[ks]), a,
+                                                         0, 0, 0);
+          }
+          st[hh] = a;
         }
-        // online softmax for head `col` over keys 4*g4 .. +3 of the chunk
+        // online softmax for column `col` over keys 4*g4 .. +3 of the chunk
         float sv[4];
         float cmax = -INFINITY;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          sv[r] = (4 * g4 + r < nv[s]) ? st[r] * scale_log2 : -INFINITY;
+          float x = st[0][r];
+          if constexpr (HP == 2) x = hsel == 0 ? x : st[1][r];
+          sv[r] = (4 * g4 + r < nv[s]) ? x * scale_log2 : -INFINITY;
           cmax = fmaxf(cmax, sv[r]);
         }
         cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
@@ -274,33 +295,40 @@ void paged_decode_split_kernel(
         const bf16x2v_t p01 = {(__bf16)p[0], (__bf16)p[1]};
         const bf16x2v_t p23 = {(__bf16)p[2], (__bf16)p[3]};
         const uint2 pw = {__builtin_bit_cast(uint32_t, p01), __builtin_bit_cast(uint32_t, p23)};
-        const i16x4_t pb4 = __builtin_bit_cast(i16x4_t, pw);
-        // O^T[dims][heads] += V^T[dims][keys] P^T[keys][heads], 16 dims per MFMA
+        // P^T per head: a column's weights only in its own head's product
+        i16x4_t pbh[HP];
+#pragma unroll
+        for (int hh = 0; hh < HP; ++hh)
+          pbh[hh] = __builtin_bit_cast(i16x4_t, (HP == 1 || hsel == hh) ? pw : uint2{0u, 0u});
+        // O^T[dims][cols] += V^T[dims][keys] P^T[keys][cols], 16 dims per MFMA
 #pragma unroll
         for (int db = 0; db < 8; ++db) {
-          const i16x4_t va = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (lds_i16x4_t*)&vbuf[tr_row * kVRow + db * 16 + tr_col]);
-          acc[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb4, acc[db], 0, 0, 0);
+#pragma unroll
+          for (int hh = 0; hh < HP; ++hh) {
+            const i16x4_t va = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_i16x4_t*)&vbuf[hh][tr_row * kVRow + db * 16 + tr_col]);
+            acc[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pbh[hh], acc[db], 0, 0, 0);
+          }
         }
       };
 
-      // Ring schedule over the window padded to a multiple of kDepth: every
+      // Ring schedule over the window padded to a multiple of kRing: every
       // group but the last refills each slot right after consuming it
       // (branch-free, so the wait counts stay exact); the last group drains.
-      const int n_groups = (wn + kDepth - 1) / kDepth;
+      const int n_groups = (wn + kRing - 1) / kRing;
 #pragma unroll
-      for (int s = 0; s < kDepth; ++s) issue(s, s);
+      for (int s = 0; s < kRing; ++s) issue(s, s);
       for (int gi = 0; gi + 1 < n_groups; ++gi) {
 #pragma unroll
-        for (int s = 0; s < kDepth; ++s) {
+        for (int s = 0; s < kRing; ++s) {
           consume(s);
           __builtin_amdgcn_sched_barrier(0);  // refill only after the slot is consumed
-          issue((gi + 1) * kDepth + s, s);
+          issue((gi + 1) * kRing + s, s);
           __builtin_amdgcn_sched_barrier(0);
         }
       }
 #pragma unroll
-      for (int s = 0; s < kDepth; ++s) consume(s);
+      for (int s = 0; s < kRing; ++s) consume(s);
     }
 
     // ---- segment epilogue: l over the four key groups, then the partial
@@ -310,8 +338,8 @@ void paged_decode_split_kernel(
 #pragma unroll
       for (int db = 0; db < 8; ++db) acc[db] *= v_scale;
     }
-    const int64_t obase = ((int64_t)b * Hq + (int64_t)kvh * G) * slots + slot;
-    if (col < G) {
+    const int64_t obase = ((int64_t)b * Hq + (int64_t)kvh0 * G) * slots + slot;
+    if (col < HP * G) {
       const int64_t prow = obase + (int64_t)col * slots;
 #pragma unroll
       for (int db = 0; db < 8; ++db)
@@ -321,7 +349,7 @@ void paged_decode_split_kernel(
         part_ml[prow * 2 + 1] = l_run;
       }
     }
-    if (c_lo + n_seg == nc && lane == 0) nslots[(int64_t)b * Hk + kvh] = slot + 1;
+    if (c_lo + n_seg == nc && lane < HP) nslots[(int64_t)b * Hk + kvh0 + lane] = slot + 1;
     k += n_seg;
   }
 }
@@ -427,7 +455,7 @@ static int decode_check(const void* q, const void* k_cache, const void* v_cache,
 }
 
 // Persistent grid: as many one-wave workgroups as are resident at once.
-template <int G, bool F8>
+template <int G, bool F8, int HP>
 static int decode_grid() {
   static int cached[64] = {0};
   int dev = 0;
@@ -438,7 +466,7 @@ static int decode_grid() {
         n_cu <= 0)
       n_cu = 256;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, reinterpret_cast<const void*>(paged_decode_split_kernel<G, F8>), 64, 0) !=
+            &per_cu, reinterpret_cast<const void*>(paged_decode_split_kernel<G, F8, HP>), 64, 0) !=
             hipSuccess ||
         per_cu <= 0)
       per_cu = 8;
@@ -501,20 +529,35 @@ static int decode_split(const void* q, int64_t q_row_stride, const void* k_cache
   const float scale_log2 = scale * k_scale * kLog2e;
   const int g = n_q_heads / n_kv_heads;
   hipStream_t s = as_stream(stream);
-#define NKV_DECODE_LAUNCH(G)                                                                  \
-  hipLaunchKernelGGL((paged_decode_split_kernel<G, F8>),                                      \
-                     dim3((unsigned)std::max(n_kv_heads, decode_grid<G, F8>() / n_kv_heads *  \
-                                                             n_kv_heads)),                    \
+  // Two KV heads per wave when the heads pair up, the 2G query heads fit the 16
+  // MFMA columns and there is enough work for every wave (upper bound from the
+  // table width: >= 32 chunks per head pair per resident wave); otherwise one.
+  const int64_t work = (int64_t)batch * max_chunks * n_kv_heads;
+  const bool pair = n_kv_heads % 2 == 0 && g <= 8 && work >= 32 * (int64_t)decode_grid<4, F8, 2>();
+#define NKV_DECODE_LAUNCH(G, HP)                                                              \
+  hipLaunchKernelGGL((paged_decode_split_kernel<G, F8, HP>),                                  \
+                     dim3((unsigned)std::max(n_kv_heads / HP,                                 \
+                                             decode_grid<G, F8, HP>() / (n_kv_heads / HP) *   \
+                                                 (n_kv_heads / HP))),                         \
                      dim3(64), 0, s, (const bf16_t*)q, q_row_stride, k_cache, v_cache,        \
                      block_tables, bt_row_stride, context_lens, batch, n_kv_heads, block_size, \
                      max_blocks_per_seq, n_blocks, (int32_t)slots, scale_log2, v_scale,       \
                      w.part_o, w.part_ml, w.nslots)
-  switch (g) {
-    case 1: NKV_DECODE_LAUNCH(1); break;
-    case 2: NKV_DECODE_LAUNCH(2); break;
-    case 4: NKV_DECODE_LAUNCH(4); break;
-    case 8: NKV_DECODE_LAUNCH(8); break;
-    default: NKV_DECODE_LAUNCH(16); break;
+  if (pair) {
+    switch (g) {
+      case 1: NKV_DECODE_LAUNCH(1, 2); break;
+      case 2: NKV_DECODE_LAUNCH(2, 2); break;
+      case 4: NKV_DECODE_LAUNCH(4, 2); break;
+      default: NKV_DECODE_LAUNCH(8, 2); break;
+    }
+  } else {
+    switch (g) {
+      case 1: NKV_DECODE_LAUNCH(1, 1); break;
+      case 2: NKV_DECODE_LAUNCH(2, 1); break;
+      case 4: NKV_DECODE_LAUNCH(4, 1); break;
+      case 8: NKV_DECODE_LAUNCH(8, 1); break;
+      default: NKV_DECODE_LAUNCH(16, 1); break;
+    }
   }
 #undef NKV_DECODE_LAUNCH
   return check_launch("nkv_paged_decode_split");
