@@ -7,17 +7,19 @@
 //
 // MI355X design (HBM-bound: every K/V byte is read exactly once):
 //  * Balanced split-K ("stream-K"): the K/V stream of the batch is cut into
-//    16-token chunks ordered (sequence, KV head, chunk). Persistent one-wave
-//    workgroups, as many as are resident at once, each take an equal
+//    16-token chunks ordered (sequence, KV head group, chunk). Persistent
+//    one-wave workgroups, as many as are resident at once, each take an equal
 //    contiguous range of C chunks, so every wave moves the same number of
 //    bytes whatever the context-length mix. A range crosses at most a few
-//    (sequence, KV head) segments; each segment it touches yields one
-//    partial (m, l, O) in slot  wave - first_wave_of_the_segment.
-//  * Within a segment the wave streams chunks through a register ring of
-//    DEPTH chunks: K and V of chunk j+DEPTH (4 whole 256-byte rows per load
-//    instruction, 8 x 16 B per lane) are issued as soon as chunk j has been
-//    consumed. Loads are non-temporal raw buffer loads whose per-chunk
-//    descriptor covers only the chunk's valid rows: keys past the context,
+//    (sequence, head group) segments; each segment it touches yields one
+//    partial (m, l, O) per query head in slot  wave - first_wave_of_the_segment.
+//    A head group is one KV head, or two (HP = 2) whose halves of every token
+//    row are read as one contiguous piece.
+//  * Within a segment the wave streams chunks through a register ring (4
+//    chunks of 256-byte rows, or 2 of 512-byte rows): K and V of the chunk one
+//    ring ahead are issued as soon as a chunk has been consumed. Loads are
+//    non-temporal raw buffer loads whose per-chunk descriptor covers only the
+//    chunk's valid rows: keys past the context,
 //    padding chunks and invalid block-table entries read as zero without
 //    touching memory. Each consumed chunk is staged row-major in LDS.
 //  * Both contractions run on the matrix cores:
