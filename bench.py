@@ -311,11 +311,36 @@ def run_compress(args, dev):
             times.append(a.elapsed_time(b) * 1000.0)
     res["compress_step_fp8_us"] = round(statistics.median(times), 2)
     del kq, vq
+    if not args.no_cpu_baseline:
+        res["compress_cpu_baseline"] = cpu_compress_baseline()
     res.update({"compress_bytes": nbytes, "compress_sequences": m,
                 "compress_config": "agg group (importance summed over each GQA group, kept "
                                    "set per KV head); compress_step_all_*: all-head importance; "
                                    "compress_step_fp8_us: agg group over an fp8 pool"})
     return res
+
+
+def cpu_compress_baseline(n_sample=4, budget_s=6.0):
+    """The oracle's compression step (the reference's chain: gather the window, bf16 SnapKV
+    scores, top-k, two-phase compaction) on the host cores, for n_sample of the 20 selected
+    sequences of the batch-500 state, scaled to the 20-sequence step."""
+    from oracle.compress_ref import compress_compact_ref
+    cw = wl_mod.compress_qwen3_8b(seed=3, device="cpu", selected_only=True)
+    sel = cw["seq_idx"][:n_sample]
+    kc, vc = cw["k_cache"], cw["v_cache"]
+    ts, t_end = [], time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(ts) < 2:
+        ctx = cw["context_lens"].clone()
+        t = time.perf_counter()
+        compress_compact_ref(cw["q"], kc, vc, cw["block_tables"], cw["context_lens"], ctx, sel,
+                             256, 4, 2, 1, 0, 1, score_dtype="bf16", agg="group")
+        ts.append(time.perf_counter() - t)
+    per_step = statistics.median(ts) * len(cw["seq_idx"]) / n_sample
+    return {"value": round(per_step * 1e6, 1), "unit": "us per step",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"oracle compress_compact_ref (torch CPU, bf16 scores, agg group) on "
+                      f"{n_sample} of the {len(cw['seq_idx'])} selected sequences, median of "
+                      f"{len(ts)} runs, scaled x{len(cw['seq_idx']) / n_sample:g}"}
 
 
 def prefill_flops(Lq, Lk, Hq, D=128):
@@ -369,7 +394,25 @@ def run_prefill_one(args, dev, name, wl):
                              torch.tensor([0, Lk_i], dtype=torch.int32), wl["scale"],
                              block_tables=bt2)
     err = float((out[r0:r0 + nq].float().cpu() - ref).abs().max())
+    extra = {}
+    if not args.no_cpu_baseline:
+        # the same oracle call timed on the host cores: the reference path's cost per flop
+        args_ref = (q[r0:r0 + nq].float().cpu(), kh, vh, torch.tensor([0, nq], dtype=torch.int32),
+                    torch.tensor([0, Lk_i], dtype=torch.int32), wl["scale"])
+        ts, t_end = [], time.perf_counter() + 6.0
+        while time.perf_counter() < t_end or len(ts) < 2:
+            t = time.perf_counter()
+            varlen_prefill_ref(*args_ref, block_tables=bt2)
+            ts.append(time.perf_counter() - t)
+        f_s = prefill_flops([nq], [Lk_i], wl["Hq"])
+        extra[f"{name}_cpu_baseline"] = {
+            "value": round(f_s / statistics.median(ts) / 1e12, 4), "unit": "TFLOP/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"oracle varlen_prefill_ref (fp32 torch CPU): the last {nq} queries of "
+                      f"one sequence over {Lk_i} paged keys ({f_s / 1e9:.1f} GFLOP), median "
+                      f"of {len(ts)} runs"}
     return {
+        **extra,
         f"{name}_us": round(pre_ms * 1e3, 1),
         f"{name}_tflops": round(tflops, 1),
         f"{name}_pct_mfma_peak": round(100.0 * tflops / MFMA_BF16_PEAK_TFLOPS, 1),
