@@ -60,3 +60,83 @@ def test_host_side_argument_checks_without_gpu():
     slots = (32 * 256 // 16 + 15) // 16 + 1
     assert lib.nkv_paged_decode_workspace_bytes(64, 32, 128, 32, 256) == \
         64 * 32 * slots * 130 * 4 + 64 * 32 * 4
+
+
+P = 0x10000  # a 16-byte aligned stand-in for a device pointer: never dereferenced, since
+# every case below is rejected by the host-side checks before anything is launched
+EINVAL, EWORKSPACE, EUNSUPPORTED = -1, -3, -4
+
+
+def _prefill(**kw):
+    a = dict(q=P, qrs=4096, k=P, v=P, krs=1024, vrs=1024, cq=P, ck=P, bt=None, btrs=0, mb=0,
+             n=1, mq=16, hq=32, hk=8, d=128, bs=256, rows=1000, scale=1.0, out=P, ors=4096)
+    a.update(kw)
+    return ("nkv_prefill_varlen", [a[x] for x in ("q", "qrs", "k", "v", "krs", "vrs", "cq", "ck",
+                                                   "bt", "btrs", "mb", "n", "mq", "hq", "hk",
+                                                   "d", "bs", "rows", "scale", "out", "ors")]
+            + [None])
+
+
+def _decode(fp8=False, **kw):
+    a = dict(q=P, qrs=4096, k=P, v=P, bt=P, btrs=32, ctx=P, b=4, hq=32, hk=8, d=128, bs=256,
+             mb=32, nb=100, scale=1.0, ks=1.0, vs=1.0, out=P, ors=4096, ws=P, wsb=1 << 30)
+    a.update(kw)
+    names = ["q", "qrs", "k", "v", "bt", "btrs", "ctx", "b", "hq", "hk", "d", "bs", "mb", "nb",
+             "scale"] + (["ks", "vs"] if fp8 else []) + ["out", "ors", "ws", "wsb"]
+    return ("nkv_paged_decode_fp8" if fp8 else "nkv_paged_decode", [a[x] for x in names] + [None])
+
+
+def _cstep(**kw):
+    a = dict(q=P, qrs=4096, k=P, v=P, bt=P, btrs=32, mb=32, base=P, ctx=P, sel=P, m=2, hq=32,
+             hk=8, d=128, bs=256, w=4, nb=100, scale=1.0, agg=1, keep=513, imp=P, keep_idx=P,
+             ws=P, wsb=1 << 30)
+    a.update(kw)
+    return ("nkv_compress_step", [a[x] for x in ("q", "qrs", "k", "v", "bt", "btrs", "mb", "base",
+                                                  "ctx", "sel", "m", "hq", "hk", "d", "bs", "w",
+                                                  "nb", "scale", "agg", "keep", "imp",
+                                                  "keep_idx", "ws", "wsb")] + [None])
+
+
+CASES = [
+    (_prefill(d=64), EUNSUPPORTED, b"head_dim"),
+    (_prefill(hq=16, hk=1), EUNSUPPORTED, b"GQA group"),
+    (_prefill(q=P + 2), EINVAL, b"aligned"),
+    (_prefill(qrs=1000), EINVAL, b"row strides"),
+    (_prefill(bt=P, btrs=4, mb=4, bs=8), EUNSUPPORTED, b"multiple of 16"),
+    (_prefill(bt=P, btrs=4, mb=4, vrs=2048), EINVAL, b"share one row stride"),
+    (_decode(hq=32, hk=1), EUNSUPPORTED, b"GQA group"),
+    (_decode(bs=8), EUNSUPPORTED, b"multiple of 16"),
+    (_decode(btrs=16), EINVAL, b"block table"),
+    (_decode(wsb=16), EWORKSPACE, b"workspace"),
+    (_decode(fp8=True, ks=0.0), EINVAL, b"scales"),
+    (_cstep(keep=2), EINVAL, b"keep_tokens"),
+    (_cstep(agg=7), EINVAL, b"agg_mode"),
+    (_cstep(hq=30), EINVAL, b"Hq % Hk"),
+    (("nkv_compress_schedule", [P, P, 20000, 256, 4, 20, 1, 0, P, P, P, P, None]),
+     EUNSUPPORTED, b"batch above"),
+    (("nkv_compress_schedule", [P, P, 64, 256, 4, 20, 1, 3, P, P, P, P, None]),
+     EINVAL, b"bad arguments"),
+    (("nkv_build_step_metadata", [P, 4, 256, 1, 4, 0, None, 0, 0, 3, P, P, P, P, P, P, P, P,
+                                  4, 4, None]), EINVAL, b""),
+    (("nkv_qk_norm_rope_store", [P, 4096, P, 1024, P, 1024, P, P, P, 1e-6, P, 4096, P, 4096,
+                                 None, P, P, P, 100, 8, 32, 8, 64, None]),
+     EUNSUPPORTED, b"head_dim"),
+    (("nkv_qk_norm_rope_store", [P, 4096, P, 1024, P, 1024, P, P, None, 1e-6, P, 4096, P,
+                                 4096, None, P, P, P, 100, 8, 32, 8, 128, None]), EINVAL, b""),
+    (("nkv_fp8_quantize", [P, 24, 1.0, P, None]), EINVAL, b""),
+    (("nkv_fp8_quantize", [P, 32, 0.0, P, None]), EINVAL, b""),
+    (("nkv_store_kvcache_fp8", [P, 1024, P, 1024, P, P, P, 8, 8, 128, 100, 0.0, 1.0, None]),
+     EINVAL, b""),
+]
+
+
+def test_entry_points_reject_bad_arguments_without_gpu():
+    """Each entry point validates sizes, strides, alignment, supported shapes and workspace
+    size on the host and returns its error code with a message, launching nothing."""
+    from importlib import import_module
+    lib = import_module("nanokv-llm_amd._lib").lib()
+    for (name, args), code, msg in CASES:
+        rc = getattr(lib, name)(*args)
+        err = lib.nkv_last_error()
+        assert rc == code, (name, rc, err)
+        assert msg in err and err, (name, err)
