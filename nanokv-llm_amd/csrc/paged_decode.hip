@@ -42,7 +42,8 @@ namespace nkv {
 
 constexpr int kD = 128;                  // head_dim
 constexpr int kChunk = 16;               // tokens per pipeline stage
-constexpr int kMinChunks = 16;           // minimum chunks per wave range
+constexpr int kMinChunks = 4;            // minimum chunks per wave range
+constexpr int kMaxSlots = 64;            // partials per (sequence, query head) at most
 constexpr int kWinBlocks = 64;           // block ids held per window (one per lane)
 constexpr int kVRow = kD + 16;           // LDS row stride of a staged V chunk (elements)
 constexpr int kBufferFlags = 0x00020000; // raw buffer resource word 3 (dword data)
@@ -52,11 +53,22 @@ typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
 typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
 
-// Partial slots per (sequence, query head): a head of n chunks is touched by
-// at most ceil(n / kMinChunks) + 1 waves.
+// Partial slots per (sequence, query head): a segment of n chunks is touched by at most
+// ceil(n / C) + 1 waves, and the kernel takes C >= decode_min_chunks, which is at least
+// kMinChunks and at least max_chunks / (slots - 1), so no segment has more than kMaxSlots
+// partials (the combine merges up to 64 with one lane each).
 static inline int64_t decode_slots(int32_t max_blocks, int32_t block_size) {
   const int64_t max_chunks = ((int64_t)max_blocks * block_size + kChunk - 1) / kChunk;
-  return (max_chunks + kMinChunks - 1) / kMinChunks + 1;
+  const int64_t s = (max_chunks + kMinChunks - 1) / kMinChunks + 1;
+  return s < kMaxSlots ? s : kMaxSlots;
+}
+// The smallest range a wave takes: kMinChunks, or longer when the table width allows
+// segments that would otherwise need more than `slots` partials.
+static inline int32_t decode_min_chunks(int32_t max_blocks, int32_t block_size) {
+  const int64_t max_chunks = ((int64_t)max_blocks * block_size + kChunk - 1) / kChunk;
+  const int64_t slots = decode_slots(max_blocks, block_size);
+  const int64_t c = (max_chunks + slots - 2) / (slots - 1);
+  return (int32_t)(c > kMinChunks ? c : kMinChunks);
 }
 
 __device__ __forceinline__ int wave_incl_scan(int v) {
@@ -106,8 +118,8 @@ void paged_decode_split_kernel(
     const void* __restrict__ k_cache, const void* __restrict__ v_cache,
     const int32_t* __restrict__ block_tables, int64_t bt_row_stride,
     const int32_t* __restrict__ context_lens, int32_t batch, int32_t Hk,
-    int32_t block_size, int32_t max_blocks, int64_t n_blocks, int32_t slots, float scale_log2,
-    float v_scale, float* __restrict__ part_o, float* __restrict__ part_ml,
+    int32_t block_size, int32_t max_blocks, int64_t n_blocks, int32_t slots, int32_t min_chunks,
+    float scale_log2, float v_scale, float* __restrict__ part_o, float* __restrict__ part_ml,
     int32_t* __restrict__ nslots) {
   static_assert(HP == 1 || HP * G <= 16, "HP heads of G query heads must fit 16 columns");
   constexpr int kEl = F8 ? 1 : 2;              // bytes per cache element
@@ -142,7 +154,9 @@ void paged_decode_split_kernel(
     seq_load(cur, context_lens, batch, max_tokens);
     T += cur.tot;
   }
-  const int C = max((T + Wh - 1) / Wh, kMinChunks);
+  // equal ranges over the resident waves, at least min_chunks (which keeps every
+  // segment within its partial slots)
+  const int C = max((T + Wh - 1) / Wh, min_chunks);
   const int k_begin = wi * C;
   if (k_begin >= T) return;
   const int k_end = min(T, k_begin + C);
@@ -543,7 +557,8 @@ static int decode_split(const void* q, int64_t q_row_stride, const void* k_cache
                                                  (n_kv_heads / HP))),                         \
                      dim3(64), 0, s, (const bf16_t*)q, q_row_stride, k_cache, v_cache,        \
                      block_tables, bt_row_stride, context_lens, batch, n_kv_heads, block_size, \
-                     max_blocks_per_seq, n_blocks, (int32_t)slots, scale_log2, v_scale,       \
+                     max_blocks_per_seq, n_blocks, (int32_t)slots,                            \
+                     decode_min_chunks(max_blocks_per_seq, block_size), scale_log2, v_scale,  \
                      w.part_o, w.part_ml, w.nslots)
   if (pair) {
     switch (g) {
