@@ -550,15 +550,22 @@ static int decode_split(const void* q, int64_t q_row_stride, const void* k_cache
   // table width: >= 32 chunks per head pair per resident wave); otherwise one.
   const int64_t work = (int64_t)batch * max_chunks * n_kv_heads;
   const bool pair = n_kv_heads % 2 == 0 && g <= 8 && work >= 32 * (int64_t)decode_grid<4, F8, 2>();
+  // Resident waves per head group, but no more than the table width lets receive a range
+  // of min_chunks (small batches launch only the waves that can get work).
+  const int32_t min_chunks = decode_min_chunks(max_blocks_per_seq, block_size);
+  const int64_t useful = std::max<int64_t>(1, (batch * max_chunks + min_chunks - 1) / min_chunks);
+  auto grid_of = [&](int resident, int hp) {
+    const int np = n_kv_heads / hp;
+    const int64_t per = std::min<int64_t>(std::max(1, resident / np), useful);
+    return (unsigned)(per * np);
+  };
 #define NKV_DECODE_LAUNCH(G, HP)                                                              \
   hipLaunchKernelGGL((paged_decode_split_kernel<G, F8, HP>),                                  \
-                     dim3((unsigned)std::max(n_kv_heads / HP,                                 \
-                                             decode_grid<G, F8, HP>() / (n_kv_heads / HP) *   \
-                                                 (n_kv_heads / HP))),                         \
+                     dim3(grid_of(decode_grid<G, F8, HP>(), HP)),                             \
                      dim3(64), 0, s, (const bf16_t*)q, q_row_stride, k_cache, v_cache,        \
                      block_tables, bt_row_stride, context_lens, batch, n_kv_heads, block_size, \
-                     max_blocks_per_seq, n_blocks, (int32_t)slots,                            \
-                     decode_min_chunks(max_blocks_per_seq, block_size), scale_log2, v_scale,  \
+                     max_blocks_per_seq, n_blocks, (int32_t)slots, min_chunks, scale_log2,    \
+                     v_scale,                                                                 \
                      w.part_o, w.part_ml, w.nslots)
   if (pair) {
     switch (g) {
