@@ -43,7 +43,7 @@ namespace nkv {
 constexpr int kD = 128;                  // head_dim
 constexpr int kChunk = 16;               // tokens per pipeline stage
 constexpr int kMinChunks = 4;            // minimum chunks per wave range
-constexpr int kMaxSlots = 64;            // partials per (sequence, query head) at most
+constexpr int kMaxSlots = 128;           // partials per (sequence, query head) at most
 constexpr int kWinBlocks = 64;           // block ids held per window (one per lane)
 constexpr int kVRow = kD + 16;           // LDS row stride of a staged V chunk (elements)
 constexpr int kBufferFlags = 0x00020000; // raw buffer resource word 3 (dword data)
@@ -56,7 +56,7 @@ typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
 // Partial slots per (sequence, query head): a segment of n chunks is touched by at most
 // ceil(n / C) + 1 waves, and the kernel takes C >= decode_min_chunks, which is at least
 // kMinChunks and at least max_chunks / (slots - 1), so no segment has more than kMaxSlots
-// partials (the combine merges up to 64 with one lane each).
+// partials (the combine holds up to 128, two per lane).
 static inline int64_t decode_slots(int32_t max_blocks, int32_t block_size) {
   const int64_t max_chunks = ((int64_t)max_blocks * block_size + kChunk - 1) / kChunk;
   const int64_t s = (max_chunks + kMinChunks - 1) / kMinChunks + 1;
@@ -371,9 +371,7 @@ void paged_decode_split_kernel(
 }
 
 // Merge the partials of one (sequence, query head): O = sum_s 2^(m_s-M) O_s /
-// sum_s 2^(m_s-M) l_s. One wave per pair: lane s reads partial s's (m, l),
-// the weights are combined with wave reductions, then each lane accumulates
-// two output dims over the partials (all loads independent).
+// sum_s 2^(m_s-M) l_s. One wave per pair.
 __global__ __launch_bounds__(64) void paged_decode_combine_kernel(
     const int32_t* __restrict__ context_lens, int32_t Hq, int32_t Hk, int32_t slots,
     const float* __restrict__ part_o, const float* __restrict__ part_ml,
@@ -390,47 +388,34 @@ __global__ __launch_bounds__(64) void paged_decode_combine_kernel(
     *reinterpret_cast<uint32_t*>(op) = 0u;
     return;
   }
-  float o0 = 0.f, o1 = 0.f, L = 0.f;
+  // lane l holds partials l and l + 64 (ns <= kMaxSlots = 128): the global max and
+  // the weights w_s = 2^(m_s - M) with two wave reductions, then each lane
+  // accumulates two output dims over the partials, eight loads in flight
+  static_assert(kMaxSlots <= 128, "two partials per lane");
   const float* po = part_o + base * kD + 2 * lane;
-  // pass 1: the global max over all partials
-  float M = -INFINITY;
-  for (int s = lane; s < ns; s += 64) M = fmaxf(M, part_ml[(base + s) * 2]);
-  M = wave_max(M);
-  // pass 2: weights (lane s holds w_s for s < 64) and the weighted sums
-  const int n1 = min(ns, 64);
-  float wl = 0.f;
-  if (lane < n1) {
-    const float2 ml = *reinterpret_cast<const float2*>(&part_ml[(base + lane) * 2]);
-    wl = (ml.x == -INFINITY) ? 0.f : fast_exp2(ml.x - M);
-    L = wl * ml.y;
-  }
-  for (int s = 64 + lane; s < ns; s += 64) {
-    const float2 ml = *reinterpret_cast<const float2*>(&part_ml[(base + s) * 2]);
-    L += (ml.x == -INFINITY) ? 0.f : fast_exp2(ml.x - M) * ml.y;
-  }
-  L = wave_sum(L);
+  float2 ml0 = {-INFINITY, 0.f}, ml1 = {-INFINITY, 0.f};
+  if (lane < ns) ml0 = *reinterpret_cast<const float2*>(&part_ml[(base + lane) * 2]);
+  if (lane + 64 < ns) ml1 = *reinterpret_cast<const float2*>(&part_ml[(base + lane + 64) * 2]);
+  const float M = wave_max(fmaxf(ml0.x, ml1.x));
+  const float w0 = (ml0.x == -INFINITY) ? 0.f : fast_exp2(ml0.x - M);
+  const float w1 = (ml1.x == -INFINITY) ? 0.f : fast_exp2(ml1.x - M);
+  const float L = wave_sum(w0 * ml0.y + w1 * ml1.y);
+  float o0 = 0.f, o1 = 0.f;
   int s = 0;
-  for (; s + 4 <= n1; s += 4) {
-    float2 v[4];
+  for (; s + 8 <= ns; s += 8) {
+    float2 v[8];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const float2*>(po + (int64_t)(s + u) * kD);
+    for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const float2*>(po + (int64_t)(s + u) * kD);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const float w = __shfl(wl, s + u, 64);
+    for (int u = 0; u < 8; ++u) {
+      const float w = __shfl(s + u < 64 ? w0 : w1, (s + u) & 63, 64);  // uniform select
       o0 = fmaf(w, v[u].x, o0);
       o1 = fmaf(w, v[u].y, o1);
     }
   }
-  for (; s < n1; ++s) {
+  for (; s < ns; ++s) {
     const float2 v = *reinterpret_cast<const float2*>(po + (int64_t)s * kD);
-    const float w = __shfl(wl, s, 64);
-    o0 = fmaf(w, v.x, o0);
-    o1 = fmaf(w, v.y, o1);
-  }
-  for (; s < ns; ++s) {  // more than 64 partials (very long contexts)
-    const float ms = part_ml[(base + s) * 2];
-    const float w = (ms == -INFINITY) ? 0.f : fast_exp2(ms - M);
-    const float2 v = *reinterpret_cast<const float2*>(po + (int64_t)s * kD);
+    const float w = __shfl(s < 64 ? w0 : w1, s & 63, 64);
     o0 = fmaf(w, v.x, o0);
     o1 = fmaf(w, v.y, o1);
   }

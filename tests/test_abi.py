@@ -57,8 +57,8 @@ def test_host_side_argument_checks_without_gpu():
     # zero tokens is a no-op
     assert lib.nkv_store_kvcache(None, 0, None, 0, None, None, None, 0, 8, 128, 0, None) == 0
     # workspace sizing is pure host arithmetic: partial slots per (sequence, query head) =
-    # min(64, ceil(chunks of the table width / 4) + 1)
-    for width, slots in ((32, 64), (2, 9)):
+    # min(128, ceil(chunks of the table width / 4) + 1)
+    for width, slots in ((32, 128), (16, 65), (2, 9)):
         assert lib.nkv_paged_decode_workspace_bytes(64, 32, 128, width, 256) == \
             64 * 32 * slots * 130 * 4 + 64 * 32 * 4
 

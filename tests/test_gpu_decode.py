@@ -163,3 +163,12 @@ def test_decode_64_block_window_boundary(nkv, dev):
     vc = torch.randn(nb, B, Hk, D, generator=g).to(torch.bfloat16)
     q = torch.randn(4, Hq, D, generator=g).to(torch.bfloat16)
     _check(nkv, dev, q, kc, vc, ctx, bt, D ** -0.5)
+
+
+@pytest.mark.parametrize("Hq,Hk", [(32, 8), (16, 2)])
+def test_decode_one_long_sequence_many_partials(nkv, dev, Hq, Hk):
+    """One 30k-token sequence: its chunk stream is split over ~120 waves per head group, so
+    the combine merges more than 64 partials per query head (two per lane)."""
+    wl = wl_mod.decode_workload(1, Hq, Hk, 29000, 30500, 130, seed=8)
+    _check(nkv, dev, wl["q"], wl["k_cache"], wl["v_cache"], wl["context_lens"],
+           wl["block_tables"][0], wl["scale"])
