@@ -379,10 +379,24 @@ __global__ __launch_bounds__(64) void paged_decode_combine_kernel(
   const int b = blockIdx.x / Hq;
   const int h = blockIdx.x % Hq;
   const int lane = threadIdx.x;
+  const int64_t base = ((int64_t)b * Hq + h) * slots;
+  const float* po = part_o + base * kD + 2 * lane;
+  // Every load is issued before any of them is used: the partial count, the context
+  // length, the (m, l) pair of every slot and the first eight partial rows. All `slots`
+  // entries of a (sequence, head) lie inside the workspace whatever the count, so the
+  // entries past it are read (unwritten or stale) and dropped by the selects below; one
+  // memory round trip instead of three dependent ones.
+  static_assert(kMaxSlots <= 128, "two partials per lane");
   const int ctx = context_lens[b];
   const int cnt = nslots[(int64_t)b * Hk + h / (Hq / Hk)];
+  float2 ml0 = {-INFINITY, 0.f}, ml1 = {-INFINITY, 0.f};
+  if (lane < slots) ml0 = *reinterpret_cast<const float2*>(&part_ml[(base + lane) * 2]);
+  if (lane + 64 < slots) ml1 = *reinterpret_cast<const float2*>(&part_ml[(base + lane + 64) * 2]);
+  float2 v0[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u)
+    v0[u] = u < slots ? *reinterpret_cast<const float2*>(po + (int64_t)u * kD) : float2{0.f, 0.f};
   const int ns = ctx > 0 ? min(cnt, slots) : 0;
-  const int64_t base = ((int64_t)b * Hq + h) * slots;
   bf16_t* op = out + (int64_t)b * out_row_stride + (int64_t)h * kD + 2 * lane;
   if (ns == 0) {
     *reinterpret_cast<uint32_t*>(op) = 0u;
@@ -391,17 +405,22 @@ __global__ __launch_bounds__(64) void paged_decode_combine_kernel(
   // lane l holds partials l and l + 64 (ns <= kMaxSlots = 128): the global max and
   // the weights w_s = 2^(m_s - M) with two wave reductions, then each lane
   // accumulates two output dims over the partials, eight loads in flight
-  static_assert(kMaxSlots <= 128, "two partials per lane");
-  const float* po = part_o + base * kD + 2 * lane;
-  float2 ml0 = {-INFINITY, 0.f}, ml1 = {-INFINITY, 0.f};
-  if (lane < ns) ml0 = *reinterpret_cast<const float2*>(&part_ml[(base + lane) * 2]);
-  if (lane + 64 < ns) ml1 = *reinterpret_cast<const float2*>(&part_ml[(base + lane + 64) * 2]);
+  if (lane >= ns) ml0 = {-INFINITY, 0.f};
+  if (lane + 64 >= ns) ml1 = {-INFINITY, 0.f};
   const float M = wave_max(fmaxf(ml0.x, ml1.x));
   const float w0 = (ml0.x == -INFINITY) ? 0.f : fast_exp2(ml0.x - M);
   const float w1 = (ml1.x == -INFINITY) ? 0.f : fast_exp2(ml1.x - M);
   const float L = wave_sum(w0 * ml0.y + w1 * ml1.y);
   float o0 = 0.f, o1 = 0.f;
-  int s = 0;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const float w = __shfl(w0, u, 64);
+    if (u < ns) {  // uniform
+      o0 = fmaf(w, v0[u].x, o0);
+      o1 = fmaf(w, v0[u].y, o1);
+    }
+  }
+  int s = 8;
   for (; s + 8 <= ns; s += 8) {
     float2 v[8];
 #pragma unroll
