@@ -105,6 +105,23 @@ def check(rc: int, what: str) -> None:
         raise NkvError(f"{what} failed (code {rc}): {msg}")
 
 
+def require_device(device: torch.device, **tensors: torch.Tensor | None) -> None:
+    """The kernels take raw device pointers: every tensor given must be a GPU tensor on
+    ``device`` (None entries are skipped). Raises ValueError naming the first that is not,
+    before anything reaches the library."""
+    if device.type != "cuda":
+        raise ValueError(f"expected GPU tensors, got a tensor on {device}")
+    for name, t in tensors.items():
+        if t is not None and t.device != device:
+            raise ValueError(f"{name} is on {t.device}, expected {device}")
+
+
+def need(cond: bool, msg: str) -> None:
+    """Argument check that survives ``python -O``: raises ValueError(msg)."""
+    if not cond:
+        raise ValueError(msg)
+
+
 def stream_of(t: torch.Tensor) -> int:
     """HIP stream handle of torch's current stream on t's device."""
     return torch.cuda.current_stream(t.device).cuda_stream

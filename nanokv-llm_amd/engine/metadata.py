@@ -88,6 +88,10 @@ def build_step_metadata(starts: list[int], num_new: list[int], tables: list[list
     """Metadata of one step for sequences s scheduling num_new[s] tokens from KV position
     starts[s]; returns device tensors plus host ints max_seqlen_q / max_seqlen_k. With a
     ``store`` (and the sequences' ``seq_ids``) only changed table entries are sent."""
+    device = torch.device(device)
+    if device.type == "cuda" and device.index is None:
+        device = torch.device("cuda", torch.cuda.current_device())
+    _lib.require_device(device, table=store.table if store is not None else None)
     n = len(starts)
     if len(num_new) != n or len(tables) != n or (pos_offsets is not None and len(pos_offsets) != n):
         raise ValueError("starts, num_new, tables (and pos_offsets) need one entry per sequence")

@@ -29,6 +29,11 @@ def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
     """
     N, num_heads, head_dim = key.shape
     D = num_heads * head_dim
+    _lib.require_device(key.device, value=value, k_cache=k_cache, v_cache=v_cache,
+                        slot_mapping=slot_mapping)
+    _lib.need(value.shape == key.shape, "store_kvcache: value shape differs from key")
+    _lib.need(v_cache.shape == k_cache.shape and v_cache.dtype == k_cache.dtype,
+              "store_kvcache: v_cache shape/dtype differ from k_cache")
     assert key.stride(-1) == 1 and value.stride(-1) == 1
     assert key.stride(1) == head_dim and value.stride(1) == head_dim
     assert k_cache.stride(1) == D and v_cache.stride(1) == D
@@ -51,9 +56,20 @@ def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
     _lib.check(rc, "store_kvcache")
 
 
-def _decode_args(q, k_cache, block_tables, context_lens):
+def _decode_args(q, k_cache, block_tables, context_lens, v_cache=None, out=None):
+    _lib.require_device(q.device, k_cache=k_cache, v_cache=v_cache, block_tables=block_tables,
+                        context_lens=context_lens, out=out)
     bs, Hq, D = q.shape
     NB, B, Hk, Dk = k_cache.shape
+    _lib.need(q.dtype == _BF16, "paged_decode: q must be bf16")
+    if v_cache is not None:
+        _lib.need(v_cache.shape == k_cache.shape and v_cache.dtype == k_cache.dtype
+                  and v_cache.is_contiguous(),
+                  "paged_decode: v_cache must be contiguous with k_cache's shape and dtype")
+    if out is not None:
+        _lib.need(out.shape == q.shape and out.dtype == _BF16 and out.stride(-1) == 1
+                  and out.stride(1) == D, "paged_decode: out must be bf16 [bs, Hq, D], "
+                  "rows of contiguous heads")
     assert Dk == D and q.stride(-1) == 1 and q.stride(1) == D
     assert k_cache.is_contiguous()
     assert block_tables.dtype == torch.int32 and block_tables.stride(1) == 1
@@ -82,7 +98,7 @@ def paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     causal=True) at attention.py:104-107. fp8 (float8_e4m3fn) caches are read
     as code * k_scale / code * v_scale.
     """
-    bs, Hq, D, NB, B, Hk = _decode_args(q, k_cache, block_tables, context_lens)
+    bs, Hq, D, NB, B, Hk = _decode_args(q, k_cache, block_tables, context_lens, v_cache, out)
     if out is None:
         out = torch.empty(bs, Hq, D, dtype=_BF16, device=q.device)
     if workspace is None:
@@ -119,9 +135,20 @@ def varlen_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     flash_attn_varlen_func(..., causal=True, block_table) at attention.py:96-102.
     """
     N, Hq, D = q.shape
+    _lib.require_device(q.device, k=k, v=v, cu_seqlens_q=cu_seqlens_q, cu_seqlens_k=cu_seqlens_k,
+                        block_tables=block_tables, out=out)
     assert q.stride(-1) == 1 and q.stride(1) == D
     assert cu_seqlens_q.dtype == torch.int32 and cu_seqlens_k.dtype == torch.int32
     n_seqs = cu_seqlens_q.numel() - 1
+    _lib.need(q.dtype == _BF16, "varlen_prefill: q must be bf16")
+    _lib.need(cu_seqlens_k.numel() == n_seqs + 1 and cu_seqlens_q.is_contiguous()
+              and cu_seqlens_k.is_contiguous(),
+              "varlen_prefill: cu_seqlens_q/k must be contiguous, one entry per sequence + 1")
+    _lib.need(v.dtype == k.dtype, "varlen_prefill: k and v dtypes differ")
+    if out is not None:
+        _lib.need(out.shape == q.shape and out.dtype == _BF16 and out.stride(-1) == 1
+                  and out.stride(1) == D, "varlen_prefill: out must be bf16 shaped like q, "
+                  "rows of contiguous heads")
     if block_tables is not None and k.dtype == torch.float8_e4m3fn:
         # fp8 pool: each sequence's rows widened into contiguous bf16, then the contiguous path
         if max_seqlen_k is None:
@@ -142,6 +169,7 @@ def varlen_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     if block_tables is not None:
         NB, B, Hk, Dk = k.shape
         assert k.is_contiguous() and v.is_contiguous() and v.shape == k.shape
+        _lib.need(k.dtype == _BF16, "varlen_prefill: paged caches must be bf16 or fp8")
         k_row_stride = v_row_stride = Hk * Dk
         n_rows = NB * B
         bt_ptr, bt_stride = block_tables.data_ptr(), block_tables.stride(0)
@@ -150,6 +178,7 @@ def varlen_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     else:
         _, Hk, Dk = k.shape
         assert v.shape == k.shape
+        _lib.need(k.dtype == _BF16, "varlen_prefill: contiguous k/v must be bf16")
         assert k.stride(1) == Dk and k.stride(2) == 1 and v.stride(1) == Dk and v.stride(2) == 1
         k_row_stride, v_row_stride = k.stride(0), v.stride(0)
         n_rows = k.size(0)

@@ -56,6 +56,47 @@ def _buffers(context, selected, device, m, n_sets, n_cand, keep_tokens, ws_bytes
     return buf
 
 
+def _check_window_args(what, q, k_cache, v_cache, block_tables, base_context_lens,
+                       context_lens, seq_idx, importance, keep_idx, workspace, n_sets, n_cand,
+                       keep_cols):
+    """Device, dtype and shape checks shared by the compression wrappers: the library
+    takes raw pointers and the geometry of k_cache, so every other tensor must agree."""
+    _lib.require_device(k_cache.device, q=q, v_cache=v_cache, block_tables=block_tables,
+                        base_context_lens=base_context_lens, context_lens=context_lens,
+                        seq_idx=seq_idx, importance=importance, keep_idx=keep_idx,
+                        workspace=workspace)
+    for name, t in (("block_tables", block_tables), ("base_context_lens", base_context_lens),
+                    ("context_lens", context_lens), ("seq_idx", seq_idx),
+                    ("keep_idx", keep_idx)):
+        if t is not None:
+            _lib.need(t.dtype == torch.int32, f"{what}: {name} must be int32")
+    _lib.need(block_tables.stride(1) == 1 and seq_idx.is_contiguous()
+              and base_context_lens.is_contiguous(),
+              f"{what}: block table rows, seq_idx and base_context_lens must be contiguous")
+    _lib.need(context_lens is None or context_lens.is_contiguous(),
+              f"{what}: context_lens must be contiguous")
+    if v_cache is not None:
+        _lib.need(v_cache.shape == k_cache.shape and v_cache.dtype == k_cache.dtype,
+                  f"{what}: v_cache shape/dtype differ from k_cache")
+    _lib.need(k_cache.is_contiguous() and (v_cache is None or v_cache.is_contiguous()),
+              f"{what}: caches must be contiguous")
+    if q is not None:
+        D = k_cache.size(-1)
+        _lib.need(q.dtype == torch.bfloat16 and q.stride(-1) == 1 and q.stride(1) == D,
+                  f"{what}: q must be bf16 rows of contiguous heads")
+    m = seq_idx.numel()
+    if importance is not None:
+        _lib.need(importance.dtype == torch.float32 and importance.is_contiguous()
+                  and importance.shape == (m, n_sets, n_cand),
+                  f"{what}: importance must be contiguous fp32 [{m}, {n_sets}, {n_cand}]")
+    if keep_idx is not None and keep_cols is not None:
+        _lib.need(keep_idx.is_contiguous() and keep_idx.shape == (m, n_sets, keep_cols),
+                  f"{what}: keep_idx must be contiguous int32 [{m}, {n_sets}, {keep_cols}]")
+    if workspace is not None:
+        _lib.need(workspace.dtype == torch.uint8 and workspace.is_contiguous(),
+                  f"{what}: workspace must be contiguous uint8")
+
+
 def select_workspace_bytes(m, n_q_heads, n_kv_heads, window_blocks, block_size):
     """Bytes of the workspace nkv_compress_select needs."""
     return _lib.lib().nkv_compress_select_workspace_bytes(m, n_q_heads, n_kv_heads,
@@ -75,6 +116,8 @@ def compress_select(q, k_cache, block_tables, base_context_lens, seq_idx, window
     Hq = q.size(1)
     n_sets = 1 if agg == "all" else Hk
     n_cand = window_blocks * B - 1
+    _check_window_args("compress_select", q, k_cache, None, block_tables, base_context_lens, None,
+                       seq_idx, importance, keep_idx, workspace, n_sets, n_cand, num_keep + 2)
     L = _lib.lib()
     if importance is None:
         importance = torch.empty(m, n_sets, n_cand, dtype=torch.float32, device=q.device)
@@ -98,6 +141,10 @@ def compress_compact(k_cache, v_cache, block_tables, base_context_lens, context_
     """Move the kept window rows (and the tail block) into place, K and V."""
     NB, B, Hk, D = k_cache.shape
     m, n_sets, keep_tokens = keep_idx.shape
+    _check_window_args("compress_compact", None, k_cache, v_cache, block_tables,
+                       base_context_lens, context_lens, seq_idx, None, keep_idx, None, n_sets,
+                       None, keep_tokens)
+    _lib.need(m == seq_idx.numel(), "compress_compact: keep_idx needs one row per seq_idx entry")
     rc = _lib.lib().nkv_compress_compact(
         k_cache.data_ptr(), v_cache.data_ptr(), block_tables.data_ptr(), block_tables.stride(0),
         block_tables.size(1), base_context_lens.data_ptr(), context_lens.data_ptr(),
@@ -119,6 +166,9 @@ def compress_step(q, k_cache, v_cache, block_tables, base_context_lens, context_
     Hq = q.size(1)
     n_sets = 1 if agg == "all" else Hk
     n_cand = window_blocks * B - 1
+    _check_window_args("compress_step", q, k_cache, v_cache, block_tables, base_context_lens,
+                       context_lens, seq_idx, importance, keep_idx, workspace, n_sets, n_cand,
+                       keep_tokens)
     if importance is None:
         importance = torch.empty(m, n_sets, n_cand, dtype=torch.float32, device=q.device)
     if keep_idx is None:
@@ -148,6 +198,11 @@ def compress_step(q, k_cache, v_cache, block_tables, base_context_lens, context_
 
 def compress_finalize(block_tables, base_context_lens, seq_idx, keep_tokens, block_size,
                       window_blocks, events, rewrite_tables=True, slot_mapping=None):
+    _lib.require_device(block_tables.device, base_context_lens=base_context_lens,
+                        seq_idx=seq_idx, events=events, slot_mapping=slot_mapping)
+    _lib.need(all(t.dtype == torch.int32 for t in (block_tables, base_context_lens, seq_idx,
+                                                   events)),
+              "compress_finalize: tables, lengths, seq_idx and events must be int32")
     rc = _lib.lib().nkv_compress_finalize(
         block_tables.data_ptr(), block_tables.stride(0), block_tables.size(1),
         base_context_lens.data_ptr(), seq_idx.data_ptr(), seq_idx.numel(), keep_tokens,
@@ -242,6 +297,9 @@ def compress_schedule(context_lens, tail_uncompressed, block_size, window_blocks
     ``n_selected`` and ``base_context_lens`` without reading anything on the host."""
     bs = context_lens.numel()
     assert tail_uncompressed.numel() >= bs and seq_idx.numel() == topk
+    _lib.require_device(context_lens.device, tail_uncompressed=tail_uncompressed,
+                        step_counter=step_counter, seq_idx=seq_idx, n_selected=n_selected,
+                        base_context_lens=base_context_lens)
     rc = _lib.lib().nkv_compress_schedule(
         context_lens.data_ptr(), tail_uncompressed.data_ptr(), bs, block_size, window_blocks,
         topk, period, {"first": 0, "longest": 1}[policy], step_counter.data_ptr(),

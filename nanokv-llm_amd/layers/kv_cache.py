@@ -26,8 +26,11 @@ def is_fp8(t: torch.Tensor) -> bool:
 def fp8_quantize(x: torch.Tensor, scale: float = 1.0, out: torch.Tensor | None = None):
     """bf16 -> E4M3FN codes of clamp(x * (1/scale), -448, 448) (NaN kept)."""
     assert x.dtype == torch.bfloat16 and x.is_contiguous() and x.numel() % 16 == 0
+    _lib.require_device(x.device, out=out)
     if out is None:
         out = torch.empty(x.shape, dtype=FP8, device=x.device)
+    _lib.need(out.element_size() == 1 and out.is_contiguous() and out.numel() == x.numel(),
+              "fp8_quantize: out must be contiguous 1-byte codes, one per element")
     rc = _lib.lib().nkv_fp8_quantize(x.data_ptr(), x.numel(), float(scale), out.data_ptr(),
                                      _lib.stream_of(x))
     _lib.check(rc, "fp8_quantize")
@@ -37,8 +40,11 @@ def fp8_quantize(x: torch.Tensor, scale: float = 1.0, out: torch.Tensor | None =
 def fp8_dequantize(codes: torch.Tensor, scale: float = 1.0, out: torch.Tensor | None = None):
     """E4M3FN codes -> bf16(value * scale)."""
     assert codes.element_size() == 1 and codes.is_contiguous() and codes.numel() % 16 == 0
+    _lib.require_device(codes.device, out=out)
     if out is None:
         out = torch.empty(codes.shape, dtype=torch.bfloat16, device=codes.device)
+    _lib.need(out.dtype == torch.bfloat16 and out.is_contiguous() and out.numel() == codes.numel(),
+              "fp8_dequantize: out must be contiguous bf16, one per code")
     rc = _lib.lib().nkv_fp8_dequantize(codes.data_ptr(), codes.numel(), float(scale),
                                        out.data_ptr(), _lib.stream_of(codes))
     _lib.check(rc, "fp8_dequantize")

@@ -46,6 +46,9 @@ def qk_norm_rope_store(positions: torch.Tensor, q: torch.Tensor, k: torch.Tensor
     """
     N, Hq, D = q.shape
     Hk = k.size(1)
+    _lib.require_device(q.device, k=k, v=v, positions=positions, cos_sin_cache=cos_sin_cache,
+                        q_norm_weight=q_norm_weight, k_norm_weight=k_norm_weight,
+                        k_cache=k_cache, v_cache=v_cache, slot_mapping=slot_mapping, q_out=q_out)
     q_ptr, q_rs = _rows(q, Hq, D)
     k_ptr, k_rs = _rows(k, Hk, D)
     assert k.size(0) == N and positions.dtype == torch.int64 and positions.is_contiguous()
@@ -61,6 +64,7 @@ def qk_norm_rope_store(positions: torch.Tensor, q: torch.Tensor, k: torch.Tensor
     if q_out is None:
         q_out = torch.empty(N, Hq, D, dtype=_BF16, device=q.device)
     _rows(q_out, Hq, D)
+    _lib.need(q_out.size(0) == N, "qk_norm_rope_store: q_out needs one row per token")
     store = k_cache is not None and k_cache.numel() > 0
     k_out = torch.empty(N, Hk, D, dtype=_BF16, device=q.device) if (need_k or not store) else None
     v_ptr, v_rs = (0, 0)
@@ -68,6 +72,7 @@ def qk_norm_rope_store(positions: torch.Tensor, q: torch.Tensor, k: torch.Tensor
     if store:
         assert v is not None and slot_mapping is not None
         v_ptr, v_rs = _rows(v, Hk, D)
+        _lib.need(v.size(0) == N, "qk_norm_rope_store: v needs one row per token")
         assert k_cache.dtype == _BF16 and v_cache.dtype == _BF16
         assert k_cache.is_contiguous() and v_cache.is_contiguous()
         assert k_cache.size(-1) == D and k_cache.size(-2) == Hk and v_cache.shape == k_cache.shape
