@@ -377,6 +377,10 @@ __device__ __forceinline__ void block_select(SelectLds& L, int n_cand, int num_k
     const uint64_t ok = __builtin_amdgcn_ballot_w64(lane >= 1 && lane < 16 && tot >= num_keep);
     const int digit = ok ? 63 - __builtin_clzll(ok) : 0;
     T += (uint32_t)digit << shift;
+    // Exactly num_keep keys are >= T: the kept set is {key >= T}, the set the remaining
+    // passes would give (they only raise T to the smallest of those keys), so stop.
+    // Every wave reads the same counts, so all leave at the same pass.
+    if (digit > 0 && __shfl(tot, digit, 64) == num_keep) break;
   }
   const bool gt = real && key > T;
   const bool eq = real && key == T;
