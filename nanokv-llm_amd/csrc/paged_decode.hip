@@ -13,8 +13,8 @@
 //    bytes whatever the context-length mix. A range crosses at most a few
 //    (sequence, head group) segments; each segment it touches yields one
 //    partial (m, l, O) per query head in slot  wave - first_wave_of_the_segment.
-//    A head group is one KV head, or two (HP = 2) whose halves of every token
-//    row are read as one contiguous piece.
+//    A head group is one KV head, or two (HP = 2; four for fp8 rows, HP = 4)
+//    whose parts of every token row are read as one contiguous piece.
 //  * Within a segment the wave streams chunks through a register ring (4
 //    chunks of 256-byte rows, or 2 of 512-byte rows): K and V of the chunk one
 //    ring ahead are issued as soon as a chunk has been consumed. Loads are
@@ -108,9 +108,11 @@ __device__ __forceinline__ void seq_load(SeqCursor& c, const int32_t* __restrict
 // token row as one contiguous piece (512 B bf16, 256 B fp8) instead of one
 // head's 256 B: on this part a stream of 256-byte pieces at 2 KiB stride runs
 // unevenly (pieces at odd 256-byte offsets come back later), and the waves of
-// the slow heads set the kernel's length. The 2G query heads fill MFMA columns
-// 0..2G-1; each head's scores use its own K, the softmax weights of a column
-// are zero for the other head, so both heads' PV products add into one O^T.
+// the slow heads set the kernel's length. The HP*G query heads fill MFMA columns
+// 0..HP*G-1; each head's scores use its own K, the softmax weights of a column
+// are zero for the other heads, so all heads' PV products add into one O^T.
+// fp8 rows (1 KiB at Hk = 8) take HP = 4 for 512-byte pieces, with K and V
+// staged through one LDS buffer so two waves per SIMD still fit.
 template <int G, bool F8, int HP>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2)))
 void paged_decode_split_kernel(
@@ -129,8 +131,13 @@ void paged_decode_split_kernel(
   constexpr int kLoads = kChunk / kRpl;        // loads per lane per K (or V) chunk
   constexpr int kRing = kLoads >= 8 ? 2 : 4;   // ring depth: at most 16 loads per lane in flight
   constexpr int kLph = kLpr / HP;              // lanes per head within a row
-  __shared__ __attribute__((aligned(16))) bf16_t kbuf[HP][kChunk * kVRow];
-  __shared__ __attribute__((aligned(16))) bf16_t vbuf[HP][kChunk * kVRow];
+  // HP = 4: K and V of a chunk share one staging buffer (V is written after the K reads
+  // of S^T), which keeps two waves per SIMD within the LDS
+  constexpr bool kShared = HP == 4;
+  static_assert(!kShared || F8, "the shared buffer is staged for fp8 rows");
+  __shared__ __attribute__((aligned(16))) bf16_t lbuf[kShared ? 1 : 2][HP][kChunk * kVRow];
+  auto& kbuf = lbuf[0];
+  auto& vbuf = lbuf[kShared ? 0 : 1];
 
   const int lane = threadIdx.x;
   const int g4 = lane >> 4;   // key group: keys 4*g4 .. 4*g4+3 of a chunk
@@ -262,9 +269,11 @@ void paged_decode_split_kernel(
             fp8x16_to_bf16(kreg[s][r], lo, hi);
             *reinterpret_cast<u32x4_t*>(&kbuf[sh][e]) = lo;
             *reinterpret_cast<u32x4_t*>(&kbuf[sh][e + 8]) = hi;
-            fp8x16_to_bf16(vreg[s][r], lo, hi);
-            *reinterpret_cast<u32x4_t*>(&vbuf[sh][e]) = lo;
-            *reinterpret_cast<u32x4_t*>(&vbuf[sh][e + 8]) = hi;
+            if constexpr (!kShared) {
+              fp8x16_to_bf16(vreg[s][r], lo, hi);
+              *reinterpret_cast<u32x4_t*>(&vbuf[sh][e]) = lo;
+              *reinterpret_cast<u32x4_t*>(&vbuf[sh][e + 8]) = hi;
+            }
           } else {
             *reinterpret_cast<u32x4_t*>(&kbuf[sh][e]) = kreg[s][r];
             *reinterpret_cast<u32x4_t*>(&vbuf[sh][e]) = vreg[s][r];
@@ -291,7 +300,8 @@ void paged_decode_split_kernel(
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           float x = st[0][r];
-          if constexpr (HP == 2) x = hsel == 0 ? x : st[1][r];
+#pragma unroll
+          for (int hh = 1; hh < HP; ++hh) x = hsel == hh ? st[hh][r] : x;
           sv[r] = (4 * g4 + r < nv[s]) ? x * scale_log2 : -INFINITY;
           cmax = fmaxf(cmax, sv[r]);
         }
@@ -311,6 +321,16 @@ void paged_decode_split_kernel(
         const bf16x2v_t p01 = {(__bf16)p[0], (__bf16)p[1]};
         const bf16x2v_t p23 = {(__bf16)p[2], (__bf16)p[3]};
         const uint2 pw = {__builtin_bit_cast(uint32_t, p01), __builtin_bit_cast(uint32_t, p23)};
+        if constexpr (kShared) {  // V over the K rows: the S^T reads above come first
+#pragma unroll
+          for (int r = 0; r < kLoads; ++r) {
+            const int e = (kRpl * r + lane / kLpr) * kVRow + sd;
+            u32x4_t lo, hi;
+            fp8x16_to_bf16(vreg[s][r], lo, hi);
+            *reinterpret_cast<u32x4_t*>(&vbuf[sh][e]) = lo;
+            *reinterpret_cast<u32x4_t*>(&vbuf[sh][e + 8]) = hi;
+          }
+        }
         // P^T per head: a column's weights only in its own head's product
         i16x4_t pbh[HP];
 #pragma unroll
@@ -554,6 +574,8 @@ static int decode_split(const void* q, int64_t q_row_stride, const void* k_cache
   // table width: >= 32 chunks per head pair per resident wave); otherwise one.
   const int64_t work = (int64_t)batch * max_chunks * n_kv_heads;
   const bool pair = n_kv_heads % 2 == 0 && g <= 8 && work >= 32 * (int64_t)decode_grid<4, F8, 2>();
+  // fp8 rows are half as wide: four heads per wave read 512-byte pieces
+  const bool quad = F8 && pair && n_kv_heads % 4 == 0 && g <= 4;
   // Resident waves per head group, but no more than the table width lets receive a range
   // of min_chunks (small batches launch only the waves that can get work).
   const int32_t min_chunks = decode_min_chunks(max_blocks_per_seq, block_size);
@@ -571,7 +593,15 @@ static int decode_split(const void* q, int64_t q_row_stride, const void* k_cache
                      max_blocks_per_seq, n_blocks, (int32_t)slots, min_chunks, scale_log2,    \
                      v_scale,                                                                 \
                      w.part_o, w.part_ml, w.nslots)
-  if (pair) {
+  if (quad) {
+    if constexpr (F8) {
+      switch (g) {
+        case 1: NKV_DECODE_LAUNCH(1, 4); break;
+        case 2: NKV_DECODE_LAUNCH(2, 4); break;
+        default: NKV_DECODE_LAUNCH(4, 4); break;
+      }
+    }
+  } else if (pair) {
     switch (g) {
       case 1: NKV_DECODE_LAUNCH(1, 2); break;
       case 2: NKV_DECODE_LAUNCH(2, 2); break;

@@ -59,10 +59,12 @@ def _fp8_state(Hq, Hk, bs=6, seed=5, lo=1, hi=8192):
     return wl
 
 
-@pytest.mark.parametrize("Hq,Hk", [(32, 8), (8, 8), (16, 8), (64, 8), (128, 8)])
+@pytest.mark.parametrize("Hq,Hk", [(32, 8), (8, 8), (16, 8), (64, 8), (128, 8), (16, 2)])
 def test_decode_fp8_equals_bf16_over_dequantized(nkv, dev, Hq, Hk):
-    """Scales 1: the fp8 kernel widens codes to the same bf16 values the bf16 kernel reads,
-    so its output equals the bf16 decode over the dequantized cache bit for bit."""
+    """Scales 1: the fp8 kernel widens codes to the same bf16 values the bf16 kernel reads.
+    Where both group the KV heads alike, the outputs are equal bit for bit. Where fp8 takes
+    four KV heads per wave (Hk % 4 == 0, group <= 4, a table this wide) and bf16 two, the
+    chunk stream is split at other points and the two agree within 1e-2."""
     wl = _fp8_state(Hq, Hk)
     kq = kvc.fp8_quantize(wl["k_cache"].to(dev))
     vq = kvc.fp8_quantize(wl["v_cache"].to(dev))
@@ -71,7 +73,10 @@ def test_decode_fp8_equals_bf16_over_dequantized(nkv, dev, Hq, Hk):
     q = wl["q"].to(dev)
     a = nkv.paged_decode(q, kq, vq, *args)
     b = nkv.paged_decode(q, kd, vd, *args)
-    assert torch.equal(a, b)
+    if Hk % 4 == 0 and Hq // Hk <= 4:
+        assert (a.float() - b.float()).abs().max().item() <= 1e-2
+    else:
+        assert torch.equal(a, b)
 
 
 @pytest.mark.parametrize("k_scale,v_scale", [(1.0, 1.0), (0.5, 2.0), (0.037, 0.011)])
