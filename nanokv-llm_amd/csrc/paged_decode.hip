@@ -37,6 +37,7 @@
 #include "nkv_common.h"
 
 #include <algorithm>
+#include <atomic>
 
 namespace nkv {
 
@@ -497,10 +498,12 @@ static int decode_check(const void* q, const void* k_cache, const void* v_cache,
 // Persistent grid: as many one-wave workgroups as are resident at once.
 template <int G, bool F8, int HP>
 static int decode_grid() {
-  static int cached[64] = {0};
+  // per device; threads that race here compute and store the same value
+  static std::atomic<int> cached[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  if (cached[dev] == 0) {
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     int n_cu = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         n_cu <= 0)
@@ -510,9 +513,10 @@ static int decode_grid() {
             hipSuccess ||
         per_cu <= 0)
       per_cu = 8;
-    cached[dev] = n_cu * per_cu;
+    n = n_cu * per_cu;
+    cached[dev].store(n, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return n;
 }
 
 struct DecodeWorkspace {
