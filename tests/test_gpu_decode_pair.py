@@ -83,3 +83,32 @@ def test_four_head_fp8_path_vs_oracle(nkv, dev, Hq, Hk, B):
     torch.cuda.synchronize()
     ref = paged_decode_ref(q.float(), kd, vd, ctx, bt_n, D ** -0.5)
     assert (out.float().cpu() - ref).abs().max().item() <= TOL
+
+
+def test_four_head_fp8_big_batch_and_window_reload(nkv, dev):
+    """Four-head fp8 path over 130 sequences (three 64-sequence cursor batches): mostly short
+    or empty contexts, plus four past 64 blocks, so the 64-entry block-id window reloads."""
+    rng = random.Random(77)
+    g = torch.Generator().manual_seed(77)
+    bs, Hq, Hk, B = 130, 32, 8, 256
+    lens = [rng.choice([0, 1, rng.randrange(1, 600), rng.randrange(1, 600)]) for _ in range(bs)]
+    for i in (3, 64, 100, 129):
+        lens[i] = 64 * B + rng.randrange(-3, 2 * B)
+    need = [(n + B - 1) // B for n in lens]
+    width = max(need)
+    n_blocks = sum(need) + 3
+    free = list(range(n_blocks))
+    rng.shuffle(free)
+    bt = torch.tensor([[free.pop() for _ in range(k)] + [-1] * (width - k) for k in need],
+                      dtype=torch.int32)
+    kc = torch.randn(n_blocks, B, Hk, D, generator=g).to(torch.bfloat16)
+    vc = torch.randn(n_blocks, B, Hk, D, generator=g).to(torch.bfloat16)
+    q = torch.randn(bs, Hq, D, generator=g).to(torch.bfloat16)
+    ctx = torch.tensor(lens, dtype=torch.int32)
+    kq, vq = kvc.fp8_quantize(kc.to(dev)), kvc.fp8_quantize(vc.to(dev))
+    out = nkv.paged_decode(q.to(dev), kq, vq, ctx.to(dev), bt.to(dev), D ** -0.5)
+    torch.cuda.synchronize()
+    kd, vd = kvc.fp8_dequantize(kq).cpu(), kvc.fp8_dequantize(vq).cpu()
+    ref = paged_decode_ref(q.float(), kd, vd, ctx, bt, D ** -0.5)
+    assert (out.float().cpu() - ref).abs().max().item() <= TOL
+    assert torch.all(out[ctx.to(dev) == 0] == 0)
