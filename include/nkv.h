@@ -137,11 +137,16 @@ int nkv_qk_norm_rope_store(const void* q, int64_t q_row_stride, const void* k,
  * with K[b,t] = k_cache row (block_tables[b, t/block_size]*block_size
  * + t%block_size). Sequences with context_lens[b] <= 0 produce zeros.
  * Balanced split-K over 16-token chunks, then a combine pass; workspace
- * must hold nkv_paged_decode_workspace_bytes(...).
+ * must hold nkv_paged_decode_workspace_bytes(...), which is sized by what the
+ * split grid can write on the current device (descriptors per sequence and
+ * KV head, then partial rows: batch*Hq plus at most 8 resident waves per CU
+ * x 16 query heads, 528 bytes each; ~35 MB at batch 500, Hq 64, 64-block
+ * tables), not by batch x table width. Calls on one stream may share one
+ * workspace (the layers of a model, one after another).
  * q[b,h,d] at q[b*q_row_stride + h*head_dim + d]; out likewise with
- * out_row_stride. head_dim must be 128; n_q_heads/n_kv_heads in {1,2,4,8,16};
- * block_size a multiple of 16. Block-table entries outside [0, n_blocks)
- * contribute nothing.
+ * out_row_stride. head_dim must be 128; any GQA group n_q_heads/n_kv_heads
+ * up to 16; block_size a multiple of 16. Block-table entries outside
+ * [0, n_blocks) contribute nothing.
  * Replaces: flash_attn_with_kvcache(q.unsqueeze(1), k_cache, v_cache,
  *           cache_seqlens=context_lens, block_table=block_tables,
  *           softmax_scale=scale, causal=True),
@@ -204,8 +209,8 @@ int nkv_paged_decode_combine(const int32_t* context_lens, int32_t batch,
  * with row strides k_row_stride / v_row_stride, e.g. a roped K next to V as a
  * view of the qkv projection; paged caches share one stride). Table entries at or beyond
  * max_blocks_per_seq, negative, or past n_rows read as zero keys/values.
- * q/out are [sum Lq, Hq, D] with row strides. head_dim must be 128;
- * Hq/Hk in {1, 2, 4, 8}. Rows with no visible key (Lk < Lq) are zero.
+ * q/out are [sum Lq, Hq, D] with row strides. head_dim must be 128; any
+ * GQA group Hq/Hk up to 16. Rows with no visible key (Lk < Lq) are zero.
  * Replaces: flash_attn_varlen_func(q, k, v, max_seqlen_q, cu_seqlens_q,
  *           max_seqlen_k, cu_seqlens_k, softmax_scale, causal=True,
  *           block_table), nanokvllm/layers/attention.py:96-102
@@ -270,10 +275,10 @@ int nkv_compress_topk(const float* importance, int32_t n_rows, int32_t n_cand,
 /*
  * Fused selection: score + importance + top-k in one launch (agg "group") or
  * two (agg "all": per-KV-head partial importance, then their sum and the
- * top-k) when
- * W*B <= 1024, B % 64 == 0 and Hq/Hk is a power of two <= 16 (the reference's
- * W = 4, B = 256 qualifies); otherwise nkv_compress_score + nkv_compress_topk
- * run on the same workspace. Outputs are those of the two calls:
+ * top-k) when W*B <= 1024 and B % 64 == 0 (the reference's W = 4, B = 256
+ * qualifies); otherwise nkv_compress_score + nkv_compress_topk run on the
+ * same workspace. Any GQA group Hq/Hk up to 16. Outputs are those of the two
+ * calls:
  *   importance_out fp32 [m, n_sets, W*B-1],
  *   keep_idx int32 [m, n_sets, num_keep+2] = [0, ascending kept..., W*B-1].
  * Workspace: caller-owned, >= nkv_compress_select_workspace_bytes bytes.
@@ -301,8 +306,7 @@ int nkv_compress_select(const void* q, int64_t q_row_stride,
  * for agg "group": each (sequence, KV head) workgroup scores, selects and
  * compacts its KV head; two for agg "all": per-KV-head partial importance,
  * then sum + select + compact). Same outputs and cache/context_lens effects
- * as the two calls; compaction additionally needs keep_tokens + B - 1 <= 768
- * and B a power of two for the fused form. Workspace as nkv_compress_select.
+ * as the two calls. Workspace as nkv_compress_select.
  * Replaces: MyCompressCompact's per-layer work (scoring, selection,
  *           compaction, context_lens), nanokvllm/layers/compress_utils.py:100-263
  */
@@ -319,14 +323,18 @@ int nkv_compress_step(const void* q, int64_t q_row_stride, void* k_cache, void* 
 /*
  * In-place compaction of the window of each selected sequence, K and V:
  * kept window token keep_idx[j,s,i] moves to window position i
- * (i < keep_tokens); the tail partial block (tail = len % B tokens, block
- * block_tables[seq, len/B]) moves right after the last kept slot. Reads of a
- * (sequence, KV head) complete before any of its writes, so overlapping
- * sources and destinations behave like the reference's two-phase
- * index_select().clone() / index_copy_. Then
- *   context_lens[seq_idx[j]] = len - W*B + keep_tokens.
+ * (i < keep_tokens); tail token u (tail = len % B tokens, block
+ * block_tables[seq, len/B]) moves to window position keep_tokens + u (the
+ * window blocks, then the tail block). That is the reference's slot
+ * slot(keep_tokens-1)+1+u whenever that slot stays in its block (always for
+ * the default keep 2*B+1); past it the reference writes into an unrelated
+ * block (compress_utils.py:210-231). Rows move in ascending rounds, each
+ * round's reads before its writes, and no row moves to a later position, so
+ * overlapping sources and destinations behave like the reference's
+ * two-phase index_select().clone() / index_copy_, for any keep_tokens <= W*B.
+ * Then context_lens[seq_idx[j]] = len - W*B + keep_tokens.
  * keep_idx: int32 [m, n_sets, keep_tokens] with n_sets 1 (shared by all KV
- * heads) or n_kv_heads. Requires keep_tokens + block_size - 1 <= 1024.
+ * heads) or n_kv_heads, ascending per row.
  * Replaces: MyCompressCompact's compaction and context_lens update,
  *           nanokvllm/layers/compress_utils.py:186-263
  */
@@ -345,7 +353,11 @@ int nkv_compress_compact(void* k_cache, void* v_cache,
  * keep_blocks = ceil(new_len / B)) write
  *   events[j, :] = [seq_idx[j], new_len, keep_blocks, n_freed, freed ids...,
  *                   -1 padding]   (int32, row length 4 + max_blocks_per_seq)
- * where the freed ids are block_tables[seq, keep_blocks:] entries >= 0; then,
+ * where the freed ids are block_tables[seq, keep_blocks:] entries >= 0. A
+ * selected sequence the step left unchanged (fewer than window_blocks full
+ * blocks, or a table too short: the reference asserts there) reads
+ * [seq, len, ceil(len/B), -1, -1...] (n_freed = -1: skipped) and its table
+ * and slot are not rewritten. Then, for the others,
  * if rewrite_tables != 0, set those block_tables entries to -1 and, if
  * slot_mapping != NULL, set slot_mapping[seq] to the slot of token position
  * new_len (-1 if that position starts a new block).
@@ -386,8 +398,8 @@ int nkv_compress_schedule(const int32_t* context_lens, const int32_t* tail_uncom
 /* The compression step over fp8 (OCP E4M3FN) caches (nkv_store_kvcache_fp8 codes):
  * same arguments and effects as nkv_compress_step with K = code * k_scale;
  * scoring widens K to bf16, compaction moves the 1-byte rows. Needs the
- * workspace of nkv_compress_workspace_bytes (or more); block_size a power of
- * two multiple of 256. -1 padded seq_idx accepted.
+ * workspace of nkv_compress_workspace_bytes (or more); block_size a multiple
+ * of 256. -1 padded seq_idx accepted.
  * Replaces: MyCompressCompact (compress_utils.py:100-290) over an fp8 pool. */
 int nkv_compress_step_fp8(const void* q, int64_t q_row_stride, void* k_cache, void* v_cache,
                           const int32_t* block_tables, int64_t bt_row_stride,

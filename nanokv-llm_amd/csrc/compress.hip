@@ -32,19 +32,19 @@ namespace nkv {
 constexpr int kCD = 128;      // head_dim
 constexpr int kChunk = 256;   // keys per scoring workgroup
 constexpr int kMaxWindowBlocks = 64;
-constexpr int kMaxRows = 1024;  // kept tokens + tail rows per compaction unit
+constexpr int kMaxRows = 1024;  // rows per read-then-write round of a compaction unit
 
 // ------------------------------------------------------------------ score
 // scores[j][h][t] for t < Lw (window tokens); t == 0 and t == Lw-1 are -inf
 // (sink mask; the last window token is not scored).
 // F8: K is fp8 (OCP E4M3FN) codes, widened to bf16 (exact) on load; the K scale is
 // folded into scale_log2 by the caller.
-template <int G, bool F8>
+template <bool F8>
 __global__ __launch_bounds__(256) void compress_score_kernel(
     const bf16_t* __restrict__ q, int64_t q_row_stride, const void* __restrict__ k,
     const int32_t* __restrict__ block_tables, int64_t bt_row_stride, int32_t max_blocks,
     const int32_t* __restrict__ base_context_lens, const int32_t* __restrict__ seq_idx,
-    int32_t Hk, int32_t block_size, int32_t window_blocks, int64_t n_blocks, float scale_log2,
+    int32_t Hk, int32_t G, int32_t block_size, int32_t window_blocks, int64_t n_blocks, float scale_log2,
     float* __restrict__ scores) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -293,7 +293,9 @@ constexpr int kSelWaves = kSelThreads / 64;
 constexpr int kSelKeysPerWave = 64;
 constexpr int kSelMaxWindow = kSelWaves * kSelKeysPerWave;  // 1024
 constexpr int kStepRounds = 12;                             // 64 rows per round
-constexpr int kStepMaxRows = 64 * kStepRounds;              // kept + tail rows
+constexpr int kStepMaxRows = 64 * kStepRounds;              // rows per read-then-write round
+// kept + tail rows (< W*B + B <= 2 * 1024), rounded up to whole rounds
+constexpr int kStepTable = (2 * kSelMaxWindow + kStepMaxRows - 1) / kStepMaxRows * kStepMaxRows;
 
 constexpr int kStageRow = kCD + 8;  // LDS row stride (elements) of a staged 16-key group
 
@@ -306,8 +308,8 @@ struct SelectLds {
   int wcnt[kSelWaves];
   int32_t keep[kSelMaxWindow];
   int32_t win_pb[kMaxWindowBlocks + 1];
-  int32_t src[kStepMaxRows];
-  int32_t dst[kStepMaxRows];
+  int32_t src[kStepTable];
+  int32_t dst[kStepTable];
 };
 
 __device__ __forceinline__ float row16_max(float v) {  // over the 16 lanes of a row
@@ -409,12 +411,12 @@ __device__ __forceinline__ void block_select(SelectLds& L, int n_cand, int num_k
 // (valid in lanes of row group 0). Uses L.red.
 // F8: the cache holds fp8 (OCP E4M3FN) codes, 128-byte head rows read by 8 lanes (8 rows
 // per load) and widened to bf16 when staged; the K scale is folded into scale_log2.
-template <int G, bool F8>
+template <bool F8>
 __device__ __forceinline__ void group_importance(
     SelectLds& L, const bf16_t* __restrict__ q, int64_t q_row_stride,
     const void* __restrict__ k, const int32_t* __restrict__ block_tables,
     int64_t bt_row_stride, int32_t max_blocks, const int32_t* __restrict__ base_context_lens,
-    const int32_t* __restrict__ seq_idx, int j, int kvh, int Hk, int block_size,
+    const int32_t* __restrict__ seq_idx, int j, int kvh, int Hk, int G, int block_size,
     int window_blocks, int64_t n_blocks, float scale_log2, float gi[4]) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -555,9 +557,62 @@ __device__ __forceinline__ void group_importance(
   }
 }
 
+// Slot of logical window position pos (0 .. W*B + B - 2: the window blocks, then the
+// tail block) from the unit's block ids, or -1.
+__device__ __forceinline__ int64_t window_slot(const int32_t* win_pb, int pos, int B) {
+  const int32_t pb = win_pb[pos / B];
+  return pb >= 0 ? (int64_t)pb * B + pos % B : -1;
+}
+
+// Row i of a compaction unit (i < keep_tokens + tail): source and destination slots, or -1
+// for both when either is missing. Kept row i moves from window position keep[i] to
+// position i; tail row u = i - keep_tokens moves from offset u of the tail block (logical
+// position W*B + u) to logical position keep_tokens + u. Every row moves to a position
+// no later than its source, and sources ascend with i (keep[] ascends and ends below W*B),
+// so rows can be moved in ascending rounds, each round's reads before its writes: a write
+// never lands on a source of a later round.
+// The reference places tail row u at physical slot slot(keep_tokens - 1) + 1 + u
+// (compress_utils.py:210-231); that is the same slot whenever it stays in the block of
+// position keep_tokens - 1, and the block past it (another sequence's) otherwise.
+__device__ __forceinline__ void unit_row(const int32_t* win_pb, const int32_t* keep, int i,
+                                         int keep_tokens, int nrows, int Lw, int B,
+                                         int64_t& src, int64_t& dst) {
+  src = dst = -1;
+  if (i < keep_tokens) {
+    const int pos = keep[i];
+    if (pos >= 0 && pos < Lw) src = window_slot(win_pb, pos, B);
+    dst = window_slot(win_pb, i, B);
+  } else if (i < nrows) {
+    src = window_slot(win_pb, Lw + (i - keep_tokens), B);
+    dst = window_slot(win_pb, i, B);
+  }
+  if (src < 0 || dst < 0) src = dst = -1;
+}
+
+// Block ids of the unit (window blocks, then the tail block or -1) into win_pb; returns
+// false (nothing to do) when the sequence is not compressible or its table is too short.
+__device__ __forceinline__ bool unit_blocks(int32_t* win_pb, const int32_t* __restrict__ bt,
+                                            int len, int B, int window_blocks, int max_blocks,
+                                            int64_t n_blocks) {
+  const int full = len / B;
+  const int tail = len - full * B;
+  if (full < window_blocks || full > max_blocks || (tail > 0 && full >= max_blocks))
+    return false;
+  const int wb0 = full - window_blocks;
+  if ((int)threadIdx.x <= window_blocks) {
+    int32_t pb = -1;
+    if ((int)threadIdx.x < window_blocks) pb = bt[wb0 + threadIdx.x];
+    else if (tail > 0) pb = bt[full];
+    win_pb[threadIdx.x] = (pb >= 0 && pb < n_blocks) ? pb : -1;
+  }
+  return true;
+}
+
 // In-place compaction of KV head kvh of sequence seq_idx[j], K and V, with the
 // kept window positions in L.keep; kvh 0 also sets the new context length. F8:
-// 1-byte rows (a 128-byte head row per 8 lanes, 128 rows per round).
+// 1-byte rows (a 128-byte head row per 8 lanes, 128 rows per round). Rows go in
+// rounds of kStepMaxRows (one for the reference's shapes), all source rows of a
+// round in registers before any destination is written.
 template <bool F8>
 __device__ __forceinline__ void compact_unit(
     SelectLds& L, void* __restrict__ k_cache, void* __restrict__ v_cache,
@@ -568,49 +623,13 @@ __device__ __forceinline__ void compact_unit(
   const int tid = threadIdx.x;
   const int seq = seq_idx[j];
   const int len = seq >= 0 ? base_context_lens[seq] : 0;  // seq -1: padding entry
-  const int full = len / B;
-  const int tail = len - full * B;
   // not compressible, or inconsistent with the table width: leave untouched
-  if (full < window_blocks || full > max_blocks || (tail > 0 && full >= max_blocks)) return;
-  const int32_t* bt = block_tables + (int64_t)seq * bt_row_stride;
-  const int wb0 = full - window_blocks;
+  if (!unit_blocks(L.win_pb, block_tables + (int64_t)seq * bt_row_stride, len, B,
+                   window_blocks, max_blocks, n_blocks))
+    return;
+  __syncthreads();
   const int Lw = window_blocks * B;
-  if (tid <= window_blocks) {
-    int32_t pb = -1;
-    if (tid < window_blocks) pb = bt[wb0 + tid];
-    else if (tail > 0) pb = bt[full];
-    L.win_pb[tid] = (pb >= 0 && pb < n_blocks) ? pb : -1;
-  }
-  __syncthreads();
-  // source and destination slot of every row (-1 = not moved); B is a power of two
-  const int lb = 31 - __builtin_clz(B);
-  const int32_t tail_pb = L.win_pb[window_blocks];
-  const int32_t last_pb = L.win_pb[(keep_tokens - 1) >> lb];
-  const int32_t last_dst = last_pb >= 0 ? last_pb * B + ((keep_tokens - 1) & (B - 1)) : -1;
-  const int nrows = keep_tokens + tail;
-  const int64_t n_slots = n_blocks * B;
-  for (int i = tid; i < kStepMaxRows; i += kSelThreads) {
-    int32_t sv = -1, d = -1;
-    if (i < keep_tokens) {
-      const int pos = L.keep[i];
-      if (pos >= 0 && pos < Lw) {
-        const int32_t pb = L.win_pb[pos >> lb];
-        if (pb >= 0) sv = pb * B + (pos & (B - 1));
-      }
-      const int32_t pd = L.win_pb[i >> lb];
-      if (pd >= 0) d = pd * B + (i & (B - 1));
-    } else if (i < nrows) {
-      const int u = i - keep_tokens;
-      if (tail_pb >= 0) sv = tail_pb * B + u;
-      if (last_dst >= 0 && (int64_t)last_dst + 1 + u < n_slots) d = last_dst + 1 + u;
-    }
-    const bool ok = sv >= 0 && d >= 0;
-    L.src[i] = ok ? sv : -1;
-    L.dst[i] = ok ? d : -1;
-  }
-  __syncthreads();
-  // all source rows (K and V) as unconditional 16-byte loads (rows that are
-  // not moved re-read slot 0, always valid), then the writes
+  const int nrows = keep_tokens + len % B;
   constexpr int kEl = F8 ? 1 : 2;
   constexpr int kLanes = 8 * kEl;                  // 16-byte lanes per head row
   constexpr int kRpr = kSelThreads / kLanes;       // rows per round: 64 (bf16), 128 (fp8)
@@ -620,34 +639,47 @@ __device__ __forceinline__ void compact_unit(
   const int64_t row = (int64_t)Hk * kCD * kEl;    // bytes
   const int64_t col = (int64_t)kvh * kCD * kEl + (tid % kLanes) * 16;
   const int rsub = tid / kLanes;  // row within a round
-  u32x4_t kr[kRounds], vr[kRounds];
-#pragma unroll
-  for (int rr = 0; rr < kRounds; ++rr) {
-    const int64_t sv = max(L.src[rr * kRpr + rsub], 0);
-    kr[rr] = *reinterpret_cast<const u32x4_t*>(kc + sv * row + col);
-    vr[rr] = *reinterpret_cast<const u32x4_t*>(vc + sv * row + col);
+  // source and destination slot of every row (-1: not moved; rows past nrows too)
+  const int n_tab = (nrows + kStepMaxRows - 1) / kStepMaxRows * kStepMaxRows;
+  for (int i = tid; i < n_tab; i += kSelThreads) {
+    int64_t sv, d;
+    unit_row(L.win_pb, L.keep, i, keep_tokens, nrows, Lw, B, sv, d);
+    L.src[i] = (int32_t)sv;
+    L.dst[i] = (int32_t)d;
   }
-  __builtin_amdgcn_sched_barrier(0);
-  __builtin_amdgcn_s_waitcnt(0);  // all reads of the unit land before any write
   __syncthreads();
+  for (int base = 0; base < nrows; base += kStepMaxRows) {  // uniform
+    // all source rows (K and V) as unconditional 16-byte loads (rows that are
+    // not moved re-read slot 0, always valid), then the writes
+    u32x4_t kr[kRounds], vr[kRounds];
 #pragma unroll
-  for (int rr = 0; rr < kRounds; ++rr) {
-    const int64_t d = L.dst[rr * kRpr + rsub];
-    if (d >= 0) {
-      *reinterpret_cast<u32x4_t*>(kc + d * row + col) = kr[rr];
-      *reinterpret_cast<u32x4_t*>(vc + d * row + col) = vr[rr];
+    for (int rr = 0; rr < kRounds; ++rr) {
+      const int64_t sv = max(L.src[base + rr * kRpr + rsub], 0);
+      kr[rr] = *reinterpret_cast<const u32x4_t*>(kc + sv * row + col);
+      vr[rr] = *reinterpret_cast<const u32x4_t*>(vc + sv * row + col);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0);  // all reads of the round land before any write
+    __syncthreads();
+#pragma unroll
+    for (int rr = 0; rr < kRounds; ++rr) {
+      const int64_t d = L.dst[base + rr * kRpr + rsub];
+      if (d >= 0) {
+        *reinterpret_cast<u32x4_t*>(kc + d * row + col) = kr[rr];
+        *reinterpret_cast<u32x4_t*>(vc + d * row + col) = vr[rr];
+      }
     }
   }
   if (kvh == 0 && tid == 0) context_lens[seq] = len - Lw + keep_tokens;
 }
 
 // agg "group": score -> select -> (if k_cache_w) compact. Grid m * Hk.
-template <int G, bool F8>
+template <bool F8>
 __global__ __launch_bounds__(kSelThreads) void compress_group_kernel(
     const bf16_t* __restrict__ q, int64_t q_row_stride, const void* __restrict__ k,
     const int32_t* __restrict__ block_tables, int64_t bt_row_stride, int32_t max_blocks,
     const int32_t* __restrict__ base_context_lens, const int32_t* __restrict__ seq_idx,
-    int32_t Hk, int32_t block_size, int32_t window_blocks, int64_t n_blocks, float scale_log2,
+    int32_t Hk, int32_t G, int32_t block_size, int32_t window_blocks, int64_t n_blocks, float scale_log2,
     int32_t num_keep, float* __restrict__ importance_out, int32_t* __restrict__ keep_idx,
     void* __restrict__ k_cache_w, void* __restrict__ v_cache_w,
     int32_t* __restrict__ context_lens) {
@@ -660,9 +692,9 @@ __global__ __launch_bounds__(kSelThreads) void compress_group_kernel(
   const int Lw = window_blocks * block_size;
   const int n_cand = Lw - 1;
   float gi[4];
-  group_importance<G, F8>(L, q, q_row_stride, k, block_tables, bt_row_stride, max_blocks,
-                          base_context_lens, seq_idx, j, kvh, Hk, block_size, window_blocks,
-                          n_blocks, scale_log2, gi);
+  group_importance<F8>(L, q, q_row_stride, k, block_tables, bt_row_stride, max_blocks,
+                       base_context_lens, seq_idx, j, kvh, Hk, G, block_size, window_blocks,
+                       n_blocks, scale_log2, gi);
   const int t0 = (tid >> 6) * kSelKeysPerWave;
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
@@ -680,12 +712,12 @@ __global__ __launch_bounds__(kSelThreads) void compress_group_kernel(
 }
 
 // agg "all", first kernel: each group's importance -> partial[j][kvh][Lw]. Grid m * Hk.
-template <int G, bool F8>
+template <bool F8>
 __global__ __launch_bounds__(kSelThreads) void compress_partial_kernel(
     const bf16_t* __restrict__ q, int64_t q_row_stride, const void* __restrict__ k,
     const int32_t* __restrict__ block_tables, int64_t bt_row_stride, int32_t max_blocks,
     const int32_t* __restrict__ base_context_lens, const int32_t* __restrict__ seq_idx,
-    int32_t Hk, int32_t block_size, int32_t window_blocks, int64_t n_blocks, float scale_log2,
+    int32_t Hk, int32_t G, int32_t block_size, int32_t window_blocks, int64_t n_blocks, float scale_log2,
     float* __restrict__ partial) {
   __shared__ SelectLds L;
   const int lane = threadIdx.x & 63;
@@ -694,9 +726,9 @@ __global__ __launch_bounds__(kSelThreads) void compress_partial_kernel(
   if (block_tables && seq_idx[j] < 0) return;  // padding entry (uniform): nothing written
   const int Lw = window_blocks * block_size;
   float gi[4];
-  group_importance<G, F8>(L, q, q_row_stride, k, block_tables, bt_row_stride, max_blocks,
-                          base_context_lens, seq_idx, j, kvh, Hk, block_size, window_blocks,
-                          n_blocks, scale_log2, gi);
+  group_importance<F8>(L, q, q_row_stride, k, block_tables, bt_row_stride, max_blocks,
+                       base_context_lens, seq_idx, j, kvh, Hk, G, block_size, window_blocks,
+                       n_blocks, scale_log2, gi);
   float* prow = partial + ((int64_t)j * Hk + kvh) * Lw;
   const int t0 = (threadIdx.x >> 6) * kSelKeysPerWave;
 #pragma unroll
@@ -750,9 +782,10 @@ __global__ __launch_bounds__(kSelThreads) void compress_sum_kernel(
 // ----------------------------------------------------------------- compact
 // Unit = (selected j, KV head, K|V, half row). Rows i < keep_tokens move from
 // window position keep_idx[i] to window position i; rows keep_tokens + u
-// (u < tail) move from the tail block offset u to slot(window pos keep-1)+1+u.
-// F8: 1-byte (fp8) cache rows: half a head row is 64 bytes, moved by 4 lanes, so a
-// round covers 64 rows instead of 32.
+// (u < tail) move from the tail block offset u to window position keep + u
+// (unit_row). Rows go in rounds of ROUNDS * rows-per-round, each round's reads
+// before its writes. F8: 1-byte (fp8) cache rows: half a head row is 64 bytes,
+// moved by 4 lanes, so a round covers 64 rows instead of 32.
 template <int ROUNDS, bool F8>
 __global__ __launch_bounds__(256) void compress_compact_kernel(
     void* __restrict__ k_cache, void* __restrict__ v_cache,
@@ -768,81 +801,53 @@ __global__ __launch_bounds__(256) void compress_compact_kernel(
   const int seq = seq_idx[j];
   const int len = seq >= 0 ? base_context_lens[seq] : 0;  // seq -1: padding entry
   const int B = block_size;
-  const int full = len / B;
-  const int tail = len - full * B;
-  // not compressible, or inconsistent with the table width: leave untouched
-  if (full < window_blocks || full > max_blocks || (tail > 0 && full >= max_blocks)) return;
-  const int32_t* bt = block_tables + (int64_t)seq * bt_row_stride;
-  const int wb0 = full - window_blocks;
-  const int32_t* kidx = keep_idx + ((int64_t)j * n_sets + (n_sets > 1 ? kvh : 0)) * keep_tokens;
-  const int Lw = window_blocks * B;
-
-  // phase 0: the unit's physical blocks (window, then tail) into LDS
   __shared__ int32_t win_pb[kMaxWindowBlocks + 1];
   __shared__ int32_t src_lds[kMaxRows];
   __shared__ int32_t dst_lds[kMaxRows];
-  if (threadIdx.x <= window_blocks) {
-    int32_t pb = -1;
-    if (threadIdx.x < window_blocks) pb = bt[wb0 + threadIdx.x];
-    else if (tail > 0) pb = bt[full];
-    win_pb[threadIdx.x] = (pb >= 0 && pb < n_blocks) ? pb : -1;
-  }
+  // not compressible, or inconsistent with the table width: leave untouched
+  if (!unit_blocks(win_pb, block_tables + (int64_t)seq * bt_row_stride, len, B, window_blocks,
+                   max_blocks, n_blocks))
+    return;
   __syncthreads();
-
-  // phase 1: source and destination slot of every row of the unit into LDS
-  // (-1 = row not moved). block_size is a power of two (checked on the host).
-  const int lb = 31 - __builtin_clz(B);
-  const int32_t tail_pb = win_pb[window_blocks];
-  const int32_t last_pb = win_pb[(keep_tokens - 1) >> lb];
-  const int32_t last_dst = last_pb >= 0 ? last_pb * B + ((keep_tokens - 1) & (B - 1)) : -1;
-  const int nrows = keep_tokens + tail;
-  const int64_t n_slots = n_blocks * B;
+  const int32_t* kidx = keep_idx + ((int64_t)j * n_sets + (n_sets > 1 ? kvh : 0)) * keep_tokens;
+  const int Lw = window_blocks * B;
+  const int nrows = keep_tokens + len % B;
   constexpr int kEl = F8 ? 1 : 2;
   constexpr int kLanesPerRow = 4 * kEl;             // 16-byte lanes per half head row
   constexpr int kRowsPerRound = 256 / kLanesPerRow;  // 32 (bf16) or 64 (fp8)
-  static_assert(ROUNDS * kRowsPerRound <= kMaxRows, "compaction table too small");
-  for (int i = threadIdx.x; i < ROUNDS * kRowsPerRound; i += blockDim.x) {
-    int32_t sv = -1, d = -1;
-    if (i < keep_tokens) {
-      const int p = kidx[i];
-      if (p >= 0 && p < Lw) {
-        const int32_t pb = win_pb[p >> lb];
-        if (pb >= 0) sv = pb * B + (p & (B - 1));
-      }
-      const int32_t pd = win_pb[i >> lb];
-      if (pd >= 0) d = pd * B + (i & (B - 1));
-    } else if (i < nrows) {
-      const int u = i - keep_tokens;
-      if (tail_pb >= 0) sv = tail_pb * B + u;
-      if (last_dst >= 0 && (int64_t)last_dst + 1 + u < n_slots) d = last_dst + 1 + u;
-    }
-    const bool ok = sv >= 0 && d >= 0;
-    src_lds[i] = ok ? sv : -1;
-    dst_lds[i] = ok ? d : -1;
-  }
-  __syncthreads();
-
-  // phase 2: every source row of the unit, as unconditional 128-bit loads
-  // (rows that are not moved re-read slot 0, always valid)
+  constexpr int kBatch = ROUNDS * kRowsPerRound;    // rows per read-then-write round
+  static_assert(kBatch <= kMaxRows, "compaction table too small");
   char* cache = static_cast<char*>(is_v ? v_cache : k_cache);
   const int64_t row = (int64_t)Hk * kCD * kEl;  // bytes
   const int64_t col = ((int64_t)kvh * kCD + half * 64) * kEl + (threadIdx.x % kLanesPerRow) * 16;
   const int rsub = threadIdx.x / kLanesPerRow;  // row within a round
-  u32x4_t reg[ROUNDS];
+  for (int base = 0; base < nrows; base += kBatch) {  // uniform
+    // source and destination slot of every row of the round (-1 = row not moved)
+    for (int i = threadIdx.x; i < kBatch; i += blockDim.x) {
+      int64_t sv, d;
+      unit_row(win_pb, kidx, base + i, keep_tokens, nrows, Lw, B, sv, d);
+      src_lds[i] = (int32_t)sv;
+      dst_lds[i] = (int32_t)d;
+    }
+    __syncthreads();
+    // every source row of the round, as unconditional 128-bit loads (rows that are not
+    // moved re-read slot 0, always valid)
+    u32x4_t reg[ROUNDS];
 #pragma unroll
-  for (int rr = 0; rr < ROUNDS; ++rr) {
-    const int32_t sv = max(src_lds[rr * kRowsPerRound + rsub], 0);
-    reg[rr] = *reinterpret_cast<const u32x4_t*>(cache + (int64_t)sv * row + col);
-  }
-  __builtin_amdgcn_sched_barrier(0);
-  // all reads of the unit land before any write (two-phase semantics)
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  // phase 3: writes
+    for (int rr = 0; rr < ROUNDS; ++rr) {
+      const int32_t sv = max(src_lds[rr * kRowsPerRound + rsub], 0);
+      reg[rr] = *reinterpret_cast<const u32x4_t*>(cache + (int64_t)sv * row + col);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // all reads of the round land before any write (two-phase semantics)
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
 #pragma unroll
-  for (int rr = 0; rr < ROUNDS; ++rr) {
-    const int32_t d = dst_lds[rr * kRowsPerRound + rsub];
-    if (d >= 0) *reinterpret_cast<u32x4_t*>(cache + (int64_t)d * row + col) = reg[rr];
+    for (int rr = 0; rr < ROUNDS; ++rr) {
+      const int32_t d = dst_lds[rr * kRowsPerRound + rsub];
+      if (d >= 0) *reinterpret_cast<u32x4_t*>(cache + (int64_t)d * row + col) = reg[rr];
+    }
+    if (base + kBatch < nrows) __syncthreads();  // the tables are rebuilt
   }
 
   if (blockIdx.x % (4 * Hk) == 0 && threadIdx.x == 0)
@@ -863,9 +868,11 @@ __global__ __launch_bounds__(64) void compress_finalize_kernel(
     int32_t* ev = events + (int64_t)j * ev_len;
     int32_t* bt = block_tables + (int64_t)seq * bt_row_stride;
     const int full = len / B, tail = len - (len / B) * B;
-    // same skip rule as the compaction: not compressible -> report unchanged
+    // same skip rule as the compaction: not compressible -> left unchanged and marked
+    // skipped (n_freed = -1), so the host changes none of its state; a padding entry
+    // (seq -1) reads [-1, 0, 0, 0, -1...]
     if (full < window_blocks || full > max_blocks || (tail > 0 && full >= max_blocks)) {
-      ev[0] = seq; ev[1] = len; ev[2] = (len + B - 1) / B; ev[3] = 0;
+      ev[0] = seq; ev[1] = len; ev[2] = (len + B - 1) / B; ev[3] = seq >= 0 ? -1 : 0;
       for (int i = 0; i < max_blocks; ++i) ev[4 + i] = -1;
       continue;
     }
@@ -1073,8 +1080,7 @@ extern "C" int nkv_compress_score(const void* q, int64_t q_row_stride, const voi
   NKV_REQUIRE(head_dim == kCD, NKV_EUNSUPPORTED, "compress_score: head_dim must be 128");
   NKV_REQUIRE(n_q_heads % n_kv_heads == 0, NKV_EINVAL, "compress_score: Hq %% Hk != 0");
   const int g = n_q_heads / n_kv_heads;
-  NKV_REQUIRE(g == 1 || g == 2 || g == 4 || g == 8 || g == 16, NKV_EUNSUPPORTED,
-              "compress_score: GQA group %d not in {1,2,4,8,16}", g);
+  NKV_REQUIRE(g <= 16, NKV_EUNSUPPORTED, "compress_score: GQA group %d above 16", g);
   NKV_REQUIRE(block_size % kChunk == 0, NKV_EUNSUPPORTED,
               "compress_score: block_size must be a multiple of 256");
   NKV_REQUIRE(agg_mode == NKV_AGG_ALL || agg_mode == NKV_AGG_GROUP, NKV_EINVAL,
@@ -1095,19 +1101,10 @@ extern "C" int nkv_compress_score(const void* q, int64_t q_row_stride, const voi
   hipStream_t s = as_stream(stream);
   const unsigned grid = (unsigned)(m * n_kv_heads * (Lw / kChunk));
   const float sl2 = scale * kLog2e;
-#define NKV_SCORE_LAUNCH(G)                                                                    \
-  hipLaunchKernelGGL((compress_score_kernel<G, false>), dim3(grid), dim3(256), 0, s,             \
-                     (const bf16_t*)q, q_row_stride, k_cache, block_tables, bt_row_stride,      \
-                     max_blocks_per_seq, base_context_lens, seq_idx, n_kv_heads, block_size, window_blocks,         \
-                     n_blocks, sl2, scores)
-  switch (g) {
-    case 1: NKV_SCORE_LAUNCH(1); break;
-    case 2: NKV_SCORE_LAUNCH(2); break;
-    case 4: NKV_SCORE_LAUNCH(4); break;
-    case 8: NKV_SCORE_LAUNCH(8); break;
-    default: NKV_SCORE_LAUNCH(16); break;
-  }
-#undef NKV_SCORE_LAUNCH
+  hipLaunchKernelGGL((compress_score_kernel<false>), dim3(grid), dim3(256), 0, s,
+                     (const bf16_t*)q, q_row_stride, k_cache, block_tables, bt_row_stride,
+                     max_blocks_per_seq, base_context_lens, seq_idx, n_kv_heads, g, block_size,
+                     window_blocks, n_blocks, sl2, scores);
   int rc = check_launch("nkv_compress_score");
   if (rc) return rc;
   const int n_sets = agg_mode == NKV_AGG_ALL ? 1 : n_kv_heads;
@@ -1166,40 +1163,23 @@ static int launch_fused(const void* q, int64_t q_row_stride, const void* k_cache
   const int Lw = window_blocks * block_size;
   const bool step = k_cache_w != nullptr;
   const bool ok = Lw <= kSelMaxWindow && block_size % kSelKeysPerWave == 0 && g <= 16 &&
-                  (g & (g - 1)) == 0 && head_dim == kCD && window_blocks <= kMaxWindowBlocks &&
-                  (!step || (num_keep + 2 + block_size - 1 <= kStepMaxRows &&
-                             (block_size & (block_size - 1)) == 0));
+                  head_dim == kCD && window_blocks <= kMaxWindowBlocks;
   if (!ok) return 1;
   const float sl2 = scale * kLog2e;
   const unsigned units = (unsigned)(m * n_kv_heads);
   float* partial = (float*)workspace;
-#define NKV_G_SWITCH(MACRO) \
-  switch (g) {              \
-    case 1: MACRO(1); break; \
-    case 2: MACRO(2); break; \
-    case 4: MACRO(4); break; \
-    case 8: MACRO(8); break; \
-    default: MACRO(16); break; \
-  }
   if (agg_mode == NKV_AGG_GROUP) {
-#define NKV_GROUP(G)                                                                          \
-  hipLaunchKernelGGL((compress_group_kernel<G, F8>), dim3(units), dim3(kSelThreads), 0, s,     \
-                     (const bf16_t*)q, q_row_stride, k_cache, block_tables, bt_row_stride,     \
-                     max_blocks_per_seq, base_context_lens, seq_idx, n_kv_heads, block_size,   \
-                     window_blocks, n_blocks, sl2, num_keep, importance_out, keep_idx,         \
-                     k_cache_w, v_cache_w, context_lens)
-    NKV_G_SWITCH(NKV_GROUP)
-#undef NKV_GROUP
+    hipLaunchKernelGGL((compress_group_kernel<F8>), dim3(units), dim3(kSelThreads), 0, s,
+                       (const bf16_t*)q, q_row_stride, k_cache, block_tables, bt_row_stride,
+                       max_blocks_per_seq, base_context_lens, seq_idx, n_kv_heads, g,
+                       block_size, window_blocks, n_blocks, sl2, num_keep, importance_out,
+                       keep_idx, k_cache_w, v_cache_w, context_lens);
     return check_launch("compress (group)") ? -1 : 0;
   }
-#define NKV_PARTIAL(G)                                                                        \
-  hipLaunchKernelGGL((compress_partial_kernel<G, F8>), dim3(units), dim3(kSelThreads), 0, s,   \
-                     (const bf16_t*)q, q_row_stride, k_cache, block_tables, bt_row_stride,     \
-                     max_blocks_per_seq, base_context_lens, seq_idx, n_kv_heads, block_size,   \
-                     window_blocks, n_blocks, sl2, partial)
-  NKV_G_SWITCH(NKV_PARTIAL)
-#undef NKV_PARTIAL
-#undef NKV_G_SWITCH
+  hipLaunchKernelGGL((compress_partial_kernel<F8>), dim3(units), dim3(kSelThreads), 0, s,
+                     (const bf16_t*)q, q_row_stride, k_cache, block_tables, bt_row_stride,
+                     max_blocks_per_seq, base_context_lens, seq_idx, n_kv_heads, g, block_size,
+                     window_blocks, n_blocks, sl2, partial);
   if (check_launch("compress (partial)")) return -1;
   const int per_seq = step ? n_kv_heads : 1;
   hipLaunchKernelGGL((compress_sum_kernel<F8>), dim3((unsigned)(m * per_seq)), dim3(kSelThreads),
@@ -1277,8 +1257,6 @@ extern "C" int nkv_compress_compact(void* k_cache, void* v_cache, const int32_t*
   NKV_REQUIRE(keep_tokens > 0 && keep_tokens <= window_blocks * block_size, NKV_EINVAL,
               "compress_compact: need 0 < keep_tokens <= window tokens");
   const int max_rows = keep_tokens + block_size - 1;
-  NKV_REQUIRE(max_rows <= 1024, NKV_EUNSUPPORTED,
-              "compress_compact: keep_tokens + block_size - 1 = %d exceeds 1024", max_rows);
   NKV_REQUIRE(k_cache && v_cache && block_tables && base_context_lens && context_lens &&
                   seq_idx && keep_idx,
               NKV_EINVAL, "compress_compact: null pointer");
@@ -1286,8 +1264,6 @@ extern "C" int nkv_compress_compact(void* k_cache, void* v_cache, const int32_t*
               "compress_compact: caches must be 16-byte aligned");
   NKV_REQUIRE(max_blocks_per_seq > 0 && bt_row_stride >= max_blocks_per_seq, NKV_EINVAL,
               "compress_compact: bad block table width/stride");
-  NKV_REQUIRE((block_size & (block_size - 1)) == 0, NKV_EUNSUPPORTED,
-              "compress_compact: block_size must be a power of two (got %d)", block_size);
   NKV_REQUIRE(window_blocks <= kMaxWindowBlocks, NKV_EUNSUPPORTED,
               "compress_compact: window_blocks > %d", kMaxWindowBlocks);
   NKV_REQUIRE(n_blocks * block_size < (1ll << 31), NKV_EUNSUPPORTED,
@@ -1303,7 +1279,7 @@ extern "C" int nkv_compress_compact(void* k_cache, void* v_cache, const int32_t*
   if (max_rows <= 256) NKV_COMPACT_LAUNCH(8);
   else if (max_rows <= 512) NKV_COMPACT_LAUNCH(16);
   else if (max_rows <= 768) NKV_COMPACT_LAUNCH(24);
-  else NKV_COMPACT_LAUNCH(32);
+  else NKV_COMPACT_LAUNCH(32);  // more rows: rounds of 1024
 #undef NKV_COMPACT_LAUNCH
   return check_launch("nkv_compress_compact");
 }
@@ -1430,11 +1406,9 @@ extern "C" int nkv_compress_step_fp8(const void* q, int64_t q_row_stride, void* 
   NKV_REQUIRE(head_dim == kCD, NKV_EUNSUPPORTED, "compress_step_fp8: head_dim must be 128");
   NKV_REQUIRE(n_q_heads % n_kv_heads == 0, NKV_EINVAL, "compress_step_fp8: Hq %% Hk != 0");
   const int g = n_q_heads / n_kv_heads;
-  NKV_REQUIRE(g == 1 || g == 2 || g == 4 || g == 8 || g == 16, NKV_EUNSUPPORTED,
-              "compress_step_fp8: GQA group %d not in {1,2,4,8,16}", g);
-  NKV_REQUIRE(block_size % kChunk == 0 && (block_size & (block_size - 1)) == 0,
-              NKV_EUNSUPPORTED, "compress_step_fp8: block_size must be a power-of-two "
-              "multiple of 256");
+  NKV_REQUIRE(g <= 16, NKV_EUNSUPPORTED, "compress_step_fp8: GQA group %d above 16", g);
+  NKV_REQUIRE(block_size % kChunk == 0, NKV_EUNSUPPORTED,
+              "compress_step_fp8: block_size must be a multiple of 256");
   NKV_REQUIRE(agg_mode == NKV_AGG_ALL || agg_mode == NKV_AGG_GROUP, NKV_EINVAL,
               "compress_step_fp8: bad agg_mode %d", agg_mode);
   NKV_REQUIRE(q && k_cache && v_cache && block_tables && base_context_lens && context_lens &&
@@ -1453,9 +1427,6 @@ extern "C" int nkv_compress_step_fp8(const void* q, int64_t q_row_stride, void* 
   NKV_REQUIRE(num_keep > 0 && num_keep < Lw - 1 && Lw - 1 <= 4096, NKV_EINVAL,
               "compress_step_fp8: need 0 < keep_tokens - 2 < W*B - 1 <= 4096");
   const int max_rows = keep_tokens + block_size - 1;
-  NKV_REQUIRE(max_rows <= kMaxRows, NKV_EUNSUPPORTED,
-              "compress_step_fp8: keep_tokens + block_size - 1 = %d exceeds %d", max_rows,
-              kMaxRows);
   const size_t need = nkv_compress_workspace_bytes(m, n_q_heads, window_blocks, block_size);
   NKV_REQUIRE(workspace && workspace_bytes >= need, NKV_EWORKSPACE,
               "compress_step_fp8: workspace needs %zu bytes (got %zu)", need, workspace_bytes);
@@ -1471,19 +1442,10 @@ extern "C" int nkv_compress_step_fp8(const void* q, int64_t q_row_stride, void* 
   float* scores = (float*)workspace;
   const unsigned sgrid = (unsigned)(m * n_kv_heads * (Lw / kChunk));
   const float sl2 = scale * k_scale * kLog2e;
-#define NKV_SCORE8_LAUNCH(G)                                                                   \
-  hipLaunchKernelGGL((compress_score_kernel<G, true>), dim3(sgrid), dim3(256), 0, s,            \
-                     (const bf16_t*)q, q_row_stride, k_cache, block_tables, bt_row_stride,      \
-                     max_blocks_per_seq, base_context_lens, seq_idx, n_kv_heads, block_size,    \
-                     window_blocks, n_blocks, sl2, scores)
-  switch (g) {
-    case 1: NKV_SCORE8_LAUNCH(1); break;
-    case 2: NKV_SCORE8_LAUNCH(2); break;
-    case 4: NKV_SCORE8_LAUNCH(4); break;
-    case 8: NKV_SCORE8_LAUNCH(8); break;
-    default: NKV_SCORE8_LAUNCH(16); break;
-  }
-#undef NKV_SCORE8_LAUNCH
+  hipLaunchKernelGGL((compress_score_kernel<true>), dim3(sgrid), dim3(256), 0, s,
+                     (const bf16_t*)q, q_row_stride, k_cache, block_tables, bt_row_stride,
+                     max_blocks_per_seq, base_context_lens, seq_idx, n_kv_heads, g, block_size,
+                     window_blocks, n_blocks, sl2, scores);
   rc = check_launch("nkv_compress_step_fp8 (score)");
   if (rc) return rc;
   const int n_sets = agg_mode == NKV_AGG_ALL ? 1 : n_kv_heads;

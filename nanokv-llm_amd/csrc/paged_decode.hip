@@ -12,7 +12,7 @@
 //    contiguous range of C chunks, so every wave moves the same number of
 //    bytes whatever the context-length mix. A range crosses at most a few
 //    (sequence, head group) segments; each segment it touches yields one
-//    partial (m, l, O) per query head in slot  wave - first_wave_of_the_segment.
+//    partial (m, l, O) per query head.
 //    A head group is one KV head, or two (HP = 2; four for fp8 rows, HP = 4)
 //    whose parts of every token row are read as one contiguous piece.
 //  * Within a segment the wave streams chunks through a register ring (4
@@ -34,6 +34,14 @@
 //  * A combine kernel merges the few partials of each (sequence, query head).
 // Scores are kept in the log2 domain (scale * log2 e folded in) so the
 // exponentials are single v_exp_f32 instructions.
+//
+// Workspace (caller-owned, sized by what the grid can write, not by the batch
+// times the table width): one descriptor per (sequence, KV head) -- first
+// partial row, partial count, row stride -- then the partial rows. Within a
+// head group, wave wi's partial of sequence b is row wi + b: a segment's
+// partials come from consecutive waves, and the next segment's first wave is
+// at least its last one, so wi + b never collides and stays below
+// waves + batch. A row holds O (128 floats), m, l and two pad floats.
 #include "nkv_common.h"
 
 #include <algorithm>
@@ -49,10 +57,14 @@ constexpr int kWinBlocks = 64;           // block ids held per window (one per l
 constexpr int kVRow = kD + 16;           // LDS row stride of a staged V chunk (elements)
 constexpr int kBufferFlags = 0x00020000; // raw buffer resource word 3 (dword data)
 constexpr int kStreamPolicy = 2;         // cache policy "nt": K/V are read exactly once
+constexpr int kWavesPerCU = 8;           // resident split waves per CU (2 per SIMD)
+constexpr int kPartRow = kD + 4;         // floats per partial row: O, m, l, 2 pad (528 B)
+constexpr int kMaxCols = 16;             // MFMA columns: query heads per wave at most
 
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
 typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
+typedef int32_t i32x4v_t __attribute__((ext_vector_type(4)));
 
 // Partial slots per (sequence, query head): a segment of n chunks is touched by at most
 // ceil(n / C) + 1 waves, and the kernel takes C >= decode_min_chunks, which is at least
@@ -114,17 +126,17 @@ __device__ __forceinline__ void seq_load(SeqCursor& c, const int32_t* __restrict
 // are zero for the other heads, so all heads' PV products add into one O^T.
 // fp8 rows (1 KiB at Hk = 8) take HP = 4 for 512-byte pieces, with K and V
 // staged through one LDS buffer so two waves per SIMD still fit.
-template <int G, bool F8, int HP>
+// G (query heads per KV head) is any value with HP*G <= 16: the columns past
+// HP*G are computed and dropped.
+template <bool F8, int HP>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2)))
 void paged_decode_split_kernel(
     const bf16_t* __restrict__ q, int64_t q_row_stride,
     const void* __restrict__ k_cache, const void* __restrict__ v_cache,
     const int32_t* __restrict__ block_tables, int64_t bt_row_stride,
-    const int32_t* __restrict__ context_lens, int32_t batch, int32_t Hk,
-    int32_t block_size, int32_t max_blocks, int64_t n_blocks, int32_t slots, int32_t min_chunks,
-    float scale_log2, float v_scale, float* __restrict__ part_o, float* __restrict__ part_ml,
-    int32_t* __restrict__ nslots) {
-  static_assert(HP == 1 || HP * G <= 16, "HP heads of G query heads must fit 16 columns");
+    const int32_t* __restrict__ context_lens, int32_t batch, int32_t Hk, int32_t G,
+    int32_t block_size, int32_t max_blocks, int64_t n_blocks, int32_t min_chunks,
+    float scale_log2, float v_scale, float* __restrict__ part, i32x4v_t* __restrict__ desc) {
   constexpr int kEl = F8 ? 1 : 2;              // bytes per cache element
   constexpr int kSeg = HP * kD * kEl;          // bytes a wave reads of each token row
   constexpr int kLpr = kSeg / 16;              // lanes per row (16-byte loads)
@@ -143,7 +155,7 @@ void paged_decode_split_kernel(
   const int lane = threadIdx.x;
   const int g4 = lane >> 4;   // key group: keys 4*g4 .. 4*g4+3 of a chunk
   const int col = lane & 15;  // MFMA column: query head (S^T, O^T) / key row (K)
-  const int Hq = Hk * G;
+  const int HPG = HP * G;     // query heads (MFMA columns) of the wave's head group
   const int row_b = Hk * kD * kEl;  // bytes of one cache row (token)
   const int max_tokens = max_blocks * block_size;
 
@@ -152,10 +164,13 @@ void paged_decode_split_kernel(
   // equal ranges, so the NP waves i*NP .. i*NP+NP-1 read the Hk heads of the
   // same cache blocks at the same time.
   const int NP = Hk / HP;
-  const int kvh0 = (blockIdx.x % NP) * HP;
+  const int grp = blockIdx.x % NP;
+  const int kvh0 = grp * HP;
   const int wi = blockIdx.x / NP;
   const int Wh = gridDim.x / NP;
   if (wi >= Wh) return;
+  // partial rows of this head group: (wave + sequence) x HPG columns
+  float* gpart = part + (int64_t)grp * (Wh + batch) * HPG * kPartRow;
   SeqCursor cur;
   int T = 0;
   for (cur.cb = 0; cur.cb < batch; cur.cb += 64) {
@@ -198,13 +213,13 @@ void paged_decode_split_kernel(
     const int g0 = cur.base + __builtin_amdgcn_readlane(cur.incl, ln) - nc;
     const int c_lo = k - g0;
     const int n_seg = min(nc - c_lo, k_end - k);
-    const int slot = wi - g0 / C;
+    const int w_first = g0 / C;  // first wave of the segment
 
     // q^T as the MFMA B operand: lane l -> query head kvh0*G + l%16 (columns
     // >= HP*G re-read the first head and are discarded), dims 8*(l/16) + 32*ks
     u32x4_t qreg[4];
     {
-      const int hc = col < HP * G ? col : 0;
+      const int hc = col < HPG ? col : 0;
       const u32x4_t* qp = reinterpret_cast<const u32x4_t*>(
           q + (int64_t)b * q_row_stride + (int64_t)(kvh0 * G + hc) * kD + g4 * 8);
 #pragma unroll
@@ -375,18 +390,22 @@ void paged_decode_split_kernel(
 #pragma unroll
       for (int db = 0; db < 8; ++db) acc[db] *= v_scale;
     }
-    const int64_t obase = ((int64_t)b * Hq + (int64_t)kvh0 * G) * slots + slot;
-    if (col < HP * G) {
-      const int64_t prow = obase + (int64_t)col * slots;
+    // partial row (wi + b) * HPG + col of the group; the wave that ends the segment
+    // writes each of its KV heads' descriptor {first row, count, row stride}
+    const int prow0 = (wi + b) * HPG;
+    if (col < HPG) {
+      float* pr = gpart + (int64_t)(prow0 + col) * kPartRow;
 #pragma unroll
       for (int db = 0; db < 8; ++db)
-        *reinterpret_cast<f32x4_t*>(&part_o[prow * kD + db * 16 + g4 * 4]) = acc[db];
-      if (g4 == 0) {
-        part_ml[prow * 2 + 0] = m_run;
-        part_ml[prow * 2 + 1] = l_run;
-      }
+        *reinterpret_cast<f32x4_t*>(&pr[db * 16 + g4 * 4]) = acc[db];
+      if (g4 == 0) *reinterpret_cast<float2*>(&pr[kD]) = float2{m_run, l_run};
     }
-    if (c_lo + n_seg == nc && lane < HP) nslots[(int64_t)b * Hk + kvh0 + lane] = slot + 1;
+    if (c_lo + n_seg == nc && lane < HP) {
+      const int64_t first = (int64_t)grp * (Wh + batch) * HPG + (int64_t)(w_first + b) * HPG +
+                            lane * G;
+      desc[(int64_t)b * Hk + kvh0 + lane] =
+          i32x4v_t{(int32_t)first, wi - w_first + 1, HPG, 0};
+    }
     k += n_seg;
   }
 }
@@ -394,40 +413,38 @@ void paged_decode_split_kernel(
 // Merge the partials of one (sequence, query head): O = sum_s 2^(m_s-M) O_s /
 // sum_s 2^(m_s-M) l_s. One wave per pair.
 __global__ __launch_bounds__(64) void paged_decode_combine_kernel(
-    const int32_t* __restrict__ context_lens, int32_t Hq, int32_t Hk, int32_t slots,
-    const float* __restrict__ part_o, const float* __restrict__ part_ml,
-    const int32_t* __restrict__ nslots, bf16_t* __restrict__ out, int64_t out_row_stride) {
+    const int32_t* __restrict__ context_lens, int32_t Hq, int32_t Hk,
+    const float* __restrict__ part, const i32x4v_t* __restrict__ desc,
+    bf16_t* __restrict__ out, int64_t out_row_stride) {
   const int b = blockIdx.x / Hq;
   const int h = blockIdx.x % Hq;
   const int lane = threadIdx.x;
-  const int64_t base = ((int64_t)b * Hq + h) * slots;
-  const float* po = part_o + base * kD + 2 * lane;
-  // Every load is issued before any of them is used: the partial count, the context
-  // length, the (m, l) pair of every slot and the first eight partial rows. All `slots`
-  // entries of a (sequence, head) lie inside the workspace whatever the count, so the
-  // entries past it are read (unwritten or stale) and dropped by the selects below; one
-  // memory round trip instead of three dependent ones.
+  const int G = Hq / Hk;
+  // The context length and the KV head's descriptor first (one round trip), then every
+  // (m, l) pair and the first eight partial rows at once (the second).
   static_assert(kMaxSlots <= 128, "two partials per lane");
   const int ctx = context_lens[b];
-  const int cnt = nslots[(int64_t)b * Hk + h / (Hq / Hk)];
-  float2 ml0 = {-INFINITY, 0.f}, ml1 = {-INFINITY, 0.f};
-  if (lane < slots) ml0 = *reinterpret_cast<const float2*>(&part_ml[(base + lane) * 2]);
-  if (lane + 64 < slots) ml1 = *reinterpret_cast<const float2*>(&part_ml[(base + lane + 64) * 2]);
-  float2 v0[8];
-#pragma unroll
-  for (int u = 0; u < 8; ++u)
-    v0[u] = u < slots ? *reinterpret_cast<const float2*>(po + (int64_t)u * kD) : float2{0.f, 0.f};
-  const int ns = ctx > 0 ? min(cnt, slots) : 0;
+  const i32x4v_t d = desc[(int64_t)b * Hk + h / G];
   bf16_t* op = out + (int64_t)b * out_row_stride + (int64_t)h * kD + 2 * lane;
+  // the descriptor is written by this call for every sequence with ctx > 0
+  const int ns = ctx > 0 ? min(d.y, kMaxSlots) : 0;
   if (ns == 0) {
     *reinterpret_cast<uint32_t*>(op) = 0u;
     return;
   }
+  const int64_t stride = (int64_t)d.z * kPartRow;  // floats between a head's partials
+  const float* pbase = part + ((int64_t)d.x + h % G) * kPartRow;
+  const float* po = pbase + 2 * lane;
+  float2 ml0 = {-INFINITY, 0.f}, ml1 = {-INFINITY, 0.f};
+  if (lane < ns) ml0 = *reinterpret_cast<const float2*>(pbase + lane * stride + kD);
+  if (lane + 64 < ns) ml1 = *reinterpret_cast<const float2*>(pbase + (lane + 64) * stride + kD);
+  float2 v0[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u)
+    v0[u] = u < ns ? *reinterpret_cast<const float2*>(po + u * stride) : float2{0.f, 0.f};
   // lane l holds partials l and l + 64 (ns <= kMaxSlots = 128): the global max and
   // the weights w_s = 2^(m_s - M) with two wave reductions, then each lane
   // accumulates two output dims over the partials, eight loads in flight
-  if (lane >= ns) ml0 = {-INFINITY, 0.f};
-  if (lane + 64 >= ns) ml1 = {-INFINITY, 0.f};
   const float M = wave_max(fmaxf(ml0.x, ml1.x));
   const float w0 = (ml0.x == -INFINITY) ? 0.f : fast_exp2(ml0.x - M);
   const float w1 = (ml1.x == -INFINITY) ? 0.f : fast_exp2(ml1.x - M);
@@ -445,7 +462,7 @@ __global__ __launch_bounds__(64) void paged_decode_combine_kernel(
   for (; s + 8 <= ns; s += 8) {
     float2 v[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const float2*>(po + (int64_t)(s + u) * kD);
+    for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const float2*>(po + (s + u) * stride);
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const float w = __shfl(s + u < 64 ? w0 : w1, (s + u) & 63, 64);  // uniform select
@@ -454,7 +471,7 @@ __global__ __launch_bounds__(64) void paged_decode_combine_kernel(
     }
   }
   for (; s < ns; ++s) {
-    const float2 v = *reinterpret_cast<const float2*>(po + (int64_t)s * kD);
+    const float2 v = *reinterpret_cast<const float2*>(po + s * stride);
     const float w = __shfl(s < 64 ? w0 : w1, s & 63, 64);
     o0 = fmaf(w, v.x, o0);
     o1 = fmaf(w, v.y, o1);
@@ -475,8 +492,8 @@ static int decode_check(const void* q, const void* k_cache, const void* v_cache,
   NKV_REQUIRE(n_q_heads % n_kv_heads == 0, NKV_EINVAL,
               "paged_decode: n_q_heads %% n_kv_heads != 0 (%d, %d)", n_q_heads, n_kv_heads);
   const int g = n_q_heads / n_kv_heads;
-  NKV_REQUIRE(g == 1 || g == 2 || g == 4 || g == 8 || g == 16, NKV_EUNSUPPORTED,
-              "paged_decode: GQA group %d not in {1,2,4,8,16}", g);
+  NKV_REQUIRE(g <= kMaxCols, NKV_EUNSUPPORTED, "paged_decode: GQA group %d above %d", g,
+              kMaxCols);
   NKV_REQUIRE(block_size > 0 && block_size % kChunk == 0, NKV_EUNSUPPORTED,
               "paged_decode: block_size must be a multiple of 16 (got %d)", block_size);
   NKV_REQUIRE(max_blocks_per_seq > 0 && bt_row_stride >= max_blocks_per_seq, NKV_EINVAL,
@@ -495,44 +512,93 @@ static int decode_check(const void* q, const void* k_cache, const void* v_cache,
   return NKV_OK;
 }
 
-// Persistent grid: as many one-wave workgroups as are resident at once.
-template <int G, bool F8, int HP>
-static int decode_grid() {
-  // per device; threads that race here compute and store the same value
+// Compute units of the current device (cached per device; 256 when it cannot be queried).
+static int device_cus() {
+  // threads that race here compute and store the same value
   static std::atomic<int> cached[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
   int n = cached[dev].load(std::memory_order_relaxed);
   if (n == 0) {
-    int n_cu = 0, per_cu = 0;
-    if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        n_cu <= 0)
-      n_cu = 256;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, reinterpret_cast<const void*>(paged_decode_split_kernel<G, F8, HP>), 64, 0) !=
-            hipSuccess ||
-        per_cu <= 0)
-      per_cu = 8;
-    n = n_cu * per_cu;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
     cached[dev].store(n, std::memory_order_relaxed);
   }
   return n;
 }
 
-struct DecodeWorkspace {
-  float* part_o;
-  float* part_ml;
-  int32_t* nslots;
+// Persistent grid: as many one-wave workgroups as are resident at once, at most
+// kWavesPerCU per CU (the workspace bound assumes no more).
+template <bool F8, int HP>
+static int decode_grid() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, reinterpret_cast<const void*>(paged_decode_split_kernel<F8, HP>), 64, 0) !=
+            hipSuccess ||
+        per_cu <= 0)
+      per_cu = kWavesPerCU;
+    n = device_cus() * std::min(per_cu, kWavesPerCU);
+    cached[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+// The launch a decode call makes: KV heads per wave, the grid and the smallest range.
+struct DecodePlan {
+  int hp;          // KV heads per wave (1, 2, or 4 for fp8)
+  unsigned grid;   // one-wave workgroups
+  int32_t min_chunks;
 };
 
-static DecodeWorkspace decode_workspace(void* ws, int32_t batch, int32_t Hq, int32_t Hk,
-                                        int64_t slots) {
-  DecodeWorkspace w;
-  w.part_o = (float*)ws;
-  w.part_ml = w.part_o + (int64_t)batch * Hq * slots * kD;
-  w.nslots = (int32_t*)(w.part_ml + (int64_t)batch * Hq * slots * 2);
-  (void)Hk;
-  return w;
+static int64_t decode_useful_waves(int32_t batch, int32_t max_blocks, int32_t block_size) {
+  const int64_t max_chunks = ((int64_t)max_blocks * block_size + kChunk - 1) / kChunk;
+  const int32_t min_chunks = decode_min_chunks(max_blocks, block_size);
+  return std::max<int64_t>(1, (batch * max_chunks + min_chunks - 1) / min_chunks);
+}
+
+template <bool F8>
+static DecodePlan decode_plan(int32_t batch, int32_t Hq, int32_t Hk, int32_t max_blocks,
+                              int32_t block_size) {
+  const int g = Hq / Hk;
+  const int64_t max_chunks = ((int64_t)max_blocks * block_size + kChunk - 1) / kChunk;
+  // Two KV heads per wave when the heads pair up, the 2G query heads fit the 16
+  // MFMA columns and there is enough work for every wave (upper bound from the
+  // table width: >= 32 chunks per head pair per resident wave); otherwise one.
+  const int64_t work = (int64_t)batch * max_chunks * Hk;
+  const bool pair = Hk % 2 == 0 && 2 * g <= kMaxCols && work >= 32 * (int64_t)decode_grid<F8, 2>();
+  // fp8 rows are half as wide: four heads per wave read 512-byte pieces
+  const bool quad = F8 && pair && Hk % 4 == 0 && 4 * g <= kMaxCols;
+  DecodePlan p;
+  p.hp = quad ? 4 : pair ? 2 : 1;
+  p.min_chunks = decode_min_chunks(max_blocks, block_size);
+  // Resident waves per head group, but no more than the table width lets receive a range
+  // of min_chunks (small batches launch only the waves that can get work).
+  int resident = p.hp == 2 ? decode_grid<F8, 2>() : decode_grid<F8, 1>();
+  if constexpr (F8) {
+    if (p.hp == 4) resident = decode_grid<true, 4>();
+  }
+  const int np = Hk / p.hp;
+  const int64_t per =
+      std::min<int64_t>(std::max(1, resident / np), decode_useful_waves(batch, max_blocks,
+                                                                        block_size));
+  p.grid = (unsigned)(per * np);
+  return p;
+}
+
+// Bytes of the descriptors (one per sequence and KV head; 16-byte aligned) and of the
+// partial rows a plan writes: per head group (waves + batch) x HP*G rows, i.e.
+// grid * HP*G + batch * Hq rows in all.
+static size_t decode_desc_bytes(int32_t batch, int32_t Hk) {
+  return (size_t)batch * Hk * sizeof(i32x4v_t);
+}
+static size_t decode_part_bytes(int64_t grid, int32_t hpg, int32_t batch, int32_t Hq) {
+  return (size_t)(grid * hpg + (int64_t)batch * Hq) * kPartRow * sizeof(float);
 }
 
 }  // namespace nkv
@@ -540,11 +606,18 @@ static DecodeWorkspace decode_workspace(void* ws, int32_t batch, int32_t Hq, int
 extern "C" size_t nkv_paged_decode_workspace_bytes(int32_t batch, int32_t n_q_heads,
                                                    int32_t head_dim, int32_t max_blocks_per_seq,
                                                    int32_t block_size) {
-  if (batch <= 0 || n_q_heads <= 0 || max_blocks_per_seq <= 0 || block_size <= 0) return 0;
-  const int64_t slots = nkv::decode_slots(max_blocks_per_seq, block_size);
-  // partial O and (m, l) per slot, then one slot count per (sequence, head)
-  return (size_t)batch * n_q_heads * slots * (head_dim + 2) * sizeof(float) +
-         (size_t)batch * n_q_heads * sizeof(int32_t);
+  using namespace nkv;
+  if (batch <= 0 || n_q_heads <= 0 || max_blocks_per_seq <= 0 || block_size <= 0 ||
+      head_dim != kD)
+    return 0;
+  // Whatever the plan: grid <= CUs * kWavesPerCU and grid <= useful * (head groups), with
+  // HP*G <= min(16, Hq) and (head groups) * HP*G = Hq; the descriptors at most batch * Hq.
+  const int64_t resident = (int64_t)device_cus() * kWavesPerCU;
+  const int64_t cols = std::min<int64_t>(
+      resident * std::min(kMaxCols, n_q_heads),
+      decode_useful_waves(batch, max_blocks_per_seq, block_size) * n_q_heads);
+  return decode_desc_bytes(batch, n_q_heads) + decode_part_bytes(0, 0, batch, n_q_heads) +
+         (size_t)cols * kPartRow * sizeof(float);
 }
 
 namespace nkv {
@@ -561,68 +634,66 @@ static int decode_split(const void* q, int64_t q_row_stride, const void* k_cache
   if (rc) return rc;
   if (batch == 0) return NKV_OK;
   NKV_REQUIRE(k_scale > 0.f && v_scale > 0.f, NKV_EINVAL, "paged_decode: scales must be > 0");
-  const size_t need = nkv_paged_decode_workspace_bytes(batch, n_q_heads, head_dim,
-                                                       max_blocks_per_seq, block_size);
-  NKV_REQUIRE(workspace && workspace_bytes >= need, NKV_EWORKSPACE,
-              "paged_decode: workspace needs %zu bytes (got %zu)", need, workspace_bytes);
-  const int64_t slots = decode_slots(max_blocks_per_seq, block_size);
   const int64_t max_chunks = ((int64_t)max_blocks_per_seq * block_size + kChunk - 1) / kChunk;
   NKV_REQUIRE(max_chunks * batch * n_kv_heads < (1ll << 31), NKV_EUNSUPPORTED,
               "paged_decode: too many chunks in one call");
-  DecodeWorkspace w = decode_workspace(workspace, batch, n_q_heads, n_kv_heads, slots);
-  const float scale_log2 = scale * k_scale * kLog2e;
   const int g = n_q_heads / n_kv_heads;
+  const DecodePlan p = decode_plan<F8>(batch, n_q_heads, n_kv_heads, max_blocks_per_seq,
+                                       block_size);
+  const size_t desc_b = decode_desc_bytes(batch, n_kv_heads);
+  const size_t need = desc_b + decode_part_bytes(p.grid, p.hp * g, batch, n_q_heads);
+  NKV_REQUIRE(workspace && workspace_bytes >= need, NKV_EWORKSPACE,
+              "paged_decode: workspace needs %zu bytes (got %zu)", need, workspace_bytes);
+  NKV_REQUIRE((int64_t)p.grid * p.hp * g + (int64_t)batch * n_q_heads < (1ll << 31),
+              NKV_EUNSUPPORTED, "paged_decode: too many partial rows");
+  i32x4v_t* desc = static_cast<i32x4v_t*>(workspace);
+  float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + desc_b);
+  const float scale_log2 = scale * k_scale * kLog2e;
   hipStream_t s = as_stream(stream);
-  // Two KV heads per wave when the heads pair up, the 2G query heads fit the 16
-  // MFMA columns and there is enough work for every wave (upper bound from the
-  // table width: >= 32 chunks per head pair per resident wave); otherwise one.
-  const int64_t work = (int64_t)batch * max_chunks * n_kv_heads;
-  const bool pair = n_kv_heads % 2 == 0 && g <= 8 && work >= 32 * (int64_t)decode_grid<4, F8, 2>();
-  // fp8 rows are half as wide: four heads per wave read 512-byte pieces
-  const bool quad = F8 && pair && n_kv_heads % 4 == 0 && g <= 4;
-  // Resident waves per head group, but no more than the table width lets receive a range
-  // of min_chunks (small batches launch only the waves that can get work).
-  const int32_t min_chunks = decode_min_chunks(max_blocks_per_seq, block_size);
-  const int64_t useful = std::max<int64_t>(1, (batch * max_chunks + min_chunks - 1) / min_chunks);
-  auto grid_of = [&](int resident, int hp) {
-    const int np = n_kv_heads / hp;
-    const int64_t per = std::min<int64_t>(std::max(1, resident / np), useful);
-    return (unsigned)(per * np);
-  };
-#define NKV_DECODE_LAUNCH(G, HP)                                                              \
-  hipLaunchKernelGGL((paged_decode_split_kernel<G, F8, HP>),                                  \
-                     dim3(grid_of(decode_grid<G, F8, HP>(), HP)),                             \
-                     dim3(64), 0, s, (const bf16_t*)q, q_row_stride, k_cache, v_cache,        \
-                     block_tables, bt_row_stride, context_lens, batch, n_kv_heads, block_size, \
-                     max_blocks_per_seq, n_blocks, (int32_t)slots, min_chunks, scale_log2,    \
-                     v_scale,                                                                 \
-                     w.part_o, w.part_ml, w.nslots)
-  if (quad) {
-    if constexpr (F8) {
-      switch (g) {
-        case 1: NKV_DECODE_LAUNCH(1, 4); break;
-        case 2: NKV_DECODE_LAUNCH(2, 4); break;
-        default: NKV_DECODE_LAUNCH(4, 4); break;
-      }
-    }
-  } else if (pair) {
-    switch (g) {
-      case 1: NKV_DECODE_LAUNCH(1, 2); break;
-      case 2: NKV_DECODE_LAUNCH(2, 2); break;
-      case 4: NKV_DECODE_LAUNCH(4, 2); break;
-      default: NKV_DECODE_LAUNCH(8, 2); break;
-    }
+#define NKV_DECODE_LAUNCH(HP)                                                                  \
+  hipLaunchKernelGGL((paged_decode_split_kernel<F8, HP>), dim3(p.grid), dim3(64), 0, s,         \
+                     (const bf16_t*)q, q_row_stride, k_cache, v_cache, block_tables,           \
+                     bt_row_stride, context_lens, batch, n_kv_heads, g, block_size,            \
+                     max_blocks_per_seq, n_blocks, p.min_chunks, scale_log2, v_scale, part,    \
+                     desc)
+  if (p.hp == 4) {
+    if constexpr (F8) NKV_DECODE_LAUNCH(4);
+  } else if (p.hp == 2) {
+    NKV_DECODE_LAUNCH(2);
   } else {
-    switch (g) {
-      case 1: NKV_DECODE_LAUNCH(1, 1); break;
-      case 2: NKV_DECODE_LAUNCH(2, 1); break;
-      case 4: NKV_DECODE_LAUNCH(4, 1); break;
-      case 8: NKV_DECODE_LAUNCH(8, 1); break;
-      default: NKV_DECODE_LAUNCH(16, 1); break;
-    }
+    NKV_DECODE_LAUNCH(1);
   }
 #undef NKV_DECODE_LAUNCH
   return check_launch("nkv_paged_decode_split");
+}
+
+// The combine of a split launched with the same arguments: the partial rows start after
+// the descriptors, whatever the plan.
+static int decode_combine(const int32_t* context_lens, int32_t batch, int32_t n_q_heads,
+                          int32_t n_kv_heads, int32_t head_dim, int32_t block_size,
+                          int32_t max_blocks_per_seq, void* out, int64_t out_row_stride,
+                          const void* workspace, size_t workspace_bytes, void* stream) {
+  NKV_REQUIRE(head_dim == kD, NKV_EUNSUPPORTED, "paged_decode: head_dim must be 128");
+  NKV_REQUIRE(batch >= 0 && n_q_heads > 0 && n_kv_heads > 0 && n_q_heads % n_kv_heads == 0 &&
+                  n_q_heads / n_kv_heads <= kMaxCols && block_size > 0 && max_blocks_per_seq > 0,
+              NKV_EINVAL, "paged_decode_combine: bad sizes");
+  if (batch == 0) return NKV_OK;
+  NKV_REQUIRE(out && context_lens, NKV_EINVAL, "paged_decode_combine: null pointer");
+  NKV_REQUIRE(out_row_stride >= (int64_t)n_q_heads * kD && out_row_stride % 2 == 0 &&
+                  (reinterpret_cast<uintptr_t>(out) & 3) == 0,
+              NKV_EINVAL,
+              "paged_decode_combine: out must be 4-byte aligned with an even row stride "
+              ">= Hq*D");
+  const size_t desc_b = decode_desc_bytes(batch, n_kv_heads);
+  NKV_REQUIRE(workspace && workspace_bytes > desc_b, NKV_EWORKSPACE,
+              "paged_decode_combine: workspace of %zu bytes holds no partials",
+              workspace_bytes);
+  const i32x4v_t* desc = static_cast<const i32x4v_t*>(workspace);
+  const float* part = reinterpret_cast<const float*>(static_cast<const char*>(workspace) + desc_b);
+  hipLaunchKernelGGL(paged_decode_combine_kernel, dim3((unsigned)(batch * n_q_heads)), dim3(64),
+                     0, as_stream(stream), context_lens, n_q_heads, n_kv_heads, part, desc,
+                     (bf16_t*)out, out_row_stride);
+  return check_launch("nkv_paged_decode_combine");
 }
 }  // namespace nkv
 
@@ -645,30 +716,10 @@ extern "C" int nkv_paged_decode_combine(const int32_t* context_lens, int32_t bat
                                         int32_t block_size, int32_t max_blocks_per_seq,
                                         void* out, int64_t out_row_stride, const void* workspace,
                                         size_t workspace_bytes, void* stream) {
-  using namespace nkv;
-  clear_error();
-  NKV_REQUIRE(head_dim == kD, NKV_EUNSUPPORTED, "paged_decode: head_dim must be 128");
-  NKV_REQUIRE(batch >= 0 && n_q_heads > 0 && n_kv_heads > 0 && n_q_heads % n_kv_heads == 0 &&
-                  block_size > 0 && max_blocks_per_seq > 0,
-              NKV_EINVAL, "paged_decode_combine: bad sizes");
-  if (batch == 0) return NKV_OK;
-  NKV_REQUIRE(out && context_lens, NKV_EINVAL, "paged_decode_combine: null pointer");
-  NKV_REQUIRE(out_row_stride >= (int64_t)n_q_heads * kD && out_row_stride % 2 == 0 &&
-                  (reinterpret_cast<uintptr_t>(out) & 3) == 0,
-              NKV_EINVAL,
-              "paged_decode_combine: out must be 4-byte aligned with an even row stride "
-              ">= Hq*D");
-  const size_t need = nkv_paged_decode_workspace_bytes(batch, n_q_heads, head_dim,
-                                                       max_blocks_per_seq, block_size);
-  NKV_REQUIRE(workspace && workspace_bytes >= need, NKV_EWORKSPACE,
-              "paged_decode: workspace needs %zu bytes (got %zu)", need, workspace_bytes);
-  const int64_t slots = decode_slots(max_blocks_per_seq, block_size);
-  DecodeWorkspace w =
-      decode_workspace(const_cast<void*>(workspace), batch, n_q_heads, n_kv_heads, slots);
-  hipLaunchKernelGGL(paged_decode_combine_kernel, dim3((unsigned)(batch * n_q_heads)), dim3(64),
-                     0, as_stream(stream), context_lens, n_q_heads, n_kv_heads, (int32_t)slots,
-                     w.part_o, w.part_ml, w.nslots, (bf16_t*)out, out_row_stride);
-  return check_launch("nkv_paged_decode_combine");
+  nkv::clear_error();
+  return nkv::decode_combine(context_lens, batch, n_q_heads, n_kv_heads, head_dim, block_size,
+                             max_blocks_per_seq, out, out_row_stride, workspace, workspace_bytes,
+                             stream);
 }
 
 extern "C" int nkv_paged_decode(const void* q, int64_t q_row_stride, const void* k_cache,

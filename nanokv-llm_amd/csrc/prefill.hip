@@ -6,10 +6,11 @@
 // j of a sequence with Lq queries and Lk keys sees keys 0 .. Lk-Lq+j).
 //
 // MI355X design (MFMA-bound):
-//  * Workgroup = (sequence, tile of 128/g queries, KV head) x 4 waves. The
-//    tile's 128 "rows" are its queries for all g query heads of the KV head,
-//    so one K/V tile in LDS serves g heads (GQA sharing). Wave w owns two
-//    16-row groups (32 rows).
+//  * Workgroup = (sequence, tile of floor(128/g) queries, KV head) x 4 waves.
+//    The tile's 128 "rows" are its queries for all g query heads of the KV
+//    head, query-major (row r = query r/g, head r%g; rows past the tile's
+//    queries x g are computed and dropped), so one K/V tile in LDS serves g
+//    heads (GQA sharing) for any g <= 128. Wave w owns two 16-row groups.
 //  * Keys advance in 64-key steps. Each step's K and V tiles (2 x 16 KiB) go
 //    from HBM straight into LDS with gfx950's 16-byte buffer-load-to-LDS
 //    (no staging registers, no LDS write instructions) through a ring of
@@ -78,16 +79,14 @@ __device__ __forceinline__ void load_to_lds(i32x4_t desc, uint32_t lds_addr, uin
                : "memory");
 }
 
-template <int G>
 __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
     const bf16_t* __restrict__ q, int64_t q_row_stride, const bf16_t* __restrict__ k_cache,
     const bf16_t* __restrict__ v_cache, int64_t k_row_stride, int64_t v_row_stride,
     const int32_t* __restrict__ cu_seqlens_q, const int32_t* __restrict__ cu_seqlens_k,
-    const int32_t* __restrict__ block_tables, int64_t bt_row_stride, int32_t Hk,
+    const int32_t* __restrict__ block_tables, int64_t bt_row_stride, int32_t Hk, int32_t G,
     int32_t block_size, int32_t max_blocks, int32_t n_limit, int32_t n_tiles, float scale_log2,
     bf16_t* __restrict__ out, int64_t out_row_stride) {
-  constexpr int QT = kWGRows / G;  // queries per tile
-  constexpr int GPH = QT / 16;     // 16-row groups per head
+  const int QT = kWGRows / G;  // queries per tile
   __shared__ __attribute__((aligned(1024))) char ring[kStages * kStageB];
 
   const int tid = threadIdx.x;
@@ -196,13 +195,15 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
     refill_window();
   }
 
-  // ---- this wave's two row groups: head and query of this lane's row
+  // ---- this wave's two row groups: head and query of this lane's row (query-major;
+  // rows past QT*G take query Lq: attended like the others, never stored)
   int head[2], jrow[2];
 #pragma unroll
   for (int rr = 0; rr < 2; ++rr) {
-    const int rg = wave * 2 + rr;
-    head[rr] = rg / GPH;
-    jrow[rr] = j0 + (rg % GPH) * 16 + col;
+    const int r = (wave * 2 + rr) * 16 + col;
+    const bool real = r < QT * G;
+    head[rr] = real ? r % G : 0;
+    jrow[rr] = real ? j0 + r / G : Lq;
   }
   // Q^T as the MFMA B operand: lane l -> row l%16, dims 8*(l/16) + 32*ks
   u32x4_t qreg[2][4];
@@ -406,8 +407,7 @@ extern "C" int nkv_prefill_varlen(const void* q, int64_t q_row_stride, const voi
   NKV_REQUIRE(head_dim == kPD, NKV_EUNSUPPORTED, "prefill_varlen: head_dim must be 128");
   NKV_REQUIRE(n_q_heads % n_kv_heads == 0, NKV_EINVAL, "prefill_varlen: Hq %% Hk != 0");
   const int g = n_q_heads / n_kv_heads;
-  NKV_REQUIRE(g == 1 || g == 2 || g == 4 || g == 8, NKV_EUNSUPPORTED,
-              "prefill_varlen: GQA group %d not in {1,2,4,8}", g);
+  NKV_REQUIRE(g <= 16, NKV_EUNSUPPORTED, "prefill_varlen: GQA group %d above 16", g);
   NKV_REQUIRE(q && k_cache && v_cache && cu_seqlens_q && cu_seqlens_k && out, NKV_EINVAL,
               "prefill_varlen: null pointer");
   NKV_REQUIRE(aligned16(q) && aligned16(k_cache) && aligned16(v_cache) && aligned16(out),
@@ -440,19 +440,10 @@ extern "C" int nkv_prefill_varlen(const void* q, int64_t q_row_stride, const voi
   NKV_REQUIRE(grid < (1ll << 31), NKV_EUNSUPPORTED, "prefill_varlen: grid too large");
   const float sl2 = scale * kLog2e;
   hipStream_t s = as_stream(stream);
-#define NKV_PREFILL_LAUNCH(G)                                                                   \
-  hipLaunchKernelGGL(prefill_varlen_kernel<G>, dim3((unsigned)grid), dim3(256), 0, s,            \
-                     (const bf16_t*)q, q_row_stride, (const bf16_t*)k_cache,                     \
-                     (const bf16_t*)v_cache, k_row_stride, v_row_stride, cu_seqlens_q,           \
-                     cu_seqlens_k,                                                               \
-                     block_tables, bt_row_stride, n_kv_heads, block_size, max_blocks, n_limit,   \
-                     n_tiles, sl2, (bf16_t*)out, out_row_stride)
-  switch (g) {
-    case 1: NKV_PREFILL_LAUNCH(1); break;
-    case 2: NKV_PREFILL_LAUNCH(2); break;
-    case 4: NKV_PREFILL_LAUNCH(4); break;
-    default: NKV_PREFILL_LAUNCH(8); break;
-  }
-#undef NKV_PREFILL_LAUNCH
+  hipLaunchKernelGGL(prefill_varlen_kernel, dim3((unsigned)grid), dim3(256), 0, s,
+                     (const bf16_t*)q, q_row_stride, (const bf16_t*)k_cache,
+                     (const bf16_t*)v_cache, k_row_stride, v_row_stride, cu_seqlens_q,
+                     cu_seqlens_k, block_tables, bt_row_stride, n_kv_heads, g, block_size,
+                     max_blocks, n_limit, n_tiles, sl2, (bf16_t*)out, out_row_stride);
   return check_launch("nkv_prefill_varlen");
 }

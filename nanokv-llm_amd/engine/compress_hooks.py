@@ -15,7 +15,15 @@
   ``tail_uncompressed_len = 0``. It also rebases ``num_computed_tokens`` by
   the number of tokens removed, which the reference leaves at the
   uncompressed count (its prepare_step would then index past the truncated
-  block table).
+  block table). Events marked skipped (``n_freed = -1`` from the device: a
+  selected sequence that was not compressible) change nothing.
+
+Sequences, scheduled items and the block manager are the caller's own objects
+(the reference's engine types), read duck-typed: a sequence has ``len()``,
+``block_table``, ``seq_id``, ``rope_pos``, ``num_tokens``,
+``num_computed_tokens`` and ``tail_uncompressed_len``; a scheduled item is a
+sequence or has ``.seq`` and ``.num_new_tokens``; the block manager has
+``truncate_blocks(seq, keep_blocks)``.
 * ``prepare_decode_metadata`` -- decode metadata as in prepare_decode
   (model_runner.py:265-285): positions = rope_pos, context_lens = physical
   length, slot = last block * B + last_block_num_tokens - 1, block tables
@@ -28,16 +36,20 @@ from __future__ import annotations
 import torch
 
 from .metadata import BlockTableStore, build_step_metadata
-from .sequence import ScheduledSeq, Sequence
 
 
-def prepare_block_tables(seqs: list[Sequence], pad: int = -1) -> list[list[int]]:
+def _seq_of(item):
+    """The sequence of a scheduled item (an object with ``.seq``) or the item itself."""
+    return getattr(item, "seq", item)
+
+
+def prepare_block_tables(seqs: list, pad: int = -1) -> list[list[int]]:
     """model_runner.py:154-158 (host lists; the caller moves them to the device)."""
     max_len = max(len(s.block_table) for s in seqs)
     return [s.block_table + [pad] * (max_len - len(s.block_table)) for s in seqs]
 
 
-def prepare_decode_metadata(seqs: list[Sequence], block_size: int, device="cuda",
+def prepare_decode_metadata(seqs: list, block_size: int, device="cuda",
                             store: BlockTableStore | None = None):
     """prepare_decode (model_runner.py:265-285) on the device: one token per sequence at KV
     position len - 1 with RoPE position rope_pos; block tables padded with -1. With a
@@ -48,7 +60,7 @@ def prepare_decode_metadata(seqs: list[Sequence], block_size: int, device="cuda"
                                store=store, seq_ids=[s.seq_id for s in seqs])
 
 
-def prepare_step_metadata(scheduled: list[ScheduledSeq], block_size: int, device="cuda",
+def prepare_step_metadata(scheduled: list, block_size: int, device="cuda",
                           store: BlockTableStore | None = None):
     """prepare_step (model_runner.py:160-219) on the device. Positions carry each sequence's
     RoPE offset (rope_pos - (len - 1)), so a compressed sequence keeps its logical positions
@@ -72,7 +84,7 @@ class CompressionScheduler:
         self.policy = policy
         self.decode_step_counter = 0
 
-    def select(self, seqs: list[Sequence]) -> tuple[bool, list[int], list[int]]:
+    def select(self, seqs: list) -> tuple[bool, list[int], list[int]]:
         B = self.block_size
         window_tokens = self.window_blocks * B
         self.decode_step_counter += 1
@@ -92,7 +104,7 @@ class CompressionScheduler:
             selected = candidates[:self.topk]
         return is_compress_step, [x[0] for x in selected], [x[1] for x in selected]
 
-    def prepare(self, context, seqs: list[Sequence]) -> None:
+    def prepare(self, context, seqs: list) -> None:
         """Fill the compression fields of ``context`` for this decode step."""
         context.compress_need_mask = None
         context.compress_any = False
@@ -160,8 +172,7 @@ def apply_compression_events_device(scheduled: list, events: torch.Tensor | None
     if events is None:
         return
     from ..layers.compress_utils import events_to_dicts
-    evs = [e for e in events_to_dicts(events, -1) if e["batch_index"] >= 0]
-    apply_compression_events(scheduled, evs, block_manager)
+    apply_compression_events(scheduled, events_to_dicts(events, -1), block_manager)
 
 
 def apply_compression_events(scheduled: list, events: list[dict] | None, block_manager) -> None:
@@ -171,11 +182,10 @@ def apply_compression_events(scheduled: list, events: list[dict] | None, block_m
     dedup = {}
     for ev in events:
         bidx = ev["batch_index"]
-        if 0 <= bidx < len(scheduled):
+        if 0 <= bidx < len(scheduled) and not ev.get("skipped", False):
             dedup[bidx] = ev
     for bidx, ev in dedup.items():
-        item = scheduled[bidx]
-        seq = item.seq if isinstance(item, ScheduledSeq) or hasattr(item, "seq") else item
+        seq = _seq_of(scheduled[bidx])
         removed = len(seq) - ev["new_context_len"]
         block_manager.truncate_blocks(seq, ev["keep_blocks"])
         seq.num_tokens = ev["new_context_len"]

@@ -78,12 +78,57 @@ def _decode_args(q, k_cache, block_tables, context_lens, v_cache=None, out=None)
     return bs, Hq, D, NB, B, Hk
 
 
+def decode_workspace_bytes(bs: int, n_q_heads: int, max_blocks_per_seq: int,
+                           block_size: int, head_dim: int = 128) -> int:
+    """Bytes nkv_paged_decode needs: partial rows for what the grid can write (resident
+    waves x 16 query heads + batch x Hq rows of 528 B), not batch x table width."""
+    return int(_lib.lib().nkv_paged_decode_workspace_bytes(bs, n_q_heads, head_dim,
+                                                            max_blocks_per_seq, block_size))
+
+
 def paged_decode_workspace(q: torch.Tensor, k_cache: torch.Tensor,
                            block_tables: torch.Tensor) -> torch.Tensor:
     bs, Hq, D = q.shape
-    nbytes = _lib.lib().nkv_paged_decode_workspace_bytes(bs, Hq, D, block_tables.size(1),
-                                                          k_cache.size(1))
+    nbytes = decode_workspace_bytes(bs, Hq, block_tables.size(1), k_cache.size(1), D)
     return torch.empty(max(nbytes, 4), dtype=torch.uint8, device=q.device)
+
+
+# One decode workspace per device, shared by every Attention layer: the layers of a step
+# run one after another on one stream, so no two decode calls use it at once (callers
+# that run layers concurrently on several streams pass their own workspaces to
+# paged_decode). It only grows; a replaced buffer is kept alive, because a HIP graph
+# captured earlier may still hold its address.
+_SHARED_WS: dict = {}
+_RETIRED_WS: list = []
+
+
+def shared_decode_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """The device's shared decode workspace, grown to at least ``nbytes``."""
+    ws = _SHARED_WS.get(device)
+    if ws is None or ws.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            raise _lib.NkvError(
+                "the shared decode workspace must be large enough before graph capture: "
+                "call reserve_decode_workspace (or run the largest batch eagerly) first")
+        size = max(int(nbytes), 4)
+        if ws is not None:
+            size = max(size, 2 * ws.numel())  # few regrowths
+            _RETIRED_WS.append(ws)
+        ws = torch.empty(size, dtype=torch.uint8, device=device)
+        _SHARED_WS[device] = ws
+    return ws
+
+
+def reserve_decode_workspace(device, max_num_seqs: int, n_q_heads: int,
+                             max_blocks_per_seq: int, block_size: int,
+                             head_dim: int = 128) -> torch.Tensor:
+    """Size the device's shared decode workspace for the largest decode batch (the
+    model runner's max_num_seqs / graph batch and table width), e.g. before capture."""
+    device = torch.device(device)
+    if device.type == "cuda" and device.index is None:
+        device = torch.device("cuda", torch.cuda.current_device())
+    return shared_decode_workspace(device, decode_workspace_bytes(
+        max_num_seqs, n_q_heads, max_blocks_per_seq, block_size, head_dim))
 
 
 def paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
@@ -218,16 +263,11 @@ class Attention(nn.Module):
             self.kv_compress_keep_blocks = vllm_config.kv_compress_keep_blocks
             self.kv_compress_keep_extra_tokens = vllm_config.kv_compress_keep_extra_tokens
             self.kv_compress_agg = getattr(vllm_config, "kv_compress_agg", "all")
-        self._decode_ws = None
 
     def _workspace(self, q, block_tables):
-        nbytes = _lib.lib().nkv_paged_decode_workspace_bytes(
-            q.size(0), q.size(1), q.size(2), block_tables.size(1), self.k_cache.size(1))
-        ws = self._decode_ws
-        if ws is None or ws.numel() < nbytes or ws.device != q.device:
-            ws = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=q.device)
-            self._decode_ws = ws
-        return ws
+        """The device's decode workspace, shared with every other layer."""
+        return shared_decode_workspace(q.device, decode_workspace_bytes(
+            q.size(0), q.size(1), block_tables.size(1), self.k_cache.size(1), q.size(2)))
 
     def forward(self, q: torch.Tensor, k: torch.Tensor | None, v: torch.Tensor, Layer,
                 kv_stored: bool = False):

@@ -212,18 +212,28 @@ def compress_finalize(block_tables, base_context_lens, seq_idx, keep_tokens, blo
 
 
 def events_to_dicts(events: torch.Tensor, layer_id: int) -> list[dict]:
-    """Decode the int32 event rows into the reference's event dicts (:280-287)."""
+    """Decode the int32 event rows into the reference's event dicts (:280-287).
+
+    Padding rows (batch index -1) give no dict. A row with n_freed = -1 is a selected
+    sequence that was not compressible (fewer than W full blocks, or a table too short):
+    the reference asserts there (:39-41); here it is left unchanged and its dict carries
+    ``skipped: True``, which apply_compression_events ignores."""
     out = []
     for row in events.cpu().tolist():
+        if row[0] < 0:
+            continue
         n = row[3]
-        out.append({
+        ev = {
             "batch_index": int(row[0]),
             "layer": int(layer_id),
             "new_context_len": int(row[1]),
             "keep_blocks": int(row[2]),
-            "freed_block_ids": [int(x) for x in row[4:4 + n]],
+            "freed_block_ids": [int(x) for x in row[4:4 + max(n, 0)]],
             "tail_uncompressed_len_after": 0,
-        })
+        }
+        if n < 0:
+            ev["skipped"] = True
+        out.append(ev)
     return out
 
 

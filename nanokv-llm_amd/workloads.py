@@ -181,7 +181,8 @@ def decode_bytes(context_lens, Hq, Hk, D=HEAD_DIM, max_blocks=0):
 
 
 def decode_qwen3_32b_longctx(seed=6, device="cpu", bs=500, n_blocks=None, frac_compressed=0.2,
-                             pool_fraction=0.85, window_tokens=1024, keep_tokens=513):
+                             pool_fraction=0.85, window_tokens=1024, keep_tokens=513,
+                             alloc_caches=True):
     """High-concurrency long-context decode state at Qwen3-32B geometry.
 
     Context lengths exp(U(ln 1024, ln 16384)); a random 20% of the sequences were
@@ -193,6 +194,7 @@ def decode_qwen3_32b_longctx(seed=6, device="cpu", bs=500, n_blocks=None, frac_c
     with N(0,1) values. Returns decode_workload's fields plus ``compressed``
     (bool per sequence) and ``tail_uncompressed`` (tokens since the last
     compression).
+    With alloc_caches=False the caches are None (tables and lengths only).
     """
     gen = torch.Generator().manual_seed(seed)
     u = torch.rand(bs, generator=gen, dtype=torch.float64)
@@ -212,12 +214,14 @@ def decode_qwen3_32b_longctx(seed=6, device="cpu", bs=500, n_blocks=None, frac_c
     need = sum(math.ceil(int(c) / BLOCK) for c in ctx.tolist())
     n_blocks = max(n_blocks, need + 8)
     table = assign_blocks(ctx.tolist(), n_blocks, gen)
-    k_cache = torch.empty(n_blocks, BLOCK, Hk, D, dtype=torch.bfloat16, device=device)
-    v_cache = torch.empty_like(k_cache)
+    k_cache = v_cache = None
     used = table[table >= 0].to(torch.int64)
-    g = torch.Generator(device=device)
-    g.manual_seed(seed * 7 + 1)
-    for i in range(0, used.numel(), 1024):  # fill the used blocks only, 1 GiB at a time
+    if alloc_caches:
+        k_cache = torch.empty(n_blocks, BLOCK, Hk, D, dtype=torch.bfloat16, device=device)
+        v_cache = torch.empty_like(k_cache)
+        g = torch.Generator(device=device)
+        g.manual_seed(seed * 7 + 1)
+    for i in range(0, used.numel() if alloc_caches else 0, 1024):  # used blocks, 1 GiB a time
         ids = used[i:i + 1024].to(device)
         k_cache[ids] = torch.randn((ids.numel(), BLOCK, Hk, D), generator=g, device=device,
                                    dtype=torch.float32).to(torch.bfloat16)

@@ -110,6 +110,9 @@ def compress_compact_ref(q_current, k_cache, v_cache, block_tables, base_context
 
     Returns (ok, keep_idx [m, n_sets, keep_tokens], events or None). If
     keep_idx is given, scoring is skipped and those positions are used.
+    Tail row u goes to logical position keep_tokens + u of the window region
+    (window blocks, then the tail block), which is the reference's slot
+    wherever the reference stays inside the last kept block.
     """
     seq_idxs = torch.as_tensor(seq_idxs, dtype=torch.long)
     m = seq_idxs.numel()
@@ -136,6 +139,10 @@ def compress_compact_ref(q_current, k_cache, v_cache, block_tables, base_context
 
     new_lens = old - window_tokens + keep_tokens
     dst_keep = slots[:, :keep_tokens]  # [m, keep]
+    # the window's slots followed by the tail block's: logical position p of the window
+    # region (p < W*B + B) is slot ext[:, p]
+    tail_slots = tail_ids.clamp(min=0).unsqueeze(1) * B + torch.arange(B).view(1, B)
+    ext = torch.cat([slots, tail_slots], dim=1)
     total_slots = NB * B
     kf = k_cache.view(total_slots, Hk, D)
     vf = v_cache.view(total_slots, Hk, D)
@@ -149,7 +156,11 @@ def compress_compact_ref(q_current, k_cache, v_cache, block_tables, base_context
             if t > 0:
                 off = torch.arange(t)
                 src.append(tail_ids[i] * B + off)
-                dst.append(dst_keep[i, -1] + 1 + off)
+                # logical position keep_tokens + u; the reference's physical slot
+                # dst_keep[-1] + 1 + u equals it while it stays inside the last kept
+                # block (keep_tokens % B + tail <= B, e.g. the default 2*B + 1 keep)
+                # and would land in an unrelated block past it
+                dst.append(ext[i, keep_tokens + off])
         src_flat = torch.cat(src)
         dst_flat = torch.cat(dst)
         assert int(src_flat.min()) >= 0 and int(src_flat.max()) < total_slots

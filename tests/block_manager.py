@@ -1,4 +1,4 @@
-"""Paged block allocator for the K/V pool (host bookkeeping, no prefix cache).
+"""TEST DOUBLE: Paged block allocator for the K/V pool (host bookkeeping, no prefix cache).
 
 Follows the allocation, append and release rules of
 nanokvllm/engine/block_manager.py:38-138 that the attention path depends on:
@@ -6,12 +6,14 @@ a sequence owns ``ceil(len / B)`` blocks, a new block is taken when
 ``len % B == 1`` after an append, and ``truncate_blocks`` releases the tail
 blocks freed by a compression step. Prefix hashing (xxhash) is not kept; a
 block is "sealed" (hash != -1) once full, which is all ``may_append`` checks.
+The package takes the caller's own block manager (any object with
+``truncate_blocks(seq, keep_blocks)``).
 """
 from __future__ import annotations
 
 from collections import deque
 
-from .sequence import Sequence
+from sequence import Sequence
 
 
 class Block:

@@ -1,4 +1,7 @@
-"""Per-request state the attention path reads (host bookkeeping).
+"""TEST DOUBLE: the per-request state the attention path reads (host bookkeeping).
+
+Used by the tests to drive the engine hooks; the package reads these fields
+duck-typed from the caller's own sequence objects and ships no Sequence.
 
 Keeps the fields of nanokvllm/engine/sequence.py:15-94 that the compression
 path depends on: ``num_tokens`` is the PHYSICAL cache length (shrinks after

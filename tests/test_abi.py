@@ -56,11 +56,24 @@ def test_host_side_argument_checks_without_gpu():
     assert rc == -1 and b"num_keep" in lib.nkv_last_error()
     # zero tokens is a no-op
     assert lib.nkv_store_kvcache(None, 0, None, 0, None, None, None, 0, 8, 128, 0, None) == 0
-    # workspace sizing is pure host arithmetic: partial slots per (sequence, query head) =
-    # min(128, ceil(chunks of the table width / 4) + 1)
-    for width, slots in ((32, 128), (16, 65), (2, 9)):
-        assert lib.nkv_paged_decode_workspace_bytes(64, 32, 128, width, 256) == \
-            64 * 32 * slots * 130 * 4 + 64 * 32 * 4
+    # workspace sizing is pure host arithmetic (no device here: 256 CUs assumed). It holds
+    # what the split grid can write: one 16-byte descriptor per (sequence, KV head) (bounded
+    # with Hq), batch*Hq partial rows of 528 bytes for the segment boundaries, and one row
+    # per query-head column (at most 16) of each resident wave (8 per CU), capped by the
+    # waves the table width can give work to
+    def expect(bs, hq, width, B=256):
+        chunks = width * B // 16
+        slots = min(128, -(-chunks // 4) + 1)
+        min_chunks = max(4, -(-chunks // (slots - 1)))
+        useful = max(1, -(-bs * chunks // min_chunks))
+        cols = min(256 * 8 * min(16, hq), useful * hq)
+        return bs * hq * 16 + (bs * hq + cols) * 528
+
+    for bs, hq, width in ((64, 32, 32), (64, 32, 2), (1, 16, 2), (500, 64, 64), (7, 40, 9)):
+        assert lib.nkv_paged_decode_workspace_bytes(bs, hq, 128, width, 256) == \
+            expect(bs, hq, width)
+    # Qwen3-32B geometry at batch 500 with 64-block tables: ~34 MB for any number of layers
+    assert lib.nkv_paged_decode_workspace_bytes(500, 64, 128, 64, 256) < 36e6
 
 
 P = 0x10000  # a 16-byte aligned stand-in for a device pointer: never dereferenced, since
@@ -100,12 +113,13 @@ def _cstep(**kw):
 
 CASES = [
     (_prefill(d=64), EUNSUPPORTED, b"head_dim"),
-    (_prefill(hq=16, hk=1), EUNSUPPORTED, b"GQA group"),
+    (_prefill(hq=17, hk=1), EUNSUPPORTED, b"GQA group"),
     (_prefill(q=P + 2), EINVAL, b"aligned"),
     (_prefill(qrs=1000), EINVAL, b"row strides"),
     (_prefill(bt=P, btrs=4, mb=4, bs=8), EUNSUPPORTED, b"multiple of 16"),
     (_prefill(bt=P, btrs=4, mb=4, vrs=2048), EINVAL, b"share one row stride"),
     (_decode(hq=32, hk=1), EUNSUPPORTED, b"GQA group"),
+    (_decode(hq=24, hk=8, wsb=16), EWORKSPACE, b"workspace"),
     (_decode(bs=8), EUNSUPPORTED, b"multiple of 16"),
     (_decode(btrs=16), EINVAL, b"block table"),
     (_decode(wsb=16), EWORKSPACE, b"workspace"),

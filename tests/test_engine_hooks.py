@@ -5,6 +5,7 @@ Follows nanokvllm/engine/model_runner.py:154-219, 265-332, scheduler.py:103-125,
 block_manager.py:94-138 and sequence.py:82-94.
 """
 import importlib
+import math
 from types import SimpleNamespace
 
 import pytest
@@ -14,8 +15,8 @@ from oracle import metadata_ref
 from oracle.compress_ref import compress_compact_ref, compress_schedule_ref
 
 hooks = importlib.import_module("nanokv-llm_amd.engine.compress_hooks")
-seqmod = importlib.import_module("nanokv-llm_amd.engine.sequence")
-bmmod = importlib.import_module("nanokv-llm_amd.engine.block_manager")
+import sequence as seqmod  # noqa: E402  (test double, tests/sequence.py)
+import block_manager as bmmod  # noqa: E402  (test double, tests/block_manager.py)
 Sequence, ScheduledSeq = seqmod.Sequence, seqmod.ScheduledSeq
 BlockManager = bmmod.BlockManager
 B, W = 256, 4
@@ -208,3 +209,30 @@ def test_device_events_skip_padding_rows():
     hooks.apply_compression_events_device([ScheduledSeq(a, 1)], ev, bm)
     assert len(a) == new_len and len(a.block_table) == keep_blocks
     assert a.tail_uncompressed_len == 0 and len(bm.free_block_ids) == n_before + len(freed)
+
+
+def test_skipped_event_changes_no_host_state():
+    """An event row marked skipped (n_freed = -1: the selected sequence was not
+    compressible) leaves the sequence and the block manager as they were."""
+    import numpy as np
+    cu = importlib.import_module("nanokv-llm_amd.layers.compress_utils")
+    bm = BlockManager(32, B)
+    s0, s1 = _seq(5 * B + 7), _seq(3 * B + 9)
+    for s in (s0, s1):
+        bm.allocate(s)
+    # a compressed row for s0 and a skipped row for s1, as nkv_compress_finalize writes them
+    kb = math.ceil((5 * B + 7 - W * B + 2 * B + 1) / B)
+    freed = s0.block_table[kb:]
+    rows = np.full((2, 4 + 8), -1, dtype=np.int32)
+    rows[0, :4] = [0, 5 * B + 7 - W * B + 2 * B + 1, kb, len(freed)]
+    rows[0, 4:4 + len(freed)] = freed
+    rows[1, :4] = [1, 3 * B + 9, 4, -1]
+    evs = cu.events_to_dicts(torch.from_numpy(rows), 0)
+    assert evs[1]["skipped"] and "skipped" not in evs[0]
+    before = (len(s1), list(s1.block_table), s1.num_computed_tokens, s1.tail_uncompressed_len)
+    free_before = len(bm.free_block_ids)
+    hooks.apply_compression_events([s0, s1], evs, bm)
+    assert (len(s1), list(s1.block_table), s1.num_computed_tokens,
+            s1.tail_uncompressed_len) == before
+    assert len(s0) == 5 * B + 7 - W * B + 2 * B + 1 and s0.tail_uncompressed_len == 0
+    assert len(bm.free_block_ids) == free_before + len(freed)

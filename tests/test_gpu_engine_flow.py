@@ -18,8 +18,8 @@ from oracle.compress_ref import compress_compact_ref
 pytestmark = pytest.mark.gpu
 TOL = 2e-2
 hooks = importlib.import_module("nanokv-llm_amd.engine.compress_hooks")
-seqmod = importlib.import_module("nanokv-llm_amd.engine.sequence")
-bmmod = importlib.import_module("nanokv-llm_amd.engine.block_manager")
+import sequence as seqmod  # noqa: E402  (test double, tests/sequence.py)
+import block_manager as bmmod  # noqa: E402  (test double, tests/block_manager.py)
 B, W, Hq, Hk, D, LAYERS = 256, 4, 16, 4, 128, 2
 
 

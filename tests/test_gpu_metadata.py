@@ -14,8 +14,8 @@ from oracle import metadata_ref
 pytestmark = pytest.mark.gpu
 md_mod = importlib.import_module("nanokv-llm_amd.engine.metadata")
 hooks = importlib.import_module("nanokv-llm_amd.engine.compress_hooks")
-seqmod = importlib.import_module("nanokv-llm_amd.engine.sequence")
-bmmod = importlib.import_module("nanokv-llm_amd.engine.block_manager")
+import sequence as seqmod  # noqa: E402  (test double, tests/sequence.py)
+import block_manager as bmmod  # noqa: E402  (test double, tests/block_manager.py)
 B = 256
 KEYS = ("positions", "slot_mapping", "context_lens", "cu_seqlens_q", "cu_seqlens_k",
         "logits_indices", "block_tables")

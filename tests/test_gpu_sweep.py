@@ -1,7 +1,7 @@
 """Seeded random sweeps of small configurations against the oracle.
 
-Each case draws its own geometry: block sizes 16-256 (compression 64-256), 1-8 KV heads,
-every GQA group the kernels take, ragged contexts including empty and one-token ones,
+Each case draws its own geometry: block sizes 16-256 (compression 64-512), 1-8 KV heads,
+GQA groups 1-8 and 16, ragged contexts including empty and one-token ones,
 tables padded with -1 or 0, and padding entries in the compression selection. Tolerances
 are the suite's: 2e-2 max abs error for bf16 attention outputs against the fp32 oracle,
 bit-exact integer work (cache rows, lengths, kept indices given the scores) and importance
@@ -45,7 +45,7 @@ def test_decode_sweep(nkv, dev, case):
     g = torch.Generator().manual_seed(1000 + case)
     B = rng.choice([16, 32, 64, 128, 256])
     Hk = rng.choice([1, 2, 4, 8])
-    G = rng.choice([1, 2, 4, 8, 16])
+    G = rng.choice([1, 2, 3, 4, 5, 6, 7, 8, 16])
     bs = rng.randrange(1, 70)
     top = rng.choice([40, 600, 3000])
     lens = [rng.choice([0, 1, rng.randrange(1, top + 1), rng.randrange(1, top + 1)])
@@ -70,7 +70,7 @@ def test_prefill_sweep(nkv, dev, case):
     paged = case % 4 != 3
     B = rng.choice([16, 32, 64, 128, 256])
     Hk = rng.choice([1, 2, 4, 8])
-    G = rng.choice([1, 2, 4, 8])
+    G = rng.choice([1, 2, 3, 4, 5, 6, 8, 16])
     n = rng.randrange(1, 7)
     Lq, Lk = [], []
     for _ in range(n):
@@ -130,15 +130,16 @@ def test_compress_step_sweep(nkv, dev, case):
     g = torch.Generator().manual_seed(4000 + case)
     B = rng.choice([64, 128, 256])
     W = rng.choice([2, 3, 4]) if B == 256 else rng.choice([2, 4])
-    # kept + tail rows fit one fused workgroup (<= 768); the last case takes the general path
-    # (up to 1024 rows)
-    choices = [(kb, ex) for kb in range(1, W) for ex in (1, B // 2) if kb * B + ex + B - 1 <= 768]
+    # any keep (one or more read-then-write rounds, tails at logical positions); the last
+    # case has a window over 1024 tokens: the general path (score, importance, top-k and a
+    # compaction of up to 1323 rows in two rounds)
+    choices = [(kb, ex) for kb in range(1, W) for ex in (0, 1, B // 2)]
     keep_blocks, extra = rng.choice(choices)
     if case == 11:
-        B, W, keep_blocks, extra = 256, 4, 2, 128
+        B, W, keep_blocks, extra = 512, 3, 1, 300
     keep = keep_blocks * B + extra
     Hk = rng.choice([1, 2, 4, 8])
-    G = rng.choice([1, 2, 4, 8, 16])
+    G = rng.choice([1, 2, 3, 4, 5, 6, 7, 8, 16])
     agg = rng.choice(["all", "group"])
     bs = rng.randrange(2, 24)
     # eligible lengths: at least W full blocks, tail != B - 1

@@ -193,3 +193,123 @@ def test_window_location_closed_form():
     assert slots[0].tolist() == [b * 4 + o for b in (9, 1, 4) for o in range(4)]
     assert slots[1].tolist() == [b * 4 + o for b in (6, 8, 0) for o in range(4)]
     assert tail.tolist() == [1, 0] and tail_ids.tolist() == [2, -1]
+
+
+def _tiny_state(seed, B, lens, nb, Hk=2, D=4):
+    g = torch.Generator().manual_seed(seed)
+    kc = torch.randn(nb, B, Hk, D, generator=g)
+    vc = torch.randn(nb, B, Hk, D, generator=g)
+    perm = torch.randperm(nb, generator=g).tolist()
+    width = max(math.ceil(n / B) for n in lens) + 1
+    bt = torch.full((len(lens), width), -1, dtype=torch.int32)
+    p = 0
+    for i, n in enumerate(lens):
+        k = math.ceil(n / B)
+        bt[i, :k] = torch.tensor(perm[p:p + k])
+        p += k
+    return kc, vc, bt, torch.tensor(lens, dtype=torch.int32)
+
+
+def _random_keep(g, m, n_sets, W, B, keep_tokens):
+    """[0, ascending random middle, W*B - 1] per (sequence, set)."""
+    rows = []
+    for _ in range(m * n_sets):
+        mid = torch.randperm(W * B - 2, generator=g)[:keep_tokens - 2] + 1
+        rows.append(torch.cat([torch.tensor([0]), mid.sort().values, torch.tensor([W * B - 1])]))
+    return torch.stack(rows).view(m, n_sets, keep_tokens)
+
+
+@pytest.mark.parametrize("keep_blocks,extra", [(1, 1), (2, 1), (2, 2), (3, 0), (1, 3)])
+def test_compaction_tail_where_the_reference_stays_in_block(keep_blocks, extra):
+    """Tails that fit after the last kept token in its block ((keep-1) % B + tail < B): the
+    oracle's logical placement equals the reference's slot(keep-1) + 1 + u, per slot."""
+    B, W = 4, 4
+    keep_tokens = keep_blocks * B + extra
+    room = B - 1 - (keep_tokens - 1) % B  # tail rows that stay in the block
+    lens = [W * B + t for t in range(0, room + 1)] + [(W + 1) * B + room]
+    kc, vc, bt, lt = _tiny_state(11 + keep_tokens, B, lens, 40)
+    sel = list(range(len(lens)))
+    keep = _random_keep(torch.Generator().manual_seed(keep_tokens), len(sel), 1, W, B,
+                        keep_tokens)
+    kc2, vc2 = kc.clone(), vc.clone()
+    compress_compact_ref(None, kc2, vc2, bt, lt, lt.clone(), sel, B, W, keep_blocks, extra, 0,
+                         1, keep_idx=keep)
+    exp_k, exp_v = kc.clone(), vc.clone()
+    _brute_compact(exp_k, exp_v, bt, lt, sel, B, W, keep[:, 0], keep_tokens)
+    assert torch.equal(kc2, exp_k) and torch.equal(vc2, exp_v)
+
+
+def _read_seq(cache, bt_row, n, B):
+    return torch.stack([cache[int(bt_row[t // B]), t % B] for t in range(n)])
+
+
+@pytest.mark.parametrize("agg_sets", [1, 2])
+@pytest.mark.parametrize("keep_blocks,extra", [(2, 0), (1, 3), (2, 2), (3, 0)])
+def test_compaction_read_back_through_the_table(agg_sets, keep_blocks, extra):
+    """Any keep and tail: the compacted sequence read through its block table is its
+    prefix, then the kept window rows in order, then the tail rows; every slot outside the
+    sequence's own blocks is untouched. (Where keep % B + tail > B the reference's
+    slot(keep-1) + 1 + u lies past the last kept token's block.)"""
+    B, W = 4, 4
+    keep_tokens = keep_blocks * B + extra
+    lens = [W * B + 3, W * B + 1, (W + 2) * B + 2, W * B, (W + 1) * B + 3]
+    kc, vc, bt, lt = _tiny_state(5 + keep_tokens * agg_sets, B, lens, 48)
+    sel = [0, 1, 2, 3, 4]
+    keep = _random_keep(torch.Generator().manual_seed(3 + keep_tokens), len(sel), agg_sets, W,
+                        B, keep_tokens)
+    kc2, vc2, ctx = kc.clone(), vc.clone(), lt.clone()
+    compress_compact_ref(None, kc2, vc2, bt, lt, ctx, sel, B, W, keep_blocks, extra, 0, 1,
+                         keep_idx=keep)
+    owned = {int(b) for b in bt.flatten().tolist() if b >= 0}
+    for b in range(kc.size(0)):
+        if b not in owned:
+            assert torch.equal(kc2[b], kc[b]) and torch.equal(vc2[b], vc[b])
+    for j, s in enumerate(sel):
+        n, new_n = lens[s], int(ctx[s])
+        assert new_n == n - W * B + keep_tokens
+        w0 = (n // B - W) * B
+        for old_c, new_c in ((kc, kc2), (vc, vc2)):
+            old = _read_seq(old_c, bt[s], n, B)
+            new = _read_seq(new_c, bt[s], new_n, B)
+            assert torch.equal(new[:w0], old[:w0])
+            for h in range(kc.size(2)):
+                ki = keep[j, 0 if agg_sets == 1 else h]
+                assert torch.equal(new[w0:w0 + keep_tokens, h], old[w0 + ki, h])
+            assert torch.equal(new[w0 + keep_tokens:], old[w0 + W * B:])
+
+
+def test_compaction_read_back_fails_for_the_physical_rule():
+    """A planted mistake: placing the tail at slot(keep-1) + 1 + u (the reference's rule)
+    where it leaves the block breaks the read-back of the previous test."""
+    B, W, keep_tokens = 4, 4, 8  # keep_blocks 2, extra 0: every tail leaves the block
+    lens = [W * B + 3]
+    kc, vc, bt, lt = _tiny_state(1, B, lens, 12)
+    keep = _random_keep(torch.Generator().manual_seed(1), 1, 1, W, B, keep_tokens)
+    exp_k, exp_v = kc.clone(), vc.clone()
+    _brute_compact(exp_k, exp_v, bt, lt, [0], B, W, keep[:, 0], keep_tokens)
+    new_n = lens[0] - W * B + keep_tokens
+    new = _read_seq(exp_k, bt[0], new_n, B)
+    old = _read_seq(kc, bt[0], lens[0], B)
+    assert not torch.equal(new[keep_tokens:], old[W * B:])
+
+
+def test_gather_kv_by_slots_explicit_loops():
+    """gather_kv_by_slots_ref (compress_utils.py:75-97): k_sub[j, h, p] = k_cache[s // B,
+    s % B, h] for s = slots[j, p], by loops; a planted head/position transposition fails."""
+    from oracle.compress_ref import gather_kv_by_slots_ref
+    g = torch.Generator().manual_seed(8)
+    NB, B, Hk, D = 6, 4, 3, 5
+    kc = torch.randn(NB, B, Hk, D, generator=g)
+    vc = torch.randn(NB, B, Hk, D, generator=g)
+    slots = torch.stack([torch.randperm(NB * B, generator=g)[:7] for _ in range(2)])
+    k_sub, v_sub = gather_kv_by_slots_ref(kc, vc, slots)
+    assert k_sub.shape == (2, Hk, 7, D) and k_sub.is_contiguous()
+    for j in range(2):
+        for h in range(Hk):
+            for p in range(7):
+                s = int(slots[j, p])
+                assert torch.equal(k_sub[j, h, p], kc[s // B, s % B, h])
+                assert torch.equal(v_sub[j, h, p], vc[s // B, s % B, h])
+    # the planted mistake: heads and positions swapped (no permute) reads other rows
+    wrong = kc.view(NB * B, Hk, D)[slots]  # [2, 7, Hk, D]
+    assert not torch.equal(wrong.reshape(2, Hk, 7, D), k_sub)
