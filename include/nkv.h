@@ -166,6 +166,29 @@ int nkv_paged_decode(const void* q, int64_t q_row_stride,
                      void* out, int64_t out_row_stride,
                      void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Paged decode that allocates nothing and takes no workspace: the same arguments
+ * (without workspace/workspace_bytes), kernels and result as nkv_paged_decode,
+ * with the partials in a fixed device array of NKV_DECODE_NOALLOC_MAX_BYTES that
+ * the library holds on every GPU it runs on until the process ends. A call whose
+ * partials would exceed it (nkv_paged_decode_workspace_bytes is an upper bound;
+ * about batch * n_q_heads <= 94k at 256 CUs) returns NKV_EUNSUPPORTED before
+ * launching anything. Nothing in the array needs to start at zero. Every call on a
+ * GPU uses that GPU's one array: calls that overlap on one GPU (different streams
+ * without ordering between them) race and give wrong results.
+ * No counterpart in the reference: for callers that cannot allocate (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ */
+#define NKV_DECODE_NOALLOC_MAX_BYTES (64u << 20)
+int nkv_paged_decode_noalloc(const void* q, int64_t q_row_stride,
+                             const void* k_cache, const void* v_cache,
+                             const int32_t* block_tables, int64_t bt_row_stride,
+                             const int32_t* context_lens, int32_t batch,
+                             int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                             int32_t block_size, int32_t max_blocks_per_seq,
+                             int64_t n_blocks, float scale,
+                             void* out, int64_t out_row_stride, void* stream);
+
 /* Paged decode over fp8 (OCP E4M3FN) caches: same arguments and result as
  * nkv_paged_decode with K = code * k_scale and V = code * v_scale (codes of
  * nkv_store_kvcache_fp8); half the cache bytes per decoded token. Same

@@ -18,6 +18,7 @@ LIB_PATH = os.path.join(PKG_DIR, "libnkv_amd.so")
 NKV_OK = 0
 NKV_AGG_ALL = 0
 NKV_AGG_GROUP = 1
+NKV_DECODE_NOALLOC_MAX_BYTES = 64 << 20  # include/nkv.h
 
 _p = C.c_void_p
 _i32 = C.c_int32
@@ -42,6 +43,8 @@ SIGNATURES = {
     "nkv_paged_decode_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
     "nkv_paged_decode": (C.c_int, [_p, _i64, _p, _p, _p, _i64, _p, _i32, _i32, _i32, _i32, _i32,
                                    _i32, _i64, _f32, _p, _i64, _p, _sz, _p]),
+    "nkv_paged_decode_noalloc": (C.c_int, [_p, _i64, _p, _p, _p, _i64, _p, _i32, _i32, _i32,
+                                           _i32, _i32, _i32, _i64, _f32, _p, _i64, _p]),
     "nkv_paged_decode_fp8": (C.c_int, [_p, _i64, _p, _p, _p, _i64, _p, _i32, _i32, _i32, _i32,
                                        _i32, _i32, _i64, _f32, _f32, _f32, _p, _i64, _p, _sz,
                                        _p]),

@@ -758,3 +758,74 @@ extern "C" int nkv_paged_decode_fp8(const void* q, int64_t q_row_stride, const v
                                   block_size, max_blocks_per_seq, out, out_row_stride, workspace,
                                   workspace_bytes, stream);
 }
+
+// ------------------------------------------------------------------ no-allocation variant
+// The decode workspace in a fixed device array: for callers that cannot allocate (code
+// under graph capture, tight serving loops). Each device holds its own copy of the array
+// for the life of the process. Host code never passes the array's name to a kernel (on
+// the host it is only a stand-in): its device address comes from hipGetSymbolAddress,
+// taken once per device on the first call there, with that device current.
+namespace nkv {
+constexpr size_t kScratchBytes = NKV_DECODE_NOALLOC_MAX_BYTES;  // batch*Hq up to ~94k heads
+}  // namespace nkv
+
+static __device__ __align__(256) unsigned char scratch[nkv::kScratchBytes];
+
+namespace nkv {
+// Device address of `scratch` on the current device, or nullptr (error text set).
+static void* scratch_ptr() {
+  static std::atomic<void*> ptrs[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    set_error("paged_decode_noalloc: no current device");
+    return nullptr;
+  }
+  void* p = ptrs[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    // threads that race here obtain the same address
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      set_error("paged_decode_noalloc: hipGetSymbolAddress failed: %s", hipGetErrorString(e));
+      return nullptr;
+    }
+    ptrs[dev].store(p, std::memory_order_release);
+  }
+  return p;
+}
+}  // namespace nkv
+
+extern "C" int nkv_paged_decode_noalloc(const void* q, int64_t q_row_stride, const void* k_cache,
+                                        const void* v_cache, const int32_t* block_tables,
+                                        int64_t bt_row_stride, const int32_t* context_lens,
+                                        int32_t batch, int32_t n_q_heads, int32_t n_kv_heads,
+                                        int32_t head_dim, int32_t block_size,
+                                        int32_t max_blocks_per_seq, int64_t n_blocks,
+                                        float scale, void* out, int64_t out_row_stride,
+                                        void* stream) {
+  using namespace nkv;
+  clear_error();
+  int rc = decode_check(q, k_cache, v_cache, block_tables, context_lens, batch, n_q_heads,
+                        n_kv_heads, head_dim, block_size, max_blocks_per_seq, q_row_stride,
+                        bt_row_stride);
+  if (rc) return rc;
+  if (batch == 0) return NKV_OK;
+  // the bytes this call's plan needs, against the array's fixed size
+  const DecodePlan p = decode_plan<false>(batch, n_q_heads, n_kv_heads, max_blocks_per_seq,
+                                          block_size);
+  const size_t need = decode_desc_bytes(batch, n_kv_heads) +
+                      decode_part_bytes(p.grid, p.hp * (n_q_heads / n_kv_heads), batch,
+                                        n_q_heads);
+  NKV_REQUIRE(need <= kScratchBytes, NKV_EUNSUPPORTED,
+              "paged_decode_noalloc: batch %d x %d query heads needs %zu bytes of partials, "
+              "above the fixed %zu-byte array; use nkv_paged_decode with a workspace",
+              batch, n_q_heads, need, kScratchBytes);
+  void* ws = scratch_ptr();
+  if (ws == nullptr) return NKV_ELAUNCH;
+  rc = decode_split<false>(q, q_row_stride, k_cache, v_cache, block_tables, bt_row_stride,
+                           context_lens, batch, n_q_heads, n_kv_heads, head_dim, block_size,
+                           max_blocks_per_seq, n_blocks, scale, 1.f, 1.f, ws, kScratchBytes,
+                           stream);
+  if (rc) return rc;
+  return decode_combine(context_lens, batch, n_q_heads, n_kv_heads, head_dim, block_size,
+                        max_blocks_per_seq, out, out_row_stride, ws, kScratchBytes, stream);
+}
