@@ -243,6 +243,44 @@ def cpu_baseline(wl, bt, kc, vc, budget_s=12.0):
                       f"{len(times)} runs; host has {os.cpu_count()} logical CPUs"}
 
 
+def compress_parity(cw, dev, agg):
+    """The timed compression step once on a fresh copy of its state, against the oracle:
+    importance within rtol 1e-4 (max relative error reported), kept sets exact given the
+    scores, caches, lengths and events bit-exact."""
+    from oracle.compress_ref import (compress_compact_ref, gather_kv_by_slots_ref,
+                                     get_tail_window_and_tail_slots_ref, select_topk_ref,
+                                     snapkv_importance_ref)
+    kg, vg = cw["k_cache"].clone(), cw["v_cache"].clone()
+    bt, lens, sel = cw["block_tables"], cw["context_lens"], cw["seq_idx"]
+    btg, base = bt.to(dev), lens.to(dev)
+    ctx = base.clone()
+    seq_idx = torch.tensor(sel, dtype=torch.int32, device=dev)
+    keep, imp = cu.compress_step(cw["q"].to(dev), kg, vg, btg, base, ctx, seq_idx, 4, 513,
+                                 128 ** -0.5, agg)
+    events = torch.empty(len(sel), 4 + bt.size(1), dtype=torch.int32, device=dev)
+    cu.compress_finalize(btg, base, seq_idx, 513, 256, 4, events, rewrite_tables=False)
+    torch.cuda.synchronize()
+    kc, vc = cw["k_cache"].cpu(), cw["v_cache"].cpu()
+    st = torch.tensor(sel)
+    slots, *_ = get_tail_window_and_tail_slots_ref(bt, lens, st, 256, 4)
+    k_sub, _ = gather_kv_by_slots_ref(kc, vc, slots)
+    ref_imp = snapkv_importance_ref(cw["q"].index_select(0, st).unsqueeze(2), k_sub, 1, "fp32",
+                                    agg)
+    imp = imp.cpu()
+    rel = float(((imp - ref_imp).abs() / ref_imp.abs().clamp(min=1e-7)).max())
+    keep = keep.cpu().long()
+    kept_exact = bool(torch.equal(keep[..., 1:-1], select_topk_ref(imp, 511)))
+    ctx_ref = lens.clone()
+    _, _, ev_ref = compress_compact_ref(None, kc, vc, bt, lens, ctx_ref, sel, 256, 4, 2, 1, 0, 1,
+                                        keep_idx=keep)
+    caches = bool(torch.equal(kg.cpu(), kc) and torch.equal(vg.cpu(), vc))
+    meta = bool(torch.equal(ctx.cpu(), ctx_ref) and cu.events_to_dicts(events, 0) == ev_ref)
+    del kg, vg
+    return {"importance_max_rel_err": rel, "importance_within_1e-4": rel <= 1e-4,
+            "kept_sets_exact_given_scores": kept_exact, "caches_bit_exact": caches,
+            "lengths_and_events_exact": meta}
+
+
 def run_compress(args, dev):
     """One layer's compression step at batch 500: scoring, top-k and compaction of the 20
     longest sequences (window 4 blocks, keep 513), per KV head (agg "group", the benchmark
@@ -262,7 +300,7 @@ def run_compress(args, dev):
     lens = cw["context_lens"][cw["seq_idx"]].to(torch.int64)
     tails = lens % 256
     nbytes = m * 1024 * 2048 + m * Hq * 128 * 2 + 2 * int((513 + tails).sum()) * 4096
-    res = {}
+    res = {f"compress_parity_{agg}": compress_parity(cw, dev, agg) for agg in ("group", "all")}
     for agg in ("group", "all"):
         n_sets = 1 if agg == "all" else Hk
         imp = torch.empty(m, n_sets, 1023, dtype=torch.float32, device=dev)

@@ -74,19 +74,6 @@ int nkv_store_kvcache(const void* key, int64_t key_row_stride,
  */
 int nkv_fp8_quantize(const void* src, int64_t n, float scale, void* dst, void* stream);
 int nkv_fp8_dequantize(const void* src, int64_t n, float scale, void* dst, void* stream);
-/* Rows of each sequence gathered from fp8 caches into contiguous bf16:
- * k_out[cu_seqlens_k[s] + t] = code(k_cache row of token t of s) * k_scale
- * (likewise v), t < Lk_s; missing or out-of-range table entries give zero
- * rows. k_out/v_out are [cu_seqlens_k[n_seqs], Hk, D]; max_seqlen_k sizes
- * the launch. Feeds nkv_prefill_varlen's contiguous mode over an fp8 pool.
- * Replaces: the paged K/V read of flash_attn_varlen_func(..., block_table)
- *           (nanokvllm/layers/attention.py:96-102) for an fp8 pool. */
-int nkv_fp8_gather_rows(const void* k_cache, const void* v_cache,
-                        const int32_t* block_tables, int64_t bt_row_stride,
-                        int32_t max_blocks_per_seq, const int32_t* cu_seqlens_k,
-                        int32_t n_seqs, int32_t max_seqlen_k, int32_t n_kv_heads,
-                        int32_t head_dim, int32_t block_size, int64_t n_blocks,
-                        float k_scale, float v_scale, void* k_out, void* v_out, void* stream);
 int nkv_store_kvcache_fp8(const void* key, int64_t key_row_stride, const void* value,
                           int64_t value_row_stride, void* k_cache, void* v_cache,
                           const int32_t* slot_mapping, int64_t n_tokens, int32_t n_kv_heads,
@@ -248,6 +235,21 @@ int nkv_prefill_varlen(const void* q, int64_t q_row_stride,
                        int32_t block_size, int64_t n_rows, float scale,
                        void* out, int64_t out_row_stride, void* stream);
 
+/* Varlen causal prefill over a paged fp8 (OCP E4M3FN) pool: the paged mode of
+ * nkv_prefill_varlen with K = code * k_scale and V = code * v_scale (codes of
+ * nkv_store_kvcache_fp8), cache rows of n_kv_heads*head_dim bytes and n_blocks
+ * blocks. The kernel widens the codes to bf16 (exact) as it stages them; no
+ * intermediate buffer. Replaces: the flash_attn_varlen_func(..., block_table)
+ * call (nanokvllm/layers/attention.py:96-102) over an fp8 pool. */
+int nkv_prefill_varlen_fp8(const void* q, int64_t q_row_stride,
+                           const void* k_cache, const void* v_cache,
+                           const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                           const int32_t* block_tables, int64_t bt_row_stride,
+                           int32_t max_blocks_per_seq, int32_t n_seqs, int32_t max_seqlen_q,
+                           int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                           int32_t block_size, int64_t n_blocks, float scale, float k_scale,
+                           float v_scale, void* out, int64_t out_row_stride, void* stream);
+
 /* Aggregation of key importance over query heads (compression scoring). */
 #define NKV_AGG_ALL 0   /* sum over all Hq heads -> one kept set per sequence
                            (nanokvllm/layers/CompressMethod.py:41-42) */
@@ -322,6 +324,29 @@ int nkv_compress_select(const void* q, int64_t q_row_stride,
                         float scale, int32_t agg_mode, int32_t num_keep,
                         float* importance_out, int32_t* keep_idx,
                         void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * SnapKV as the compression plug-in calls it (contiguous tensors): Q [m, Hq,
+ * window, D], K [m, Hk, seq_len, D] (bf16, both contiguous). With w = window and
+ * n_cand = seq_len - w, the importance of key t < n_cand is
+ *   imp[j, s, t] = sum_{h in set s} sum_{i < w} softmax_t(scale * Q[j,h,i].K[j,h/g,t])
+ * with key 0 masked (attention sink) and the w query-window keys not scored;
+ * importance_out fp32 [m, n_sets, n_cand] (n_sets 1 for ALL, Hk for GROUP),
+ * keep_idx int32 [m, n_sets, num_keep + 1 + w] =
+ *   [0, ascending top-num_keep (ties -> lower index), n_cand, ..., seq_len - 1].
+ * window 1 is nkv_compress_select on the contiguous K; a window > 1 needs
+ * seq_len a multiple of 256 and n_cand <= 4096. Workspace:
+ * nkv_snapkv_workspace_bytes(...).
+ * Replaces: SnapKV(Q, K, V, num_keep, window), nanokvllm/layers/CompressMethod.py:4-57
+ *           (the policy API of CHANGE_LOG.md:197-208).
+ */
+size_t nkv_snapkv_workspace_bytes(int32_t m, int32_t n_q_heads, int32_t n_kv_heads,
+                                  int32_t seq_len, int32_t window);
+int nkv_snapkv_select(const void* q, const void* k, int32_t m, int32_t n_q_heads,
+                      int32_t n_kv_heads, int32_t head_dim, int32_t seq_len, int32_t window,
+                      float scale, int32_t agg_mode, int32_t num_keep, float* importance_out,
+                      int32_t* keep_idx, void* workspace, size_t workspace_bytes,
+                      void* stream);
 
 /*
  * One layer's compression step: nkv_compress_select (num_keep = keep_tokens-2)

@@ -33,8 +33,6 @@ SIGNATURES = {
     "nkv_store_kvcache": (C.c_int, [_p, _i64, _p, _i64, _p, _p, _p, _i64, _i32, _i32, _i64, _p]),
     "nkv_fp8_quantize": (C.c_int, [_p, _i64, _f32, _p, _p]),
     "nkv_fp8_dequantize": (C.c_int, [_p, _i64, _f32, _p, _p]),
-    "nkv_fp8_gather_rows": (C.c_int, [_p, _p, _p, _i64, _i32, _p, _i32, _i32, _i32, _i32, _i32,
-                                      _i64, _f32, _f32, _p, _p, _p]),
     "nkv_store_kvcache_fp8": (C.c_int, [_p, _i64, _p, _i64, _p, _p, _p, _i64, _i32, _i32, _i64,
                                         _f32, _f32, _p]),
     "nkv_qk_norm_rope_store": (C.c_int, [_p, _i64, _p, _i64, _p, _i64, _p, _p, _p, _f32, _p,
@@ -54,6 +52,9 @@ SIGNATURES = {
                                            _sz, _p]),
     "nkv_prefill_varlen": (C.c_int, [_p, _i64, _p, _p, _i64, _i64, _p, _p, _p, _i64, _i32, _i32,
                                      _i32, _i32, _i32, _i32, _i32, _i64, _f32, _p, _i64, _p]),
+    "nkv_prefill_varlen_fp8": (C.c_int, [_p, _i64, _p, _p, _p, _p, _p, _i64, _i32, _i32, _i32,
+                                         _i32, _i32, _i32, _i32, _i64, _f32, _f32, _f32, _p,
+                                         _i64, _p]),
     "nkv_compress_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32]),
     "nkv_compress_score": (C.c_int, [_p, _i64, _p, _p, _i64, _i32, _p, _p, _i32, _i32, _i32, _i32,
                                      _i32, _i32, _i64, _f32, _i32, _p, _p, _sz, _p]),
@@ -62,6 +63,9 @@ SIGNATURES = {
     "nkv_compress_select": (C.c_int, [_p, _i64, _p, _p, _i64, _i32, _p, _p, _i32, _i32, _i32,
                                       _i32, _i32, _i32, _i64, _f32, _i32, _i32, _p, _p, _p, _sz,
                                       _p]),
+    "nkv_snapkv_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
+    "nkv_snapkv_select": (C.c_int, [_p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _i32,
+                                    _p, _p, _p, _sz, _p]),
     "nkv_compress_step": (C.c_int, [_p, _i64, _p, _p, _p, _i64, _i32, _p, _p, _p, _i32, _i32, _i32,
                                     _i32, _i32, _i32, _i64, _f32, _i32, _i32, _p, _p, _p, _sz,
                                     _p]),

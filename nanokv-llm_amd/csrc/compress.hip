@@ -35,8 +35,11 @@ constexpr int kMaxWindowBlocks = 64;
 constexpr int kMaxRows = 1024;  // rows per read-then-write round of a compaction unit
 
 // ------------------------------------------------------------------ score
-// scores[j][h][t] for t < Lw (window tokens); t == 0 and t == Lw-1 are -inf
-// (sink mask; the last window token is not scored).
+// scores[j][h][t] for t < Lw (window tokens); t == 0 and t >= n_cand are -inf
+// (sink mask; the query-window tokens are not scored: n_cand = Lw - query window).
+// G query rows per KV head, any number (16 per MFMA pass): a query window of w
+// tokens per head is G = heads x w rows, consecutive per head (q row stride = the
+// row of one sequence).
 // F8: K is fp8 (OCP E4M3FN) codes, widened to bf16 (exact) on load; the K scale is
 // folded into scale_log2 by the caller.
 template <bool F8>
@@ -44,8 +47,8 @@ __global__ __launch_bounds__(256) void compress_score_kernel(
     const bf16_t* __restrict__ q, int64_t q_row_stride, const void* __restrict__ k,
     const int32_t* __restrict__ block_tables, int64_t bt_row_stride, int32_t max_blocks,
     const int32_t* __restrict__ base_context_lens, const int32_t* __restrict__ seq_idx,
-    int32_t Hk, int32_t G, int32_t block_size, int32_t window_blocks, int64_t n_blocks, float scale_log2,
-    float* __restrict__ scores) {
+    int32_t Hk, int32_t G, int32_t block_size, int32_t window_blocks, int64_t n_blocks,
+    float scale_log2, int32_t n_cand, float* __restrict__ scores) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int Lw = window_blocks * block_size;
@@ -107,13 +110,14 @@ __global__ __launch_bounds__(256) void compress_score_kernel(
   }
   __builtin_amdgcn_sched_barrier(0);  // all loads issued before the first MFMA
   uint4 qreg[4];
-  {
-    const int hr = lane & 15;
-    const int hc = hr < G ? hr : 0;  // MFMA rows >= g are computed and discarded
+  auto load_q = [&](int h0) {  // query rows h0 .. h0+15 of the KV head as the MFMA A operand
+    const int hr = h0 + (lane & 15);
+    const int hc = hr < G ? hr : 0;  // MFMA rows >= G are computed and discarded
     const bf16_t* qp = q + qrow * q_row_stride + (int64_t)(kvh * G + hc) * kCD + (lane >> 4) * 8;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) qreg[ks] = *reinterpret_cast<const uint4*>(qp + ks * 32);
-  }
+  };
+  load_q(0);
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
     if constexpr (F8) {
@@ -131,30 +135,35 @@ __global__ __launch_bounds__(256) void compress_score_kernel(
         *reinterpret_cast<u32x4_t*>(&stage[(4 * r + (lane >> 4)) * kSR + (lane & 15) * 8]) =
             kraw[g][r];
     }
-    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const uint4 kb = *reinterpret_cast<const uint4*>(
-          &stage[(lane & 15) * kSR + (lane >> 4) * 8 + ks * 32]);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(qreg[ks]), as_bf16x8(kb), acc, 0,
-                                                     0, 0);
-    }
     const int tw = wave * 64 + g * 16 + (lane & 15);
     const int t = t0 + tw;
+    for (int h0 = 0; h0 < G; h0 += 16) {  // uniform; one pass for G <= 16
+      if (h0 > 0 || g > 0) {
+        if (G > 16) load_q(h0);
+      }
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int h = (lane >> 4) * 4 + r;
-      if (h < G)
-        srow[(int64_t)h * Lw + tw] = (t == 0 || t == Lw - 1) ? -INFINITY : acc[r] * scale_log2;
+      for (int ks = 0; ks < 4; ++ks) {
+        const uint4 kb = *reinterpret_cast<const uint4*>(
+            &stage[(lane & 15) * kSR + (lane >> 4) * 8 + ks * 32]);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(qreg[ks]), as_bf16x8(kb), acc,
+                                                       0, 0, 0);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int h = h0 + (lane >> 4) * 4 + r;
+        if (h < G)
+          srow[(int64_t)h * Lw + tw] = (t == 0 || t >= n_cand) ? -INFINITY : acc[r] * scale_log2;
+      }
     }
   }
 }
 
 // -------------------------------------------------------------- importance
-// importance[r][t] (t < Lw-1) for kept set r = j*n_sets + s, heads of the set
-// are [s*hps, (s+1)*hps) with hps = Hq / n_sets.
+// importance[r][t] (t < n_cand) for kept set r = j*n_sets + s, heads of the set
+// are [s*hps, (s+1)*hps) with hps = Hq / n_sets (query rows: heads x query window).
 __global__ __launch_bounds__(256) void compress_importance_kernel(
-    const float* __restrict__ scores, int32_t Hq, int32_t n_sets, int32_t Lw,
+    const float* __restrict__ scores, int32_t Hq, int32_t n_sets, int32_t Lw, int32_t n_cand,
     float* __restrict__ importance) {
   extern __shared__ float stats[];  // [hps][2]: max, 1/sum
   const int lane = threadIdx.x & 63;
@@ -178,7 +187,6 @@ __global__ __launch_bounds__(256) void compress_importance_kernel(
     }
   }
   __syncthreads();
-  const int n_cand = Lw - 1;
   float* irow = importance + (int64_t)r * n_cand;
   for (int t = threadIdx.x; t < n_cand; t += blockDim.x) {
     float acc = 0.f;
@@ -217,7 +225,7 @@ __device__ __forceinline__ int wave_excl_scan_i(int v) {
 // One wavefront per row; lane l holds candidates [l*ITEMS, (l+1)*ITEMS).
 template <int ITEMS>
 __global__ __launch_bounds__(64) void compress_topk_kernel(
-    const float* __restrict__ importance, int32_t n_cand, int32_t num_keep,
+    const float* __restrict__ importance, int32_t n_cand, int32_t num_keep, int32_t n_tail,
     int32_t* __restrict__ keep_idx) {
   const int lane = threadIdx.x;
   const int r = blockIdx.x;
@@ -258,14 +266,12 @@ __global__ __launch_bounds__(64) void compress_topk_kernel(
     selmask |= (uint64_t)sel << e;
   }
   int pos = wave_excl_scan_i(__builtin_popcountll(selmask));
-  int32_t* out = keep_idx + (int64_t)r * (num_keep + 2);
+  int32_t* out = keep_idx + (int64_t)r * (num_keep + 1 + n_tail);
 #pragma unroll
   for (int e = 0; e < ITEMS; ++e)
     if (selmask & (1ull << e)) out[1 + pos++] = lane * ITEMS + e;
-  if (lane == 0) {
-    out[0] = 0;
-    out[num_keep + 1] = n_cand;
-  }
+  if (lane == 0) out[0] = 0;
+  for (int i = lane; i < n_tail; i += 64) out[num_keep + 1 + i] = n_cand + i;  // query window
 }
 
 // ------------------------------------------------------------- fused step
@@ -1104,13 +1110,13 @@ extern "C" int nkv_compress_score(const void* q, int64_t q_row_stride, const voi
   hipLaunchKernelGGL((compress_score_kernel<false>), dim3(grid), dim3(256), 0, s,
                      (const bf16_t*)q, q_row_stride, k_cache, block_tables, bt_row_stride,
                      max_blocks_per_seq, base_context_lens, seq_idx, n_kv_heads, g, block_size,
-                     window_blocks, n_blocks, sl2, scores);
+                     window_blocks, n_blocks, sl2, Lw - 1, scores);
   int rc = check_launch("nkv_compress_score");
   if (rc) return rc;
   const int n_sets = agg_mode == NKV_AGG_ALL ? 1 : n_kv_heads;
   const int hps = n_q_heads / n_sets;
   hipLaunchKernelGGL(compress_importance_kernel, dim3((unsigned)(m * n_sets)), dim3(256),
-                     (size_t)hps * 2 * sizeof(float), s, scores, n_q_heads, n_sets, Lw,
+                     (size_t)hps * 2 * sizeof(float), s, scores, n_q_heads, n_sets, Lw, Lw - 1,
                      importance_out);
   return check_launch("nkv_compress_score(importance)");
 }
@@ -1127,10 +1133,10 @@ extern "C" int nkv_compress_topk(const float* importance, int32_t n_rows, int32_
   hipStream_t s = as_stream(stream);
   if (n_cand <= 64 * 16) {
     hipLaunchKernelGGL(compress_topk_kernel<16>, dim3((unsigned)n_rows), dim3(64), 0, s,
-                       importance, n_cand, num_keep, keep_idx);
+                       importance, n_cand, num_keep, 1, keep_idx);
   } else {
     hipLaunchKernelGGL(compress_topk_kernel<64>, dim3((unsigned)n_rows), dim3(64), 0, s,
-                       importance, n_cand, num_keep, keep_idx);
+                       importance, n_cand, num_keep, 1, keep_idx);
   }
   return check_launch("nkv_compress_topk");
 }
@@ -1445,13 +1451,13 @@ extern "C" int nkv_compress_step_fp8(const void* q, int64_t q_row_stride, void* 
   hipLaunchKernelGGL((compress_score_kernel<true>), dim3(sgrid), dim3(256), 0, s,
                      (const bf16_t*)q, q_row_stride, k_cache, block_tables, bt_row_stride,
                      max_blocks_per_seq, base_context_lens, seq_idx, n_kv_heads, g, block_size,
-                     window_blocks, n_blocks, sl2, scores);
+                     window_blocks, n_blocks, sl2, Lw - 1, scores);
   rc = check_launch("nkv_compress_step_fp8 (score)");
   if (rc) return rc;
   const int n_sets = agg_mode == NKV_AGG_ALL ? 1 : n_kv_heads;
   const int hps = n_q_heads / n_sets;
   hipLaunchKernelGGL(compress_importance_kernel, dim3((unsigned)(m * n_sets)), dim3(256),
-                     (size_t)hps * 2 * sizeof(float), s, scores, n_q_heads, n_sets, Lw,
+                     (size_t)hps * 2 * sizeof(float), s, scores, n_q_heads, n_sets, Lw, Lw - 1,
                      importance_out);
   rc = check_launch("nkv_compress_step_fp8 (importance)");
   if (rc) return rc;
@@ -1469,4 +1475,76 @@ extern "C" int nkv_compress_step_fp8(const void* q, int64_t q_row_stride, void* 
   else NKV_COMPACT8_LAUNCH(16);
 #undef NKV_COMPACT8_LAUNCH
   return check_launch("nkv_compress_step_fp8 (compact)");
+}
+
+// SnapKV as called directly (the plug-in API): Q [m, Hq, window, D], contiguous K
+// [m, Hk, L, D]. A query window of w tokens is scored as G*w query rows per KV head (rows
+// of one head consecutive, which is Q's layout); the w window keys are not scored and are
+// always kept. window 1 with L <= 1024, L % 64 == 0 takes the fused selection.
+extern "C" size_t nkv_snapkv_workspace_bytes(int32_t m, int32_t n_q_heads, int32_t n_kv_heads,
+                                             int32_t seq_len, int32_t window) {
+  if (m <= 0 || n_q_heads <= 0 || n_kv_heads <= 0 || seq_len <= 0 || window <= 0) return 0;
+  const size_t scores = (size_t)m * n_q_heads * window * seq_len * sizeof(float);
+  const size_t fused = nkv_compress_select_workspace_bytes(m, n_q_heads, n_kv_heads, 1, seq_len);
+  return scores > fused ? scores : fused;
+}
+
+extern "C" int nkv_snapkv_select(const void* q, const void* k, int32_t m, int32_t n_q_heads,
+                                 int32_t n_kv_heads, int32_t head_dim, int32_t seq_len,
+                                 int32_t window, float scale, int32_t agg_mode, int32_t num_keep,
+                                 float* importance_out, int32_t* keep_idx, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+  clear_error();
+  NKV_REQUIRE(m >= 0 && n_q_heads > 0 && n_kv_heads > 0 && seq_len > 0 && window > 0,
+              NKV_EINVAL, "snapkv_select: bad sizes");
+  if (m == 0) return NKV_OK;
+  NKV_REQUIRE(head_dim == kCD, NKV_EUNSUPPORTED, "snapkv_select: head_dim must be 128");
+  NKV_REQUIRE(n_q_heads % n_kv_heads == 0, NKV_EINVAL, "snapkv_select: Hq %% Hk != 0");
+  NKV_REQUIRE(agg_mode == NKV_AGG_ALL || agg_mode == NKV_AGG_GROUP, NKV_EINVAL,
+              "snapkv_select: bad agg_mode %d", agg_mode);
+  const int n_cand = seq_len - window;
+  NKV_REQUIRE(n_cand > 0 && num_keep > 0 && num_keep < n_cand, NKV_EINVAL,
+              "snapkv_select: need 0 < num_keep < seq_len - window (%d, %d, %d)", num_keep,
+              seq_len, window);
+  NKV_REQUIRE(q && k && importance_out && keep_idx, NKV_EINVAL, "snapkv_select: null pointer");
+  NKV_REQUIRE(aligned16(q) && aligned16(k), NKV_EINVAL,
+              "snapkv_select: q/k must be 16-byte aligned");
+  const size_t need = nkv_snapkv_workspace_bytes(m, n_q_heads, n_kv_heads, seq_len, window);
+  NKV_REQUIRE(workspace && workspace_bytes >= need, NKV_EWORKSPACE,
+              "snapkv_select: workspace needs %zu bytes (got %zu)", need, workspace_bytes);
+  if (window == 1)  // the periodic step's own shape: fused when it fits
+    return nkv_compress_select(q, (int64_t)n_q_heads * kCD, k, nullptr, 0, 0, nullptr, nullptr,
+                               m, n_q_heads, n_kv_heads, head_dim, seq_len, 1, 0, scale,
+                               agg_mode, num_keep, importance_out, keep_idx, workspace,
+                               workspace_bytes, stream);
+  NKV_REQUIRE(seq_len % kChunk == 0, NKV_EUNSUPPORTED,
+              "snapkv_select: seq_len must be a multiple of %d with a query window > 1 (got %d)",
+              kChunk, seq_len);
+  NKV_REQUIRE(n_cand <= 4096, NKV_EUNSUPPORTED, "snapkv_select: more than 4096 candidates");
+  const int g = n_q_heads / n_kv_heads;
+  const int rows = g * window;  // query rows per KV head
+  float* scores = (float*)workspace;
+  hipStream_t s = as_stream(stream);
+  const unsigned grid = (unsigned)(m * n_kv_heads * (seq_len / kChunk));
+  hipLaunchKernelGGL((compress_score_kernel<false>), dim3(grid), dim3(256), 0, s,
+                     (const bf16_t*)q, (int64_t)n_q_heads * window * kCD, k, nullptr, 0, 0,
+                     nullptr, nullptr, n_kv_heads, rows, seq_len, 1, 0, scale * kLog2e, n_cand,
+                     scores);
+  int rc = check_launch("nkv_snapkv_select (score)");
+  if (rc) return rc;
+  const int n_sets = agg_mode == NKV_AGG_ALL ? 1 : n_kv_heads;
+  const int hps = n_q_heads * window / n_sets;
+  hipLaunchKernelGGL(compress_importance_kernel, dim3((unsigned)(m * n_sets)), dim3(256),
+                     (size_t)hps * 2 * sizeof(float), s, scores, n_q_heads * window, n_sets,
+                     seq_len, n_cand, importance_out);
+  rc = check_launch("nkv_snapkv_select (importance)");
+  if (rc) return rc;
+  if (n_cand <= 64 * 16) {
+    hipLaunchKernelGGL(compress_topk_kernel<16>, dim3((unsigned)(m * n_sets)), dim3(64), 0, s,
+                       importance_out, n_cand, num_keep, window, keep_idx);
+  } else {
+    hipLaunchKernelGGL(compress_topk_kernel<64>, dim3((unsigned)(m * n_sets)), dim3(64), 0, s,
+                       importance_out, n_cand, num_keep, window, keep_idx);
+  }
+  return check_launch("nkv_snapkv_select (top-k)");
 }

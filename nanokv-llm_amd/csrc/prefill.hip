@@ -30,6 +30,11 @@
 //    element only where needed. Tiles are dispatched largest-first and the
 //    KV head is the fastest grid index, so with 8 KV heads each head's tiles
 //    share one XCD's L2.
+//  * F8 (paged fp8 pool): K/V tiles come as 1-byte E4M3FN codes through
+//    registers instead of straight into LDS: the next step's codes are loaded
+//    while this step computes, then widened to bf16 (exact) and written to the
+//    same swizzled LDS rows, so the MFMA part is the bf16 kernel's. The K scale
+//    is folded into the softmax scale, the V scale into the final 1/l.
 #include "nkv_common.h"
 
 #include <algorithm>
@@ -79,13 +84,15 @@ __device__ __forceinline__ void load_to_lds(i32x4_t desc, uint32_t lds_addr, uin
                : "memory");
 }
 
+template <bool F8>
 __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
-    const bf16_t* __restrict__ q, int64_t q_row_stride, const bf16_t* __restrict__ k_cache,
-    const bf16_t* __restrict__ v_cache, int64_t k_row_stride, int64_t v_row_stride,
+    const bf16_t* __restrict__ q, int64_t q_row_stride, const void* __restrict__ k_cache,
+    const void* __restrict__ v_cache, int64_t k_row_stride, int64_t v_row_stride,
     const int32_t* __restrict__ cu_seqlens_q, const int32_t* __restrict__ cu_seqlens_k,
     const int32_t* __restrict__ block_tables, int64_t bt_row_stride, int32_t Hk, int32_t G,
     int32_t block_size, int32_t max_blocks, int32_t n_limit, int32_t n_tiles, float scale_log2,
-    bf16_t* __restrict__ out, int64_t out_row_stride) {
+    float v_scale, bf16_t* __restrict__ out, int64_t out_row_stride) {
+  constexpr int kEl = F8 ? 1 : 2;  // bytes per cache element
   const int QT = kWGRows / G;  // queries per tile
   __shared__ __attribute__((aligned(1024))) char ring[kStages * kStageB];
 
@@ -117,8 +124,8 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
   // window covering only its valid keys: keys past Lk and keys of invalid
   // blocks read as 0. vol[] are the K offsets; V rows may have another stride
   // (contiguous mode), and their offsets differ by r * (row_bv - row_b).
-  const uint32_t row_b = (uint32_t)k_row_stride * 2u;
-  const uint32_t row_bv = (uint32_t)v_row_stride * 2u;
+  const uint32_t row_b = (uint32_t)k_row_stride * kEl;
+  const uint32_t row_bv = (uint32_t)v_row_stride * kEl;
   const int lrow = lane >> 4;  // 0..3
   const int slot = lane & 15;
   uint32_t vol[4];
@@ -129,6 +136,11 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
   }
   const uint32_t ring_base =
       (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)ring + (uint32_t)wave * 4096u;
+  // F8: load f of the wave's K (or V) codes brings rows 8f + lane/8, bytes 16*(lane%8) of the
+  // head's 128-byte piece, i.e. logical bf16 chunks 2c, 2c+1 (c = lane%8) of that LDS row
+  const int f8_row0 = lane >> 3;
+  const int f8_c = lane & 7;
+  u32x4_t kq[2], vq[2];  // F8: the next step's codes
 
   // Block ids: lane i holds entry bt_base + i of the sequence's table row, read
   // by the uniform v_readlane of the wave's block (reloaded every 64 blocks).
@@ -164,14 +176,34 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
       nv = 0;
       row0 = 0;
     }
-    const i32x4_t dk = buffer_desc(k_cache + row0 * k_row_stride, (uint32_t)nv * row_b);
-    const i32x4_t dv = buffer_desc(v_cache + row0 * v_row_stride, (uint32_t)nv * row_bv);
-    const uint32_t at = ring_base + (uint32_t)stage * kStageB;
+    const char* kp = static_cast<const char*>(k_cache) + row0 * k_row_stride * kEl;
+    const char* vp = static_cast<const char*>(v_cache) + row0 * v_row_stride * kEl;
+    if constexpr (F8) {  // into registers; widened into the stage by commit()
+      (void)stage;
+      const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)kp, (short)0, (uint32_t)nv * row_b, kBufferFlags);
+      const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)vp, (short)0, (uint32_t)nv * row_bv, kBufferFlags);
 #pragma unroll
-    for (int h = 0; h < 4; ++h) load_to_lds(dk, at + 1024u * h, vol[h]);
+      for (int f = 0; f < 2; ++f) {
+        const uint32_t r = (uint32_t)(8 * f + f8_row0);
+        const uint32_t col = (uint32_t)kvh * kPD + (uint32_t)f8_c * 16u;
+        kq[f] = __builtin_bit_cast(
+            u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rk, r * row_b + col, 0, 0));
+        vq[f] = __builtin_bit_cast(
+            u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rv, r * row_bv + col, 0, 0));
+      }
+    } else {
+      const i32x4_t dk = buffer_desc(kp, (uint32_t)nv * row_b);
+      const i32x4_t dv = buffer_desc(vp, (uint32_t)nv * row_bv);
+      const uint32_t at = ring_base + (uint32_t)stage * kStageB;
 #pragma unroll
-    for (int h = 0; h < 4; ++h)
-      load_to_lds(dv, at + kTileB + 1024u * h, vol[h] + (uint32_t)(4 * h + lrow) * (row_bv - row_b));
+      for (int h = 0; h < 4; ++h) load_to_lds(dk, at + 1024u * h, vol[h]);
+#pragma unroll
+      for (int h = 0; h < 4; ++h)
+        load_to_lds(dv, at + kTileB + 1024u * h,
+                    vol[h] + (uint32_t)(4 * h + lrow) * (row_bv - row_b));
+    }
     c_t0 += kStep;
     if (bt) {
       c_off += kStep;
@@ -185,6 +217,24 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
     if (bt && c_blk - bt_base >= 64) {
       bt_base = c_blk & ~63;
       load_window();
+    }
+  };
+  // F8: the codes of the last issue() (after their loads land) widened into LDS stage
+  // `stage`, rows 16w .. 16w+15 of the K and V tiles, in the bf16 path's swizzled layout
+  auto commit = [&](int stage) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    char* at = ring + stage * kStageB + wave * 4096;
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+      const int r = 8 * f + f8_row0;  // row within the wave's 16 (16w + r within the tile)
+      const int off = r * 256 + ((2 * f8_c) ^ (2 * (r & 7))) * 16;  // chunks 2c, 2c+1: adjacent
+      u32x4_t lo, hi;
+      fp8x16_to_bf16(kq[f], lo, hi);
+      *reinterpret_cast<u32x4_t*>(at + off) = lo;
+      *reinterpret_cast<u32x4_t*>(at + off + 16) = hi;
+      fp8x16_to_bf16(vq[f], lo, hi);
+      *reinterpret_cast<u32x4_t*>(at + kTileB + off) = lo;
+      *reinterpret_cast<u32x4_t*>(at + kTileB + off + 16) = hi;
     }
   };
 
@@ -248,7 +298,11 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
     for (int ks = 0; ks < 4; ++ks) asm volatile("" ::"v"(qreg[rr][ks]));
   // first step's tile landed (each wave waits for its own loads; the barrier
   // publishes all of them)
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(8 * (kStages - 2)) : "memory");
+  if constexpr (F8) {
+    commit(0);
+  } else {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(8 * (kStages - 2)) : "memory");
+  }
   __syncthreads();
 
   const char* lds = (const char*)(__attribute__((address_space(3))) char*)ring;
@@ -358,7 +412,11 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
       }
     }
     // next step's tile landed (own loads), then publish and free this stage
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(8 * (kStages - 2)) : "memory");
+    if constexpr (F8) {
+      if (s + 1 < n_steps) commit((ST + 1) % kStages);  // uniform
+    } else {
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(8 * (kStages - 2)) : "memory");
+    }
     __syncthreads();
     refill_window();
   };
@@ -376,7 +434,7 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
   for (int rr = 0; rr < 2; ++rr) {
     const float l = col_sum4(l_run[rr]);
     if (jrow[rr] >= Lq) continue;
-    const float inv = l > 0.f ? 1.f / l : 0.f;
+    const float inv = l > 0.f ? (F8 ? v_scale : 1.f) / l : 0.f;
     bf16_t* op = out + (int64_t)(q0 + jrow[rr]) * out_row_stride +
                  (int64_t)(kvh * G + head[rr]) * kPD + g4 * 4;
 #pragma unroll
@@ -390,45 +448,48 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
 
 }  // namespace nkv
 
-extern "C" int nkv_prefill_varlen(const void* q, int64_t q_row_stride, const void* k_cache,
-                                  const void* v_cache, int64_t k_row_stride,
-                                  int64_t v_row_stride,
-                                  const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
-                                  const int32_t* block_tables, int64_t bt_row_stride,
-                                  int32_t max_blocks_per_seq, int32_t n_seqs, int32_t max_seqlen_q, int32_t n_q_heads,
-                                  int32_t n_kv_heads, int32_t head_dim, int32_t block_size,
-                                  int64_t n_rows, float scale, void* out, int64_t out_row_stride,
-                                  void* stream) {
-  using namespace nkv;
-  clear_error();
+namespace nkv {
+template <bool F8>
+static int prefill_launch(const void* q, int64_t q_row_stride, const void* k_cache,
+                          const void* v_cache, int64_t k_row_stride, int64_t v_row_stride,
+                          const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                          const int32_t* block_tables, int64_t bt_row_stride,
+                          int32_t max_blocks_per_seq, int32_t n_seqs, int32_t max_seqlen_q,
+                          int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                          int32_t block_size, int64_t n_rows, float scale, float k_scale,
+                          float v_scale, void* out, int64_t out_row_stride, void* stream) {
+  constexpr int kEl = F8 ? 1 : 2;
+  const char* what = F8 ? "prefill_varlen_fp8" : "prefill_varlen";
   NKV_REQUIRE(n_seqs >= 0 && max_seqlen_q >= 0 && n_q_heads > 0 && n_kv_heads > 0, NKV_EINVAL,
-              "prefill_varlen: bad sizes");
+              "%s: bad sizes", what);
   if (n_seqs == 0 || max_seqlen_q == 0) return NKV_OK;
-  NKV_REQUIRE(head_dim == kPD, NKV_EUNSUPPORTED, "prefill_varlen: head_dim must be 128");
-  NKV_REQUIRE(n_q_heads % n_kv_heads == 0, NKV_EINVAL, "prefill_varlen: Hq %% Hk != 0");
+  NKV_REQUIRE(head_dim == kPD, NKV_EUNSUPPORTED, "%s: head_dim must be 128", what);
+  NKV_REQUIRE(n_q_heads % n_kv_heads == 0, NKV_EINVAL, "%s: Hq %% Hk != 0", what);
   const int g = n_q_heads / n_kv_heads;
-  NKV_REQUIRE(g <= 16, NKV_EUNSUPPORTED, "prefill_varlen: GQA group %d above 16", g);
+  NKV_REQUIRE(g <= 16, NKV_EUNSUPPORTED, "%s: GQA group %d above 16", what, g);
   NKV_REQUIRE(q && k_cache && v_cache && cu_seqlens_q && cu_seqlens_k && out, NKV_EINVAL,
-              "prefill_varlen: null pointer");
+              "%s: null pointer", what);
   NKV_REQUIRE(aligned16(q) && aligned16(k_cache) && aligned16(v_cache) && aligned16(out),
-              NKV_EINVAL, "prefill_varlen: q/k/v/out must be 16-byte aligned");
+              NKV_EINVAL, "%s: q/k/v/out must be 16-byte aligned", what);
   NKV_REQUIRE(q_row_stride >= (int64_t)n_q_heads * kPD && q_row_stride % 8 == 0 &&
                   out_row_stride >= (int64_t)n_q_heads * kPD && out_row_stride % 8 == 0 &&
-                  k_row_stride >= (int64_t)n_kv_heads * kPD && k_row_stride % 8 == 0 &&
-                  v_row_stride >= (int64_t)n_kv_heads * kPD && v_row_stride % 8 == 0,
-              NKV_EINVAL, "prefill_varlen: row strides must cover the heads, multiples of 8");
-  NKV_REQUIRE(n_rows > 0, NKV_EINVAL, "prefill_varlen: empty K/V");
-  NKV_REQUIRE(k_row_stride * 2 * kStep < (1ll << 31) && v_row_stride * 2 * kStep < (1ll << 31),
-              NKV_EUNSUPPORTED, "prefill_varlen: K/V row stride too large");
+                  k_row_stride >= (int64_t)n_kv_heads * kPD && k_row_stride % (16 / kEl) == 0 &&
+                  v_row_stride >= (int64_t)n_kv_heads * kPD && v_row_stride % (16 / kEl) == 0,
+              NKV_EINVAL, "%s: row strides must cover the heads, in 16-byte multiples", what);
+  NKV_REQUIRE(n_rows > 0, NKV_EINVAL, "%s: empty K/V", what);
+  NKV_REQUIRE(k_row_stride * kEl * kStep < (1ll << 31) && v_row_stride * kEl * kStep < (1ll << 31),
+              NKV_EUNSUPPORTED, "%s: K/V row stride too large", what);
   NKV_REQUIRE(!block_tables || k_row_stride == v_row_stride, NKV_EINVAL,
-              "prefill_varlen: paged K and V caches share one row stride");
+              "%s: paged K and V caches share one row stride", what);
+  NKV_REQUIRE(!F8 || block_tables, NKV_EINVAL, "%s: fp8 K/V are read from a paged pool", what);
+  NKV_REQUIRE(k_scale > 0.f && v_scale > 0.f, NKV_EINVAL, "%s: scales must be > 0", what);
   int max_blocks = 0;
   if (block_tables) {
     NKV_REQUIRE(block_size > 0 && block_size % 16 == 0, NKV_EUNSUPPORTED,
-                "prefill_varlen: block_size must be a positive multiple of 16");
+                "%s: block_size must be a positive multiple of 16", what);
     NKV_REQUIRE(max_blocks_per_seq > 0 && bt_row_stride >= max_blocks_per_seq,
-                NKV_EINVAL, "prefill_varlen: paged mode needs block_size, max_blocks_per_seq "
-                "and bt_row_stride >= max_blocks_per_seq");
+                NKV_EINVAL, "%s: paged mode needs block_size, max_blocks_per_seq "
+                "and bt_row_stride >= max_blocks_per_seq", what);
     max_blocks = max_blocks_per_seq;
   }
   // paged: valid block ids are [0, n_rows / block_size); contiguous: valid rows
@@ -437,13 +498,48 @@ extern "C" int nkv_prefill_varlen(const void* q, int64_t q_row_stride, const voi
   const int qt = kWGRows / g;
   const int n_tiles = (max_seqlen_q + qt - 1) / qt;
   const int64_t grid = (int64_t)n_seqs * n_tiles * n_kv_heads;
-  NKV_REQUIRE(grid < (1ll << 31), NKV_EUNSUPPORTED, "prefill_varlen: grid too large");
-  const float sl2 = scale * kLog2e;
-  hipStream_t s = as_stream(stream);
-  hipLaunchKernelGGL(prefill_varlen_kernel, dim3((unsigned)grid), dim3(256), 0, s,
-                     (const bf16_t*)q, q_row_stride, (const bf16_t*)k_cache,
-                     (const bf16_t*)v_cache, k_row_stride, v_row_stride, cu_seqlens_q,
-                     cu_seqlens_k, block_tables, bt_row_stride, n_kv_heads, g, block_size,
-                     max_blocks, n_limit, n_tiles, sl2, (bf16_t*)out, out_row_stride);
-  return check_launch("nkv_prefill_varlen");
+  NKV_REQUIRE(grid < (1ll << 31), NKV_EUNSUPPORTED, "%s: grid too large", what);
+  const float sl2 = scale * k_scale * kLog2e;
+  hipLaunchKernelGGL(prefill_varlen_kernel<F8>, dim3((unsigned)grid), dim3(256), 0,
+                     as_stream(stream), (const bf16_t*)q, q_row_stride, k_cache, v_cache,
+                     k_row_stride, v_row_stride, cu_seqlens_q, cu_seqlens_k, block_tables,
+                     bt_row_stride, n_kv_heads, g, block_size, max_blocks, n_limit, n_tiles, sl2,
+                     v_scale, (bf16_t*)out, out_row_stride);
+  return check_launch(F8 ? "nkv_prefill_varlen_fp8" : "nkv_prefill_varlen");
+}
+}  // namespace nkv
+
+extern "C" int nkv_prefill_varlen(const void* q, int64_t q_row_stride, const void* k_cache,
+                                  const void* v_cache, int64_t k_row_stride,
+                                  int64_t v_row_stride, const int32_t* cu_seqlens_q,
+                                  const int32_t* cu_seqlens_k, const int32_t* block_tables,
+                                  int64_t bt_row_stride, int32_t max_blocks_per_seq,
+                                  int32_t n_seqs, int32_t max_seqlen_q, int32_t n_q_heads,
+                                  int32_t n_kv_heads, int32_t head_dim, int32_t block_size,
+                                  int64_t n_rows, float scale, void* out, int64_t out_row_stride,
+                                  void* stream) {
+  nkv::clear_error();
+  return nkv::prefill_launch<false>(q, q_row_stride, k_cache, v_cache, k_row_stride,
+                                    v_row_stride, cu_seqlens_q, cu_seqlens_k, block_tables,
+                                    bt_row_stride, max_blocks_per_seq, n_seqs, max_seqlen_q,
+                                    n_q_heads, n_kv_heads, head_dim, block_size, n_rows, scale,
+                                    1.f, 1.f, out, out_row_stride, stream);
+}
+
+extern "C" int nkv_prefill_varlen_fp8(const void* q, int64_t q_row_stride, const void* k_cache,
+                                      const void* v_cache, const int32_t* cu_seqlens_q,
+                                      const int32_t* cu_seqlens_k, const int32_t* block_tables,
+                                      int64_t bt_row_stride, int32_t max_blocks_per_seq,
+                                      int32_t n_seqs, int32_t max_seqlen_q, int32_t n_q_heads,
+                                      int32_t n_kv_heads, int32_t head_dim, int32_t block_size,
+                                      int64_t n_blocks, float scale, float k_scale,
+                                      float v_scale, void* out, int64_t out_row_stride,
+                                      void* stream) {
+  nkv::clear_error();
+  const int64_t row = (int64_t)n_kv_heads * head_dim;  // codes (bytes) per cache row
+  return nkv::prefill_launch<true>(q, q_row_stride, k_cache, v_cache, row, row, cu_seqlens_q,
+                                   cu_seqlens_k, block_tables, bt_row_stride, max_blocks_per_seq,
+                                   n_seqs, max_seqlen_q, n_q_heads, n_kv_heads, head_dim,
+                                   block_size, n_blocks * block_size, scale, k_scale, v_scale,
+                                   out, out_row_stride, stream);
 }

@@ -195,22 +195,22 @@ def varlen_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                   and out.stride(1) == D, "varlen_prefill: out must be bf16 shaped like q, "
                   "rows of contiguous heads")
     if block_tables is not None and k.dtype == torch.float8_e4m3fn:
-        # fp8 pool: each sequence's rows widened into contiguous bf16, then the contiguous path
-        if max_seqlen_k is None:
-            raise ValueError("prefill over an fp8 pool needs max_seqlen_k")
+        # fp8 pool: the kernel widens the codes as it stages them (no bf16 copy)
         NB, B, Hk, Dk = k.shape
-        rows = max(n_seqs * int(max_seqlen_k), 1)
-        kw = torch.empty(rows, Hk, Dk, dtype=_BF16, device=q.device)
-        vw = torch.empty_like(kw)
-        assert block_tables.dtype == torch.int32 and block_tables.stride(1) == 1
-        rc = _lib.lib().nkv_fp8_gather_rows(
-            k.data_ptr(), v.data_ptr(), block_tables.data_ptr(), block_tables.stride(0),
-            block_tables.size(1), cu_seqlens_k.data_ptr(), n_seqs, int(max_seqlen_k), Hk, Dk,
-            B, NB, float(k_scale), float(v_scale), kw.data_ptr(), vw.data_ptr(),
-            _lib.stream_of(q))
-        _lib.check(rc, "fp8_gather_rows")
-        return varlen_prefill(q, kw, vw, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, scale,
-                              out=out)
+        _lib.need(v.shape == k.shape and k.is_contiguous() and v.is_contiguous(),
+                  "varlen_prefill: fp8 caches must be contiguous, v shaped like k")
+        _lib.need(block_tables.dtype == torch.int32 and block_tables.stride(1) == 1,
+                  "varlen_prefill: block_tables must be int32 rows")
+        assert Dk == D
+        if out is None:
+            out = torch.empty(N, Hq, D, dtype=_BF16, device=q.device)
+        rc = _lib.lib().nkv_prefill_varlen_fp8(
+            q.data_ptr(), q.stride(0), k.data_ptr(), v.data_ptr(), cu_seqlens_q.data_ptr(),
+            cu_seqlens_k.data_ptr(), block_tables.data_ptr(), block_tables.stride(0),
+            block_tables.size(1), n_seqs, int(max_seqlen_q), Hq, Hk, D, B, NB, float(scale),
+            float(k_scale), float(v_scale), out.data_ptr(), out.stride(0), _lib.stream_of(q))
+        _lib.check(rc, "varlen_prefill_fp8")
+        return out
     if block_tables is not None:
         NB, B, Hk, Dk = k.shape
         assert k.is_contiguous() and v.is_contiguous() and v.shape == k.shape

@@ -128,8 +128,8 @@ def test_attention_with_fp8_pool(nkv, dev):
 
 
 def test_prefill_over_fp8_pool(nkv, dev):
-    """Chunked prefill reading a paged fp8 cache (gathered and widened on the GPU) vs the
-    oracle on the fp32-dequantized cache."""
+    """Chunked prefill reading a paged fp8 cache (the kernel widens the codes as it stages
+    them) vs the oracle on the fp32-dequantized cache."""
     from oracle.attention_ref import varlen_prefill_ref
     wl = wl_mod.prefill_workload(3, 32, 8, 0, 0, seed=12, prefix_lo=0, prefix_hi=900, chunk=200)
     kq = fp8_ref.fp8_quantize_ref(wl["k_cache"], 0.5)
@@ -144,6 +144,50 @@ def test_prefill_over_fp8_pool(nkv, dev):
     vf = vq.view(torch.float8_e4m3fn).float() * 2.0
     ref = varlen_prefill_ref(wl["q"].float(), kf, vf, wl["cu_seqlens_q"], wl["cu_seqlens_k"],
                              wl["scale"], block_tables=wl["block_tables"])
+    assert (out.float().cpu() - ref).abs().max().item() <= 2e-2
+
+
+@pytest.mark.parametrize("G", [4, 5])
+def test_prefill_over_fp8_pool_mixed_batch(nkv, dev, G):
+    """A mixed chunked-prefill step over an fp8 pool: decode rows (one query over a long
+    context) beside prompt chunks, block size 16 and 256-token blocks' worth of context,
+    within 2e-2 of the oracle; the call allocates nothing beyond its output (the codes are
+    widened inside the kernel, not into per-sequence bf16 copies)."""
+    import random
+    from oracle.attention_ref import varlen_prefill_ref
+    rng = random.Random(77 + G)
+    g = torch.Generator().manual_seed(77 + G)
+    Hk, D, B = 8, 128, 16
+    Lq = [1, 1, 300, 1, 64, 1]
+    Lk = [9000, 4000, 300 + 2000, 17, 64, 1]
+    width = max((k + B - 1) // B for k in Lk)
+    n_blocks = sum((k + B - 1) // B for k in Lk) + 5
+    free = list(range(n_blocks))
+    rng.shuffle(free)
+    bt = torch.full((len(Lk), width), -1, dtype=torch.int32)
+    for i, k in enumerate(Lk):
+        nb = (k + B - 1) // B
+        bt[i, :nb] = torch.tensor([free.pop() for _ in range(nb)], dtype=torch.int32)
+    kc = torch.randn(n_blocks, B, Hk, D, generator=g).to(torch.bfloat16)
+    vc = torch.randn(n_blocks, B, Hk, D, generator=g).to(torch.bfloat16)
+    kq, vq = fp8_ref.fp8_quantize_ref(kc, 0.5), fp8_ref.fp8_quantize_ref(vc, 0.25)
+    cq = torch.tensor([0] + torch.tensor(Lq).cumsum(0).tolist(), dtype=torch.int32)
+    ck = torch.tensor([0] + torch.tensor(Lk).cumsum(0).tolist(), dtype=torch.int32)
+    q = torch.randn(int(cq[-1]), Hk * G, D, generator=g).to(torch.bfloat16)
+    args = [x.to(dev) for x in (q, kq, vq, cq, ck, bt)]
+    out = torch.empty(int(cq[-1]), Hk * G, D, dtype=torch.bfloat16, device=dev)
+    torch.cuda.synchronize()
+    before = torch.cuda.memory_allocated(dev)
+    torch.cuda.reset_peak_memory_stats(dev)
+    nkv.varlen_prefill(args[0], args[1].view(torch.float8_e4m3fn),
+                       args[2].view(torch.float8_e4m3fn), args[3], args[4], max(Lq), D ** -0.5,
+                       block_tables=args[5], out=out, max_seqlen_k=max(Lk), k_scale=0.5,
+                       v_scale=0.25)
+    torch.cuda.synchronize()
+    assert torch.cuda.max_memory_allocated(dev) - before < 1 << 20
+    kf = kq.view(torch.float8_e4m3fn).float() * 0.5
+    vf = vq.view(torch.float8_e4m3fn).float() * 0.25
+    ref = varlen_prefill_ref(q.float(), kf, vf, cq, ck, D ** -0.5, block_tables=bt)
     assert (out.float().cpu() - ref).abs().max().item() <= 2e-2
 
 

@@ -313,3 +313,47 @@ def test_gather_kv_by_slots_explicit_loops():
     # the planted mistake: heads and positions swapped (no permute) reads other rows
     wrong = kc.view(NB * B, Hk, D)[slots]  # [2, 7, Hk, D]
     assert not torch.equal(wrong.reshape(2, Hk, 7, D), k_sub)
+
+
+def _brute_importance_window(Q, K, scale, agg, w):
+    """float64 loops with a query window of w tokens: each window query's softmax over
+    keys 1 .. L-w-1 (key 0 masked, the window keys unscored), summed over queries and heads."""
+    m, Hk, L, D = K.shape
+    Hq = Q.size(1)
+    g = Hq // Hk
+    n = L - w
+    imp = torch.zeros(m, 1 if agg == "all" else Hk, n, dtype=torch.float64)
+    for b in range(m):
+        for h in range(Hq):
+            for i in range(w):
+                s = [float((Q[b, h, i].double() * K[b, h // g, t].double()).sum()) * scale
+                     for t in range(n)]
+                mx = max(s[1:])
+                e = [0.0] + [math.exp(x - mx) for x in s[1:]]
+                z = sum(e)
+                for t in range(n):
+                    imp[b, 0 if agg == "all" else h // g, t] += e[t] / z
+    return imp
+
+
+@pytest.mark.parametrize("agg", ["all", "group"])
+@pytest.mark.parametrize("w", [2, 3])
+def test_importance_query_window_matches_brute_force(agg, w):
+    """SnapKV's window (CompressMethod.py:14-42): the softmax of every window query is
+    summed over the window, then over heads; the window keys are not candidates."""
+    g = torch.Generator().manual_seed(40 + w)
+    m, Hq, Hk, L, D = 2, 4, 2, 14, 8
+    Q = torch.randn(m, Hq, w, D, generator=g)
+    K = torch.randn(m, Hk, L, D, generator=g)
+    Q[:, 1] *= 3  # a sharper head
+    imp = snapkv_importance_ref(Q, K, w, "fp32", agg)
+    exp = _brute_importance_window(Q, K, D ** -0.5, agg, w)
+    assert imp.shape == exp.shape
+    assert torch.allclose(imp.double(), exp, atol=1e-6)
+    final = snapkv_ref(Q, K, None, num_keep=4, window=w, score_dtype="fp32", agg=agg)
+    final = final.view(m, -1, 4 + 1 + w)
+    for b in range(m):
+        for s_ in range(final.size(1)):
+            row = final[b, s_].tolist()
+            assert row[0] == 0 and row[-w:] == list(range(L - w, L))
+            assert row[1:5] == _brute_topk(exp[b, s_].tolist(), 4)
