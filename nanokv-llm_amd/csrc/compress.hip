@@ -288,9 +288,10 @@ __global__ __launch_bounds__(64) void compress_topk_kernel(
 //    selects and compacts. The kernel boundary makes the partials visible
 //    across XCDs; a device-scope fence inside a kernel would write back the
 //    whole L2.
-// Selection: 8-pass 4-bit radix select of the num_keep-th largest order key
-// (one candidate per thread), ties to the lower index, ascending output by a
-// workgroup prefix count -- no sort. Compaction: every source row of the
+// Selection: the num_keep-th largest order key is bracketed by 256-bucket histograms of
+// the candidates' keys (one candidate per thread, LDS atomics), 8 key bits per level,
+// until its bucket holds at most 64 keys, which are ranked exactly; ties to the lower
+// index; ascending output by a workgroup prefix count -- no sort. Compaction: every source row of the
 // (sequence, KV head) unit, K and V, is loaded into registers before any
 // destination is written (the reference's two-phase index_select().clone() /
 // index_copy_), one 256-byte row per 16 lanes.
@@ -310,10 +311,15 @@ struct SelectLds {
   __attribute__((aligned(16))) bf16_t kstage[kSelWaves][16 * kStageRow];
   float red[kSelWaves][16];
   __attribute__((aligned(16))) float imp[kSelMaxWindow];
-  __attribute__((aligned(16))) int cnt[2][16][kSelWaves];  // [pass parity][digit][wave]
   int wcnt[kSelWaves];
+  uint32_t wmax[kSelWaves];
+  uint32_t wmin[kSelWaves];
+  int sel_bucket, sel_above, sel_nb;  // selection: boundary bucket, keys above it, its size
   int32_t keep[kSelMaxWindow];
   int32_t win_pb[kMaxWindowBlocks + 1];
+  int32_t sel_hist[256];             // selection: bucket counts
+  uint32_t sel_key[kSelMaxWindow];   // selection: keys and indices of the last bucket
+  int32_t sel_idx[kSelMaxWindow];
   int32_t src[kStepTable];
   int32_t dst[kStepTable];
 };
@@ -349,54 +355,131 @@ __device__ __forceinline__ int block_excl_count(bool flag, int* wcnt, int& total
   return base + before;
 }
 
-// Selects the num_keep largest of L.imp[0, n_cand) and writes
-// [0, ascending kept indices, n_cand] to L.keep and (if out) to out.
+// Workgroup barrier ordering LDS only: waits for this wave's LDS operations, not for its
+// global loads (a __syncthreads() waits for every outstanding load), so loads issued
+// before it stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Selects the num_keep largest of L.imp[0, n_cand) (ties: the lower index) and writes
+// [0, ascending kept indices, n_cand] to L.keep and (if out) to out. One candidate per
+// thread. The candidates' order-preserving keys are counted into 256 buckets spanning
+// [min key, max key] (LDS atomics); one wave finds the bucket holding the num_keep-th
+// largest; keys in higher buckets are kept, lower ones dropped, and the bucket is split
+// again into 256 (8 more key bits) until it holds at most 64 keys; those are ranked
+// exactly by (key, index) against each other (all of them when the keys are equal). Two
+// levels for these scores (the masked sink key, importance 0, widens the first level's
+// span).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o, 64));
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = min(v, (uint32_t)__shfl_xor((int)v, o, 64));
+  return v;
+}
+
 __device__ __forceinline__ void block_select(SelectLds& L, int n_cand, int num_keep,
                                              int32_t* __restrict__ out) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const bool real = tid < n_cand;
-  const uint32_t key = real ? order_key(L.imp[tid]) : 0u;  // padding sorts last
-  uint32_t T = 0;
-#pragma unroll 1
-  for (int pass = 0; pass < 8; ++pass) {
-    const int shift = 28 - 4 * pass;
-    // c = number of digits d in 1..15 with key >= T + (d << shift)
-    const uint32_t above = key >= T ? (key - T) >> shift : 0u;
-    int c = (int)(above < 15u ? above : 15u);
-    asm volatile("" : "+v"(c));  // one VGPR: each ballot below is a single v_cmp
-    int mine = 0;  // lane d: this wave's count of candidates with c >= d
-#pragma unroll
-    for (int d = 1; d < 16; ++d) {
-      const int n = __builtin_popcountll(__builtin_amdgcn_ballot_w64(c >= d));
-      asm volatile("v_writelane_b32 %0, %1, %2" : "+v"(mine) : "s"(n), "i"(d));
-    }
-    int(*cnt)[kSelWaves] = L.cnt[pass & 1];
-    if (lane < 16) cnt[lane][wave] = mine;
-    __syncthreads();
-    int tot = 0;
-    const u32x4_t* row = reinterpret_cast<const u32x4_t*>(cnt[lane & 15]);
-#pragma unroll
-    for (int w4 = 0; w4 < kSelWaves / 4; ++w4) {
-      const u32x4_t v = row[w4];
-      tot += (int)(v.x + v.y + v.z + v.w);
-    }
-    const uint64_t ok = __builtin_amdgcn_ballot_w64(lane >= 1 && lane < 16 && tot >= num_keep);
-    const int digit = ok ? 63 - __builtin_clzll(ok) : 0;
-    T += (uint32_t)digit << shift;
-    // Exactly num_keep keys are >= T: the kept set is {key >= T}, the set the remaining
-    // passes would give (they only raise T to the smallest of those keys), so stop.
-    // Every wave reads the same counts, so all leave at the same pass.
-    if (digit > 0 && __shfl(tot, digit, 64) == num_keep) break;
+  const uint32_t key = real ? order_key(L.imp[tid]) : 0u;
+  int* hist = L.sel_hist;
+  uint32_t* bkey = L.sel_key;  // members of the last bucket
+  int* bidx = L.sel_idx;
+  // ---- key range of the candidates
+  uint32_t kmax = wave_max_u32(real ? key : 0u);
+  uint32_t kmin = wave_min_u32(real ? key : 0xffffffffu);
+  if (lane == 0) {
+    L.wmax[wave] = kmax;
+    L.wmin[wave] = kmin;
   }
-  const bool gt = real && key > T;
-  const bool eq = real && key == T;
-  int n_gt = 0, n_eq = 0, n_sel = 0;
-  (void)block_excl_count(gt, L.wcnt, n_gt);
-  const int eq_rank = block_excl_count(eq, L.wcnt, n_eq);
-  const bool sel = gt || (eq && eq_rank < num_keep - n_gt);  // ties: lower index first
-  const int pos = block_excl_count(sel, L.wcnt, n_sel);
+  if (tid < 256) hist[tid] = 0;
+  if (tid == 0) L.sel_nb = 0;
+  lds_barrier();
+#pragma unroll
+  for (int w = 0; w < kSelWaves; ++w) {
+    kmax = max(kmax, L.wmax[w]);
+    kmin = min(kmin, L.wmin[w]);
+  }
+  // ---- levels: bucket = (key - lo) >> sh in 0..255 among the keys still undecided
+  uint32_t lo = kmin;
+  const uint32_t span = kmax - kmin;
+  int sh = span == 0 ? 0 : max(0, 32 - __builtin_clz(span) - 8);
+  int need = num_keep;  // keys still to take from the undecided ones
+  bool active = real, sel = false;
+  for (;;) {  // uniform: every thread reads the same bucket and counts
+    const int b = active ? (int)((key - lo) >> sh) : -1;
+    if (active) atomicAdd(&hist[b], 1);
+    lds_barrier();
+    if (wave == 0) {  // lane l: buckets 255-4l .. 252-4l, scanned from the top
+      int h[4], sum = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        h[i] = hist[255 - 4 * lane - i];
+        hist[255 - 4 * lane - i] = 0;  // ready for the next level (ordered by the barrier)
+        sum += h[i];
+      }
+      int incl = sum;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += y;
+      }
+      int before = incl - sum;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (before < need && before + h[i] >= need) {  // exactly one (bucket, lane)
+          L.sel_bucket = 255 - 4 * lane - i;
+          L.sel_above = before;
+          L.sel_nb = h[i];
+        }
+        before += h[i];
+      }
+    }
+    lds_barrier();
+    const int bb = L.sel_bucket;
+    if (active) {
+      sel = b > bb;
+      active = b == bb;
+    }
+    need -= L.sel_above;
+    if (L.sel_nb <= 64 || sh == 0) break;
+    lo += (uint32_t)bb << sh;
+    sh = max(sh - 8, 0);
+  }
+  // ---- the last bucket's members, ranked by (larger key, then lower index)
+  if (tid == 0) L.sel_nb = 0;
+  lds_barrier();
+  if (active) {
+    const int slot = atomicAdd(&L.sel_nb, 1);
+    bkey[slot] = key;
+    bidx[slot] = tid;
+  }
+  lds_barrier();
+  if (active) {
+    const int nb = L.sel_nb;
+    int rk = 0;
+    for (int i = 0; i < nb; ++i) {
+      const uint32_t k2 = bkey[i];
+      rk += k2 > key || (k2 == key && bidx[i] < tid);
+    }
+    sel = rk < need;
+  }
+  // ---- kept positions: exclusive count of the kept keys before each (index order)
+  const uint64_t bs = __builtin_amdgcn_ballot_w64(sel);
+  if (lane == 0) L.wcnt[wave] = __builtin_popcountll(bs);
+  lds_barrier();
+  int pos = __builtin_popcountll(bs & ((1ull << lane) - 1ull));
+#pragma unroll
+  for (int w = 0; w < kSelWaves; ++w) pos += w < wave ? L.wcnt[w] : 0;
   if (sel) {
     L.keep[1 + pos] = tid;
     if (out) out[1 + pos] = tid;
@@ -409,7 +492,7 @@ __device__ __forceinline__ void block_select(SelectLds& L, int n_cand, int num_k
       out[num_keep + 1] = n_cand;
     }
   }
-  __syncthreads();
+  lds_barrier();
 }
 
 // Window of (sequence j, KV head kvh): the importance of each key summed over
