@@ -698,25 +698,20 @@ __device__ __forceinline__ bool unit_blocks(int32_t* win_pb, const int32_t* __re
 }
 
 // In-place compaction of KV head kvh of sequence seq_idx[j], K and V, with the
-// kept window positions in L.keep; kvh 0 also sets the new context length. F8:
+// kept window positions in L.keep and the unit's block ids in L.win_pb (unit_blocks,
+// visible); kvh 0 also sets the new context length. F8:
 // 1-byte rows (a 128-byte head row per 8 lanes, 128 rows per round). Rows go in
 // rounds of kStepMaxRows (one for the reference's shapes), all source rows of a
 // round in registers before any destination is written.
 template <bool F8>
 __device__ __forceinline__ void compact_unit(
     SelectLds& L, void* __restrict__ k_cache, void* __restrict__ v_cache,
-    const int32_t* __restrict__ block_tables, int64_t bt_row_stride, int32_t max_blocks,
     const int32_t* __restrict__ base_context_lens, int32_t* __restrict__ context_lens,
     const int32_t* __restrict__ seq_idx, int j, int kvh, int keep_tokens, int Hk, int B,
-    int window_blocks, int64_t n_blocks) {
+    int window_blocks) {
   const int tid = threadIdx.x;
   const int seq = seq_idx[j];
-  const int len = seq >= 0 ? base_context_lens[seq] : 0;  // seq -1: padding entry
-  // not compressible, or inconsistent with the table width: leave untouched
-  if (!unit_blocks(L.win_pb, block_tables + (int64_t)seq * bt_row_stride, len, B,
-                   window_blocks, max_blocks, n_blocks))
-    return;
-  __syncthreads();
+  const int len = base_context_lens[seq];
   const int Lw = window_blocks * B;
   const int nrows = keep_tokens + len % B;
   constexpr int kEl = F8 ? 1 : 2;
@@ -780,6 +775,16 @@ __global__ __launch_bounds__(kSelThreads) void compress_group_kernel(
   if (block_tables && seq_idx[j] < 0) return;  // padding entry (uniform): nothing written
   const int Lw = window_blocks * block_size;
   const int n_cand = Lw - 1;
+  // compaction: the unit's block ids (published by the scoring's barriers), read while the
+  // scoring's loads are in flight; not compressible or inconsistent with the table width:
+  // left untouched
+  bool compact = false;
+  if (k_cache_w) {
+    const int seq = seq_idx[j];
+    compact = unit_blocks(L.win_pb, block_tables + (int64_t)seq * bt_row_stride,
+                          base_context_lens[seq], block_size, window_blocks, max_blocks,
+                          n_blocks);
+  }
   float gi[4];
   group_importance<F8>(L, q, q_row_stride, k, block_tables, bt_row_stride, max_blocks,
                        base_context_lens, seq_idx, j, kvh, Hk, G, block_size, window_blocks,
@@ -794,10 +799,9 @@ __global__ __launch_bounds__(kSelThreads) void compress_group_kernel(
   float* irow = importance_out + ((int64_t)j * Hk + kvh) * n_cand;
   for (int t = tid; t < n_cand; t += kSelThreads) irow[t] = L.imp[t];
   block_select(L, n_cand, num_keep, keep_idx + ((int64_t)j * Hk + kvh) * (num_keep + 2));
-  if (k_cache_w)
-    compact_unit<F8>(L, k_cache_w, v_cache_w, block_tables, bt_row_stride, max_blocks,
-                 base_context_lens, context_lens, seq_idx, j, kvh, num_keep + 2, Hk, block_size,
-                 window_blocks, n_blocks);
+  if (compact)
+    compact_unit<F8>(L, k_cache_w, v_cache_w, base_context_lens, context_lens, seq_idx, j, kvh,
+                     num_keep + 2, Hk, block_size, window_blocks);
 }
 
 // agg "all", first kernel: each group's importance -> partial[j][kvh][Lw]. Grid m * Hk.
@@ -845,6 +849,13 @@ __global__ __launch_bounds__(kSelThreads) void compress_sum_kernel(
   if (block_tables && seq_idx[j] < 0) return;  // padding entry (uniform): nothing written
   const int Lw = window_blocks * block_size;
   const int n_cand = Lw - 1;
+  bool compact = false;  // as in compress_group_kernel
+  if (k_cache_w) {
+    const int seq = seq_idx[j];
+    compact = unit_blocks(L.win_pb, block_tables + (int64_t)seq * bt_row_stride,
+                          base_context_lens[seq], block_size, window_blocks, max_blocks,
+                          n_blocks);
+  }
   const float* pj = partial + (int64_t)j * Hk * Lw;
   const bool writer = kvh == 0;
   float* irow = importance_out + (int64_t)j * n_cand;
@@ -862,10 +873,9 @@ __global__ __launch_bounds__(kSelThreads) void compress_sum_kernel(
   }
   __syncthreads();
   block_select(L, n_cand, num_keep, writer ? keep_idx + (int64_t)j * (num_keep + 2) : nullptr);
-  if (k_cache_w)
-    compact_unit<F8>(L, k_cache_w, v_cache_w, block_tables, bt_row_stride, max_blocks,
-                 base_context_lens, context_lens, seq_idx, j, kvh, num_keep + 2, Hk, block_size,
-                 window_blocks, n_blocks);
+  if (compact)
+    compact_unit<F8>(L, k_cache_w, v_cache_w, base_context_lens, context_lens, seq_idx, j, kvh,
+                     num_keep + 2, Hk, block_size, window_blocks);
 }
 
 // ----------------------------------------------------------------- compact
