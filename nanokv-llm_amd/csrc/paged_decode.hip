@@ -114,6 +114,21 @@ __device__ __forceinline__ void seq_load(SeqCursor& c, const int32_t* __restrict
   c.tot = __builtin_amdgcn_readlane(c.incl, 63);
 }
 
+// Element offset of head dim `dim` (a multiple of 4) in a staged LDS row. bf16 rows are
+// dense. fp8 rows are staged as 8-dim pieces with the even pieces first (piece 2c at slot
+// c, piece 2c+1 at slot 8 + c): a lane widens 16 codes into pieces 2c and 2c+1, and each
+// of its two 16-byte writes then lands beside its neighbours' (the 32-byte stride of a
+// dense row would leave half the banks idle and pair the others up).
+template <bool F8>
+__device__ __forceinline__ int stage_off(int dim) {
+  if constexpr (F8) {
+    const int piece = dim >> 3;
+    return ((piece >> 1) + 8 * (piece & 1)) * 8 + (dim & 7);
+  } else {
+    return dim;
+  }
+}
+
 // F8: the caches hold fp8 (OCP E4M3FN) codes; a chunk's rows are half as many
 // bytes and are widened to bf16 (exact) when staged in LDS; the K scale is
 // folded into scale_log2 and the V scale multiplies the partial O.
@@ -279,16 +294,18 @@ void paged_decode_split_kernel(
         // stage the chunk's K and V rows (row-major per head, bf16) in LDS
 #pragma unroll
         for (int r = 0; r < kLoads; ++r) {
-          const int e = (kRpl * r + lane / kLpr) * kVRow + sd;
+          const int row = (kRpl * r + lane / kLpr) * kVRow;
+          const int e = row + stage_off<F8>(sd);
           if constexpr (F8) {
+            const int e2 = row + stage_off<F8>(sd + 8);
             u32x4_t lo, hi;
             fp8x16_to_bf16(kreg[s][r], lo, hi);
             *reinterpret_cast<u32x4_t*>(&kbuf[sh][e]) = lo;
-            *reinterpret_cast<u32x4_t*>(&kbuf[sh][e + 8]) = hi;
+            *reinterpret_cast<u32x4_t*>(&kbuf[sh][e2]) = hi;
             if constexpr (!kShared) {
               fp8x16_to_bf16(vreg[s][r], lo, hi);
               *reinterpret_cast<u32x4_t*>(&vbuf[sh][e]) = lo;
-              *reinterpret_cast<u32x4_t*>(&vbuf[sh][e + 8]) = hi;
+              *reinterpret_cast<u32x4_t*>(&vbuf[sh][e2]) = hi;
             }
           } else {
             *reinterpret_cast<u32x4_t*>(&kbuf[sh][e]) = kreg[s][r];
@@ -304,7 +321,8 @@ void paged_decode_split_kernel(
 #pragma unroll
           for (int ks = 0; ks < 4; ++ks) {
             const u32x4_t ka =
-                *reinterpret_cast<const u32x4_t*>(&kbuf[hh][col * kVRow + g4 * 8 + ks * 32]);
+                *reinterpret_cast<const u32x4_t*>(
+                    &kbuf[hh][col * kVRow + stage_off<F8>(g4 * 8 + ks * 32)]);
             a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8_v(ka), as_bf16x8_v(qreg[ks]), a,
                                                          0, 0, 0);
           }
@@ -340,11 +358,11 @@ void paged_decode_split_kernel(
         if constexpr (kShared) {  // V over the K rows: the S^T reads above come first
 #pragma unroll
           for (int r = 0; r < kLoads; ++r) {
-            const int e = (kRpl * r + lane / kLpr) * kVRow + sd;
+            const int row = (kRpl * r + lane / kLpr) * kVRow;
             u32x4_t lo, hi;
             fp8x16_to_bf16(vreg[s][r], lo, hi);
-            *reinterpret_cast<u32x4_t*>(&vbuf[sh][e]) = lo;
-            *reinterpret_cast<u32x4_t*>(&vbuf[sh][e + 8]) = hi;
+            *reinterpret_cast<u32x4_t*>(&vbuf[sh][row + stage_off<F8>(sd)]) = lo;
+            *reinterpret_cast<u32x4_t*>(&vbuf[sh][row + stage_off<F8>(sd + 8)]) = hi;
           }
         }
         // P^T per head: a column's weights only in its own head's product
@@ -358,7 +376,7 @@ void paged_decode_split_kernel(
 #pragma unroll
           for (int hh = 0; hh < HP; ++hh) {
             const i16x4_t va = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (lds_i16x4_t*)&vbuf[hh][tr_row * kVRow + db * 16 + tr_col]);
+                (lds_i16x4_t*)&vbuf[hh][tr_row * kVRow + stage_off<F8>(db * 16 + tr_col)]);
             acc[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pbh[hh], acc[db], 0, 0, 0);
           }
         }
