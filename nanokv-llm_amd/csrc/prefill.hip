@@ -221,6 +221,10 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
   };
   // F8: the codes of the last issue() (after their loads land) widened into LDS stage
   // `stage`, rows 16w .. 16w+15 of the K and V tiles, in the bf16 path's swizzled layout
+  // Lanes with c >= 4 write their pair's second chunk first (their codes' halves swapped
+  // before widening), so each 16-byte write instruction covers 8 distinct bank groups per
+  // row instead of pairing them up.
+  const bool f8_swap = f8_c >= 4;
   auto commit = [&](int stage) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     char* at = ring + stage * kStageB + wave * 4096;
@@ -228,13 +232,18 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
     for (int f = 0; f < 2; ++f) {
       const int r = 8 * f + f8_row0;  // row within the wave's 16 (16w + r within the tile)
       const int off = r * 256 + ((2 * f8_c) ^ (2 * (r & 7))) * 16;  // chunks 2c, 2c+1: adjacent
+      const int o1 = off + (f8_swap ? 16 : 0), o2 = off + (f8_swap ? 0 : 16);
       u32x4_t lo, hi;
-      fp8x16_to_bf16(kq[f], lo, hi);
-      *reinterpret_cast<u32x4_t*>(at + off) = lo;
-      *reinterpret_cast<u32x4_t*>(at + off + 16) = hi;
-      fp8x16_to_bf16(vq[f], lo, hi);
-      *reinterpret_cast<u32x4_t*>(at + kTileB + off) = lo;
-      *reinterpret_cast<u32x4_t*>(at + kTileB + off + 16) = hi;
+      u32x4_t c = kq[f];
+      if (f8_swap) c = u32x4_t{c[2], c[3], c[0], c[1]};
+      fp8x16_to_bf16(c, lo, hi);
+      *reinterpret_cast<u32x4_t*>(at + o1) = lo;
+      *reinterpret_cast<u32x4_t*>(at + o2) = hi;
+      c = vq[f];
+      if (f8_swap) c = u32x4_t{c[2], c[3], c[0], c[1]};
+      fp8x16_to_bf16(c, lo, hi);
+      *reinterpret_cast<u32x4_t*>(at + kTileB + o1) = lo;
+      *reinterpret_cast<u32x4_t*>(at + kTileB + o2) = hi;
     }
   };
 
