@@ -78,6 +78,44 @@ def test_topk_ties_and_extremes(nkv, dev):
 
 
 @pytest.mark.parametrize("agg", ["all", "group"])
+@pytest.mark.parametrize("pattern", ["tied", "three_values", "wide_range"])
+def test_fused_select_ties_and_range(nkv, dev, agg, pattern):
+    """The fused kernels' selection on importance it cannot split by value: every window key
+    of a KV head equal (all tied: the lowest indices win), keys taking three values (ties
+    at the threshold), and K rows scaled over six orders of magnitude (a wide key range for
+    the bucket levels). Kept sets must equal the oracle's top-k of the GPU importance."""
+    wl = _state(seed=11, bs=16, topk=4)
+    kc = wl["k_cache"].clone()
+    sel = torch.tensor(wl["seq_idx"])
+    slots, *_ = get_tail_window_and_tail_slots_ref(wl["block_tables"], wl["context_lens"], sel,
+                                                   256, W)
+    g = torch.Generator().manual_seed(5)
+    for r in range(slots.size(0)):
+        if pattern != "wide_range":  # window rows copied from its first one or three rows
+            n_src = 1 if pattern == "tied" else 3
+            src = [wl["k_cache"][int(slots[r, i]) // 256, int(slots[r, i]) % 256]
+                   for i in range(n_src)]
+            for t in range(W * 256):
+                s = int(slots[r, t])
+                kc[s // 256, s % 256] = src[t % n_src]
+        else:
+            ids = slots[r].to(torch.int64)
+            scale = torch.pow(10.0, torch.rand(ids.numel(), generator=g) * 6 - 3)
+            rows = kc.view(-1, 8, 128)[ids].float() * scale[:, None, None]
+            kc.view(-1, 8, 128)[ids] = rows.to(torch.bfloat16)
+    keep, imp = cu.compress_select(
+        wl["q"].to(dev), kc.to(dev), wl["block_tables"].to(dev), wl["context_lens"].to(dev),
+        sel.to(torch.int32).to(dev), W, KEEP - 2, 128 ** -0.5, agg)
+    torch.cuda.synchronize()
+    imp = imp.cpu()
+    assert torch.isfinite(imp).all()
+    if pattern == "tied":  # one value per KV head besides the masked sink and last key
+        assert (imp[..., 1:] == imp[..., 1:2]).all()
+    got = keep.cpu().to(torch.int64)
+    assert torch.equal(got[..., 1:-1], select_topk_ref(imp, KEEP - 2))
+
+
+@pytest.mark.parametrize("agg", ["all", "group"])
 def test_compact_and_finalize_bit_exact(nkv, dev, agg):
     wl = _state(seed=5)
     bt = wl["block_tables"]
