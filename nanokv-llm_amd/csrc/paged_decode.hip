@@ -41,7 +41,9 @@
 // head group, wave wi's partial of sequence b is row wi + b: a segment's
 // partials come from consecutive waves, and the next segment's first wave is
 // at least its last one, so wi + b never collides and stays below
-// waves + batch. A row holds O (128 floats), m, l and two pad floats.
+// waves + batch. A row holds O (D floats), m, l and two pad floats.
+//
+// head_dim D is 64, 128 or 256 (a template parameter of both kernels).
 #include "nkv_common.h"
 
 #include <algorithm>
@@ -49,16 +51,16 @@
 
 namespace nkv {
 
-constexpr int kD = 128;                  // head_dim
 constexpr int kChunk = 16;               // tokens per pipeline stage
 constexpr int kMinChunks = 4;            // minimum chunks per wave range
 constexpr int kMaxSlots = 128;           // partials per (sequence, query head) at most
 constexpr int kWinBlocks = 64;           // block ids held per window (one per lane)
-constexpr int kVRow = kD + 16;           // LDS row stride of a staged V chunk (elements)
 constexpr int kBufferFlags = 0x00020000; // raw buffer resource word 3 (dword data)
 constexpr int kStreamPolicy = 2;         // cache policy "nt": K/V are read exactly once
 constexpr int kWavesPerCU = 8;           // resident split waves per CU (2 per SIMD)
-constexpr int kPartRow = kD + 4;         // floats per partial row: O, m, l, 2 pad (528 B)
+// floats per partial row: O, m, l, 2 pad (528 B at D = 128)
+constexpr int part_row(int D) { return D + 4; }
+constexpr bool decode_dim_ok(int D) { return D == 64 || D == 128 || D == 256; }
 constexpr int kMaxCols = 16;             // MFMA columns: query heads per wave at most
 
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
@@ -116,14 +118,14 @@ __device__ __forceinline__ void seq_load(SeqCursor& c, const int32_t* __restrict
 
 // Element offset of head dim `dim` (a multiple of 4) in a staged LDS row. bf16 rows are
 // dense. fp8 rows are staged as 8-dim pieces with the even pieces first (piece 2c at slot
-// c, piece 2c+1 at slot 8 + c): a lane widens 16 codes into pieces 2c and 2c+1, and each
-// of its two 16-byte writes then lands beside its neighbours' (the 32-byte stride of a
-// dense row would leave half the banks idle and pair the others up).
-template <bool F8>
+// c, piece 2c+1 at slot D/16 + c): a lane widens 16 codes into pieces 2c and 2c+1, and
+// each of its two 16-byte writes then lands beside its neighbours' (the 32-byte stride of
+// a dense row would leave half the banks idle and pair the others up).
+template <bool F8, int D>
 __device__ __forceinline__ int stage_off(int dim) {
   if constexpr (F8) {
     const int piece = dim >> 3;
-    return ((piece >> 1) + 8 * (piece & 1)) * 8 + (dim & 7);
+    return ((piece >> 1) + (D / 16) * (piece & 1)) * 8 + (dim & 7);
   } else {
     return dim;
   }
@@ -142,9 +144,10 @@ __device__ __forceinline__ int stage_off(int dim) {
 // fp8 rows (1 KiB at Hk = 8) take HP = 4 for 512-byte pieces, with K and V
 // staged through one LDS buffer so two waves per SIMD still fit.
 // G (query heads per KV head) is any value with HP*G <= 16: the columns past
-// HP*G are computed and dropped.
-template <bool F8, int HP>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2)))
+// HP*G are computed and dropped. D: head_dim (64, 128 or 256); a wave's piece of
+// a token row (HP*D elements) is 128 to 512 bytes.
+template <bool F8, int HP, int D>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 2)))
 void paged_decode_split_kernel(
     const bf16_t* __restrict__ q, int64_t q_row_stride,
     const void* __restrict__ k_cache, const void* __restrict__ v_cache,
@@ -152,17 +155,23 @@ void paged_decode_split_kernel(
     const int32_t* __restrict__ context_lens, int32_t batch, int32_t Hk, int32_t G,
     int32_t block_size, int32_t max_blocks, int64_t n_blocks, int32_t min_chunks,
     float scale_log2, float v_scale, float* __restrict__ part, i32x4v_t* __restrict__ desc) {
+  static_assert(decode_dim_ok(D), "head_dim 64, 128 or 256");
   constexpr int kEl = F8 ? 1 : 2;              // bytes per cache element
-  constexpr int kSeg = HP * kD * kEl;          // bytes a wave reads of each token row
+  constexpr int kSeg = HP * D * kEl;           // bytes a wave reads of each token row
+  static_assert(kSeg >= 64 && kSeg <= 512, "a wave's piece of a row is 64..512 bytes");
+  constexpr int kKs = D / 32;                  // k-steps of S^T (32 dims each)
+  constexpr int kDb = D / 16;                  // 16-dim blocks of O^T
+  constexpr int kVRow = D + 16;                // LDS row stride of a staged chunk (elements)
+  constexpr int kPartRow = part_row(D);
   constexpr int kLpr = kSeg / 16;              // lanes per row (16-byte loads)
   constexpr int kRpl = 64 / kLpr;              // rows per load instruction
   constexpr int kLoads = kChunk / kRpl;        // loads per lane per K (or V) chunk
   constexpr int kRing = kLoads >= 8 ? 2 : 4;   // ring depth: at most 16 loads per lane in flight
   constexpr int kLph = kLpr / HP;              // lanes per head within a row
-  // HP = 4: K and V of a chunk share one staging buffer (V is written after the K reads
-  // of S^T), which keeps two waves per SIMD within the LDS
-  constexpr bool kShared = HP == 4;
-  static_assert(!kShared || F8, "the shared buffer is staged for fp8 rows");
+  // K and V of a chunk share one staging buffer (V is written after the K reads of S^T)
+  // where two would take 20 KiB or more (four heads at D <= 128, two at D = 256), which
+  // keeps two waves per SIMD within the LDS
+  constexpr bool kShared = 2 * HP * kChunk * kVRow * 2 >= 20480;
   __shared__ __attribute__((aligned(16))) bf16_t lbuf[kShared ? 1 : 2][HP][kChunk * kVRow];
   auto& kbuf = lbuf[0];
   auto& vbuf = lbuf[kShared ? 0 : 1];
@@ -171,7 +180,7 @@ void paged_decode_split_kernel(
   const int g4 = lane >> 4;   // key group: keys 4*g4 .. 4*g4+3 of a chunk
   const int col = lane & 15;  // MFMA column: query head (S^T, O^T) / key row (K)
   const int HPG = HP * G;     // query heads (MFMA columns) of the wave's head group
-  const int row_b = Hk * kD * kEl;  // bytes of one cache row (token)
+  const int row_b = Hk * D * kEl;  // bytes of one cache row (token)
   const int max_tokens = max_blocks * block_size;
 
   // ---- this wave's KV heads and chunk range. Every head group has the same
@@ -232,21 +241,21 @@ void paged_decode_split_kernel(
 
     // q^T as the MFMA B operand: lane l -> query head kvh0*G + l%16 (columns
     // >= HP*G re-read the first head and are discarded), dims 8*(l/16) + 32*ks
-    u32x4_t qreg[4];
+    u32x4_t qreg[kKs];
     {
       const int hc = col < HPG ? col : 0;
       const u32x4_t* qp = reinterpret_cast<const u32x4_t*>(
-          q + (int64_t)b * q_row_stride + (int64_t)(kvh0 * G + hc) * kD + g4 * 8);
+          q + (int64_t)b * q_row_stride + (int64_t)(kvh0 * G + hc) * D + g4 * 8);
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) qreg[ks] = qp[ks * 4];
+      for (int ks = 0; ks < kKs; ++ks) qreg[ks] = qp[ks * 4];
     }
-    const char* kbase = static_cast<const char*>(k_cache) + (int64_t)kvh0 * kD * kEl;
-    const char* vbase = static_cast<const char*>(v_cache) + (int64_t)kvh0 * kD * kEl;
+    const char* kbase = static_cast<const char*>(k_cache) + (int64_t)kvh0 * D * kEl;
+    const char* vbase = static_cast<const char*>(v_cache) + (int64_t)kvh0 * D * kEl;
     const int32_t* bt_row = block_tables + (int64_t)b * bt_row_stride;
 
-    f32x4_t acc[8];  // O^T: lane l -> column l%16, dims 16*db + 4*(l/16) .. +3
+    f32x4_t acc[kDb];  // O^T: lane l -> column l%16, dims 16*db + 4*(l/16) .. +3
 #pragma unroll
-    for (int db = 0; db < 8; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int db = 0; db < kDb; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     float m_run = -INFINITY, l_run = 0.f;
 
     // windows of at most kWinBlocks cache blocks (block ids one per lane)
@@ -295,9 +304,9 @@ void paged_decode_split_kernel(
 #pragma unroll
         for (int r = 0; r < kLoads; ++r) {
           const int row = (kRpl * r + lane / kLpr) * kVRow;
-          const int e = row + stage_off<F8>(sd);
+          const int e = row + stage_off<F8, D>(sd);
           if constexpr (F8) {
-            const int e2 = row + stage_off<F8>(sd + 8);
+            const int e2 = row + stage_off<F8, D>(sd + 8);
             u32x4_t lo, hi;
             fp8x16_to_bf16(kreg[s][r], lo, hi);
             *reinterpret_cast<u32x4_t*>(&kbuf[sh][e]) = lo;
@@ -309,7 +318,7 @@ void paged_decode_split_kernel(
             }
           } else {
             *reinterpret_cast<u32x4_t*>(&kbuf[sh][e]) = kreg[s][r];
-            *reinterpret_cast<u32x4_t*>(&vbuf[sh][e]) = vreg[s][r];
+            if constexpr (!kShared) *reinterpret_cast<u32x4_t*>(&vbuf[sh][e]) = vreg[s][r];
           }
         }
         // S^T for 16 keys x 16 columns per head; A operand: lane l -> key l%16,
@@ -319,10 +328,10 @@ void paged_decode_split_kernel(
         for (int hh = 0; hh < HP; ++hh) {
           f32x4_t a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int ks = 0; ks < 4; ++ks) {
+          for (int ks = 0; ks < kKs; ++ks) {
             const u32x4_t ka =
                 *reinterpret_cast<const u32x4_t*>(
-                    &kbuf[hh][col * kVRow + stage_off<F8>(g4 * 8 + ks * 32)]);
+                    &kbuf[hh][col * kVRow + stage_off<F8, D>(g4 * 8 + ks * 32)]);
             a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8_v(ka), as_bf16x8_v(qreg[ks]), a,
                                                          0, 0, 0);
           }
@@ -350,7 +359,7 @@ void paged_decode_split_kernel(
         m_run = m_new;
         if (alpha != 1.f) {
 #pragma unroll
-          for (int db = 0; db < 8; ++db) acc[db] *= alpha;
+          for (int db = 0; db < kDb; ++db) acc[db] *= alpha;
         }
         const bf16x2v_t p01 = {(__bf16)p[0], (__bf16)p[1]};
         const bf16x2v_t p23 = {(__bf16)p[2], (__bf16)p[3]};
@@ -359,10 +368,14 @@ void paged_decode_split_kernel(
 #pragma unroll
           for (int r = 0; r < kLoads; ++r) {
             const int row = (kRpl * r + lane / kLpr) * kVRow;
-            u32x4_t lo, hi;
-            fp8x16_to_bf16(vreg[s][r], lo, hi);
-            *reinterpret_cast<u32x4_t*>(&vbuf[sh][row + stage_off<F8>(sd)]) = lo;
-            *reinterpret_cast<u32x4_t*>(&vbuf[sh][row + stage_off<F8>(sd + 8)]) = hi;
+            if constexpr (F8) {
+              u32x4_t lo, hi;
+              fp8x16_to_bf16(vreg[s][r], lo, hi);
+              *reinterpret_cast<u32x4_t*>(&vbuf[sh][row + stage_off<F8, D>(sd)]) = lo;
+              *reinterpret_cast<u32x4_t*>(&vbuf[sh][row + stage_off<F8, D>(sd + 8)]) = hi;
+            } else {
+              *reinterpret_cast<u32x4_t*>(&vbuf[sh][row + sd]) = vreg[s][r];
+            }
           }
         }
         // P^T per head: a column's weights only in its own head's product
@@ -372,11 +385,11 @@ void paged_decode_split_kernel(
           pbh[hh] = __builtin_bit_cast(i16x4_t, (HP == 1 || hsel == hh) ? pw : uint2{0u, 0u});
         // O^T[dims][cols] += V^T[dims][keys] P^T[keys][cols], 16 dims per MFMA
 #pragma unroll
-        for (int db = 0; db < 8; ++db) {
+        for (int db = 0; db < kDb; ++db) {
 #pragma unroll
           for (int hh = 0; hh < HP; ++hh) {
             const i16x4_t va = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (lds_i16x4_t*)&vbuf[hh][tr_row * kVRow + stage_off<F8>(db * 16 + tr_col)]);
+                (lds_i16x4_t*)&vbuf[hh][tr_row * kVRow + stage_off<F8, D>(db * 16 + tr_col)]);
             acc[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pbh[hh], acc[db], 0, 0, 0);
           }
         }
@@ -406,7 +419,7 @@ void paged_decode_split_kernel(
     l_run += __shfl_xor(l_run, 32, 64);
     if constexpr (F8) {
 #pragma unroll
-      for (int db = 0; db < 8; ++db) acc[db] *= v_scale;
+      for (int db = 0; db < kDb; ++db) acc[db] *= v_scale;
     }
     // partial row (wi + b) * HPG + col of the group; the wave that ends the segment
     // writes each of its KV heads' descriptor {first row, count, row stride}
@@ -414,9 +427,9 @@ void paged_decode_split_kernel(
     if (col < HPG) {
       float* pr = gpart + (int64_t)(prow0 + col) * kPartRow;
 #pragma unroll
-      for (int db = 0; db < 8; ++db)
+      for (int db = 0; db < kDb; ++db)
         *reinterpret_cast<f32x4_t*>(&pr[db * 16 + g4 * 4]) = acc[db];
-      if (g4 == 0) *reinterpret_cast<float2*>(&pr[kD]) = float2{m_run, l_run};
+      if (g4 == 0) *reinterpret_cast<float2*>(&pr[D]) = float2{m_run, l_run};
     }
     if (c_lo + n_seg == nc && lane < HP) {
       const int64_t first = (int64_t)grp * (Wh + batch) * HPG + (int64_t)(w_first + b) * HPG +
@@ -428,12 +441,47 @@ void paged_decode_split_kernel(
   }
 }
 
+// N consecutive floats of a partial row (N = D / 64 output dims per lane).
+template <int N>
+__device__ __forceinline__ void load_dims(const float* p, float (&v)[N]) {
+  if constexpr (N == 1) {
+    v[0] = *p;
+  } else if constexpr (N == 2) {
+    const float2 t = *reinterpret_cast<const float2*>(p);
+    v[0] = t.x;
+    v[1] = t.y;
+  } else {
+    static_assert(N == 4, "1, 2 or 4 dims per lane");
+    const float4 t = *reinterpret_cast<const float4*>(p);
+    v[0] = t.x;
+    v[1] = t.y;
+    v[2] = t.z;
+    v[3] = t.w;
+  }
+}
+// N output dims of one lane as bf16 (2, 4 or 8 bytes).
+template <int N>
+__device__ __forceinline__ void store_dims(bf16_t* op, const float (&o)[N], float scale) {
+  if constexpr (N == 1) {
+    *reinterpret_cast<uint16_t*>(op) = (uint16_t)(pack_bf16x2(o[0] * scale, 0.f) & 0xffffu);
+  } else if constexpr (N == 2) {
+    *reinterpret_cast<uint32_t*>(op) = pack_bf16x2(o[0] * scale, o[1] * scale);
+  } else {
+    *reinterpret_cast<uint2*>(op) =
+        uint2{pack_bf16x2(o[0] * scale, o[1] * scale), pack_bf16x2(o[2] * scale, o[3] * scale)};
+  }
+}
+
 // Merge the partials of one (sequence, query head): O = sum_s 2^(m_s-M) O_s /
-// sum_s 2^(m_s-M) l_s. One wave per pair.
+// sum_s 2^(m_s-M) l_s. One wave per pair; lane l owns output dims N*l .. N*l+N-1.
+template <int D>
 __global__ __launch_bounds__(64) void paged_decode_combine_kernel(
     const int32_t* __restrict__ context_lens, int32_t Hq, int32_t Hk,
     const float* __restrict__ part, const i32x4v_t* __restrict__ desc,
     bf16_t* __restrict__ out, int64_t out_row_stride) {
+  static_assert(decode_dim_ok(D), "head_dim 64, 128 or 256");
+  constexpr int N = D / 64;
+  constexpr int kPartRow = part_row(D);
   const int b = blockIdx.x / Hq;
   const int h = blockIdx.x % Hq;
   const int lane = threadIdx.x;
@@ -443,59 +491,67 @@ __global__ __launch_bounds__(64) void paged_decode_combine_kernel(
   static_assert(kMaxSlots <= 128, "two partials per lane");
   const int ctx = context_lens[b];
   const i32x4v_t d = desc[(int64_t)b * Hk + h / G];
-  bf16_t* op = out + (int64_t)b * out_row_stride + (int64_t)h * kD + 2 * lane;
+  bf16_t* op = out + (int64_t)b * out_row_stride + (int64_t)h * D + N * lane;
+  float o[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) o[i] = 0.f;
   // the descriptor is written by this call for every sequence with ctx > 0
   const int ns = ctx > 0 ? min(d.y, kMaxSlots) : 0;
   if (ns == 0) {
-    *reinterpret_cast<uint32_t*>(op) = 0u;
+    store_dims<N>(op, o, 0.f);
     return;
   }
   const int64_t stride = (int64_t)d.z * kPartRow;  // floats between a head's partials
   const float* pbase = part + ((int64_t)d.x + h % G) * kPartRow;
-  const float* po = pbase + 2 * lane;
+  const float* po = pbase + N * lane;
   float2 ml0 = {-INFINITY, 0.f}, ml1 = {-INFINITY, 0.f};
-  if (lane < ns) ml0 = *reinterpret_cast<const float2*>(pbase + lane * stride + kD);
-  if (lane + 64 < ns) ml1 = *reinterpret_cast<const float2*>(pbase + (lane + 64) * stride + kD);
-  float2 v0[8];
+  if (lane < ns) ml0 = *reinterpret_cast<const float2*>(pbase + lane * stride + D);
+  if (lane + 64 < ns) ml1 = *reinterpret_cast<const float2*>(pbase + (lane + 64) * stride + D);
+  float v0[8][N];
 #pragma unroll
-  for (int u = 0; u < 8; ++u)
-    v0[u] = u < ns ? *reinterpret_cast<const float2*>(po + u * stride) : float2{0.f, 0.f};
+  for (int u = 0; u < 8; ++u) {
+    if (u < ns) {
+      load_dims<N>(po + u * stride, v0[u]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < N; ++i) v0[u][i] = 0.f;
+    }
+  }
   // lane l holds partials l and l + 64 (ns <= kMaxSlots = 128): the global max and
   // the weights w_s = 2^(m_s - M) with two wave reductions, then each lane
-  // accumulates two output dims over the partials, eight loads in flight
+  // accumulates its output dims over the partials, eight loads in flight
   const float M = wave_max(fmaxf(ml0.x, ml1.x));
   const float w0 = (ml0.x == -INFINITY) ? 0.f : fast_exp2(ml0.x - M);
   const float w1 = (ml1.x == -INFINITY) ? 0.f : fast_exp2(ml1.x - M);
   const float L = wave_sum(w0 * ml0.y + w1 * ml1.y);
-  float o0 = 0.f, o1 = 0.f;
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
     const float w = __shfl(w0, u, 64);
     if (u < ns) {  // uniform
-      o0 = fmaf(w, v0[u].x, o0);
-      o1 = fmaf(w, v0[u].y, o1);
+#pragma unroll
+      for (int i = 0; i < N; ++i) o[i] = fmaf(w, v0[u][i], o[i]);
     }
   }
   int s = 8;
   for (; s + 8 <= ns; s += 8) {
-    float2 v[8];
+    float v[8][N];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const float2*>(po + (s + u) * stride);
+    for (int u = 0; u < 8; ++u) load_dims<N>(po + (s + u) * stride, v[u]);
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const float w = __shfl(s + u < 64 ? w0 : w1, (s + u) & 63, 64);  // uniform select
-      o0 = fmaf(w, v[u].x, o0);
-      o1 = fmaf(w, v[u].y, o1);
+#pragma unroll
+      for (int i = 0; i < N; ++i) o[i] = fmaf(w, v[u][i], o[i]);
     }
   }
   for (; s < ns; ++s) {
-    const float2 v = *reinterpret_cast<const float2*>(po + s * stride);
+    float v[N];
+    load_dims<N>(po + s * stride, v);
     const float w = __shfl(s < 64 ? w0 : w1, s & 63, 64);
-    o0 = fmaf(w, v.x, o0);
-    o1 = fmaf(w, v.y, o1);
+#pragma unroll
+    for (int i = 0; i < N; ++i) o[i] = fmaf(w, v[i], o[i]);
   }
-  const float inv = L > 0.f ? 1.f / L : 0.f;
-  *reinterpret_cast<uint32_t*>(op) = pack_bf16x2(o0 * inv, o1 * inv);
+  store_dims<N>(op, o, L > 0.f ? 1.f / L : 0.f);
 }
 
 static int decode_check(const void* q, const void* k_cache, const void* v_cache,
@@ -505,8 +561,8 @@ static int decode_check(const void* q, const void* k_cache, const void* v_cache,
                         int64_t bt_row_stride) {
   NKV_REQUIRE(batch >= 0 && n_kv_heads > 0 && n_q_heads > 0, NKV_EINVAL,
               "paged_decode: bad sizes (batch=%d, Hq=%d, Hk=%d)", batch, n_q_heads, n_kv_heads);
-  NKV_REQUIRE(head_dim == kD, NKV_EUNSUPPORTED, "paged_decode: head_dim must be 128 (got %d)",
-              head_dim);
+  NKV_REQUIRE(decode_dim_ok(head_dim), NKV_EUNSUPPORTED,
+              "paged_decode: head_dim must be 64, 128 or 256 (got %d)", head_dim);
   NKV_REQUIRE(n_q_heads % n_kv_heads == 0, NKV_EINVAL,
               "paged_decode: n_q_heads %% n_kv_heads != 0 (%d, %d)", n_q_heads, n_kv_heads);
   const int g = n_q_heads / n_kv_heads;
@@ -519,10 +575,10 @@ static int decode_check(const void* q, const void* k_cache, const void* v_cache,
               (long long)bt_row_stride);
   NKV_REQUIRE((int64_t)max_blocks_per_seq * block_size < (1ll << 30), NKV_EUNSUPPORTED,
               "paged_decode: max_blocks_per_seq * block_size too large");
-  NKV_REQUIRE((int64_t)block_size * n_kv_heads * kD * 2 < (1ll << 31), NKV_EUNSUPPORTED,
+  NKV_REQUIRE((int64_t)block_size * n_kv_heads * head_dim * 2 < (1ll << 31), NKV_EUNSUPPORTED,
               "paged_decode: cache block too large for 32-bit buffer offsets");
-  NKV_REQUIRE(q_row_stride >= (int64_t)n_q_heads * kD && q_row_stride % 8 == 0, NKV_EINVAL,
-              "paged_decode: q row stride must be >= Hq*D and a multiple of 8");
+  NKV_REQUIRE(q_row_stride >= (int64_t)n_q_heads * head_dim && q_row_stride % 8 == 0,
+              NKV_EINVAL, "paged_decode: q row stride must be >= Hq*D and a multiple of 8");
   NKV_REQUIRE(q && k_cache && v_cache && block_tables && context_lens, NKV_EINVAL,
               "paged_decode: null pointer");
   NKV_REQUIRE(aligned16(q) && aligned16(k_cache) && aligned16(v_cache), NKV_EINVAL,
@@ -548,7 +604,7 @@ static int device_cus() {
 
 // Persistent grid: as many one-wave workgroups as are resident at once, at most
 // kWavesPerCU per CU (the workspace bound assumes no more).
-template <bool F8, int HP>
+template <bool F8, int HP, int D>
 static int decode_grid() {
   static std::atomic<int> cached[64];
   int dev = 0;
@@ -557,8 +613,8 @@ static int decode_grid() {
   if (n == 0) {
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, reinterpret_cast<const void*>(paged_decode_split_kernel<F8, HP>), 64, 0) !=
-            hipSuccess ||
+            &per_cu, reinterpret_cast<const void*>(paged_decode_split_kernel<F8, HP, D>), 64,
+            0) != hipSuccess ||
         per_cu <= 0)
       per_cu = kWavesPerCU;
     n = device_cus() * std::min(per_cu, kWavesPerCU);
@@ -567,9 +623,36 @@ static int decode_grid() {
   return n;
 }
 
+// KV heads per wave at most for head_dim D: a 512-byte piece of every token row
+// (bf16: 4 / 2 / 1 at D = 64 / 128 / 256; fp8: 4 / 4 / 2).
+template <bool F8>
+static constexpr int decode_max_hp(int D) {
+  const int hp = 512 / (D * (F8 ? 1 : 2));
+  return hp > 4 ? 4 : hp;
+}
+
+// The resident grid of instance (F8, hp, D) -- hp and D from the plan.
+template <bool F8>
+static int decode_grid_of(int hp, int D) {
+  if (D == 64) {
+    return hp == 4 ? decode_grid<F8, 4, 64>() : hp == 2 ? decode_grid<F8, 2, 64>()
+                                                        : decode_grid<F8, 1, 64>();
+  }
+  if (D == 128) {
+    if constexpr (F8) {
+      if (hp == 4) return decode_grid<true, 4, 128>();
+    }
+    return hp == 2 ? decode_grid<F8, 2, 128>() : decode_grid<F8, 1, 128>();
+  }
+  if constexpr (F8) {
+    if (hp == 2) return decode_grid<true, 2, 256>();
+  }
+  return decode_grid<F8, 1, 256>();
+}
+
 // The launch a decode call makes: KV heads per wave, the grid and the smallest range.
 struct DecodePlan {
-  int hp;          // KV heads per wave (1, 2, or 4 for fp8)
+  int hp;          // KV heads per wave (1, 2 or 4)
   unsigned grid;   // one-wave workgroups
   int32_t min_chunks;
 };
@@ -582,25 +665,26 @@ static int64_t decode_useful_waves(int32_t batch, int32_t max_blocks, int32_t bl
 
 template <bool F8>
 static DecodePlan decode_plan(int32_t batch, int32_t Hq, int32_t Hk, int32_t max_blocks,
-                              int32_t block_size) {
+                              int32_t block_size, int32_t D) {
   const int g = Hq / Hk;
   const int64_t max_chunks = ((int64_t)max_blocks * block_size + kChunk - 1) / kChunk;
-  // Two KV heads per wave when the heads pair up, the 2G query heads fit the 16
-  // MFMA columns and there is enough work for every wave (upper bound from the
-  // table width: >= 32 chunks per head pair per resident wave); otherwise one.
+  // Several KV heads per wave (up to a 512-byte piece of every token row) when the heads
+  // group evenly, the hp*G query heads fit the 16 MFMA columns and there is enough work
+  // for every wave (upper bound from the table width: >= 32 chunks per head group per
+  // resident wave of the two-head instance); otherwise one.
   const int64_t work = (int64_t)batch * max_chunks * Hk;
-  const bool pair = Hk % 2 == 0 && 2 * g <= kMaxCols && work >= 32 * (int64_t)decode_grid<F8, 2>();
-  // fp8 rows are half as wide: four heads per wave read 512-byte pieces
-  const bool quad = F8 && pair && Hk % 4 == 0 && 4 * g <= kMaxCols;
+  int hp = 1;
+  if (decode_max_hp<F8>(D) >= 2 && Hk % 2 == 0 && 2 * g <= kMaxCols &&
+      work >= 32 * (int64_t)decode_grid_of<F8>(2, D)) {
+    hp = 2;
+    if (decode_max_hp<F8>(D) >= 4 && Hk % 4 == 0 && 4 * g <= kMaxCols) hp = 4;
+  }
   DecodePlan p;
-  p.hp = quad ? 4 : pair ? 2 : 1;
+  p.hp = hp;
   p.min_chunks = decode_min_chunks(max_blocks, block_size);
   // Resident waves per head group, but no more than the table width lets receive a range
   // of min_chunks (small batches launch only the waves that can get work).
-  int resident = p.hp == 2 ? decode_grid<F8, 2>() : decode_grid<F8, 1>();
-  if constexpr (F8) {
-    if (p.hp == 4) resident = decode_grid<true, 4>();
-  }
+  const int resident = decode_grid_of<F8>(hp, D);
   const int np = Hk / p.hp;
   const int64_t per =
       std::min<int64_t>(std::max(1, resident / np), decode_useful_waves(batch, max_blocks,
@@ -615,8 +699,9 @@ static DecodePlan decode_plan(int32_t batch, int32_t Hq, int32_t Hk, int32_t max
 static size_t decode_desc_bytes(int32_t batch, int32_t Hk) {
   return (size_t)batch * Hk * sizeof(i32x4v_t);
 }
-static size_t decode_part_bytes(int64_t grid, int32_t hpg, int32_t batch, int32_t Hq) {
-  return (size_t)(grid * hpg + (int64_t)batch * Hq) * kPartRow * sizeof(float);
+static size_t decode_part_bytes(int64_t grid, int32_t hpg, int32_t batch, int32_t Hq,
+                                int32_t D) {
+  return (size_t)(grid * hpg + (int64_t)batch * Hq) * part_row(D) * sizeof(float);
 }
 
 }  // namespace nkv
@@ -626,7 +711,7 @@ extern "C" size_t nkv_paged_decode_workspace_bytes(int32_t batch, int32_t n_q_he
                                                    int32_t block_size) {
   using namespace nkv;
   if (batch <= 0 || n_q_heads <= 0 || max_blocks_per_seq <= 0 || block_size <= 0 ||
-      head_dim != kD)
+      !decode_dim_ok(head_dim))
     return 0;
   // Whatever the plan: grid <= CUs * kWavesPerCU and grid <= useful * (head groups), with
   // HP*G <= min(16, Hq) and (head groups) * HP*G = Hq; the descriptors at most batch * Hq.
@@ -634,8 +719,9 @@ extern "C" size_t nkv_paged_decode_workspace_bytes(int32_t batch, int32_t n_q_he
   const int64_t cols = std::min<int64_t>(
       resident * std::min(kMaxCols, n_q_heads),
       decode_useful_waves(batch, max_blocks_per_seq, block_size) * n_q_heads);
-  return decode_desc_bytes(batch, n_q_heads) + decode_part_bytes(0, 0, batch, n_q_heads) +
-         (size_t)cols * kPartRow * sizeof(float);
+  return decode_desc_bytes(batch, n_q_heads) +
+         decode_part_bytes(0, 0, batch, n_q_heads, head_dim) +
+         (size_t)cols * part_row(head_dim) * sizeof(float);
 }
 
 namespace nkv {
@@ -657,9 +743,9 @@ static int decode_split(const void* q, int64_t q_row_stride, const void* k_cache
               "paged_decode: too many chunks in one call");
   const int g = n_q_heads / n_kv_heads;
   const DecodePlan p = decode_plan<F8>(batch, n_q_heads, n_kv_heads, max_blocks_per_seq,
-                                       block_size);
+                                       block_size, head_dim);
   const size_t desc_b = decode_desc_bytes(batch, n_kv_heads);
-  const size_t need = desc_b + decode_part_bytes(p.grid, p.hp * g, batch, n_q_heads);
+  const size_t need = desc_b + decode_part_bytes(p.grid, p.hp * g, batch, n_q_heads, head_dim);
   NKV_REQUIRE(workspace && workspace_bytes >= need, NKV_EWORKSPACE,
               "paged_decode: workspace needs %zu bytes (got %zu)", need, workspace_bytes);
   NKV_REQUIRE((int64_t)p.grid * p.hp * g + (int64_t)batch * n_q_heads < (1ll << 31),
@@ -668,18 +754,30 @@ static int decode_split(const void* q, int64_t q_row_stride, const void* k_cache
   float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + desc_b);
   const float scale_log2 = scale * k_scale * kLog2e;
   hipStream_t s = as_stream(stream);
-#define NKV_DECODE_LAUNCH(HP)                                                                  \
-  hipLaunchKernelGGL((paged_decode_split_kernel<F8, HP>), dim3(p.grid), dim3(64), 0, s,         \
+#define NKV_DECODE_LAUNCH(HP, D)                                                               \
+  hipLaunchKernelGGL((paged_decode_split_kernel<F8, HP, D>), dim3(p.grid), dim3(64), 0, s,      \
                      (const bf16_t*)q, q_row_stride, k_cache, v_cache, block_tables,           \
                      bt_row_stride, context_lens, batch, n_kv_heads, g, block_size,            \
                      max_blocks_per_seq, n_blocks, p.min_chunks, scale_log2, v_scale, part,    \
                      desc)
-  if (p.hp == 4) {
-    if constexpr (F8) NKV_DECODE_LAUNCH(4);
-  } else if (p.hp == 2) {
-    NKV_DECODE_LAUNCH(2);
+  if (head_dim == 64) {
+    if (p.hp == 4) NKV_DECODE_LAUNCH(4, 64);
+    else if (p.hp == 2) NKV_DECODE_LAUNCH(2, 64);
+    else NKV_DECODE_LAUNCH(1, 64);
+  } else if (head_dim == 128) {
+    if (p.hp == 4) {
+      if constexpr (F8) NKV_DECODE_LAUNCH(4, 128);
+    } else if (p.hp == 2) {
+      NKV_DECODE_LAUNCH(2, 128);
+    } else {
+      NKV_DECODE_LAUNCH(1, 128);
+    }
   } else {
-    NKV_DECODE_LAUNCH(1);
+    if (p.hp == 2) {
+      if constexpr (F8) NKV_DECODE_LAUNCH(2, 256);
+    } else {
+      NKV_DECODE_LAUNCH(1, 256);
+    }
   }
 #undef NKV_DECODE_LAUNCH
   return check_launch("nkv_paged_decode_split");
@@ -691,26 +789,35 @@ static int decode_combine(const int32_t* context_lens, int32_t batch, int32_t n_
                           int32_t n_kv_heads, int32_t head_dim, int32_t block_size,
                           int32_t max_blocks_per_seq, void* out, int64_t out_row_stride,
                           const void* workspace, size_t workspace_bytes, void* stream) {
-  NKV_REQUIRE(head_dim == kD, NKV_EUNSUPPORTED, "paged_decode: head_dim must be 128");
+  NKV_REQUIRE(decode_dim_ok(head_dim), NKV_EUNSUPPORTED,
+              "paged_decode: head_dim must be 64, 128 or 256 (got %d)", head_dim);
   NKV_REQUIRE(batch >= 0 && n_q_heads > 0 && n_kv_heads > 0 && n_q_heads % n_kv_heads == 0 &&
                   n_q_heads / n_kv_heads <= kMaxCols && block_size > 0 && max_blocks_per_seq > 0,
               NKV_EINVAL, "paged_decode_combine: bad sizes");
   if (batch == 0) return NKV_OK;
   NKV_REQUIRE(out && context_lens, NKV_EINVAL, "paged_decode_combine: null pointer");
-  NKV_REQUIRE(out_row_stride >= (int64_t)n_q_heads * kD && out_row_stride % 2 == 0 &&
-                  (reinterpret_cast<uintptr_t>(out) & 3) == 0,
+  // each lane stores D/64 consecutive bf16 (2, 4 or 8 bytes)
+  const int al = head_dim / 64;  // elements per lane store
+  NKV_REQUIRE(out_row_stride >= (int64_t)n_q_heads * head_dim && out_row_stride % al == 0 &&
+                  (reinterpret_cast<uintptr_t>(out) & (2 * al - 1)) == 0,
               NKV_EINVAL,
-              "paged_decode_combine: out must be 4-byte aligned with an even row stride "
-              ">= Hq*D");
+              "paged_decode_combine: out must be %d-byte aligned with a row stride >= Hq*D "
+              "that is a multiple of %d", 2 * al, al);
   const size_t desc_b = decode_desc_bytes(batch, n_kv_heads);
   NKV_REQUIRE(workspace && workspace_bytes > desc_b, NKV_EWORKSPACE,
               "paged_decode_combine: workspace of %zu bytes holds no partials",
               workspace_bytes);
   const i32x4v_t* desc = static_cast<const i32x4v_t*>(workspace);
   const float* part = reinterpret_cast<const float*>(static_cast<const char*>(workspace) + desc_b);
-  hipLaunchKernelGGL(paged_decode_combine_kernel, dim3((unsigned)(batch * n_q_heads)), dim3(64),
-                     0, as_stream(stream), context_lens, n_q_heads, n_kv_heads, part, desc,
-                     (bf16_t*)out, out_row_stride);
+  const dim3 grid((unsigned)(batch * n_q_heads));
+#define NKV_COMBINE_LAUNCH(D)                                                                  \
+  hipLaunchKernelGGL((paged_decode_combine_kernel<D>), grid, dim3(64), 0, as_stream(stream),    \
+                     context_lens, n_q_heads, n_kv_heads, part, desc, (bf16_t*)out,            \
+                     out_row_stride)
+  if (head_dim == 64) NKV_COMBINE_LAUNCH(64);
+  else if (head_dim == 128) NKV_COMBINE_LAUNCH(128);
+  else NKV_COMBINE_LAUNCH(256);
+#undef NKV_COMBINE_LAUNCH
   return check_launch("nkv_paged_decode_combine");
 }
 }  // namespace nkv
@@ -829,10 +936,10 @@ extern "C" int nkv_paged_decode_noalloc(const void* q, int64_t q_row_stride, con
   if (batch == 0) return NKV_OK;
   // the bytes this call's plan needs, against the array's fixed size
   const DecodePlan p = decode_plan<false>(batch, n_q_heads, n_kv_heads, max_blocks_per_seq,
-                                          block_size);
+                                          block_size, head_dim);
   const size_t need = decode_desc_bytes(batch, n_kv_heads) +
                       decode_part_bytes(p.grid, p.hp * (n_q_heads / n_kv_heads), batch,
-                                        n_q_heads);
+                                        n_q_heads, head_dim);
   NKV_REQUIRE(need <= kScratchBytes, NKV_EUNSUPPORTED,
               "paged_decode_noalloc: batch %d x %d query heads needs %zu bytes of partials, "
               "above the fixed %zu-byte array; use nkv_paged_decode with a workspace",

@@ -64,7 +64,7 @@ def slot_of(block_tables: torch.Tensor, positions: torch.Tensor, block=BLOCK):
 
 
 def decode_workload(bs, Hq, Hk, ctx_lo, ctx_hi, n_blocks, seed, device="cpu", value_scale=1.0,
-                    n_table_sets=1):
+                    n_table_sets=1, head_dim=HEAD_DIM):
     """Paged decode inputs; context lengths include the token stored this step.
 
     Returns a dict with q [bs,Hq,D], new key/value [bs,Hk,D], k_cache/v_cache,
@@ -74,7 +74,7 @@ def decode_workload(bs, Hq, Hk, ctx_lo, ctx_hi, n_blocks, seed, device="cpu", va
     gen = torch.Generator().manual_seed(seed)
     ctx = torch.randint(ctx_lo, ctx_hi + 1, (bs,), generator=gen, dtype=torch.int64)
     tables = [assign_blocks(ctx.tolist(), n_blocks, gen) for _ in range(n_table_sets)]
-    D = HEAD_DIM
+    D = head_dim
     k_cache = _randn((n_blocks, BLOCK, Hk, D), seed * 7 + 1, device, scale=value_scale)
     v_cache = _randn((n_blocks, BLOCK, Hk, D), seed * 7 + 2, device, scale=value_scale)
     q = _randn((bs, Hq, D), seed * 7 + 3, "cpu", scale=value_scale)

@@ -47,8 +47,8 @@ def test_host_side_argument_checks_without_gpu():
     from importlib import import_module
     L = import_module("nanokv-llm_amd._lib")
     lib = L.lib()
-    # head_dim 64 is not supported by paged decode
-    rc = lib.nkv_paged_decode_split(None, 0, None, None, None, 0, None, 1, 8, 8, 64, 256, 1, 1,
+    # head_dim 96 is not one of paged decode's instances (64, 128, 256)
+    rc = lib.nkv_paged_decode_split(None, 0, None, None, None, 0, None, 1, 8, 8, 96, 256, 1, 1,
                                     1.0, None, 0, None)
     assert rc == -4 and b"head_dim" in lib.nkv_last_error()
     # top-k needs num_keep < n_cand
@@ -61,17 +61,18 @@ def test_host_side_argument_checks_without_gpu():
     # with Hq), batch*Hq partial rows of 528 bytes for the segment boundaries, and one row
     # per query-head column (at most 16) of each resident wave (8 per CU), capped by the
     # waves the table width can give work to
-    def expect(bs, hq, width, B=256):
+    def expect(bs, hq, width, B=256, D=128):
         chunks = width * B // 16
         slots = min(128, -(-chunks // 4) + 1)
         min_chunks = max(4, -(-chunks // (slots - 1)))
         useful = max(1, -(-bs * chunks // min_chunks))
         cols = min(256 * 8 * min(16, hq), useful * hq)
-        return bs * hq * 16 + (bs * hq + cols) * 528
+        return bs * hq * 16 + (bs * hq + cols) * (D + 4) * 4
 
     for bs, hq, width in ((64, 32, 32), (64, 32, 2), (1, 16, 2), (500, 64, 64), (7, 40, 9)):
-        assert lib.nkv_paged_decode_workspace_bytes(bs, hq, 128, width, 256) == \
-            expect(bs, hq, width)
+        for D in (64, 128, 256):
+            assert lib.nkv_paged_decode_workspace_bytes(bs, hq, D, width, 256) == \
+                expect(bs, hq, width, D=D)
     # Qwen3-32B geometry at batch 500 with 64-block tables: ~34 MB for any number of layers
     assert lib.nkv_paged_decode_workspace_bytes(500, 64, 128, 64, 256) < 36e6
 
