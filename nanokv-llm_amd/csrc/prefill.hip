@@ -10,13 +10,16 @@
 //    The tile's 128 "rows" are its queries for all g query heads of the KV
 //    head, query-major (row r = query r/g, head r%g; rows past the tile's
 //    queries x g are computed and dropped), so one K/V tile in LDS serves g
-//    heads (GQA sharing) for any g <= 128. Wave w owns two 16-row groups.
-//  * Keys advance in 64-key steps. Each step's K and V tiles (2 x 16 KiB) go
-//    from HBM straight into LDS with gfx950's 16-byte buffer-load-to-LDS
+//    heads (GQA sharing) for any g <= 16. Wave w owns two 16-row groups.
+//    head_dim D is 64, 128 or 256 (a template parameter); at 256 a wave owns
+//    one 16-row group (64-row tiles) and the 128 KiB ring leaves one
+//    workgroup per CU.
+//  * Keys advance in 64-key steps. Each step's K and V tiles (2 x 16 KiB at
+//    D = 128) go from HBM straight into LDS with gfx950's 16-byte buffer-load-to-LDS
 //    (no staging registers, no LDS write instructions) through a ring of
 //    kStages tiles, issued kStages-1 steps ahead; one barrier per step.
-//    LDS rows are dense (256 B) with the 16-byte chunks of row r XOR-permuted
-//    by 2*(r & 7), which keeps both the K row reads and the V transpose reads
+//    LDS rows are dense (2D bytes) with the 16-byte chunks of row r XOR-permuted
+//    by chunk_swz(r), which keeps both the K row reads and the V transpose reads
 //    free of bank conflicts; the permutation is applied on the global side
 //    (each lane fetches the chunk that belongs at its fixed LDS slot).
 //  * S^T = K Q^T  (v_mfma_f32_16x16x32_bf16: A = 16 keys from LDS, B = the
@@ -42,14 +45,23 @@
 
 namespace nkv {
 
-constexpr int kPD = 128;                  // head_dim
 constexpr int kStep = 64;                 // keys per step
 constexpr int kStages = 2;                // LDS ring depth (steps)
-constexpr int kTileB = kStep * kPD * 2;   // bytes of one K or V tile
-constexpr int kStageB = 2 * kTileB;       // K tile then V tile
 constexpr int kBufferFlags = 0x00020000;  // raw buffer descriptor word 3 for gfx950
-constexpr int kRowsPerWave = 32;          // two 16-row groups
-constexpr int kWGRows = 4 * kRowsPerWave;
+constexpr bool prefill_dim_ok(int D) { return D == 64 || D == 128 || D == 256; }
+// 16-row groups per wave: two (32 rows), one at head_dim 256 (its O^T and Q^T registers
+// would not fit two waves per SIMD otherwise)
+constexpr int prefill_row_groups(int D) { return D == 256 ? 1 : 2; }
+// rows (query, head pairs) of a workgroup's tile: 4 waves
+constexpr int prefill_tile_rows(int D) { return 64 * prefill_row_groups(D); }
+// XOR applied to the 16-byte chunk index of LDS row r (even: chunk pairs stay together).
+// Keeps the K row reads and the V transpose reads free of bank conflicts: 2*(r & 7) for
+// 256- and 512-byte rows, 2*((r >> 1) & 3) for 128-byte rows (two rows per bank line).
+template <int D>
+__device__ __forceinline__ int chunk_swz(int r) {
+  if constexpr (D == 64) return 2 * ((r >> 1) & 3);
+  else return 2 * (r & 7);
+}
 constexpr float kLazy = 8.f;              // log2 headroom before the running max is raised
 
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
@@ -84,16 +96,29 @@ __device__ __forceinline__ void load_to_lds(i32x4_t desc, uint32_t lds_addr, uin
                : "memory");
 }
 
-template <bool F8>
-__global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
+template <bool F8, int D>
+__global__ __launch_bounds__(256, D == 256 ? 1 : 2) void prefill_varlen_kernel(
     const bf16_t* __restrict__ q, int64_t q_row_stride, const void* __restrict__ k_cache,
     const void* __restrict__ v_cache, int64_t k_row_stride, int64_t v_row_stride,
     const int32_t* __restrict__ cu_seqlens_q, const int32_t* __restrict__ cu_seqlens_k,
     const int32_t* __restrict__ block_tables, int64_t bt_row_stride, int32_t Hk, int32_t G,
     int32_t block_size, int32_t max_blocks, int32_t n_limit, int32_t n_tiles, float scale_log2,
     float v_scale, bf16_t* __restrict__ out, int64_t out_row_stride) {
-  constexpr int kEl = F8 ? 1 : 2;  // bytes per cache element
-  const int QT = kWGRows / G;  // queries per tile
+  static_assert(prefill_dim_ok(D), "head_dim 64, 128 or 256");
+  constexpr int kEl = F8 ? 1 : 2;          // bytes per cache element
+  constexpr int kRB = D * 2;               // bytes of a staged (bf16) K or V row
+  constexpr int kNC = D / 8;               // 16-byte chunks per staged row
+  constexpr int kRG = prefill_row_groups(D);
+  constexpr int kTileB = kStep * kRB;      // bytes of one K or V tile
+  constexpr int kStageB = 2 * kTileB;      // K tile then V tile
+  constexpr int kKs = D / 32;              // k-steps of S^T
+  constexpr int kDb = D / 16;              // 16-dim blocks of O^T
+  constexpr int kRpl = 1024 / kRB;         // rows per 1 KiB load into LDS
+  constexpr int kNl = 16 / kRpl;           // such loads per wave per tile
+  constexpr int kLpr8 = D / 16;            // F8: lanes per row (16 codes each)
+  constexpr int kRpl8 = 64 / kLpr8;        // F8: rows per load
+  constexpr int kNl8 = 16 / kRpl8;         // F8: loads per wave per tile
+  const int QT = prefill_tile_rows(D) / G;  // queries per tile
   __shared__ __attribute__((aligned(1024))) char ring[kStages * kStageB];
 
   const int tid = threadIdx.x;
@@ -116,9 +141,10 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
   const int last_key = min(Lk - 1, diag + j0 + QT - 1);
   const int n_steps = last_key >= 0 ? last_key / kStep + 1 : 0;
 
-  // ---- K/V tile loads. Wave w fills rows 16w .. 16w+15 of a tile with four
-  // 1 KiB loads (4 rows each); lane i of load h lands at row 16w + 4h + i/16,
-  // slot i%16, and fetches the row's chunk (i%16) ^ 2*(row & 7). A wave's 16
+  // ---- K/V tile loads. Wave w fills rows 16w .. 16w+15 of a tile with 1 KiB
+  // loads (kRpl rows each: 4 at head_dim 128); lane i of load h lands at row
+  // 16w + kRpl*h + i/kNC, slot i%kNC, and fetches the row's chunk
+  // (i%kNC) ^ chunk_swz(row). A wave's 16
   // keys are consecutive rows (one cache block, B % 16 == 0, or the contiguous
   // K/V), so each wave's share of a step is one uniform base row and a byte
   // window covering only its valid keys: keys past Lk and keys of invalid
@@ -126,21 +152,24 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
   // (contiguous mode), and their offsets differ by r * (row_bv - row_b).
   const uint32_t row_b = (uint32_t)k_row_stride * kEl;
   const uint32_t row_bv = (uint32_t)v_row_stride * kEl;
-  const int lrow = lane >> 4;  // 0..3
-  const int slot = lane & 15;
-  uint32_t vol[4];
+  const int lrow = lane / kNC;
+  const int slot = lane % kNC;
+  uint32_t vol[kNl];
 #pragma unroll
-  for (int h = 0; h < 4; ++h) {
-    const int r = 4 * h + lrow;  // row within the wave's 16 (16w + r within the tile)
-    vol[h] = (uint32_t)r * row_b + (uint32_t)kvh * (kPD * 2) + (uint32_t)(slot ^ (2 * (r & 7))) * 16u;
+  for (int h = 0; h < kNl; ++h) {
+    const int r = kRpl * h + lrow;  // row within the wave's 16 (16w + r within the tile)
+    vol[h] = (uint32_t)r * row_b + (uint32_t)kvh * (D * 2) +
+             (uint32_t)(slot ^ chunk_swz<D>(r)) * 16u;
   }
   const uint32_t ring_base =
-      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)ring + (uint32_t)wave * 4096u;
-  // F8: load f of the wave's K (or V) codes brings rows 8f + lane/8, bytes 16*(lane%8) of the
-  // head's 128-byte piece, i.e. logical bf16 chunks 2c, 2c+1 (c = lane%8) of that LDS row
-  const int f8_row0 = lane >> 3;
-  const int f8_c = lane & 7;
-  u32x4_t kq[2], vq[2];  // F8: the next step's codes
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)ring +
+      (uint32_t)wave * (16u * kRB);
+  // F8: load f of the wave's K (or V) codes brings rows kRpl8*f + lane/kLpr8, bytes
+  // 16*(lane%kLpr8) of the head's D-byte piece, i.e. logical bf16 chunks 2c, 2c+1
+  // (c = lane%kLpr8) of that LDS row
+  const int f8_row0 = lane / kLpr8;
+  const int f8_c = lane % kLpr8;
+  u32x4_t kq[kNl8], vq[kNl8];  // F8: the next step's codes
 
   // Block ids: lane i holds entry bt_base + i of the sequence's table row, read
   // by the uniform v_readlane of the wave's block (reloaded every 64 blocks).
@@ -185,9 +214,9 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
       const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
           (void*)vp, (short)0, (uint32_t)nv * row_bv, kBufferFlags);
 #pragma unroll
-      for (int f = 0; f < 2; ++f) {
-        const uint32_t r = (uint32_t)(8 * f + f8_row0);
-        const uint32_t col = (uint32_t)kvh * kPD + (uint32_t)f8_c * 16u;
+      for (int f = 0; f < kNl8; ++f) {
+        const uint32_t r = (uint32_t)(kRpl8 * f + f8_row0);
+        const uint32_t col = (uint32_t)kvh * D + (uint32_t)f8_c * 16u;
         kq[f] = __builtin_bit_cast(
             u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rk, r * row_b + col, 0, 0));
         vq[f] = __builtin_bit_cast(
@@ -198,11 +227,11 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
       const i32x4_t dv = buffer_desc(vp, (uint32_t)nv * row_bv);
       const uint32_t at = ring_base + (uint32_t)stage * kStageB;
 #pragma unroll
-      for (int h = 0; h < 4; ++h) load_to_lds(dk, at + 1024u * h, vol[h]);
+      for (int h = 0; h < kNl; ++h) load_to_lds(dk, at + 1024u * h, vol[h]);
 #pragma unroll
-      for (int h = 0; h < 4; ++h)
+      for (int h = 0; h < kNl; ++h)
         load_to_lds(dv, at + kTileB + 1024u * h,
-                    vol[h] + (uint32_t)(4 * h + lrow) * (row_bv - row_b));
+                    vol[h] + (uint32_t)(kRpl * h + lrow) * (row_bv - row_b));
     }
     c_t0 += kStep;
     if (bt) {
@@ -221,17 +250,17 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
   };
   // F8: the codes of the last issue() (after their loads land) widened into LDS stage
   // `stage`, rows 16w .. 16w+15 of the K and V tiles, in the bf16 path's swizzled layout
-  // Lanes with c >= 4 write their pair's second chunk first (their codes' halves swapped
-  // before widening), so each 16-byte write instruction covers 8 distinct bank groups per
-  // row instead of pairing them up.
-  const bool f8_swap = f8_c >= 4;
+  // Lanes in the second half of a row write their pair's second chunk first (their codes'
+  // halves swapped before widening), so each 16-byte write instruction covers distinct
+  // bank groups of a row instead of pairing them up.
+  const bool f8_swap = f8_c >= kLpr8 / 2;
   auto commit = [&](int stage) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    char* at = ring + stage * kStageB + wave * 4096;
+    char* at = ring + stage * kStageB + wave * (16 * kRB);
 #pragma unroll
-    for (int f = 0; f < 2; ++f) {
-      const int r = 8 * f + f8_row0;  // row within the wave's 16 (16w + r within the tile)
-      const int off = r * 256 + ((2 * f8_c) ^ (2 * (r & 7))) * 16;  // chunks 2c, 2c+1: adjacent
+    for (int f = 0; f < kNl8; ++f) {
+      const int r = kRpl8 * f + f8_row0;  // row within the wave's 16 (16w + r within the tile)
+      const int off = r * kRB + ((2 * f8_c) ^ chunk_swz<D>(r)) * 16;  // chunks 2c, 2c+1: adjacent
       const int o1 = off + (f8_swap ? 16 : 0), o2 = off + (f8_swap ? 0 : 16);
       u32x4_t lo, hi;
       u32x4_t c = kq[f];
@@ -254,57 +283,62 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
     refill_window();
   }
 
-  // ---- this wave's two row groups: head and query of this lane's row (query-major;
+  // ---- this wave's row groups: head and query of this lane's row (query-major;
   // rows past QT*G take query Lq: attended like the others, never stored)
-  int head[2], jrow[2];
+  int head[kRG], jrow[kRG];
 #pragma unroll
-  for (int rr = 0; rr < 2; ++rr) {
-    const int r = (wave * 2 + rr) * 16 + col;
+  for (int rr = 0; rr < kRG; ++rr) {
+    const int r = (wave * kRG + rr) * 16 + col;
     const bool real = r < QT * G;
     head[rr] = real ? r % G : 0;
     jrow[rr] = real ? j0 + r / G : Lq;
   }
   // Q^T as the MFMA B operand: lane l -> row l%16, dims 8*(l/16) + 32*ks
-  u32x4_t qreg[2][4];
+  u32x4_t qreg[kRG][kKs];
 #pragma unroll
-  for (int rr = 0; rr < 2; ++rr) {
+  for (int rr = 0; rr < kRG; ++rr) {
     const int jc = jrow[rr] < Lq ? jrow[rr] : j0;  // rows past the sequence: discarded
     const u32x4_t* qp = reinterpret_cast<const u32x4_t*>(
-        q + (int64_t)(q0 + jc) * q_row_stride + (int64_t)(kvh * G + head[rr]) * kPD + g4 * 8);
+        q + (int64_t)(q0 + jc) * q_row_stride + (int64_t)(kvh * G + head[rr]) * D + g4 * 8);
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) qreg[rr][ks] = qp[ks * 4];
+    for (int ks = 0; ks < kKs; ++ks) qreg[rr][ks] = qp[ks * 4];
   }
 
   // LDS read offsets (bytes from a tile's start). K A operand, 16-key half hh,
   // dims 32ks + 8*g4: row 16hh + col, logical chunk g4 + 4ks.
-  uint32_t ko[4];
+  uint32_t ko[kKs];
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks)
-    ko[ks] = (uint32_t)col * 256u + (uint32_t)((g4 + 4 * ks) ^ (2 * (col & 7))) * 16u;
+  for (int ks = 0; ks < kKs; ++ks)
+    ko[ks] = (uint32_t)col * kRB + (uint32_t)((g4 + 4 * ks) ^ chunk_swz<D>(col)) * 16u;
   // V^T via ds_read_b64_tr_b16: lane 16g + 4r + c reads row 4g + r (and +16),
   // dims 16db + 4c .. +3 = logical chunk 2db + c/2, half c%2.
   const int vrow = 4 * g4 + (col >> 2);
   const int vc = col & 3;
-  uint32_t vo[8];
+  uint32_t vo[kDb];
 #pragma unroll
-  for (int db = 0; db < 8; ++db)
-    vo[db] = (uint32_t)vrow * 256u + (uint32_t)(db ^ (vrow & 7)) * 32u + (uint32_t)vc * 8u;
+  for (int db = 0; db < kDb; ++db)
+    vo[db] = (uint32_t)vrow * kRB + (uint32_t)(db ^ (chunk_swz<D>(vrow) >> 1)) * 32u +
+             (uint32_t)vc * 8u;
 
-  f32x4_t acc[2][8];  // O^T: lane l -> row l%16, dims 16*db + 4*(l/16) .. +3
+  f32x4_t acc[kRG][kDb];  // O^T: lane l -> row l%16, dims 16*db + 4*(l/16) .. +3
 #pragma unroll
-  for (int rr = 0; rr < 2; ++rr)
+  for (int rr = 0; rr < kRG; ++rr)
 #pragma unroll
-    for (int db = 0; db < 8; ++db) acc[rr][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  float m_run[2] = {-INFINITY, -INFINITY};
-  float l_run[2] = {0.f, 0.f};
+    for (int db = 0; db < kDb; ++db) acc[rr][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m_run[kRG], l_run[kRG];
+#pragma unroll
+  for (int rr = 0; rr < kRG; ++rr) {
+    m_run[rr] = -INFINITY;
+    l_run[rr] = 0.f;
+  }
 
   // Q is in registers before the loop: the empty asm uses pin the loads'
   // completion here, so no wait for them (which would also wait for the ring's
   // loads) lands inside the loop.
 #pragma unroll
-  for (int rr = 0; rr < 2; ++rr)
+  for (int rr = 0; rr < kRG; ++rr)
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) asm volatile("" ::"v"(qreg[rr][ks]));
+    for (int ks = 0; ks < kKs; ++ks) asm volatile("" ::"v"(qreg[rr][ks]));
   // first step's tile landed (each wave waits for its own loads; the barrier
   // publishes all of them)
   if constexpr (F8) {
@@ -321,19 +355,19 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
     const char* kt = lds + ST * kStageB;
     const char* vt = kt + kTileB;
 
-    // S^T for the four 16-key quarters and both row groups
-    f32x4_t st[2][4];
+    // S^T for the four 16-key quarters and the wave's row groups
+    f32x4_t st[kRG][4];
 #pragma unroll
     for (int h = 0; h < 4; ++h) {
-      u32x4_t ka[4];
+      u32x4_t ka[kKs];
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-        ka[ks] = *reinterpret_cast<const u32x4_t*>(kt + h * 4096 + ko[ks]);
+      for (int ks = 0; ks < kKs; ++ks)
+        ka[ks] = *reinterpret_cast<const u32x4_t*>(kt + h * (16 * kRB) + ko[ks]);
 #pragma unroll
-      for (int rr = 0; rr < 2; ++rr) {
+      for (int rr = 0; rr < kRG; ++rr) {
         f32x4_t a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
+        for (int ks = 0; ks < kKs; ++ks)
           a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8_v(ka[ks]), as_bf16x8_v(qreg[rr][ks]),
                                                        a, 0, 0, 0);
         st[rr][h] = a;
@@ -347,16 +381,16 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
     // MFMAs: chunk 1's exp work overlaps chunk 0's MFMAs. The row sum is taken
     // over the same bf16 weights that multiply V.
     const bool edge = (s * kStep + kStep - 1 > diag + j0) || (s * kStep + kStep > Lk);  // uniform
-    float sv[2][16];
+    float sv[kRG][16];
 #pragma unroll
-    for (int rr = 0; rr < 2; ++rr)
+    for (int rr = 0; rr < kRG; ++rr)
 #pragma unroll
       for (int h = 0; h < 4; ++h)
 #pragma unroll
         for (int r = 0; r < 4; ++r) sv[rr][4 * h + r] = st[rr][h][r];
     if (edge) {
 #pragma unroll
-      for (int rr = 0; rr < 2; ++rr) {
+      for (int rr = 0; rr < kRG; ++rr) {
         const int lim = min(diag + jrow[rr], Lk - 1);  // last visible key of this row
 #pragma unroll
         for (int h = 0; h < 4; ++h)
@@ -365,10 +399,11 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
             if (s * kStep + 16 * h + 4 * g4 + r > lim) sv[rr][4 * h + r] = -INFINITY;
       }
     }
-    float cm[2];
-    bool raise[2];
+    float cm[kRG];
+    bool raise[kRG];
+    bool any_raise = false;
 #pragma unroll
-    for (int rr = 0; rr < 2; ++rr) {
+    for (int rr = 0; rr < kRG; ++rr) {
       const float* v = sv[rr];
       const float cmax = fmax3(fmax3(fmax3(v[0], v[1], v[2]), fmax3(v[3], v[4], v[5]),
                                      fmax3(v[6], v[7], v[8])),
@@ -376,27 +411,28 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
                                fmax3(fmax3(v[12], v[13], v[14]), v[15], -INFINITY));
       cm[rr] = col_max4(cmax) * scale_log2;
       raise[rr] = cm[rr] > m_run[rr] + kLazy;  // false while the row has no visible key
+      any_raise = any_raise || raise[rr];
     }
-    if (__builtin_amdgcn_ballot_w64(raise[0] || raise[1]) != 0) {
+    if (__builtin_amdgcn_ballot_w64(any_raise) != 0) {
 #pragma unroll
-      for (int rr = 0; rr < 2; ++rr) {
+      for (int rr = 0; rr < kRG; ++rr) {
         const float alpha = raise[rr] ? fast_exp2(m_run[rr] - cm[rr]) : 1.f;  // exp2(-inf) = 0
         m_run[rr] = raise[rr] ? cm[rr] : m_run[rr];
         l_run[rr] *= alpha;
 #pragma unroll
-        for (int db = 0; db < 8; ++db) acc[rr][db] *= alpha;
+        for (int db = 0; db < kDb; ++db) acc[rr][db] *= alpha;
       }
     }
-    float mb[2];
+    float mb[kRG];
 #pragma unroll
-    for (int rr = 0; rr < 2; ++rr) mb[rr] = m_run[rr] == -INFINITY ? 0.f : m_run[rr];
+    for (int rr = 0; rr < kRG; ++rr) mb[rr] = m_run[rr] == -INFINITY ? 0.f : m_run[rr];
     // O^T[dims][rows] += V^T[dims][keys] P^T[keys][rows] per 32-key chunk c:
     // k-slot j of lane group g is key 32c+4g+j (j<4), or 32c+16+4g+(j-4)
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-      u32x4_t pb[2];
+      u32x4_t pb[kRG];
 #pragma unroll
-      for (int rr = 0; rr < 2; ++rr) {
+      for (int rr = 0; rr < kRG; ++rr) {
         float p[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e)
@@ -408,14 +444,15 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
         l_run[rr] = l;
       }
 #pragma unroll
-      for (int db = 0; db < 8; ++db) {
-        const char* vc = vt + c * 8192 + vo[db];
+      for (int db = 0; db < kDb; ++db) {
+        const char* vc = vt + c * (32 * kRB) + vo[db];
         const i16x4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)vc);
-        const i16x4_t v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(vc + 4096));
+        const i16x4_t v1 =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(vc + 16 * kRB));
         const u32x4_t va = {__builtin_bit_cast(uint2, v0).x, __builtin_bit_cast(uint2, v0).y,
                             __builtin_bit_cast(uint2, v1).x, __builtin_bit_cast(uint2, v1).y};
 #pragma unroll
-        for (int rr = 0; rr < 2; ++rr)
+        for (int rr = 0; rr < kRG; ++rr)
           acc[rr][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
               as_bf16x8_v(va), as_bf16x8_v(pb[rr]), acc[rr][db], 0, 0, 0);
       }
@@ -440,14 +477,14 @@ __global__ __launch_bounds__(256, 2) void prefill_varlen_kernel(
 
   // ---- epilogue: normalise and store this lane's 4 dims of each 16-dim block
 #pragma unroll
-  for (int rr = 0; rr < 2; ++rr) {
+  for (int rr = 0; rr < kRG; ++rr) {
     const float l = col_sum4(l_run[rr]);
     if (jrow[rr] >= Lq) continue;
     const float inv = l > 0.f ? (F8 ? v_scale : 1.f) / l : 0.f;
     bf16_t* op = out + (int64_t)(q0 + jrow[rr]) * out_row_stride +
-                 (int64_t)(kvh * G + head[rr]) * kPD + g4 * 4;
+                 (int64_t)(kvh * G + head[rr]) * D + g4 * 4;
 #pragma unroll
-    for (int db = 0; db < 8; ++db) {
+    for (int db = 0; db < kDb; ++db) {
       const uint2 w = {pack_bf16x2(acc[rr][db][0] * inv, acc[rr][db][1] * inv),
                        pack_bf16x2(acc[rr][db][2] * inv, acc[rr][db][3] * inv)};
       *reinterpret_cast<uint2*>(op + db * 16) = w;
@@ -472,7 +509,8 @@ static int prefill_launch(const void* q, int64_t q_row_stride, const void* k_cac
   NKV_REQUIRE(n_seqs >= 0 && max_seqlen_q >= 0 && n_q_heads > 0 && n_kv_heads > 0, NKV_EINVAL,
               "%s: bad sizes", what);
   if (n_seqs == 0 || max_seqlen_q == 0) return NKV_OK;
-  NKV_REQUIRE(head_dim == kPD, NKV_EUNSUPPORTED, "%s: head_dim must be 128", what);
+  NKV_REQUIRE(prefill_dim_ok(head_dim), NKV_EUNSUPPORTED,
+              "%s: head_dim must be 64, 128 or 256 (got %d)", what, head_dim);
   NKV_REQUIRE(n_q_heads % n_kv_heads == 0, NKV_EINVAL, "%s: Hq %% Hk != 0", what);
   const int g = n_q_heads / n_kv_heads;
   NKV_REQUIRE(g <= 16, NKV_EUNSUPPORTED, "%s: GQA group %d above 16", what, g);
@@ -480,10 +518,12 @@ static int prefill_launch(const void* q, int64_t q_row_stride, const void* k_cac
               "%s: null pointer", what);
   NKV_REQUIRE(aligned16(q) && aligned16(k_cache) && aligned16(v_cache) && aligned16(out),
               NKV_EINVAL, "%s: q/k/v/out must be 16-byte aligned", what);
-  NKV_REQUIRE(q_row_stride >= (int64_t)n_q_heads * kPD && q_row_stride % 8 == 0 &&
-                  out_row_stride >= (int64_t)n_q_heads * kPD && out_row_stride % 8 == 0 &&
-                  k_row_stride >= (int64_t)n_kv_heads * kPD && k_row_stride % (16 / kEl) == 0 &&
-                  v_row_stride >= (int64_t)n_kv_heads * kPD && v_row_stride % (16 / kEl) == 0,
+  NKV_REQUIRE(q_row_stride >= (int64_t)n_q_heads * head_dim && q_row_stride % 8 == 0 &&
+                  out_row_stride >= (int64_t)n_q_heads * head_dim && out_row_stride % 8 == 0 &&
+                  k_row_stride >= (int64_t)n_kv_heads * head_dim &&
+                  k_row_stride % (16 / kEl) == 0 &&
+                  v_row_stride >= (int64_t)n_kv_heads * head_dim &&
+                  v_row_stride % (16 / kEl) == 0,
               NKV_EINVAL, "%s: row strides must cover the heads, in 16-byte multiples", what);
   NKV_REQUIRE(n_rows > 0, NKV_EINVAL, "%s: empty K/V", what);
   NKV_REQUIRE(k_row_stride * kEl * kStep < (1ll << 31) && v_row_stride * kEl * kStep < (1ll << 31),
@@ -504,16 +544,21 @@ static int prefill_launch(const void* q, int64_t q_row_stride, const void* k_cac
   // paged: valid block ids are [0, n_rows / block_size); contiguous: valid rows
   const int32_t n_limit = (int32_t)std::min<int64_t>(block_tables ? n_rows / block_size : n_rows,
                                                      INT32_MAX);
-  const int qt = kWGRows / g;
+  const int qt = prefill_tile_rows(head_dim) / g;
   const int n_tiles = (max_seqlen_q + qt - 1) / qt;
   const int64_t grid = (int64_t)n_seqs * n_tiles * n_kv_heads;
   NKV_REQUIRE(grid < (1ll << 31), NKV_EUNSUPPORTED, "%s: grid too large", what);
   const float sl2 = scale * k_scale * kLog2e;
-  hipLaunchKernelGGL(prefill_varlen_kernel<F8>, dim3((unsigned)grid), dim3(256), 0,
-                     as_stream(stream), (const bf16_t*)q, q_row_stride, k_cache, v_cache,
-                     k_row_stride, v_row_stride, cu_seqlens_q, cu_seqlens_k, block_tables,
-                     bt_row_stride, n_kv_heads, g, block_size, max_blocks, n_limit, n_tiles, sl2,
-                     v_scale, (bf16_t*)out, out_row_stride);
+#define NKV_PREFILL_LAUNCH(D)                                                                  \
+  hipLaunchKernelGGL((prefill_varlen_kernel<F8, D>), dim3((unsigned)grid), dim3(256), 0,         \
+                     as_stream(stream), (const bf16_t*)q, q_row_stride, k_cache, v_cache,        \
+                     k_row_stride, v_row_stride, cu_seqlens_q, cu_seqlens_k, block_tables,       \
+                     bt_row_stride, n_kv_heads, g, block_size, max_blocks, n_limit, n_tiles, sl2, \
+                     v_scale, (bf16_t*)out, out_row_stride)
+  if (head_dim == 64) NKV_PREFILL_LAUNCH(64);
+  else if (head_dim == 128) NKV_PREFILL_LAUNCH(128);
+  else NKV_PREFILL_LAUNCH(256);
+#undef NKV_PREFILL_LAUNCH
   return check_launch(F8 ? "nkv_prefill_varlen_fp8" : "nkv_prefill_varlen");
 }
 }  // namespace nkv

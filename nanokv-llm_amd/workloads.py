@@ -126,7 +126,7 @@ def compress_qwen3_8b(seed=3, device="cpu", selected_only=True):
 
 
 def prefill_workload(n_seqs, Hq, Hk, len_lo, len_hi, seed, device="cpu", prefix_lo=None,
-                     prefix_hi=None, chunk=None):
+                     prefix_hi=None, chunk=None, head_dim=HEAD_DIM):
     """Varlen prefill over the paged cache.
 
     One-shot: Lq = Lk = L ~ U[len_lo, len_hi]. Chunked (chunk given): prefix
@@ -148,7 +148,7 @@ def prefill_workload(n_seqs, Hq, Hk, len_lo, len_hi, seed, device="cpu", prefix_
     cu_q = torch.tensor([0] + list(torch.tensor(Lq).cumsum(0).tolist()), dtype=torch.int32)
     cu_k = torch.tensor([0] + list(torch.tensor(Lk).cumsum(0).tolist()), dtype=torch.int32)
     N = int(cu_q[-1])
-    D = HEAD_DIM
+    D = head_dim
     positions = torch.cat([torch.arange(k - q, k) for q, k in zip(Lq, Lk)])
     seq_of = torch.cat([torch.full((q,), i, dtype=torch.int64) for i, q in enumerate(Lq)])
     blk = table.to(torch.int64)[seq_of, positions // BLOCK]

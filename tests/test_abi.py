@@ -113,7 +113,7 @@ def _cstep(**kw):
 
 
 CASES = [
-    (_prefill(d=64), EUNSUPPORTED, b"head_dim"),
+    (_prefill(d=96), EUNSUPPORTED, b"head_dim"),
     (_prefill(hq=17, hk=1), EUNSUPPORTED, b"GQA group"),
     (_prefill(q=P + 2), EINVAL, b"aligned"),
     (_prefill(qrs=1000), EINVAL, b"row strides"),

@@ -1,14 +1,15 @@
 """head_dim 64 and 256 on the GPU vs the fp32 oracle (128, the Qwen3 head size, is what every
 other GPU test runs). Decode: bf16 and fp8 caches, every KV-heads-per-wave instance the plan
-picks (the batch and table width below decide it), edge context lengths; max abs error
-<= 2e-2 on bf16 outputs, as for head_dim 128."""
+picks (the batch and table width below decide it), edge context lengths. Prefill: paged
+one-shot and chunked, contiguous K/V with V a view of a fused qkv row, an fp8 pool, edge
+lengths. Max abs error <= 2e-2 on bf16 outputs, as for head_dim 128."""
 import importlib
 
 import pytest
 import torch
 
 from oracle import fp8_ref
-from oracle.attention_ref import paged_decode_ref
+from oracle.attention_ref import paged_decode_ref, store_kvcache_ref, varlen_prefill_ref
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-2
@@ -86,3 +87,93 @@ def test_decode_head_dim_edge_lengths(nkv, dev, D):
     assert torch.all(out[0] == 0)  # empty context -> zeros
     # ctx = 1 -> exactly the first value row (softmax weight 1)
     assert torch.equal(out[1, :4].cpu(), vc[int(bt[1, 0]), 0, 0].expand(4, D))
+
+
+@pytest.mark.parametrize("D", [64, 256])
+@pytest.mark.parametrize("Hq,Hk", [(32, 8), (64, 4), (40, 8), (16, 16), (48, 4)])
+def test_prefill_paged_head_dim(nkv, dev, D, Hq, Hk):
+    wl = wl_mod.prefill_workload(3, Hq, Hk, 1, 500, seed=D + Hq, head_dim=D)
+    kc, vc = wl["k_cache"].clone(), wl["v_cache"].clone()
+    store_kvcache_ref(wl["key"], wl["value"], kc, vc, wl["slot_mapping"])
+    out = nkv.varlen_prefill(wl["q"].to(dev), kc.to(dev), vc.to(dev), wl["cu_seqlens_q"].to(dev),
+                             wl["cu_seqlens_k"].to(dev), wl["max_seqlen_q"], wl["scale"],
+                             block_tables=wl["block_tables"].to(dev))
+    torch.cuda.synchronize()
+    ref = varlen_prefill_ref(wl["q"].float(), kc, vc, wl["cu_seqlens_q"], wl["cu_seqlens_k"],
+                             wl["scale"], block_tables=wl["block_tables"])
+    assert _err(out, ref) <= TOL
+
+
+@pytest.mark.parametrize("D", [64, 256])
+def test_prefill_chunked_head_dim(nkv, dev, D):
+    """Chunks of 200 queries after random prefixes (bottom-right causal alignment), then the
+    same over an fp8 copy of the pool."""
+    wl = wl_mod.prefill_workload(3, 32, 8, 0, 0, seed=D, prefix_lo=0, prefix_hi=900, chunk=200,
+                                 head_dim=D)
+    kc, vc = wl["k_cache"].clone(), wl["v_cache"].clone()
+    store_kvcache_ref(wl["key"], wl["value"], kc, vc, wl["slot_mapping"])
+    args = (wl["cu_seqlens_q"].to(dev), wl["cu_seqlens_k"].to(dev), wl["max_seqlen_q"],
+            wl["scale"])
+    bt = wl["block_tables"]
+    out = nkv.varlen_prefill(wl["q"].to(dev), kc.to(dev), vc.to(dev), *args,
+                             block_tables=bt.to(dev))
+    torch.cuda.synchronize()
+    ref = varlen_prefill_ref(wl["q"].float(), kc, vc, wl["cu_seqlens_q"], wl["cu_seqlens_k"],
+                             wl["scale"], block_tables=bt)
+    assert _err(out, ref) <= TOL
+    kq, vq = fp8_ref.fp8_quantize_ref(kc, 0.5), fp8_ref.fp8_quantize_ref(vc, 2.0)
+    out8 = nkv.varlen_prefill(wl["q"].to(dev), kq.to(dev).view(torch.float8_e4m3fn),
+                              vq.to(dev).view(torch.float8_e4m3fn), *args,
+                              block_tables=bt.to(dev), max_seqlen_k=wl["max_seqlen_k"],
+                              k_scale=0.5, v_scale=2.0)
+    torch.cuda.synchronize()
+    kf = kq.view(torch.float8_e4m3fn).float() * 0.5
+    vf = vq.view(torch.float8_e4m3fn).float() * 2.0
+    ref8 = varlen_prefill_ref(wl["q"].float(), kf, vf, wl["cu_seqlens_q"], wl["cu_seqlens_k"],
+                              wl["scale"], block_tables=bt)
+    assert _err(out8, ref8) <= TOL
+
+
+@pytest.mark.parametrize("D", [64, 256])
+def test_prefill_contiguous_head_dim(nkv, dev, D):
+    """No block table: K roped into its own rows, V a view of a fused qkv row (its own
+    stride), q a view of the same rows."""
+    g = torch.Generator().manual_seed(D + 5)
+    Hq, Hk = 16, 4
+    Lq = [1, 37, 300, 65]
+    cu = torch.tensor([0] + torch.tensor(Lq).cumsum(0).tolist(), dtype=torch.int32)
+    N = int(cu[-1])
+    qkv = torch.randn(N, (Hq + 2 * Hk) * D, generator=g).to(torch.bfloat16)
+    q = qkv[:, :Hq * D].view(N, Hq, D)
+    k = qkv[:, Hq * D:(Hq + Hk) * D].contiguous().view(N, Hk, D)
+    v = qkv[:, (Hq + Hk) * D:].view(N, Hk, D)
+    qg = qkv.to(dev)
+    qd = qg[:, :Hq * D].view(N, Hq, D)
+    vd = qg[:, (Hq + Hk) * D:].view(N, Hk, D)
+    out = nkv.varlen_prefill(qd, k.to(dev), vd, cu.to(dev), cu.to(dev), max(Lq), D ** -0.5)
+    torch.cuda.synchronize()
+    ref = varlen_prefill_ref(q.float(), k, v.contiguous(), cu, cu, D ** -0.5)
+    assert _err(out, ref) <= TOL
+
+
+@pytest.mark.parametrize("D", [64, 256])
+def test_prefill_edge_lengths_head_dim(nkv, dev, D):
+    """Empty, single-token and tile-boundary sequences; Lk < Lq rows are zero."""
+    g = torch.Generator().manual_seed(D + 14)
+    Hq, Hk = 32, 8
+    Lq = [0, 1, 31, 32, 33, 127, 128, 129, 5, 40]
+    Lk = [0, 1, 31, 32, 33, 127, 128, 129, 300, 17]  # last: 23 queries see nothing
+    cu_q = torch.tensor([0] + torch.tensor(Lq).cumsum(0).tolist(), dtype=torch.int32)
+    cu_k = torch.tensor([0] + torch.tensor(Lk).cumsum(0).tolist(), dtype=torch.int32)
+    q = torch.randn(int(cu_q[-1]), Hq, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(int(cu_k[-1]), Hk, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(int(cu_k[-1]), Hk, D, generator=g).to(torch.bfloat16)
+    out = nkv.varlen_prefill(q.to(dev), k.to(dev), v.to(dev), cu_q.to(dev), cu_k.to(dev),
+                             max(Lq), D ** -0.5)
+    torch.cuda.synchronize()
+    ref = varlen_prefill_ref(q.float(), k, v, cu_q, cu_k, D ** -0.5)
+    assert _err(out, ref) <= TOL
+    o = out.cpu()
+    last = int(cu_q[-2])
+    assert torch.all(o[last:last + 23] == 0)
+    assert torch.equal(o[0], v[0].repeat_interleave(Hq // Hk, dim=0))
