@@ -29,7 +29,9 @@
 
 namespace nkv {
 
-constexpr int kCD = 128;      // head_dim
+constexpr int kCD = 128;      // head_dim of the fused kernels
+// head_dim of the general path (score and compaction kernels): 64, 128 or 256
+constexpr bool compress_dim_ok(int D) { return D == 64 || D == 128 || D == 256; }
 constexpr int kChunk = 256;   // keys per scoring workgroup
 constexpr int kMaxWindowBlocks = 64;
 constexpr int kMaxRows = 1024;  // rows per read-then-write round of a compaction unit
@@ -41,14 +43,20 @@ constexpr int kMaxRows = 1024;  // rows per read-then-write round of a compactio
 // tokens per head is G = heads x w rows, consecutive per head (q row stride = the
 // row of one sequence).
 // F8: K is fp8 (OCP E4M3FN) codes, widened to bf16 (exact) on load; the K scale is
-// folded into scale_log2 by the caller.
-template <bool F8>
+// folded into scale_log2 by the caller. D: head_dim (64, 128 or 256).
+template <bool F8, int D>
 __global__ __launch_bounds__(256) void compress_score_kernel(
     const bf16_t* __restrict__ q, int64_t q_row_stride, const void* __restrict__ k,
     const int32_t* __restrict__ block_tables, int64_t bt_row_stride, int32_t max_blocks,
     const int32_t* __restrict__ base_context_lens, const int32_t* __restrict__ seq_idx,
     int32_t Hk, int32_t G, int32_t block_size, int32_t window_blocks, int64_t n_blocks,
     float scale_log2, int32_t n_cand, float* __restrict__ scores) {
+  static_assert(compress_dim_ok(D), "head_dim 64, 128 or 256");
+  constexpr int kEl = F8 ? 1 : 2;
+  constexpr int kLpr = D * kEl / 16;  // lanes per K row (16-byte loads)
+  constexpr int kRpl = 64 / kLpr;     // K rows per load
+  constexpr int kNld = 16 / kRpl;     // loads per 16-key group
+  constexpr int kKs = D / 32;         // k-steps of the product
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int Lw = window_blocks * block_size;
@@ -72,12 +80,12 @@ __global__ __launch_bounds__(256) void compress_score_kernel(
     if (full >= window_blocks && full <= max_blocks)
       pb = block_tables[(int64_t)seq * bt_row_stride + wblk];
     valid = pb >= 0 && pb < n_blocks;
-    base = ((pb * block_size + t0 % block_size) * Hk + kvh) * (int64_t)kCD;
-    tok_stride = (int64_t)Hk * kCD;
+    base = ((pb * block_size + t0 % block_size) * Hk + kvh) * (int64_t)D;
+    tok_stride = (int64_t)Hk * D;
     qrow = seq;
   } else {  // contiguous K [m, Hk, Lw, D]
-    base = (((int64_t)j * Hk + kvh) * Lw + t0) * kCD;
-    tok_stride = kCD;
+    base = (((int64_t)j * Hk + kvh) * Lw + t0) * D;
+    tok_stride = D;
     qrow = j;
   }
   float* srow = scores + ((int64_t)j * Hq + (int64_t)kvh * G) * Lw + t0;
@@ -86,53 +94,52 @@ __global__ __launch_bounds__(256) void compress_score_kernel(
       srow[(int64_t)(i / kChunk) * Lw + i % kChunk] = -INFINITY;
     return;
   }
-  // K rows are read whole (bf16: one 256-byte head row per 16 lanes, 4 rows per load;
-  // fp8: one 128-byte row per 8 lanes, 8 rows per load), staged row-major in LDS as bf16
+  // K rows are read whole (one head row per kLpr lanes: at head_dim 128, 256 bytes per
+  // 16 lanes for bf16, 128 bytes per 8 lanes for fp8), staged row-major in LDS as bf16
   // and re-read in the MFMA operand layout (lane l: key l%16, dims 8*(l/16) + 32ks).
-  __shared__ __attribute__((aligned(16))) bf16_t stage_all[4][16 * (kCD + 8)];
+  constexpr int kSR = D + 8;
+  __shared__ __attribute__((aligned(16))) bf16_t stage_all[4][16 * kSR];
   bf16_t* stage = stage_all[wave];
-  constexpr int kSR = kCD + 8;
-  u32x4_t kraw[4][F8 ? 2 : 4];
+  u32x4_t kraw[4][kNld];
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
 #pragma unroll
-    for (int r = 0; r < (F8 ? 2 : 4); ++r) {
+    for (int r = 0; r < kNld; ++r) {
+      const int key = wave * 64 + g * 16 + kRpl * r + lane / kLpr;
       if constexpr (F8) {
-        const int key = wave * 64 + g * 16 + 8 * r + (lane >> 3);
         kraw[g][r] = *reinterpret_cast<const u32x4_t*>(static_cast<const uint8_t*>(k) + base +
-                                                      key * tok_stride + (lane & 7) * 16);
+                                                      key * tok_stride + (lane % kLpr) * 16);
       } else {
-        const int key = wave * 64 + g * 16 + 4 * r + (lane >> 4);
         kraw[g][r] = *reinterpret_cast<const u32x4_t*>(static_cast<const bf16_t*>(k) + base +
-                                                      key * tok_stride + (lane & 15) * 8);
+                                                      key * tok_stride + (lane % kLpr) * 8);
       }
     }
   }
   __builtin_amdgcn_sched_barrier(0);  // all loads issued before the first MFMA
-  uint4 qreg[4];
+  uint4 qreg[kKs];
   auto load_q = [&](int h0) {  // query rows h0 .. h0+15 of the KV head as the MFMA A operand
     const int hr = h0 + (lane & 15);
     const int hc = hr < G ? hr : 0;  // MFMA rows >= G are computed and discarded
-    const bf16_t* qp = q + qrow * q_row_stride + (int64_t)(kvh * G + hc) * kCD + (lane >> 4) * 8;
+    const bf16_t* qp = q + qrow * q_row_stride + (int64_t)(kvh * G + hc) * D + (lane >> 4) * 8;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) qreg[ks] = *reinterpret_cast<const uint4*>(qp + ks * 32);
+    for (int ks = 0; ks < kKs; ++ks) qreg[ks] = *reinterpret_cast<const uint4*>(qp + ks * 32);
   };
   load_q(0);
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
     if constexpr (F8) {
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
+      for (int r = 0; r < kNld; ++r) {
         u32x4_t lo, hi;
         fp8x16_to_bf16(kraw[g][r], lo, hi);
-        bf16_t* d = &stage[(8 * r + (lane >> 3)) * kSR + (lane & 7) * 16];
+        bf16_t* d = &stage[(kRpl * r + lane / kLpr) * kSR + (lane % kLpr) * 16];
         *reinterpret_cast<u32x4_t*>(d) = lo;
         *reinterpret_cast<u32x4_t*>(d + 8) = hi;
       }
     } else {
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        *reinterpret_cast<u32x4_t*>(&stage[(4 * r + (lane >> 4)) * kSR + (lane & 15) * 8]) =
+      for (int r = 0; r < kNld; ++r)
+        *reinterpret_cast<u32x4_t*>(&stage[(kRpl * r + lane / kLpr) * kSR + (lane % kLpr) * 8]) =
             kraw[g][r];
     }
     const int tw = wave * 64 + g * 16 + (lane & 15);
@@ -143,7 +150,7 @@ __global__ __launch_bounds__(256) void compress_score_kernel(
       }
       f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
+      for (int ks = 0; ks < kKs; ++ks) {
         const uint4 kb = *reinterpret_cast<const uint4*>(
             &stage[(lane & 15) * kSR + (lane >> 4) * 8 + ks * 32]);
         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(qreg[ks]), as_bf16x8(kb), acc,
@@ -879,24 +886,25 @@ __global__ __launch_bounds__(kSelThreads) void compress_sum_kernel(
 }
 
 // ----------------------------------------------------------------- compact
-// Unit = (selected j, KV head, K|V, half row). Rows i < keep_tokens move from
-// window position keep_idx[i] to window position i; rows keep_tokens + u
-// (u < tail) move from the tail block offset u to window position keep + u
-// (unit_row). Rows go in rounds of ROUNDS * rows-per-round, each round's reads
-// before its writes. F8: 1-byte (fp8) cache rows: half a head row is 64 bytes,
-// moved by 4 lanes, so a round covers 64 rows instead of 32.
+// Unit = (selected j, KV head, K|V, 64-dim part of the head row: two at head_dim 128).
+// Rows i < keep_tokens move from window position keep_idx[i] to window position i; rows
+// keep_tokens + u (u < tail) move from the tail block offset u to window position
+// keep + u (unit_row). Rows go in rounds of ROUNDS * rows-per-round, each round's reads
+// before its writes. F8: 1-byte (fp8) cache rows: a 64-dim part is 64 bytes, moved by 4
+// lanes, so a round covers 64 rows instead of 32.
 template <int ROUNDS, bool F8>
 __global__ __launch_bounds__(256) void compress_compact_kernel(
     void* __restrict__ k_cache, void* __restrict__ v_cache,
     const int32_t* __restrict__ block_tables, int64_t bt_row_stride, int32_t max_blocks,
     const int32_t* __restrict__ base_context_lens, int32_t* __restrict__ context_lens,
     const int32_t* __restrict__ seq_idx, const int32_t* __restrict__ keep_idx, int32_t n_sets,
-    int32_t keep_tokens, int32_t Hk, int32_t block_size, int32_t window_blocks,
-    int64_t n_blocks) {
-  const int half = blockIdx.x & 1;
-  const int is_v = (blockIdx.x >> 1) & 1;
-  const int kvh = (blockIdx.x >> 2) % Hk;
-  const int j = (blockIdx.x >> 2) / Hk;
+    int32_t keep_tokens, int32_t Hk, int32_t head_dim, int32_t block_size,
+    int32_t window_blocks, int64_t n_blocks) {
+  const int parts = head_dim / 64;  // 64-dim parts per head row
+  const int half = blockIdx.x % parts;
+  const int is_v = (blockIdx.x / parts) & 1;
+  const int kvh = (blockIdx.x / (2 * parts)) % Hk;
+  const int j = (blockIdx.x / (2 * parts)) / Hk;
   const int seq = seq_idx[j];
   const int len = seq >= 0 ? base_context_lens[seq] : 0;  // seq -1: padding entry
   const int B = block_size;
@@ -912,13 +920,14 @@ __global__ __launch_bounds__(256) void compress_compact_kernel(
   const int Lw = window_blocks * B;
   const int nrows = keep_tokens + len % B;
   constexpr int kEl = F8 ? 1 : 2;
-  constexpr int kLanesPerRow = 4 * kEl;             // 16-byte lanes per half head row
+  constexpr int kLanesPerRow = 4 * kEl;             // 16-byte lanes per 64-dim part
   constexpr int kRowsPerRound = 256 / kLanesPerRow;  // 32 (bf16) or 64 (fp8)
   constexpr int kBatch = ROUNDS * kRowsPerRound;    // rows per read-then-write round
   static_assert(kBatch <= kMaxRows, "compaction table too small");
   char* cache = static_cast<char*>(is_v ? v_cache : k_cache);
-  const int64_t row = (int64_t)Hk * kCD * kEl;  // bytes
-  const int64_t col = ((int64_t)kvh * kCD + half * 64) * kEl + (threadIdx.x % kLanesPerRow) * 16;
+  const int64_t row = (int64_t)Hk * head_dim * kEl;  // bytes
+  const int64_t col =
+      ((int64_t)kvh * head_dim + half * 64) * kEl + (threadIdx.x % kLanesPerRow) * 16;
   const int rsub = threadIdx.x / kLanesPerRow;  // row within a round
   for (int base = 0; base < nrows; base += kBatch) {  // uniform
     // source and destination slot of every row of the round (-1 = row not moved)
@@ -949,7 +958,7 @@ __global__ __launch_bounds__(256) void compress_compact_kernel(
     if (base + kBatch < nrows) __syncthreads();  // the tables are rebuilt
   }
 
-  if (blockIdx.x % (4 * Hk) == 0 && threadIdx.x == 0)
+  if (blockIdx.x % (2 * parts * Hk) == 0 && threadIdx.x == 0)
     context_lens[seq] = len - Lw + keep_tokens;
 }
 
@@ -1157,6 +1166,27 @@ __global__ __launch_bounds__(kSchedThreads) void compress_schedule_kernel(
 // ============================================================= C ABI
 using namespace nkv;
 
+namespace nkv {
+// The score kernel's head_dim instance (64, 128 or 256; checked by the caller).
+template <bool F8>
+static void launch_score(int32_t head_dim, unsigned grid, hipStream_t s, const bf16_t* q,
+                         int64_t q_row_stride, const void* k, const int32_t* block_tables,
+                         int64_t bt_row_stride, int32_t max_blocks,
+                         const int32_t* base_context_lens, const int32_t* seq_idx, int32_t Hk,
+                         int32_t G, int32_t block_size, int32_t window_blocks, int64_t n_blocks,
+                         float scale_log2, int32_t n_cand, float* scores) {
+#define NKV_SCORE_LAUNCH(D)                                                                    \
+  hipLaunchKernelGGL((compress_score_kernel<F8, D>), dim3(grid), dim3(256), 0, s, q,             \
+                     q_row_stride, k, block_tables, bt_row_stride, max_blocks,                   \
+                     base_context_lens, seq_idx, Hk, G, block_size, window_blocks, n_blocks,     \
+                     scale_log2, n_cand, scores)
+  if (head_dim == 64) NKV_SCORE_LAUNCH(64);
+  else if (head_dim == 128) NKV_SCORE_LAUNCH(128);
+  else NKV_SCORE_LAUNCH(256);
+#undef NKV_SCORE_LAUNCH
+}
+}  // namespace nkv
+
 extern "C" size_t nkv_compress_workspace_bytes(int32_t m, int32_t n_q_heads,
                                                int32_t window_blocks, int32_t block_size) {
   if (m <= 0 || n_q_heads <= 0 || window_blocks <= 0 || block_size <= 0) return 0;
@@ -1176,7 +1206,8 @@ extern "C" int nkv_compress_score(const void* q, int64_t q_row_stride, const voi
   NKV_REQUIRE(m >= 0 && n_q_heads > 0 && n_kv_heads > 0 && window_blocks > 0 && block_size > 0,
               NKV_EINVAL, "compress_score: bad sizes");
   if (m == 0) return NKV_OK;
-  NKV_REQUIRE(head_dim == kCD, NKV_EUNSUPPORTED, "compress_score: head_dim must be 128");
+  NKV_REQUIRE(compress_dim_ok(head_dim), NKV_EUNSUPPORTED,
+              "compress_score: head_dim must be 64, 128 or 256 (got %d)", head_dim);
   NKV_REQUIRE(n_q_heads % n_kv_heads == 0, NKV_EINVAL, "compress_score: Hq %% Hk != 0");
   const int g = n_q_heads / n_kv_heads;
   NKV_REQUIRE(g <= 16, NKV_EUNSUPPORTED, "compress_score: GQA group %d above 16", g);
@@ -1200,10 +1231,9 @@ extern "C" int nkv_compress_score(const void* q, int64_t q_row_stride, const voi
   hipStream_t s = as_stream(stream);
   const unsigned grid = (unsigned)(m * n_kv_heads * (Lw / kChunk));
   const float sl2 = scale * kLog2e;
-  hipLaunchKernelGGL((compress_score_kernel<false>), dim3(grid), dim3(256), 0, s,
-                     (const bf16_t*)q, q_row_stride, k_cache, block_tables, bt_row_stride,
-                     max_blocks_per_seq, base_context_lens, seq_idx, n_kv_heads, g, block_size,
-                     window_blocks, n_blocks, sl2, Lw - 1, scores);
+  launch_score<false>(head_dim, grid, s, (const bf16_t*)q, q_row_stride, k_cache, block_tables,
+                      bt_row_stride, max_blocks_per_seq, base_context_lens, seq_idx, n_kv_heads,
+                      g, block_size, window_blocks, n_blocks, sl2, Lw - 1, scores);
   int rc = check_launch("nkv_compress_score");
   if (rc) return rc;
   const int n_sets = agg_mode == NKV_AGG_ALL ? 1 : n_kv_heads;
@@ -1350,7 +1380,8 @@ extern "C" int nkv_compress_compact(void* k_cache, void* v_cache, const int32_t*
   NKV_REQUIRE(m >= 0 && n_kv_heads > 0 && block_size > 0 && window_blocks > 0, NKV_EINVAL,
               "compress_compact: bad sizes");
   if (m == 0) return NKV_OK;
-  NKV_REQUIRE(head_dim == kCD, NKV_EUNSUPPORTED, "compress_compact: head_dim must be 128");
+  NKV_REQUIRE(compress_dim_ok(head_dim), NKV_EUNSUPPORTED,
+              "compress_compact: head_dim must be 64, 128 or 256 (got %d)", head_dim);
   NKV_REQUIRE(n_sets == 1 || n_sets == n_kv_heads, NKV_EINVAL,
               "compress_compact: n_sets must be 1 or n_kv_heads");
   NKV_REQUIRE(keep_tokens > 0 && keep_tokens <= window_blocks * block_size, NKV_EINVAL,
@@ -1368,13 +1399,13 @@ extern "C" int nkv_compress_compact(void* k_cache, void* v_cache, const int32_t*
   NKV_REQUIRE(n_blocks * block_size < (1ll << 31), NKV_EUNSUPPORTED,
               "compress_compact: pool of %lld slots exceeds 2^31", (long long)(n_blocks * block_size));
   hipStream_t s = as_stream(stream);
-  const unsigned grid = (unsigned)(m * n_kv_heads * 4);
+  const unsigned grid = (unsigned)(m * n_kv_heads * 2 * (head_dim / 64));
 #define NKV_COMPACT_LAUNCH(R)                                                                  \
   hipLaunchKernelGGL((compress_compact_kernel<R, false>), dim3(grid), dim3(256), 0, s, k_cache, \
                      v_cache, block_tables, bt_row_stride, max_blocks_per_seq,                  \
                      base_context_lens,                                                         \
                      context_lens, seq_idx, keep_idx, n_sets, keep_tokens, n_kv_heads,          \
-                     block_size, window_blocks, n_blocks)
+                     head_dim, block_size, window_blocks, n_blocks)
   if (max_rows <= 256) NKV_COMPACT_LAUNCH(8);
   else if (max_rows <= 512) NKV_COMPACT_LAUNCH(16);
   else if (max_rows <= 768) NKV_COMPACT_LAUNCH(24);
@@ -1502,7 +1533,8 @@ extern "C" int nkv_compress_step_fp8(const void* q, int64_t q_row_stride, void* 
                   block_size > 0 && k_scale > 0.f,
               NKV_EINVAL, "compress_step_fp8: bad sizes");
   if (m == 0) return NKV_OK;
-  NKV_REQUIRE(head_dim == kCD, NKV_EUNSUPPORTED, "compress_step_fp8: head_dim must be 128");
+  NKV_REQUIRE(compress_dim_ok(head_dim), NKV_EUNSUPPORTED,
+              "compress_step_fp8: head_dim must be 64, 128 or 256 (got %d)", head_dim);
   NKV_REQUIRE(n_q_heads % n_kv_heads == 0, NKV_EINVAL, "compress_step_fp8: Hq %% Hk != 0");
   const int g = n_q_heads / n_kv_heads;
   NKV_REQUIRE(g <= 16, NKV_EUNSUPPORTED, "compress_step_fp8: GQA group %d above 16", g);
@@ -1541,10 +1573,9 @@ extern "C" int nkv_compress_step_fp8(const void* q, int64_t q_row_stride, void* 
   float* scores = (float*)workspace;
   const unsigned sgrid = (unsigned)(m * n_kv_heads * (Lw / kChunk));
   const float sl2 = scale * k_scale * kLog2e;
-  hipLaunchKernelGGL((compress_score_kernel<true>), dim3(sgrid), dim3(256), 0, s,
-                     (const bf16_t*)q, q_row_stride, k_cache, block_tables, bt_row_stride,
-                     max_blocks_per_seq, base_context_lens, seq_idx, n_kv_heads, g, block_size,
-                     window_blocks, n_blocks, sl2, Lw - 1, scores);
+  launch_score<true>(head_dim, sgrid, s, (const bf16_t*)q, q_row_stride, k_cache, block_tables,
+                     bt_row_stride, max_blocks_per_seq, base_context_lens, seq_idx, n_kv_heads,
+                     g, block_size, window_blocks, n_blocks, sl2, Lw - 1, scores);
   rc = check_launch("nkv_compress_step_fp8 (score)");
   if (rc) return rc;
   const int n_sets = agg_mode == NKV_AGG_ALL ? 1 : n_kv_heads;
@@ -1556,12 +1587,12 @@ extern "C" int nkv_compress_step_fp8(const void* q, int64_t q_row_stride, void* 
   if (rc) return rc;
   rc = nkv_compress_topk(importance_out, m * n_sets, Lw - 1, num_keep, keep_idx, stream);
   if (rc) return rc;
-  const unsigned cgrid = (unsigned)(m * n_kv_heads * 4);
+  const unsigned cgrid = (unsigned)(m * n_kv_heads * 2 * (head_dim / 64));
 #define NKV_COMPACT8_LAUNCH(R)                                                                 \
   hipLaunchKernelGGL((compress_compact_kernel<R, true>), dim3(cgrid), dim3(256), 0, s, k_cache, \
                      v_cache, block_tables, bt_row_stride, max_blocks_per_seq,                  \
                      base_context_lens, context_lens, seq_idx, keep_idx, n_sets, keep_tokens,   \
-                     n_kv_heads, block_size, window_blocks, n_blocks)
+                     n_kv_heads, head_dim, block_size, window_blocks, n_blocks)
   if (max_rows <= 256) NKV_COMPACT8_LAUNCH(4);
   else if (max_rows <= 512) NKV_COMPACT8_LAUNCH(8);
   else if (max_rows <= 768) NKV_COMPACT8_LAUNCH(12);
@@ -1591,7 +1622,8 @@ extern "C" int nkv_snapkv_select(const void* q, const void* k, int32_t m, int32_
   NKV_REQUIRE(m >= 0 && n_q_heads > 0 && n_kv_heads > 0 && seq_len > 0 && window > 0,
               NKV_EINVAL, "snapkv_select: bad sizes");
   if (m == 0) return NKV_OK;
-  NKV_REQUIRE(head_dim == kCD, NKV_EUNSUPPORTED, "snapkv_select: head_dim must be 128");
+  NKV_REQUIRE(compress_dim_ok(head_dim), NKV_EUNSUPPORTED,
+              "snapkv_select: head_dim must be 64, 128 or 256 (got %d)", head_dim);
   NKV_REQUIRE(n_q_heads % n_kv_heads == 0, NKV_EINVAL, "snapkv_select: Hq %% Hk != 0");
   NKV_REQUIRE(agg_mode == NKV_AGG_ALL || agg_mode == NKV_AGG_GROUP, NKV_EINVAL,
               "snapkv_select: bad agg_mode %d", agg_mode);
@@ -1606,7 +1638,8 @@ extern "C" int nkv_snapkv_select(const void* q, const void* k, int32_t m, int32_
   NKV_REQUIRE(workspace && workspace_bytes >= need, NKV_EWORKSPACE,
               "snapkv_select: workspace needs %zu bytes (got %zu)", need, workspace_bytes);
   if (window == 1)  // the periodic step's own shape: fused when it fits
-    return nkv_compress_select(q, (int64_t)n_q_heads * kCD, k, nullptr, 0, 0, nullptr, nullptr,
+    return nkv_compress_select(q, (int64_t)n_q_heads * head_dim, k, nullptr, 0, 0, nullptr,
+                               nullptr,
                                m, n_q_heads, n_kv_heads, head_dim, seq_len, 1, 0, scale,
                                agg_mode, num_keep, importance_out, keep_idx, workspace,
                                workspace_bytes, stream);
@@ -1619,10 +1652,9 @@ extern "C" int nkv_snapkv_select(const void* q, const void* k, int32_t m, int32_
   float* scores = (float*)workspace;
   hipStream_t s = as_stream(stream);
   const unsigned grid = (unsigned)(m * n_kv_heads * (seq_len / kChunk));
-  hipLaunchKernelGGL((compress_score_kernel<false>), dim3(grid), dim3(256), 0, s,
-                     (const bf16_t*)q, (int64_t)n_q_heads * window * kCD, k, nullptr, 0, 0,
-                     nullptr, nullptr, n_kv_heads, rows, seq_len, 1, 0, scale * kLog2e, n_cand,
-                     scores);
+  launch_score<false>(head_dim, grid, s, (const bf16_t*)q, (int64_t)n_q_heads * window * head_dim,
+                      k, nullptr, 0, 0, nullptr, nullptr, n_kv_heads, rows, seq_len, 1, 0,
+                      scale * kLog2e, n_cand, scores);
   int rc = check_launch("nkv_snapkv_select (score)");
   if (rc) return rc;
   const int n_sets = agg_mode == NKV_AGG_ALL ? 1 : n_kv_heads;

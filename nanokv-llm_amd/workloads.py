@@ -97,7 +97,7 @@ def decode_qwen3_8b(seed=2, device="cpu", bs=64, n_blocks=4096, n_table_sets=1):
 
 
 def compress_workload(bs, Hq, Hk, ctx_lo, ctx_hi, topk, seed, device="cpu", n_blocks=None,
-                      selected_only=False):
+                      selected_only=False, head_dim=HEAD_DIM):
     """Decode state for a compression step; selection = the topk longest sequences.
 
     With selected_only, only the selected sequences get blocks (the others
@@ -112,7 +112,7 @@ def compress_workload(bs, Hq, Hk, ctx_lo, ctx_hi, topk, seed, device="cpu", n_bl
     need = sum(math.ceil(c / BLOCK) for c in lens_for_tables)
     n_blocks = n_blocks or need + 8
     table = assign_blocks(lens_for_tables, n_blocks, gen)
-    D = HEAD_DIM
+    D = head_dim
     k_cache = _randn((n_blocks, BLOCK, Hk, D), seed * 7 + 1, device)
     v_cache = _randn((n_blocks, BLOCK, Hk, D), seed * 7 + 2, device)
     q = _randn((bs, Hq, D), seed * 7 + 3, "cpu")

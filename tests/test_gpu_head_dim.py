@@ -2,7 +2,10 @@
 other GPU test runs). Decode: bf16 and fp8 caches, every KV-heads-per-wave instance the plan
 picks (the batch and table width below decide it), edge context lengths. Prefill: paged
 one-shot and chunked, contiguous K/V with V a view of a fused qkv row, an fp8 pool, edge
-lengths. Max abs error <= 2e-2 on bf16 outputs, as for head_dim 128."""
+lengths. Max abs error <= 2e-2 on bf16 outputs, as for head_dim 128. Compression (the general
+path: score, importance, top-k and compaction kernels): importance within rtol 1e-4 of the
+oracle's fp32 SnapKV, kept sets exact given those scores, compaction bit-exact, on bf16 and
+fp8 pools and through the SnapKV plug-in call."""
 import importlib
 
 import pytest
@@ -10,10 +13,14 @@ import torch
 
 from oracle import fp8_ref
 from oracle.attention_ref import paged_decode_ref, store_kvcache_ref, varlen_prefill_ref
+from oracle.compress_ref import (compress_compact_ref, gather_kv_by_slots_ref,
+                                 get_tail_window_and_tail_slots_ref, select_topk_ref,
+                                 snapkv_importance_ref)
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-2
 wl_mod = importlib.import_module("nanokv-llm_amd.workloads")
+cu = importlib.import_module("nanokv-llm_amd.layers.compress_utils")
 
 
 def _err(out, ref):
@@ -177,3 +184,72 @@ def test_prefill_edge_lengths_head_dim(nkv, dev, D):
     last = int(cu_q[-2])
     assert torch.all(o[last:last + 23] == 0)
     assert torch.equal(o[0], v[0].repeat_interleave(Hq // Hk, dim=0))
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+@pytest.mark.parametrize("agg", ["all", "group"])
+@pytest.mark.parametrize("D", [64, 256])
+def test_compress_step_head_dim(nkv, dev, D, agg, fp8):
+    """A compression step (window of 4 blocks, keep 2*256+1) with a -1 padding entry in
+    seq_idx, on a bf16 or an fp8 pool."""
+    W, KEEP, ks, vs = 4, 2 * 256 + 1, 0.5, 2.0
+    wl = wl_mod.compress_workload(24, 32, 8, 1500, 4096, 5, 4 + D, selected_only=True,
+                                  head_dim=D)
+    if fp8:
+        kq = fp8_ref.fp8_quantize_ref(wl["k_cache"], ks)
+        vq = fp8_ref.fp8_quantize_ref(wl["v_cache"], vs)
+        kg = kq.to(dev).view(torch.float8_e4m3fn)
+        vg = vq.to(dev).view(torch.float8_e4m3fn)
+        kf = kq.view(torch.float8_e4m3fn).float() * ks
+    else:
+        kg, vg = wl["k_cache"].to(dev), wl["v_cache"].to(dev)
+        kf = wl["k_cache"]
+    sel = wl["seq_idx"]
+    seq_idx = torch.tensor(sel[:2] + [-1] + sel[2:], dtype=torch.int32, device=dev)
+    base = wl["context_lens"].to(dev)
+    ctx = base.clone()
+    keep, imp = cu.compress_step(wl["q"].to(dev), kg, vg, wl["block_tables"].to(dev), base, ctx,
+                                 seq_idx, W, KEEP, D ** -0.5, agg,
+                                 **({"k_scale": ks} if fp8 else {}))
+    torch.cuda.synchronize()
+    real = [i for i in range(seq_idx.numel()) if i != 2]
+    imp, keep = imp.cpu()[real], keep.cpu()[real]
+    st = torch.tensor(sel)
+    slots, *_ = get_tail_window_and_tail_slots_ref(wl["block_tables"], wl["context_lens"], st,
+                                                   256, W)
+    k_sub, _ = gather_kv_by_slots_ref(kf, kf, slots)
+    ref_imp = snapkv_importance_ref(wl["q"].index_select(0, st).unsqueeze(2), k_sub, 1, "fp32",
+                                    agg)
+    assert torch.allclose(imp, ref_imp, rtol=1e-4, atol=1e-7)
+    assert torch.equal(keep[..., 1:-1].long(), select_topk_ref(imp, KEEP - 2))
+    if fp8:
+        kc, vc = kq.clone(), vq.clone()
+    else:
+        kc, vc = wl["k_cache"].clone(), wl["v_cache"].clone()
+    ctx_ref = wl["context_lens"].clone()
+    ok, _, _ = compress_compact_ref(None, kc, vc, wl["block_tables"], wl["context_lens"], ctx_ref,
+                                    sel, 256, W, 2, 1, 0, 1, keep_idx=keep.long())
+    assert ok
+    got_k = kg.view(torch.uint8).cpu() if fp8 else kg.cpu()
+    got_v = vg.view(torch.uint8).cpu() if fp8 else vg.cpu()
+    assert torch.equal(got_k, kc) and torch.equal(got_v, vc)
+    assert torch.equal(ctx.cpu(), ctx_ref)
+
+
+@pytest.mark.parametrize("window", [1, 5])
+@pytest.mark.parametrize("D", [64, 256])
+def test_snapkv_head_dim(nkv, dev, D, window):
+    """SnapKV(Q, K, V, num_keep, window) on contiguous [m, H, L, D] tensors."""
+    g = torch.Generator().manual_seed(D + window)
+    L, agg = 1024, "group"
+    Q = torch.randn(2, 16, window, D, generator=g).to(torch.bfloat16)
+    K = torch.randn(2, 4, L, D, generator=g).to(torch.bfloat16)
+    num_keep = L // 2 - 1
+    out, imp = nkv.SnapKV(Q.to(dev), K.to(dev), None, num_keep=num_keep, window=window, agg=agg,
+                          return_importance=True)
+    torch.cuda.synchronize()
+    out = out.cpu().view(2, 4, num_keep + 1 + window)
+    ref_imp = snapkv_importance_ref(Q, K, window, "fp32", agg)
+    assert torch.allclose(imp.cpu(), ref_imp, rtol=1e-4, atol=1e-7)
+    assert torch.equal(out[..., 1:num_keep + 1], select_topk_ref(imp.cpu(), num_keep))
+    assert torch.equal(out[..., num_keep + 1:], torch.arange(L - window, L).expand(2, 4, window))
