@@ -13,20 +13,21 @@
 // MI355X design: one pass over the qkv projection output instead of the
 // reference's five (norm q, norm k, rope q, rope k, store k and v). q, k, v
 // are row-strided views (normally the three parts of one qkv row). HBM-bound:
-// per token it reads the (Hq + 2 Hk) head rows, one 512-byte cos|sin
-// row and writes q, the K and V cache rows and optionally a contiguous K.
-// An 8-lane group owns one (token, head) unit; lane i holds elements
-// [8i, 8i+8) and [64+8i, 64+8i+8) of the 128-wide head, so both halves of a
-// rotary pair sit in the same lane (no exchange), the RMS reduction is a
-// 3-step butterfly and every access is 16 bytes. Consecutive units are
-// consecutive head rows, so a wave reads 2 KiB contiguous.
+// per token it reads the (Hq + 2 Hk) head rows, one cos|sin row (512 bytes at
+// head_dim 128) and writes q, the K and V cache rows and optionally a contiguous K.
+// A group of D/16 lanes owns one (token, head) unit; lane i holds elements
+// [8i, 8i+8) and [D/2+8i, D/2+8i+8) of the head (D = head_dim: 64, 128 or 256),
+// so both halves of a rotary pair sit in the same lane (no exchange), the RMS
+// reduction is a log2(D/16)-step butterfly and every access is 16 bytes.
+// Consecutive units are consecutive head rows, so a wave reads 2 KiB contiguous.
 #include "nkv_common.h"
 
 namespace nkv {
 
-constexpr int kRD = 128;  // head_dim
 constexpr int kRopeThreads = 256;
-constexpr int kRopeUnitsPerBlock = kRopeThreads / 8;  // one unit per 8-lane group
+constexpr bool rope_dim_ok(int D) { return D == 64 || D == 128 || D == 256; }
+// units per block: one per group of D/16 lanes
+constexpr int rope_units_per_block(int D) { return kRopeThreads / (D / 16); }
 
 __device__ __forceinline__ float bf(uint32_t b16) { return __uint_as_float(b16 << 16); }
 __device__ __forceinline__ float round_bf(float f) { return bf(f32_to_bf16_bits(f)); }
@@ -57,38 +58,42 @@ struct RopeArgs {
   int32_t Hk;
 };
 
-// Units per token: Hq q heads, Hk k heads, then (when storing) Hk v heads. An
-// 8-lane group owns one unit; lane i holds elements [8i, 8i+8) and
-// [64+8i, 64+8i+8) of the head (16-byte accesses). The head row, the position
+// Units per token: Hq q heads, Hk k heads, then (when storing) Hk v heads. A
+// group of D/16 lanes owns one unit; lane i holds elements [8i, 8i+8) and
+// [D/2+8i, D/2+8i+8) of the head (16-byte accesses). The head row, the position
 // and the slot are loaded together; the cos|sin row (which needs the position)
 // is the only dependent load. One unit per group measured fastest at every size
 // (more units per group serialise their dependent loads).
+template <int D>
 __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_store_kernel(const RopeArgs a) {
   // Every product is rounded on its own, as the reference's separate torch ops are:
   // no a*b - c*d -> fma contraction.
 #pragma clang fp contract(off)
-  const uint32_t u = blockIdx.x * kRopeUnitsPerBlock + (threadIdx.x >> 3);
+  static_assert(rope_dim_ok(D), "head_dim 64, 128 or 256");
+  constexpr int kL = D / 16;   // lanes per unit
+  constexpr int kH = D / 2;    // offset of the rotary partners
+  const uint32_t u = blockIdx.x * rope_units_per_block(D) + threadIdx.x / kL;
   if (u >= a.n_units) return;
-  const int l8 = threadIdx.x & 7;
+  const int l8 = threadIdx.x % kL;
   const uint32_t t = u / a.units_per_token;
   const int h = (int)(u - t * a.units_per_token);
   const bool is_q = h < a.Hq;
   const bool is_k = !is_q && h < a.Hq + a.Hk;
   const int kvh = is_q ? 0 : (is_k ? h - a.Hq : h - a.Hq - a.Hk);
-  const bf16_t* src = is_q ? a.q_in + (int64_t)t * a.q_row_stride + (int64_t)h * kRD
-                      : is_k ? a.k_in + (int64_t)t * a.k_row_stride + (int64_t)kvh * kRD
-                             : a.v_in + (int64_t)t * a.v_row_stride + (int64_t)kvh * kRD;
+  const bf16_t* src = is_q ? a.q_in + (int64_t)t * a.q_row_stride + (int64_t)h * D
+                      : is_k ? a.k_in + (int64_t)t * a.k_row_stride + (int64_t)kvh * D
+                             : a.v_in + (int64_t)t * a.v_row_stride + (int64_t)kvh * D;
   u32x4_t vlo = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(src + 8 * l8));
-  u32x4_t vhi = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(src + 64 + 8 * l8));
+  u32x4_t vhi = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(src + kH + 8 * l8));
   const int64_t sl = (!is_q && a.k_cache) ? (int64_t)a.slot_mapping[t] : -1;
   if (is_q || is_k) {  // uniform over the unit's 8 lanes
     int64_t pos = a.positions[t];
     pos = pos < 0 ? 0 : (pos >= a.max_position ? a.max_position - 1 : pos);
-    const float* cs = a.cos_sin + pos * kRD + 8 * l8;
+    const float* cs = a.cos_sin + pos * D + 8 * l8;
     const f32x4_t c0 = *reinterpret_cast<const f32x4_t*>(cs);
     const f32x4_t c1 = *reinterpret_cast<const f32x4_t*>(cs + 4);
-    const f32x4_t s0 = *reinterpret_cast<const f32x4_t*>(cs + 64);
-    const f32x4_t s1 = *reinterpret_cast<const f32x4_t*>(cs + 68);
+    const f32x4_t s0 = *reinterpret_cast<const f32x4_t*>(cs + kH);
+    const f32x4_t s1 = *reinterpret_cast<const f32x4_t*>(cs + kH + 4);
     float x[16];  // x[0..7] first half, x[8..15] the rotary partners
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -100,14 +105,13 @@ __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_store_kernel(const 
     if (a.q_weight) {
       const bf16_t* w = is_q ? a.q_weight : a.k_weight;
       const u32x4_t wlo = *reinterpret_cast<const u32x4_t*>(w + 8 * l8);
-      const u32x4_t whi = *reinterpret_cast<const u32x4_t*>(w + 64 + 8 * l8);
+      const u32x4_t whi = *reinterpret_cast<const u32x4_t*>(w + kH + 8 * l8);
       float ss = 0.f;
 #pragma unroll
       for (int e = 0; e < 16; ++e) ss += x[e] * x[e];
-      ss += __shfl_xor(ss, 1, 64);
-      ss += __shfl_xor(ss, 2, 64);
-      ss += __shfl_xor(ss, 4, 64);
-      const float r = rsqrtf(ss * (1.0f / kRD) + a.eps);
+#pragma unroll
+      for (int o = 1; o < kL; o <<= 1) ss += __shfl_xor(ss, o, 64);
+      const float r = rsqrtf(ss * (1.0f / D) + a.eps);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         x[2 * e] = round_bf(round_bf(x[2 * e] * r) * bf(wlo[e] & 0xffffu));
@@ -132,20 +136,20 @@ __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_store_kernel(const 
     }
   }
   if (is_q) {
-    bf16_t* dst = a.q_out + (int64_t)t * a.q_out_row_stride + (int64_t)h * kRD;
+    bf16_t* dst = a.q_out + (int64_t)t * a.q_out_row_stride + (int64_t)h * D;
     *reinterpret_cast<u32x4_t*>(dst + 8 * l8) = vlo;
-    *reinterpret_cast<u32x4_t*>(dst + 64 + 8 * l8) = vhi;
+    *reinterpret_cast<u32x4_t*>(dst + kH + 8 * l8) = vhi;
     return;
   }
   if (sl >= 0 && sl < a.n_slots) {  // -1 (padding) or out of range: skipped
-    bf16_t* dst = (is_k ? a.k_cache : a.v_cache) + (sl * a.Hk + kvh) * (int64_t)kRD;
+    bf16_t* dst = (is_k ? a.k_cache : a.v_cache) + (sl * a.Hk + kvh) * (int64_t)D;
     *reinterpret_cast<u32x4_t*>(dst + 8 * l8) = vlo;
-    *reinterpret_cast<u32x4_t*>(dst + 64 + 8 * l8) = vhi;
+    *reinterpret_cast<u32x4_t*>(dst + kH + 8 * l8) = vhi;
   }
   if (is_k && a.k_out) {
-    bf16_t* dst = a.k_out + ((int64_t)t * a.Hk + kvh) * kRD;
+    bf16_t* dst = a.k_out + ((int64_t)t * a.Hk + kvh) * D;
     *reinterpret_cast<u32x4_t*>(dst + 8 * l8) = vlo;
-    *reinterpret_cast<u32x4_t*>(dst + 64 + 8 * l8) = vhi;
+    *reinterpret_cast<u32x4_t*>(dst + kH + 8 * l8) = vhi;
   }
 }
 
@@ -165,7 +169,8 @@ extern "C" int nkv_qk_norm_rope_store(const void* q, int64_t q_row_stride, const
   NKV_REQUIRE(n_tokens >= 0 && n_q_heads > 0 && n_kv_heads > 0 && n_slots >= 0, NKV_EINVAL,
               "qk_norm_rope_store: bad sizes");
   if (n_tokens == 0) return NKV_OK;
-  NKV_REQUIRE(head_dim == kRD, NKV_EUNSUPPORTED, "qk_norm_rope_store: head_dim must be 128");
+  NKV_REQUIRE(rope_dim_ok(head_dim), NKV_EUNSUPPORTED,
+              "qk_norm_rope_store: head_dim must be 64, 128 or 256 (got %d)", head_dim);
   NKV_REQUIRE(q && k && positions && cos_sin_cache && q_out && max_position > 0, NKV_EINVAL,
               "qk_norm_rope_store: null pointer or empty rotary cache");
   NKV_REQUIRE(!q_norm_weight == !k_norm_weight, NKV_EINVAL,
@@ -175,7 +180,7 @@ extern "C" int nkv_qk_norm_rope_store(const void* q, int64_t q_row_stride, const
   NKV_REQUIRE(k_cache || k_out, NKV_EINVAL,
               "qk_norm_rope_store: nowhere to put K (no cache and no k_out)");
   const int64_t per_tok = (int64_t)n_q_heads + n_kv_heads + (k_cache ? n_kv_heads : 0);
-  const int64_t qw = (int64_t)n_q_heads * kRD, kw = (int64_t)n_kv_heads * kRD;
+  const int64_t qw = (int64_t)n_q_heads * head_dim, kw = (int64_t)n_kv_heads * head_dim;
   NKV_REQUIRE(q_row_stride >= qw && q_out_row_stride >= qw && k_row_stride >= kw &&
                   (!k_cache || v_row_stride >= kw) &&
                   ((q_row_stride | q_out_row_stride | k_row_stride | v_row_stride) % 8) == 0,
@@ -187,7 +192,8 @@ extern "C" int nkv_qk_norm_rope_store(const void* q, int64_t q_row_stride, const
                   aligned16(v_cache) && aligned16(q_norm_weight) && aligned16(k_norm_weight),
               NKV_EINVAL, "qk_norm_rope_store: pointers must be 16-byte aligned");
   const uint32_t n_units = (uint32_t)(n_tokens * per_tok);
-  const unsigned grid = (unsigned)((n_units + kRopeUnitsPerBlock - 1) / kRopeUnitsPerBlock);
+  const uint32_t upb = (uint32_t)rope_units_per_block(head_dim);
+  const unsigned grid = (unsigned)((n_units + upb - 1) / upb);
   RopeArgs a;
   a.q_in = (const bf16_t*)q;
   a.q_row_stride = q_row_stride;
@@ -212,7 +218,14 @@ extern "C" int nkv_qk_norm_rope_store(const void* q, int64_t q_row_stride, const
   a.units_per_token = (uint32_t)per_tok;
   a.Hq = n_q_heads;
   a.Hk = n_kv_heads;
-  hipLaunchKernelGGL(qk_norm_rope_store_kernel, dim3(grid), dim3(kRopeThreads), 0,
-                     as_stream(stream), a);
+  if (head_dim == 64)
+    hipLaunchKernelGGL(qk_norm_rope_store_kernel<64>, dim3(grid), dim3(kRopeThreads), 0,
+                       as_stream(stream), a);
+  else if (head_dim == 128)
+    hipLaunchKernelGGL(qk_norm_rope_store_kernel<128>, dim3(grid), dim3(kRopeThreads), 0,
+                       as_stream(stream), a);
+  else
+    hipLaunchKernelGGL(qk_norm_rope_store_kernel<256>, dim3(grid), dim3(kRopeThreads), 0,
+                       as_stream(stream), a);
   return check_launch("nkv_qk_norm_rope_store");
 }

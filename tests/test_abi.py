@@ -135,7 +135,7 @@ CASES = [
     (("nkv_build_step_metadata", [P, 4, 256, 1, 4, 0, None, 0, 0, 3, P, P, P, P, P, P, P, P,
                                   4, 4, None]), EINVAL, b""),
     (("nkv_qk_norm_rope_store", [P, 4096, P, 1024, P, 1024, P, P, P, 1e-6, P, 4096, P, 4096,
-                                 None, P, P, P, 100, 8, 32, 8, 64, None]),
+                                 None, P, P, P, 100, 8, 32, 8, 96, None]),
      EUNSUPPORTED, b"head_dim"),
     (("nkv_qk_norm_rope_store", [P, 4096, P, 1024, P, 1024, P, P, None, 1e-6, P, 4096, P,
                                  4096, None, P, P, P, 100, 8, 32, 8, 128, None]), EINVAL, b""),

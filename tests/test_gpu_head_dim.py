@@ -5,7 +5,9 @@ one-shot and chunked, contiguous K/V with V a view of a fused qkv row, an fp8 po
 lengths. Max abs error <= 2e-2 on bf16 outputs, as for head_dim 128. Compression (the general
 path: score, importance, top-k and compaction kernels): importance within rtol 1e-4 of the
 oracle's fp32 SnapKV, kept sets exact given those scores, compaction bit-exact, on bf16 and
-fp8 pools and through the SnapKV plug-in call."""
+fp8 pools and through the SnapKV plug-in call. Fused q/k RMSNorm + RoPE + K/V store: to
+the bar of the head_dim 128 tests (bit-exact without the norm; with it at most 0.1% of
+elements one or two bf16 ulps of the row maximum away)."""
 import importlib
 
 import pytest
@@ -13,6 +15,7 @@ import torch
 
 from oracle import fp8_ref
 from oracle.attention_ref import paged_decode_ref, store_kvcache_ref, varlen_prefill_ref
+from oracle.rope_ref import qk_norm_rope_store_ref, rotary_cos_sin_cache_ref
 from oracle.compress_ref import (compress_compact_ref, gather_kv_by_slots_ref,
                                  get_tail_window_and_tail_slots_ref, select_topk_ref,
                                  snapkv_importance_ref)
@@ -253,3 +256,84 @@ def test_snapkv_head_dim(nkv, dev, D, window):
     assert torch.allclose(imp.cpu(), ref_imp, rtol=1e-4, atol=1e-7)
     assert torch.equal(out[..., 1:num_keep + 1], select_topk_ref(imp.cpu(), num_keep))
     assert torch.equal(out[..., num_keep + 1:], torch.arange(L - window, L).expand(2, 4, window))
+
+
+def _rope_close(out, ref):
+    out, ref = out.float().cpu(), ref.float()
+    rowmax = ref.abs().amax(dim=-1, keepdim=True)
+    diff = (out - ref).abs()
+    assert torch.all(diff <= rowmax * 2.0 ** -6), f"max diff {diff.max().item()}"
+    assert (diff > 0).float().mean().item() <= 1e-3
+
+
+@pytest.mark.parametrize("D", [64, 256])
+@pytest.mark.parametrize("Hq,Hk", [(32, 8), (8, 1)])
+def test_norm_rope_store_head_dim(nkv, dev, D, Hq, Hk):
+    g = torch.Generator().manual_seed(D + Hq)
+    N, nb, B, max_pos = 300, 8, 256, 40960
+    qkv = (torch.randn(N, (Hq + 2 * Hk) * D, generator=g) * 3.0).to(torch.bfloat16)
+    qw = (1 + 0.3 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    kw = (1 + 0.3 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    pos = torch.randint(0, max_pos, (N,), generator=g)
+    cache = rotary_cos_sin_cache_ref(D, max_pos, 1e6)
+    kc = torch.randn(nb, B, Hk, D, generator=g).to(torch.bfloat16)
+    vc = torch.randn(nb, B, Hk, D, generator=g).to(torch.bfloat16)
+    slots = torch.randperm(nb * B, generator=g)[:N].to(torch.int32)
+    slots[5] = -1
+    kg, vg = kc.to(dev), vc.to(dev)
+    qkvg = qkv.to(dev)
+    q = qkvg[:, :Hq * D].view(N, Hq, D)
+    k = qkvg[:, Hq * D:(Hq + Hk) * D].view(N, Hk, D)
+    v = qkvg[:, (Hq + Hk) * D:].view(N, Hk, D)
+    qo, ko, _ = nkv.qk_norm_rope_store(pos.to(dev), q, k, v, cache.to(dev), qw.to(dev),
+                                       kw.to(dev), 1e-6, k_cache=kg, v_cache=vg,
+                                       slot_mapping=slots.to(dev))
+    torch.cuda.synchronize()
+    qr, kr, _ = qk_norm_rope_store_ref(qkv, pos, qw, kw, 1e-6, cache, Hq, Hk, head_dim=D,
+                                       k_cache=kc, v_cache=vc, slot_mapping=slots)
+    _rope_close(qo, qr)
+    _rope_close(ko, kr)
+    _rope_close(kg.cpu().view(-1, Hk, D), kc.view(-1, Hk, D))
+    assert torch.equal(vg.cpu(), vc)
+    # without the norm: bit-exact
+    qo2, ko2, _ = nkv.qk_norm_rope_store(pos.to(dev), q, k, None, cache.to(dev))
+    torch.cuda.synchronize()
+    qr2, kr2, _ = qk_norm_rope_store_ref(qkv, pos, None, None, 0.0, cache, Hq, Hk, head_dim=D)
+    assert torch.equal(qo2.cpu(), qr2) and torch.equal(ko2.cpu(), kr2)
+
+
+@pytest.mark.parametrize("D", [64, 256])
+def test_attention_module_head_dim(nkv, dev, D):
+    """Attention.forward with head_dim 64 / 256: the decode branch (store, then attend) and
+    the prefill branch (store, then varlen attention over the paged cache)."""
+    from types import SimpleNamespace
+    cfg = SimpleNamespace(kv_compress_enabled=False)
+    wl = wl_mod.decode_workload(4, 16, 8, 300, 1000, 16, seed=D, value_scale=D ** -0.5,
+                                head_dim=D)
+    attn = nkv.Attention(16, D, D ** -0.5, 8, cfg, 1)
+    attn.k_cache, attn.v_cache = wl["k_cache"].to(dev), wl["v_cache"].to(dev)
+    bt, slots = wl["block_tables"][0], wl["slot_mappings"][0]
+    nkv.set_context(True, slot_mapping=slots.to(dev), context_lens=wl["context_lens"].to(dev),
+                    block_tables=bt.to(dev))
+    o = attn(wl["q"].to(dev), wl["key"].to(dev), wl["value"].to(dev), 0)
+    nkv.reset_context()
+    kc, vc = wl["k_cache"].clone(), wl["v_cache"].clone()
+    store_kvcache_ref(wl["key"], wl["value"], kc, vc, slots)
+    ref = paged_decode_ref(wl["q"].float(), kc, vc, wl["context_lens"], bt, wl["scale"])
+    assert o.shape == (4, 1, 16, D)
+    assert _err(o[:, 0], ref) <= TOL
+
+    pw = wl_mod.prefill_workload(3, 16, 8, 0, 0, seed=D + 1, prefix_lo=0, prefix_hi=600,
+                                 chunk=100, head_dim=D)
+    attn.k_cache, attn.v_cache = pw["k_cache"].to(dev), pw["v_cache"].to(dev)
+    nkv.set_context(False, cu_seqlens_q=pw["cu_seqlens_q"].to(dev),
+                    cu_seqlens_k=pw["cu_seqlens_k"].to(dev), max_seqlen_q=pw["max_seqlen_q"],
+                    max_seqlen_k=pw["max_seqlen_k"], slot_mapping=pw["slot_mapping"].to(dev),
+                    block_tables=pw["block_tables"].to(dev))
+    o = attn(pw["q"].to(dev), pw["key"].to(dev), pw["value"].to(dev), 0)
+    nkv.reset_context()
+    kc, vc = pw["k_cache"].clone(), pw["v_cache"].clone()
+    store_kvcache_ref(pw["key"], pw["value"], kc, vc, pw["slot_mapping"])
+    ref = varlen_prefill_ref(pw["q"].float(), kc, vc, pw["cu_seqlens_q"], pw["cu_seqlens_k"],
+                             pw["scale"], block_tables=pw["block_tables"])
+    assert _err(o.view(ref.shape), ref) <= TOL

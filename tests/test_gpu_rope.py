@@ -135,13 +135,13 @@ def test_bad_arguments_raise(nkv, dev):
     q, k, v = _split(qkv.to(dev), Hq, Hk)
     with pytest.raises(ValueError):
         nkv.qk_norm_rope_store(pos.to(dev), q, k, v, cache.to(dev), qw.to(dev), None)
-    # head_dim 64 is rejected by the library itself, before any launch
+    # head_dim 96 is rejected by the library itself, before any launch
     lib = importlib.import_module("nanokv-llm_amd._lib").lib()
     pg, cg = pos.to(dev), cache.to(dev)
     rc = lib.nkv_qk_norm_rope_store(q.data_ptr(), q.stride(0), k.data_ptr(), k.stride(0), None,
                                     0, pg.data_ptr(), None, None, 1e-6, cg.data_ptr(), 4096,
                                     q.data_ptr(), q.stride(0), k.data_ptr(), None, None, None,
-                                    0, N, Hq, Hk, 64, None)
+                                    0, N, Hq, Hk, 96, None)
     assert rc != 0
 
 
