@@ -85,18 +85,18 @@ int nkv_store_kvcache_fp8(const void* key, int64_t key_row_stride, const void* v
  * projection and attention. q, k, v are row-strided bf16 views: element
  * (i, h, d) of q at q[i*q_row_stride + h*head_dim + d], likewise k and v
  * (normally the three parts of one fused qkv row). For every token i and q or
- * k head (head_dim 128):
+ * k head (head_dim D = 64, 128 or 256; Qwen3: 128):
  *   x   = head row (fp32);
  *   if norm weights are given (both, or neither = no norm):
  *     x = bf16(bf16(x * rsqrt(mean(x^2) + eps)) * w)   (w = q or k weight)
- *   x1, x2 = x[:64], x[64:];  c, s = cos_sin_cache[p][:64], [p][64:]
+ *   x1, x2 = x[:D/2], x[D/2:];  c, s = cos_sin_cache[p][:D/2], [p][D/2:]
  *   y   = bf16([x1*c - x2*s | x2*c + x1*s])            (p = positions[i])
- * q heads -> q_out[i*q_out_row_stride + h*128 ...]; k heads -> k_out
- * ([n_tokens, n_kv_heads, 128] contiguous, optional) and, with a cache, the
+ * q heads -> q_out[i*q_out_row_stride + h*D ...]; k heads -> k_out
+ * ([n_tokens, n_kv_heads, D] contiguous, optional) and, with a cache, the
  * k_cache row slot_mapping[i]; v heads are copied unchanged to the v_cache
  * row. Slots -1 or outside [0, n_slots) are skipped; positions outside
  * [0, max_position) are clamped (the reference would raise an index error).
- * positions is int64 and cos_sin_cache fp32 [max_position, 128] as the
+ * positions is int64 and cos_sin_cache fp32 [max_position, D] as the
  * reference builds them. k_cache, v_cache, v and slot_mapping are all given
  * or all NULL; at least one of k_out and k_cache is given. Pointers are
  * 16-byte aligned and row strides multiples of 8 elements.
@@ -127,13 +127,14 @@ int nkv_qk_norm_rope_store(const void* q, int64_t q_row_stride, const void* k,
  * must hold nkv_paged_decode_workspace_bytes(...), which is sized by what the
  * split grid can write on the current device (descriptors per sequence and
  * KV head, then partial rows: batch*Hq plus at most 8 resident waves per CU
- * x 16 query heads, 528 bytes each; ~35 MB at batch 500, Hq 64, 64-block
- * tables), not by batch x table width. Calls on one stream may share one
- * workspace (the layers of a model, one after another).
+ * x 16 query heads, (head_dim + 4) * 4 bytes each; ~35 MB at batch 500, Hq 64,
+ * head_dim 128, 64-block tables), not by batch x table width. Calls on one
+ * stream may share one workspace (the layers of a model, one after another).
  * q[b,h,d] at q[b*q_row_stride + h*head_dim + d]; out likewise with
- * out_row_stride. head_dim must be 128; any GQA group n_q_heads/n_kv_heads
- * up to 16; block_size a multiple of 16. Block-table entries outside
- * [0, n_blocks) contribute nothing.
+ * out_row_stride. head_dim 64, 128 or 256 (out then 2-, 4- or 8-byte aligned
+ * with a row stride that is a multiple of head_dim/64); any GQA group
+ * n_q_heads/n_kv_heads up to 16; block_size a multiple of 16. Block-table
+ * entries outside [0, n_blocks) contribute nothing.
  * Replaces: flash_attn_with_kvcache(q.unsqueeze(1), k_cache, v_cache,
  *           cache_seqlens=context_lens, block_table=block_tables,
  *           softmax_scale=scale, causal=True),
@@ -219,7 +220,7 @@ int nkv_paged_decode_combine(const int32_t* context_lens, int32_t batch,
  * with row strides k_row_stride / v_row_stride, e.g. a roped K next to V as a
  * view of the qkv projection; paged caches share one stride). Table entries at or beyond
  * max_blocks_per_seq, negative, or past n_rows read as zero keys/values.
- * q/out are [sum Lq, Hq, D] with row strides. head_dim must be 128; any
+ * q/out are [sum Lq, Hq, D] with row strides. head_dim 64, 128 or 256; any
  * GQA group Hq/Hk up to 16. Rows with no visible key (Lk < Lq) are zero.
  * Replaces: flash_attn_varlen_func(q, k, v, max_seqlen_q, cu_seqlens_q,
  *           max_seqlen_k, cu_seqlens_k, softmax_scale, causal=True,
@@ -264,7 +265,11 @@ int nkv_prefill_varlen_fp8(const void* q, int64_t q_row_stride,
  *   imp[j, s, t] = sum_{h in set s} softmax_t(scale * q[h].K[t, h/g])
  * with key 0 masked to -inf (attention sink) before the softmax.
  * importance_out: fp32 [m, n_sets, W*B-1], n_sets = 1 (ALL) or n_kv_heads
- * (GROUP). workspace: nkv_compress_workspace_bytes(...).
+ * (GROUP). workspace: nkv_compress_workspace_bytes(...). head_dim 64, 128 or
+ * 256 (every compression entry point; the fused one-launch kernels of
+ * nkv_compress_select / nkv_compress_step serve head_dim 128 with windows of
+ * up to 1024 tokens, other shapes take the score / importance / top-k /
+ * compaction kernels, same results).
  * If block_tables == NULL the keys come from a contiguous K tensor
  * [m, Hk, L, D] (k_cache points at it, L = window_blocks*block_size), as in
  * SnapKV(Q, K, V, ...) called directly; seq_idx and base_context_lens are
