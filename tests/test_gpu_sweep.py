@@ -2,7 +2,8 @@
 
 Each case draws its own geometry: block sizes 16-256 (compression 64-512), 1-8 KV heads,
 GQA groups 1-8 and 16, ragged contexts including empty and one-token ones,
-tables padded with -1 or 0, and padding entries in the compression selection. Tolerances
+tables padded with -1 or 0, and padding entries in the compression selection; head_dim 128,
+with extra cases at 64 and 256. Tolerances
 are the suite's: 2e-2 max abs error for bf16 attention outputs against the fp32 oracle,
 bit-exact integer work (cache rows, lengths, kept indices given the scores) and importance
 within rtol 1e-4.
@@ -20,8 +21,14 @@ from oracle.compress_ref import (compress_compact_ref, gather_kv_by_slots_ref,
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-2
-D = 128
 cu = importlib.import_module("nanokv-llm_amd.layers.compress_utils")
+
+
+def _cases(n128, n_other, base=0):
+    """(case, head_dim): n128 cases at 128, then n_other each at 64 and 256."""
+    return ([(c, 128) for c in range(n128)] +
+            [(n128 + i, 64) for i in range(n_other)] +
+            [(n128 + n_other + i, 256) for i in range(n_other)])
 
 
 def _randn(shape, g, scale=1.0):
@@ -39,8 +46,8 @@ def _tables(rng, lens, B, n_blocks, width, pad):
     return torch.tensor(rows, dtype=torch.int32).reshape(len(lens), width)
 
 
-@pytest.mark.parametrize("case", range(24))
-def test_decode_sweep(nkv, dev, case):
+@pytest.mark.parametrize("case,D", _cases(24, 6))
+def test_decode_sweep(nkv, dev, case, D):
     rng = random.Random(1000 + case)
     g = torch.Generator().manual_seed(1000 + case)
     B = rng.choice([16, 32, 64, 128, 256])
@@ -56,15 +63,16 @@ def test_decode_sweep(nkv, dev, case):
     kc, vc = _randn((n_blocks, B, Hk, D), g), _randn((n_blocks, B, Hk, D), g)
     q = _randn((bs, Hk * G, D), g)
     ctx = torch.tensor(lens, dtype=torch.int32)
-    print(f"decode case {case}: B={B} Hk={Hk} G={G} bs={bs} max_len={max(lens)}", flush=True)
+    print(f"decode case {case}: D={D} B={B} Hk={Hk} G={G} bs={bs} max_len={max(lens)}",
+          flush=True)
     out = nkv.paged_decode(q.to(dev), kc.to(dev), vc.to(dev), ctx.to(dev), bt.to(dev), D ** -0.5)
     torch.cuda.synchronize()
     ref = paged_decode_ref(q.float(), kc, vc, ctx, bt, D ** -0.5)
     assert (out.float().cpu() - ref).abs().max().item() <= TOL
 
 
-@pytest.mark.parametrize("case", range(16))
-def test_prefill_sweep(nkv, dev, case):
+@pytest.mark.parametrize("case,D", _cases(16, 6))
+def test_prefill_sweep(nkv, dev, case, D):
     rng = random.Random(2000 + case)
     g = torch.Generator().manual_seed(2000 + case)
     paged = case % 4 != 3
@@ -81,7 +89,8 @@ def test_prefill_sweep(nkv, dev, case):
     cq = torch.tensor([0] + torch.tensor(Lq).cumsum(0).tolist(), dtype=torch.int32)
     ck = torch.tensor([0] + torch.tensor(Lk).cumsum(0).tolist(), dtype=torch.int32)
     q = _randn((int(cq[-1]), Hk * G, D), g)
-    print(f"prefill case {case}: paged={paged} B={B} Hk={Hk} G={G} Lq={Lq} Lk={Lk}", flush=True)
+    print(f"prefill case {case}: D={D} paged={paged} B={B} Hk={Hk} G={G} Lq={Lq} Lk={Lk}",
+          flush=True)
     if paged:
         n_blocks = sum((k + B - 1) // B for k in Lk) + 3
         width = max((k + B - 1) // B for k in Lk) + rng.randrange(0, 2)
@@ -99,8 +108,8 @@ def test_prefill_sweep(nkv, dev, case):
     assert (out.float().cpu() - ref).abs().max().item() <= TOL
 
 
-@pytest.mark.parametrize("case", range(8))
-def test_store_sweep(nkv, dev, case):
+@pytest.mark.parametrize("case,D", _cases(8, 2))
+def test_store_sweep(nkv, dev, case, D):
     rng = random.Random(3000 + case)
     g = torch.Generator().manual_seed(3000 + case)
     B = rng.choice([16, 64, 256])
@@ -116,7 +125,8 @@ def test_store_sweep(nkv, dev, case):
     value = _randn((N, Hk * D + extra), g)[:, :Hk * D].reshape(N, Hk, D)
     kc, vc = _randn((n_blocks, B, Hk, D), g), _randn((n_blocks, B, Hk, D), g)
     sm = torch.tensor(slots, dtype=torch.int32)
-    print(f"store case {case}: B={B} Hk={Hk} N={N} row_stride={key.stride(0)}", flush=True)
+    print(f"store case {case}: D={D} B={B} Hk={Hk} N={N} row_stride={key.stride(0)}",
+          flush=True)
     kg, vg = kc.to(dev), vc.to(dev)
     nkv.store_kvcache(key.to(dev), value.to(dev), kg, vg, sm.to(dev))
     torch.cuda.synchronize()
@@ -124,11 +134,12 @@ def test_store_sweep(nkv, dev, case):
     assert torch.equal(kg.cpu(), kc) and torch.equal(vg.cpu(), vc)
 
 
-@pytest.mark.parametrize("case", range(12))
-def test_compress_step_sweep(nkv, dev, case):
+@pytest.mark.parametrize("case,D", _cases(12, 3))
+def test_compress_step_sweep(nkv, dev, case, D):
     rng = random.Random(4000 + case)
     g = torch.Generator().manual_seed(4000 + case)
-    B = rng.choice([64, 128, 256])
+    # head_dim 64 / 256 take the general path, whose scoring reads 256-key chunks of one block
+    B = rng.choice([64, 128, 256]) if D == 128 else 256
     W = rng.choice([2, 3, 4]) if B == 256 else rng.choice([2, 4])
     # any keep (one or more read-then-write rounds, tails at logical positions); the last
     # case has a window over 1024 tokens: the general path (score, importance, top-k and a
@@ -156,8 +167,8 @@ def test_compress_step_sweep(nkv, dev, case):
     padded = list(sel)
     if case % 3 == 0:
         padded.insert(rng.randrange(0, len(padded) + 1), -1)
-    print(f"compress case {case}: B={B} W={W} keep={keep} Hk={Hk} G={G} agg={agg} sel={padded}",
-          flush=True)
+    print(f"compress case {case}: D={D} B={B} W={W} keep={keep} Hk={Hk} G={G} agg={agg} "
+          f"sel={padded}", flush=True)
     base = torch.tensor(lens, dtype=torch.int32)
     kg, vg, ctx = kc.to(dev), vc.to(dev), base.clone().to(dev)
     seq_idx = torch.tensor(padded, dtype=torch.int32, device=dev)
