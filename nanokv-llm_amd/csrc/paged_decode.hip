@@ -15,9 +15,10 @@
 //    partial (m, l, O) per query head.
 //    A head group is one KV head, or two (HP = 2; four for fp8 rows, HP = 4)
 //    whose parts of every token row are read as one contiguous piece.
-//  * Within a segment the wave streams chunks through a register ring (4
-//    chunks of 256-byte rows, or 2 of 512-byte rows): K and V of the chunk one
-//    ring ahead are issued as soon as a chunk has been consumed. Loads are
+//  * Within a segment the wave streams chunks through a register ring holding
+//    16 KiB of K and V (one chunk of 512-byte rows, two of 256-byte rows): the
+//    chunk one ring ahead is issued as soon as the current chunk's rows are
+//    staged in LDS, before its products are computed. Loads are
 //    non-temporal raw buffer loads whose per-chunk descriptor covers only the
 //    chunk's valid rows: keys past the context,
 //    padding chunks and invalid block-table entries read as zero without
@@ -48,6 +49,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <type_traits>
 
 namespace nkv {
 
@@ -147,7 +149,7 @@ __device__ __forceinline__ int stage_off(int dim) {
 // HP*G are computed and dropped. D: head_dim (64, 128 or 256); a wave's piece of
 // a token row (HP*D elements) is 128 to 512 bytes.
 template <bool F8, int HP, int D>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 2)))
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2)))
 void paged_decode_split_kernel(
     const bf16_t* __restrict__ q, int64_t q_row_stride,
     const void* __restrict__ k_cache, const void* __restrict__ v_cache,
@@ -166,7 +168,9 @@ void paged_decode_split_kernel(
   constexpr int kLpr = kSeg / 16;              // lanes per row (16-byte loads)
   constexpr int kRpl = 64 / kLpr;              // rows per load instruction
   constexpr int kLoads = kChunk / kRpl;        // loads per lane per K (or V) chunk
-  constexpr int kRing = kLoads >= 8 ? 2 : 4;   // ring depth: at most 16 loads per lane in flight
+  // ring depth: 16 KiB of K and V in flight per wave (one chunk of 512-byte pieces, two of
+  // 256-byte ones ...); a chunk's slot is refilled as soon as its rows are staged in LDS
+  constexpr int kRing = kLoads >= 8 ? 1 : kLoads >= 4 ? 2 : 4;
   constexpr int kLph = kLpr / HP;              // lanes per head within a row
   // K and V of a chunk share one staging buffer (V is written after the K reads of S^T)
   // where two would take 20 KiB or more (four heads at D <= 128, two at D = 256), which
@@ -299,7 +303,9 @@ void paged_decode_split_kernel(
                                                              kStreamPolicy));
       };
 
-      auto consume = [&](int s) {
+      auto consume = [&](int s, auto refill, int nxt) {
+        constexpr bool kRefill = decltype(refill)::value;
+        const int nv_cur = nv[s];  // the refill below overwrites the slot's count
         // stage the chunk's K and V rows (row-major per head, bf16) in LDS
 #pragma unroll
         for (int r = 0; r < kLoads; ++r) {
@@ -320,6 +326,11 @@ void paged_decode_split_kernel(
             *reinterpret_cast<u32x4_t*>(&kbuf[sh][e]) = kreg[s][r];
             if constexpr (!kShared) *reinterpret_cast<u32x4_t*>(&vbuf[sh][e]) = vreg[s][r];
           }
+        }
+        if constexpr (kRefill && !kShared) {
+          __builtin_amdgcn_sched_barrier(0);
+          issue(nxt, s);  // the slot's registers are staged: refill now
+          __builtin_amdgcn_sched_barrier(0);
         }
         // S^T for 16 keys x 16 columns per head; A operand: lane l -> key l%16,
         // dims 8*(l/16) + 32*ks
@@ -345,7 +356,7 @@ void paged_decode_split_kernel(
           float x = st[0][r];
 #pragma unroll
           for (int hh = 1; hh < HP; ++hh) x = hsel == hh ? st[hh][r] : x;
-          sv[r] = (4 * g4 + r < nv[s]) ? x * scale_log2 : -INFINITY;
+          sv[r] = (4 * g4 + r < nv_cur) ? x * scale_log2 : -INFINITY;
           cmax = fmaxf(cmax, sv[r]);
         }
         cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
@@ -377,6 +388,11 @@ void paged_decode_split_kernel(
               *reinterpret_cast<u32x4_t*>(&vbuf[sh][row + sd]) = vreg[s][r];
             }
           }
+          if constexpr (kRefill) {
+            __builtin_amdgcn_sched_barrier(0);
+            issue(nxt, s);
+            __builtin_amdgcn_sched_barrier(0);
+          }
         }
         // P^T per head: a column's weights only in its own head's product
         i16x4_t pbh[HP];
@@ -396,22 +412,18 @@ void paged_decode_split_kernel(
       };
 
       // Ring schedule over the window padded to a multiple of kRing: every
-      // group but the last refills each slot right after consuming it
+      // group but the last refills each slot once its rows are staged
       // (branch-free, so the wait counts stay exact); the last group drains.
       const int n_groups = (wn + kRing - 1) / kRing;
 #pragma unroll
       for (int s = 0; s < kRing; ++s) issue(s, s);
       for (int gi = 0; gi + 1 < n_groups; ++gi) {
 #pragma unroll
-        for (int s = 0; s < kRing; ++s) {
-          consume(s);
-          __builtin_amdgcn_sched_barrier(0);  // refill only after the slot is consumed
-          issue((gi + 1) * kRing + s, s);
-          __builtin_amdgcn_sched_barrier(0);
-        }
+        for (int s = 0; s < kRing; ++s)
+          consume(s, std::integral_constant<bool, true>{}, (gi + 1) * kRing + s);
       }
 #pragma unroll
-      for (int s = 0; s < kRing; ++s) consume(s);
+      for (int s = 0; s < kRing; ++s) consume(s, std::integral_constant<bool, false>{}, 0);
     }
 
     // ---- segment epilogue: l over the four key groups, then the partial
