@@ -43,6 +43,29 @@ const char* nkv_last_error(void);
 const char* nkv_version(void);
 
 /*
+ * Input checks of the debug build. The kernels run asynchronously and cannot
+ * return an error, so inputs the reference would stop on (its asserts, e.g.
+ * nanokvllm/layers/attention.py:36-39 and layers/compress_utils.py:39-41) or
+ * would read or write out of bounds with are skipped or clamped silently: a
+ * slot past the pool, a block-table entry outside the pool where a sequence
+ * needs a block, a context longer than its table row. libnkv_amd_debug.so
+ * (the same sources built with NKV_DEBUG) also records each such input as one
+ * of the bits below, in a word per device. nkv_debug_flags waits for the
+ * current device (hipDeviceSynchronize: the one call of this ABI that
+ * synchronises), stores the bits recorded there since the last clearing call
+ * in *flags and clears them if `clear` is non-zero. The release library sets
+ * *flags = 0 and returns NKV_EUNSUPPORTED. No counterpart in the reference.
+ */
+#define NKV_DEBUG_SLOT 1u     /* store: slot_mapping entry < -1 or >= n_slots (row skipped) */
+#define NKV_DEBUG_BLOCK 2u    /* a needed block-table entry (or contiguous K/V row) outside
+                                 the cache: its rows read as zeros */
+#define NKV_DEBUG_LENGTH 4u   /* a context longer than its table row covers, a negative
+                                 length, or a prefill sequence with Lq > Lk (clamped) */
+#define NKV_DEBUG_POSITION 8u /* q/k norm + RoPE: position outside [0, max_position)
+                                 (clamped) */
+int nkv_debug_flags(uint32_t* flags, int clear);
+
+/*
  * store_kvcache: for every token i < n_tokens with slot_mapping[i] != -1,
  * copy key[i] and value[i] (n_kv_heads*head_dim contiguous elements each)
  * into row slot_mapping[i] of k_cache / v_cache. Rows with slot -1 are

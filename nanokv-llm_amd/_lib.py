@@ -1,7 +1,10 @@
 """ctypes binding of libnkv_amd.so (declared in include/nkv.h).
 
 The library is the only compute path of this package: if it is missing the
-loader raises, there is no CPU or PyTorch fallback. torch is imported first
+loader raises, there is no CPU or PyTorch fallback. With NKV_DEBUG=1 in the
+environment the loader opens libnkv_amd_debug.so instead (the same kernels
+built with NKV_DEBUG, which also record the inputs they skip or clamp; see
+debug_flags). torch is imported first
 so that the HIP runtime torch ships (SONAME libamdhip64.so.7) is the one the
 library binds to; the streams handed over are torch's own.
 """
@@ -14,11 +17,16 @@ import torch  # noqa: F401  (must be loaded before the HIP library)
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG_DIR, "libnkv_amd.so")
+DEBUG_LIB_PATH = os.path.join(PKG_DIR, "libnkv_amd_debug.so")
 
 NKV_OK = 0
 NKV_AGG_ALL = 0
 NKV_AGG_GROUP = 1
 NKV_DECODE_NOALLOC_MAX_BYTES = 64 << 20  # include/nkv.h
+NKV_DEBUG_SLOT = 1  # include/nkv.h: bits of nkv_debug_flags
+NKV_DEBUG_BLOCK = 2
+NKV_DEBUG_LENGTH = 4
+NKV_DEBUG_POSITION = 8
 
 _p = C.c_void_p
 _i32 = C.c_int32
@@ -30,6 +38,7 @@ _sz = C.c_size_t
 SIGNATURES = {
     "nkv_last_error": (C.c_char_p, []),
     "nkv_version": (C.c_char_p, []),
+    "nkv_debug_flags": (C.c_int, [_p, _i32]),
     "nkv_store_kvcache": (C.c_int, [_p, _i64, _p, _i64, _p, _p, _p, _i64, _i32, _i32, _i64, _p]),
     "nkv_fp8_quantize": (C.c_int, [_p, _i64, _f32, _p, _p]),
     "nkv_fp8_dequantize": (C.c_int, [_p, _i64, _f32, _p, _p]),
@@ -89,21 +98,36 @@ class NkvError(RuntimeError):
     pass
 
 
+def lib_path() -> str:
+    """libnkv_amd.so, or libnkv_amd_debug.so when NKV_DEBUG=1 is set."""
+    return DEBUG_LIB_PATH if os.environ.get("NKV_DEBUG") == "1" else LIB_PATH
+
+
 def lib() -> C.CDLL:
-    """Load libnkv_amd.so once; raise if it has not been built."""
+    """Load the library once; raise if it has not been built."""
     global _LIB
     if _LIB is None:
-        if not os.path.exists(LIB_PATH):
+        path = lib_path()
+        if not os.path.exists(path):
             raise NkvError(
-                f"{LIB_PATH} is missing: build it with `python __graft_entry__.py build` "
+                f"{path} is missing: build it with `python __graft_entry__.py build` "
                 "(or nanokv-llm_amd/build.py); there is no fallback path")
-        handle = C.CDLL(LIB_PATH)
+        handle = C.CDLL(path)
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(handle, name)
             fn.restype = res
             fn.argtypes = args
         _LIB = handle
     return _LIB
+
+
+def debug_flags(clear: bool = True) -> int:
+    """NKV_DEBUG_* bits the debug library's kernels recorded on the current device since
+    the last clearing call (waits for the device). Raises NkvError with the release
+    library, which records nothing."""
+    v = C.c_uint32(0)
+    check(lib().nkv_debug_flags(C.addressof(v), 1 if clear else 0), "debug_flags")
+    return v.value
 
 
 def check(rc: int, what: str) -> None:

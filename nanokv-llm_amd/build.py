@@ -3,7 +3,10 @@
 Every ``csrc/*.hip`` file is compiled to an object in ``_build/`` (in
 parallel) and linked into ``libnkv_amd.so`` next to this file, which the
 ctypes loader in ``_lib.py`` opens. Runs on a machine without a GPU: hipcc
-cross-compiles for gfx950.
+cross-compiles for gfx950. ``debug=True`` builds the same sources with
+NKV_DEBUG into ``libnkv_amd_debug.so`` (objects in ``_build_debug/``): its
+kernels also record the inputs they skip or clamp, read back with
+nkv_debug_flags.
 """
 from __future__ import annotations
 
@@ -18,6 +21,8 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_NAME = "libnkv_amd.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
+DEBUG_BUILD_DIR = os.path.join(PKG_DIR, "_build_debug")
+DEBUG_LIB_PATH = os.path.join(PKG_DIR, "libnkv_amd_debug.so")
 ARCH = os.environ.get("NKV_OFFLOAD_ARCH", "gfx950")
 
 # -packed-fp32-ops: keep the compiler from forming v_pk_{add,mul,fma}_f32.
@@ -38,9 +43,9 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found (set HIPCC)")
 
 
-def _compile(hipcc: str, src: str, verbose: bool) -> str:
-    obj = os.path.join(BUILD_DIR, os.path.basename(src) + ".o")
-    cmd = [hipcc, *HIP_FLAGS, "-c", src, "-o", obj]
+def _compile(hipcc: str, src: str, verbose: bool, debug: bool = False) -> str:
+    obj = os.path.join(DEBUG_BUILD_DIR if debug else BUILD_DIR, os.path.basename(src) + ".o")
+    cmd = [hipcc, *HIP_FLAGS, *(["-DNKV_DEBUG"] if debug else []), "-c", src, "-o", obj]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -53,24 +58,26 @@ def _compile(hipcc: str, src: str, verbose: bool) -> str:
     return obj
 
 
-def build_library(verbose: bool = False, jobs: int | None = None) -> str:
-    """Compile all kernels and link libnkv_amd.so; returns its path."""
+def build_library(verbose: bool = False, jobs: int | None = None, debug: bool = False) -> str:
+    """Compile all kernels and link libnkv_amd.so (libnkv_amd_debug.so with debug=True);
+    returns its path."""
     hipcc = _hipcc()
-    os.makedirs(BUILD_DIR, exist_ok=True)
+    out = DEBUG_LIB_PATH if debug else LIB_PATH
+    os.makedirs(DEBUG_BUILD_DIR if debug else BUILD_DIR, exist_ok=True)
     srcs = sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
     jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 4)))
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(lambda s: _compile(hipcc, s, verbose), srcs))
-    tmp = LIB_PATH + ".tmp"
+        objs = list(ex.map(lambda s: _compile(hipcc, s, verbose, debug), srcs))
+    tmp = out + ".tmp"
     cmd = [hipcc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":
-    print(build_library(verbose="-v" in sys.argv))
+    print(build_library(verbose="-v" in sys.argv, debug="--debug" in sys.argv))

@@ -79,6 +79,8 @@ __global__ __launch_bounds__(256) void compress_score_kernel(
     int64_t pb = -1;
     if (full >= window_blocks && full <= max_blocks)
       pb = block_tables[(int64_t)seq * bt_row_stride + wblk];
+    NKV_DBG(seq >= 0 && full >= window_blocks && full <= max_blocks && (pb < 0 || pb >= n_blocks),
+            NKV_DEBUG_BLOCK);
     valid = pb >= 0 && pb < n_blocks;
     base = ((pb * block_size + t0 % block_size) * Hk + kvh) * (int64_t)D;
     tok_stride = (int64_t)Hk * D;
@@ -531,6 +533,9 @@ __device__ __forceinline__ void group_importance(
     int64_t pb = -1;
     if (valid && full >= window_blocks && full <= max_blocks)
       pb = block_tables[(int64_t)seq * bt_row_stride + full - window_blocks + t0 / block_size];
+    NKV_DBG(valid && seq >= 0 && full >= window_blocks && full <= max_blocks &&
+                (pb < 0 || pb >= n_blocks),
+            NKV_DEBUG_BLOCK);
     valid = valid && pb >= 0 && pb < n_blocks;
     base = ((pb * block_size + t0 % block_size) * Hk + kvh) * (int64_t)kCD;
     tok_stride = (int64_t)Hk * kCD;
@@ -699,6 +704,8 @@ __device__ __forceinline__ bool unit_blocks(int32_t* win_pb, const int32_t* __re
     int32_t pb = -1;
     if ((int)threadIdx.x < window_blocks) pb = bt[wb0 + threadIdx.x];
     else if (tail > 0) pb = bt[full];
+    NKV_DBG(((int)threadIdx.x < window_blocks || tail > 0) && (pb < 0 || pb >= n_blocks),
+            NKV_DEBUG_BLOCK);
     win_pb[threadIdx.x] = (pb >= 0 && pb < n_blocks) ? pb : -1;
   }
   return true;

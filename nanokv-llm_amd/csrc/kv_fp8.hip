@@ -70,6 +70,7 @@ __global__ __launch_bounds__(kF8Threads) void store_kvcache_fp8_kernel(
     const bool is_v = r >= chunks_per_row;
     const int c = is_v ? r - chunks_per_row : r;
     const int64_t slot = slot_mapping[t];
+    NKV_DBG(slot < -1 || slot >= n_slots, NKV_DEBUG_SLOT);
     if (slot < 0 || slot >= n_slots) continue;
     const bf16_t* src = (is_v ? value + t * value_row_stride : key + t * key_row_stride) + 16 * c;
     const float s = is_v ? inv_v_scale : inv_k_scale;

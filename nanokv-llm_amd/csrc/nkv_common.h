@@ -26,6 +26,12 @@ void clear_error();
 // Checks the launch just issued on the current thread.
 int check_launch(const char* what);
 
+// Input checks of the debug build (-DNKV_DEBUG, libnkv_amd_debug.so): NKV_DBG(cond, bit)
+// ORs an NKV_DEBUG_* bit into this source file's device word when cond holds, and each
+// source file registers a reader of its word with nkv_debug_flags. Without NKV_DEBUG the
+// checks compile to nothing.
+bool debug_register(int (*take)(uint32_t* bits, int clear));
+
 // ---------------------------------------------------------------- types
 typedef uint16_t bf16_t;  // raw bf16 bits in memory
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
@@ -138,3 +144,33 @@ __device__ __forceinline__ uint32_t f32x4_to_fp8x4(float x0, float x1, float x2,
 }
 
 }  // namespace nkv
+
+#ifdef NKV_DEBUG
+namespace nkv {
+// This source file's debug word (one per device) and its reader.
+static __device__ unsigned int g_debug_bits;
+static int debug_take(uint32_t* bits, int clear) {
+  unsigned int v = 0;
+  if (hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_debug_bits), sizeof(v), 0,
+                          hipMemcpyDeviceToHost) != hipSuccess)
+    return NKV_ELAUNCH;
+  if (clear && v) {
+    const unsigned int zero = 0;
+    if (hipMemcpyToSymbol(HIP_SYMBOL(g_debug_bits), &zero, sizeof(zero), 0,
+                          hipMemcpyHostToDevice) != hipSuccess)
+      return NKV_ELAUNCH;
+  }
+  *bits |= v;
+  return NKV_OK;
+}
+[[maybe_unused]] static const bool g_debug_registered = debug_register(&debug_take);
+}  // namespace nkv
+#define NKV_DBG(cond, bit)                                                   \
+  do {                                                                       \
+    if (cond) atomicOr(&::nkv::g_debug_bits, (unsigned int)(bit));           \
+  } while (0)
+#else
+#define NKV_DBG(cond, bit) \
+  do {                     \
+  } while (0)
+#endif

@@ -113,6 +113,7 @@ __device__ __forceinline__ void seq_load(SeqCursor& c, const int32_t* __restrict
                                          int batch, int max_tokens) {
   const int s = c.cb + (int)threadIdx.x;
   c.ctx = s < batch ? ctx_lens[s] : 0;
+  NKV_DBG(c.ctx < 0 || c.ctx > max_tokens, NKV_DEBUG_LENGTH);
   c.nc = c.ctx > 0 ? (min(c.ctx, max_tokens) + kChunk - 1) / kChunk : 0;
   c.incl = wave_incl_scan(c.nc);
   c.tot = __builtin_amdgcn_readlane(c.incl, 63);
@@ -273,6 +274,7 @@ void paged_decode_split_kernel(
         const int bi = blk0 + lane;
         if (bi < max_blocks && bi * block_size < (wlo + wn) * kChunk) {
           const int id = bt_row[bi];
+          NKV_DBG(id < 0 || id >= n_blocks, NKV_DEBUG_BLOCK);  // every block here is needed
           blk_id = (id >= 0 && id < n_blocks) ? id : -1;
         }
       }

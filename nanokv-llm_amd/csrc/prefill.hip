@@ -136,6 +136,7 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void prefill_varlen_kernel(
   const int kb0 = cu_seqlens_k[seq];
   const int Lk = cu_seqlens_k[seq + 1] - kb0;
   const int j0 = tile * QT;
+  NKV_DBG(tid == 0 && tile == 0 && (Lq < 0 || Lk < 0 || Lq > Lk), NKV_DEBUG_LENGTH);
   if (j0 >= Lq) return;  // uniform
   const int diag = Lk - Lq;  // query j sees keys <= diag + j
   const int last_key = min(Lk - 1, diag + j0 + QT - 1);
@@ -179,6 +180,8 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void prefill_varlen_kernel(
   auto load_window = [&]() {
     const int e = bt_base + lane;
     const int id = e < max_blocks ? bt[e] : -1;
+    NKV_DBG((int64_t)e * block_size < Lk && (e >= max_blocks || id < 0 || id >= n_limit),
+            e >= max_blocks ? NKV_DEBUG_LENGTH : NKV_DEBUG_BLOCK);
     bt_lane = (id >= 0 && id < n_limit) ? id : -1;
   };
   // cursor of this wave's rows in the step loaded next: first key c_t0,
@@ -199,6 +202,7 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void prefill_varlen_kernel(
       row0 = (int64_t)pb * block_size + c_off;
     } else {
       row0 = (int64_t)kb0 + c_t0;
+      NKV_DBG(nv > 0 && (kb0 + c_t0 < 0 || kb0 + c_t0 > n_limit - nv), NKV_DEBUG_BLOCK);
       if (kb0 + c_t0 < 0 || kb0 + c_t0 > n_limit - nv) nv = 0;  // outside the K/V rows
     }
     if (nv <= 0) {

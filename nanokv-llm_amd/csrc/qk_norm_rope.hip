@@ -88,6 +88,7 @@ __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_store_kernel(const 
   const int64_t sl = (!is_q && a.k_cache) ? (int64_t)a.slot_mapping[t] : -1;
   if (is_q || is_k) {  // uniform over the unit's 8 lanes
     int64_t pos = a.positions[t];
+    NKV_DBG(pos < 0 || pos >= a.max_position, NKV_DEBUG_POSITION);
     pos = pos < 0 ? 0 : (pos >= a.max_position ? a.max_position - 1 : pos);
     const float* cs = a.cos_sin + pos * D + 8 * l8;
     const f32x4_t c0 = *reinterpret_cast<const f32x4_t*>(cs);
@@ -141,6 +142,7 @@ __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_store_kernel(const 
     *reinterpret_cast<u32x4_t*>(dst + kH + 8 * l8) = vhi;
     return;
   }
+  NKV_DBG(sl < -1 || sl >= a.n_slots, NKV_DEBUG_SLOT);
   if (sl >= 0 && sl < a.n_slots) {  // -1 (padding) or out of range: skipped
     bf16_t* dst = (is_k ? a.k_cache : a.v_cache) + (sl * a.Hk + kvh) * (int64_t)D;
     *reinterpret_cast<u32x4_t*>(dst + 8 * l8) = vlo;

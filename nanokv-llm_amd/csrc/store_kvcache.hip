@@ -45,6 +45,7 @@ __global__ __launch_bounds__(kStoreThreads) void store_kvcache_kernel(
       val[u] = reinterpret_cast<const Chunk*>(src)[c];
       const int64_t slot = slot_mapping[tok];
       // -1 = padding; slots outside the cache are skipped
+      NKV_DBG(ok && (slot < -1 || slot >= n_slots), NKV_DEBUG_SLOT);
       dst[u] = (ok && slot >= 0 && slot < n_slots) ? slot * row_bytes + c * (int64_t)sizeof(Chunk)
                                                   : -1;
     }

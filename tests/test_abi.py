@@ -143,6 +143,7 @@ CASES = [
     (("nkv_fp8_quantize", [P, 32, 0.0, P, None]), EINVAL, b""),
     (("nkv_store_kvcache_fp8", [P, 1024, P, 1024, P, P, P, 8, 8, 128, 100, 0.0, 1.0, None]),
      EINVAL, b""),
+    (("nkv_debug_flags", [None, 1]), EINVAL, b"null pointer"),
 ]
 
 
@@ -156,3 +157,28 @@ def test_entry_points_reject_bad_arguments_without_gpu():
         err = lib.nkv_last_error()
         assert rc == code, (name, rc, err)
         assert msg in err and err, (name, err)
+
+
+def test_debug_library_matches_and_release_reports_no_debug_checks():
+    """libnkv_amd_debug.so (the NKV_DEBUG build) exports the same functions; the release
+    library answers nkv_debug_flags with NKV_EUNSUPPORTED and zero bits, without a device.
+    (The checks themselves run in tests/test_gpu_debug_checks.py.)"""
+    from importlib import import_module
+    L = import_module("nanokv-llm_amd._lib")
+    assert os.path.exists(L.DEBUG_LIB_PATH), "build() also builds the debug library"
+
+    def exported(path):
+        out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True,
+                             text=True, check=True).stdout
+        return set(re.findall(r" T (nkv_[a-z0-9_]+)", out))
+
+    assert exported(L.DEBUG_LIB_PATH) == exported(L.LIB_PATH)
+    rel = ctypes.CDLL(L.LIB_PATH)
+    rel.nkv_debug_flags.argtypes = [ctypes.c_void_p, ctypes.c_int32]
+    rel.nkv_last_error.restype = ctypes.c_char_p
+    v = ctypes.c_uint32(0xffffffff)
+    assert rel.nkv_debug_flags(ctypes.addressof(v), 1) == EUNSUPPORTED and v.value == 0
+    assert b"NKV_DEBUG" in rel.nkv_last_error()
+    dbg = ctypes.CDLL(L.DEBUG_LIB_PATH)
+    dbg.nkv_debug_flags.argtypes = [ctypes.c_void_p, ctypes.c_int32]
+    assert dbg.nkv_debug_flags(None, 0) == EINVAL  # checked before the device is touched
