@@ -1,7 +1,8 @@
 """Seeded synthetic inputs for the paged-attention workloads (no checkpoints).
 
-Each generator builds a paged K/V pool ``[n_blocks, 256, Hk, 128]`` (bf16),
-assigns every sequence ``ceil(ctx / B)`` physical blocks drawn without
+Each generator builds a paged K/V pool ``[n_blocks, 256, Hk, 128]`` (bf16; K and
+V are the two halves of one ``[2, n_blocks, ...]`` tensor, as the reference's
+pool holds them), assigns every sequence ``ceil(ctx / B)`` physical blocks drawn without
 replacement from a random permutation of the pool, and derives block tables
 (right-padded with -1) and the slot of the newest token. Integer choices use
 a CPU ``torch.Generator`` seeded with ``seed`` so they are identical on every
@@ -40,6 +41,16 @@ def _randn(shape, gen_seed, device, dtype=torch.bfloat16, scale=1.0):
     return x.to(dtype)
 
 
+def _kv_pool(shape, seed, device, scale=1.0):
+    """K and V caches laid out as the reference allocates them: the two halves of one
+    [2, num_blocks, block_size, Hk, D] tensor (nanokvllm/engine/model_runner.py:145, one
+    layer), filled as _randn(shape, seed*7+1) and _randn(shape, seed*7+2) would be."""
+    kv = torch.empty((2,) + tuple(shape), dtype=torch.bfloat16, device=device)
+    kv[0].copy_(_randn(shape, seed * 7 + 1, device, scale=scale))
+    kv[1].copy_(_randn(shape, seed * 7 + 2, device, scale=scale))
+    return kv[0], kv[1]
+
+
 def assign_blocks(ctx_lens: list[int], n_blocks: int, gen: torch.Generator, block=BLOCK,
                   extra_tokens: int = 0):
     """Block tables for sequences of the given lengths (+extra_tokens headroom)."""
@@ -75,8 +86,7 @@ def decode_workload(bs, Hq, Hk, ctx_lo, ctx_hi, n_blocks, seed, device="cpu", va
     ctx = torch.randint(ctx_lo, ctx_hi + 1, (bs,), generator=gen, dtype=torch.int64)
     tables = [assign_blocks(ctx.tolist(), n_blocks, gen) for _ in range(n_table_sets)]
     D = head_dim
-    k_cache = _randn((n_blocks, BLOCK, Hk, D), seed * 7 + 1, device, scale=value_scale)
-    v_cache = _randn((n_blocks, BLOCK, Hk, D), seed * 7 + 2, device, scale=value_scale)
+    k_cache, v_cache = _kv_pool((n_blocks, BLOCK, Hk, D), seed, device, scale=value_scale)
     q = _randn((bs, Hq, D), seed * 7 + 3, "cpu", scale=value_scale)
     key = _randn((bs, Hk, D), seed * 7 + 4, "cpu", scale=value_scale)
     value = _randn((bs, Hk, D), seed * 7 + 5, "cpu", scale=value_scale)
@@ -113,8 +123,7 @@ def compress_workload(bs, Hq, Hk, ctx_lo, ctx_hi, topk, seed, device="cpu", n_bl
     n_blocks = n_blocks or need + 8
     table = assign_blocks(lens_for_tables, n_blocks, gen)
     D = head_dim
-    k_cache = _randn((n_blocks, BLOCK, Hk, D), seed * 7 + 1, device)
-    v_cache = _randn((n_blocks, BLOCK, Hk, D), seed * 7 + 2, device)
+    k_cache, v_cache = _kv_pool((n_blocks, BLOCK, Hk, D), seed, device)
     q = _randn((bs, Hq, D), seed * 7 + 3, "cpu")
     return dict(q=q, k_cache=k_cache, v_cache=v_cache, context_lens=ctx.to(torch.int32),
                 block_tables=table, seq_idx=selected, Hq=Hq, Hk=Hk)
@@ -153,12 +162,12 @@ def prefill_workload(n_seqs, Hq, Hk, len_lo, len_hi, seed, device="cpu", prefix_
     seq_of = torch.cat([torch.full((q,), i, dtype=torch.int64) for i, q in enumerate(Lq)])
     blk = table.to(torch.int64)[seq_of, positions // BLOCK]
     slots = (blk * BLOCK + positions % BLOCK).to(torch.int32)
+    k_cache, v_cache = _kv_pool((n_blocks, BLOCK, Hk, D), seed, device)
     return dict(
         q=_randn((N, Hq, D), seed * 7 + 3, device),
         key=_randn((N, Hk, D), seed * 7 + 4, device),
         value=_randn((N, Hk, D), seed * 7 + 5, device),
-        k_cache=_randn((n_blocks, BLOCK, Hk, D), seed * 7 + 1, device),
-        v_cache=_randn((n_blocks, BLOCK, Hk, D), seed * 7 + 2, device),
+        k_cache=k_cache, v_cache=v_cache,
         block_tables=table, cu_seqlens_q=cu_q, cu_seqlens_k=cu_k, slot_mapping=slots,
         max_seqlen_q=max(Lq), max_seqlen_k=max(Lk), Lq=Lq, Lk=Lk, Hq=Hq, Hk=Hk,
         scale=D ** -0.5, positions=positions.to(device))
@@ -216,9 +225,9 @@ def decode_qwen3_32b_longctx(seed=6, device="cpu", bs=500, n_blocks=None, frac_c
     table = assign_blocks(ctx.tolist(), n_blocks, gen)
     k_cache = v_cache = None
     used = table[table >= 0].to(torch.int64)
-    if alloc_caches:
-        k_cache = torch.empty(n_blocks, BLOCK, Hk, D, dtype=torch.bfloat16, device=device)
-        v_cache = torch.empty_like(k_cache)
+    if alloc_caches:  # one [2, n_blocks, ...] tensor, as the reference's pool
+        kv = torch.empty(2, n_blocks, BLOCK, Hk, D, dtype=torch.bfloat16, device=device)
+        k_cache, v_cache = kv[0], kv[1]
         g = torch.Generator(device=device)
         g.manual_seed(seed * 7 + 1)
     for i in range(0, used.numel() if alloc_caches else 0, 1024):  # used blocks, 1 GiB a time
