@@ -521,9 +521,9 @@ __global__ __launch_bounds__(64) void paged_decode_combine_kernel(
   float2 ml0 = {-INFINITY, 0.f}, ml1 = {-INFINITY, 0.f};
   if (lane < ns) ml0 = *reinterpret_cast<const float2*>(pbase + lane * stride + D);
   if (lane + 64 < ns) ml1 = *reinterpret_cast<const float2*>(pbase + (lane + 64) * stride + D);
-  float v0[8][N];
+  float v0[16][N];
 #pragma unroll
-  for (int u = 0; u < 8; ++u) {
+  for (int u = 0; u < 16; ++u) {
     if (u < ns) {
       load_dims<N>(po + u * stride, v0[u]);
     } else {
@@ -533,37 +533,34 @@ __global__ __launch_bounds__(64) void paged_decode_combine_kernel(
   }
   // lane l holds partials l and l + 64 (ns <= kMaxSlots = 128): the global max and
   // the weights w_s = 2^(m_s - M) with two wave reductions, then each lane
-  // accumulates its output dims over the partials, eight loads in flight
+  // accumulates its output dims over the partials in order (the first sixteen came
+  // with the (m, l) pairs; the rest in batches of eight loads in flight)
   const float M = wave_max(fmaxf(ml0.x, ml1.x));
   const float w0 = (ml0.x == -INFINITY) ? 0.f : fast_exp2(ml0.x - M);
   const float w1 = (ml1.x == -INFINITY) ? 0.f : fast_exp2(ml1.x - M);
   const float L = wave_sum(w0 * ml0.y + w1 * ml1.y);
 #pragma unroll
-  for (int u = 0; u < 8; ++u) {
+  for (int u = 0; u < 16; ++u) {
     const float w = __shfl(w0, u, 64);
     if (u < ns) {  // uniform
 #pragma unroll
       for (int i = 0; i < N; ++i) o[i] = fmaf(w, v0[u][i], o[i]);
     }
   }
-  int s = 8;
-  for (; s + 8 <= ns; s += 8) {
+  for (int s = 16; s < ns; s += 8) {  // uniform
     float v[8][N];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) load_dims<N>(po + (s + u) * stride, v[u]);
+    for (int u = 0; u < 8; ++u) {
+      if (s + u < ns) load_dims<N>(po + (s + u) * stride, v[u]);
+    }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const float w = __shfl(s + u < 64 ? w0 : w1, (s + u) & 63, 64);  // uniform select
+      if (s + u < ns) {
 #pragma unroll
-      for (int i = 0; i < N; ++i) o[i] = fmaf(w, v[u][i], o[i]);
+        for (int i = 0; i < N; ++i) o[i] = fmaf(w, v[u][i], o[i]);
+      }
     }
-  }
-  for (; s < ns; ++s) {
-    float v[N];
-    load_dims<N>(po + s * stride, v);
-    const float w = __shfl(s < 64 ? w0 : w1, s & 63, 64);
-#pragma unroll
-    for (int i = 0; i < N; ++i) o[i] = fmaf(w, v[i], o[i]);
   }
   store_dims<N>(op, o, L > 0.f ? 1.f / L : 0.f);
 }
