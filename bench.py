@@ -243,51 +243,71 @@ def cpu_baseline(wl, bt, kc, vc, budget_s=12.0):
                       f"{len(times)} runs; host has {os.cpu_count()} logical CPUs"}
 
 
-def compress_parity(cw, dev, agg):
-    """The timed compression step once on a fresh copy of its state, against the oracle:
-    importance within rtol 1e-4 (max relative error reported), kept sets exact given the
-    scores, caches, lengths and events bit-exact."""
+def compress_parity(q, kg, vg, bt, lens, sel, agg, dev):
+    """The compression step (compress_step + compress_finalize with the table and slot
+    rewrite) once on a device copy of the selected sequences' blocks, against the oracle on a
+    host copy of the same blocks: importance within rtol 1e-4 (max relative error reported),
+    kept sets exact given the scores, caches, lengths, events, tables and slots bit-exact. The
+    timed state is left untouched, so this works on a pool that fills most of HBM."""
     from oracle.compress_ref import (compress_compact_ref, gather_kv_by_slots_ref,
                                      get_tail_window_and_tail_slots_ref, select_topk_ref,
                                      snapkv_importance_ref)
-    kg, vg = cw["k_cache"].clone(), cw["v_cache"].clone()
-    bt, lens, sel = cw["block_tables"], cw["context_lens"], cw["seq_idx"]
-    btg, base = bt.to(dev), lens.to(dev)
+    bt, lens = bt.cpu(), lens.cpu()
+    ids = sorted({int(x) for x in bt[sel].flatten().tolist() if x >= 0})
+    remap = {b: j for j, b in enumerate(ids)}
+    bt2 = torch.full_like(bt, -1)
+    for i in sel:
+        bt2[i] = torch.tensor([remap.get(int(x), -1) for x in bt[i].tolist()], dtype=torch.int32)
+    idx = torch.tensor(ids, device=dev)
+    kc, vc = kg.index_select(0, idx), vg.index_select(0, idx)
+    kh, vh = kc.cpu(), vc.cpu()
+    bs, Hq, D = q.shape
+    B = kg.size(1)
+    btg, base = bt2.to(dev), lens.to(dev)
     ctx = base.clone()
     seq_idx = torch.tensor(sel, dtype=torch.int32, device=dev)
-    keep, imp = cu.compress_step(cw["q"].to(dev), kg, vg, btg, base, ctx, seq_idx, 4, 513,
-                                 128 ** -0.5, agg)
+    slot_map = torch.arange(bs, dtype=torch.int32, device=dev) * 3
+    keep, imp = cu.compress_step(q, kc, vc, btg, base, ctx, seq_idx, 4, 513, D ** -0.5, agg)
     events = torch.empty(len(sel), 4 + bt.size(1), dtype=torch.int32, device=dev)
-    cu.compress_finalize(btg, base, seq_idx, 513, 256, 4, events, rewrite_tables=False)
+    cu.compress_finalize(btg, base, seq_idx, 513, B, 4, events, rewrite_tables=True,
+                         slot_mapping=slot_map)
     torch.cuda.synchronize()
-    kc, vc = cw["k_cache"].cpu(), cw["v_cache"].cpu()
     st = torch.tensor(sel)
-    slots, *_ = get_tail_window_and_tail_slots_ref(bt, lens, st, 256, 4)
-    k_sub, _ = gather_kv_by_slots_ref(kc, vc, slots)
-    ref_imp = snapkv_importance_ref(cw["q"].index_select(0, st).unsqueeze(2), k_sub, 1, "fp32",
+    slots, *_ = get_tail_window_and_tail_slots_ref(bt2, lens, st, B, 4)
+    k_sub, _ = gather_kv_by_slots_ref(kh, vh, slots)
+    ref_imp = snapkv_importance_ref(q.cpu().index_select(0, st).unsqueeze(2), k_sub, 1, "fp32",
                                     agg)
     imp = imp.cpu()
     rel = float(((imp - ref_imp).abs() / ref_imp.abs().clamp(min=1e-7)).max())
     keep = keep.cpu().long()
     kept_exact = bool(torch.equal(keep[..., 1:-1], select_topk_ref(imp, 511)))
     ctx_ref = lens.clone()
-    _, _, ev_ref = compress_compact_ref(None, kc, vc, bt, lens, ctx_ref, sel, 256, 4, 2, 1, 0, 1,
+    _, _, ev_ref = compress_compact_ref(None, kh, vh, bt2, lens, ctx_ref, sel, B, 4, 2, 1, 0, 1,
                                         keep_idx=keep)
-    caches = bool(torch.equal(kg.cpu(), kc) and torch.equal(vg.cpu(), vc))
-    meta = bool(torch.equal(ctx.cpu(), ctx_ref) and cu.events_to_dicts(events, 0) == ev_ref)
-    del kg, vg
+    caches = bool(torch.equal(kc.cpu(), kh) and torch.equal(vc.cpu(), vh))
+    bt_exp, slot_exp = bt2.clone(), torch.arange(bs, dtype=torch.int32) * 3
+    for ev in ev_ref:
+        i, n = ev["batch_index"], ev["new_context_len"]
+        bt_exp[i, ev["keep_blocks"]:] = -1
+        slot_exp[i] = -1 if n % B == 0 else int(bt2[i, n // B]) * B + n % B
+    meta = bool(torch.equal(ctx.cpu(), ctx_ref) and cu.events_to_dicts(events, 0) == ev_ref
+                and torch.equal(btg.cpu(), bt_exp) and torch.equal(slot_map.cpu(), slot_exp))
+    del kc, vc
     return {"importance_max_rel_err": rel, "importance_within_1e-4": rel <= 1e-4,
             "kept_sets_exact_given_scores": kept_exact, "caches_bit_exact": caches,
-            "lengths_and_events_exact": meta}
+            "lengths_events_tables_slots_exact": meta}
 
 
 def run_compress(args, dev):
-    """One layer's compression step at batch 500: scoring, top-k and compaction of the 20
-    longest sequences (window 4 blocks, keep 513), per KV head (agg "group", the benchmark
-    configuration) and with the reference's all-head importance (agg "all")."""
+    """One layer's compression step at batch 500 as the configuration states it: scoring,
+    top-k and compaction of the 20 longest sequences (window 4 blocks, keep 513), then the
+    block-table, slot-mapping and event update (compress_finalize), per KV head (agg "group",
+    the benchmark configuration) and with the reference's all-head importance (agg "all").
+    compress_select_compact_us: the same without the finalize launch."""
     cw = wl_mod.compress_qwen3_8b(seed=3, device=dev, selected_only=True)
     kg, vg = cw["k_cache"], cw["v_cache"]
-    btg, base = cw["block_tables"].to(dev), cw["context_lens"].to(dev)
+    bt0 = cw["block_tables"].to(dev)
+    btg, base = bt0.clone(), cw["context_lens"].to(dev)
     ctx = base.clone()
     sel = torch.tensor(cw["seq_idx"], dtype=torch.int32, device=dev)
     q = cw["q"].to(dev)
@@ -295,25 +315,21 @@ def run_compress(args, dev):
     Hq, Hk = q.size(1), kg.size(2)
     wsb = cu.select_workspace_bytes(m, Hq, Hk, 4, 256)
     ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    events = torch.empty(m, 4 + btg.size(1), dtype=torch.int32, device=dev)
+    slot_map = torch.zeros(base.numel(), dtype=torch.int32, device=dev)
     flush = torch.ones(128 * 1024 * 1024, dtype=torch.int32, device=dev)  # 512 MiB
     stream = torch.cuda.current_stream()
     lens = cw["context_lens"][cw["seq_idx"]].to(torch.int64)
     tails = lens % 256
     nbytes = m * 1024 * 2048 + m * Hq * 128 * 2 + 2 * int((513 + tails).sum()) * 4096
-    res = {f"compress_parity_{agg}": compress_parity(cw, dev, agg) for agg in ("group", "all")}
-    for agg in ("group", "all"):
-        n_sets = 1 if agg == "all" else Hk
-        imp = torch.empty(m, n_sets, 1023, dtype=torch.float32, device=dev)
-        keep = torch.empty(m, n_sets, 513, dtype=torch.int32, device=dev)
+    res = {f"compress_parity_{agg}": compress_parity(q, kg, vg, cw["block_tables"],
+                                                     cw["context_lens"], cw["seq_idx"], agg, dev)
+           for agg in ("group", "all")}
 
-        def one():
-            cu.compress_step(q, kg, vg, btg, base, ctx, sel, 4, 513, 128 ** -0.5, agg,
-                             importance=imp, keep_idx=keep, workspace=ws)
-
-        for _ in range(3):
-            one()
+    def timed(fn, reps):
         times = []
-        for _ in range(args.compress_reps):
+        for i in range(3 + reps):
+            btg.copy_(bt0)  # the finalize's table rewrite is undone outside the timed region
             # evict the window from the 256 MB last-level cache by READING 512 MiB: the
             # cache is left holding clean lines, as after the decode kernels that run
             # between compression steps (a fill would leave 256 MB of dirty lines
@@ -322,14 +338,33 @@ def run_compress(args, dev):
             a = torch.cuda.Event(enable_timing=True)
             b = torch.cuda.Event(enable_timing=True)
             a.record(stream)
-            one()
+            fn()
             b.record(stream)
             torch.cuda.synchronize()
-            times.append(a.elapsed_time(b) * 1000.0)
-        med = statistics.median(times)
+            if i >= 3:
+                times.append(a.elapsed_time(b) * 1000.0)
+        return statistics.median(times)
+
+    for agg in ("group", "all"):
+        n_sets = 1 if agg == "all" else Hk
+        imp = torch.empty(m, n_sets, 1023, dtype=torch.float32, device=dev)
+        keep = torch.empty(m, n_sets, 513, dtype=torch.int32, device=dev)
+
+        def step():
+            cu.compress_step(q, kg, vg, btg, base, ctx, sel, 4, 513, 128 ** -0.5, agg,
+                             importance=imp, keep_idx=keep, workspace=ws)
+
+        def full_step():
+            step()
+            cu.compress_finalize(btg, base, sel, 513, 256, 4, events, rewrite_tables=True,
+                                 slot_mapping=slot_map)
+
+        med = timed(full_step, args.compress_reps)
         key = "compress_step_us" if agg == "group" else "compress_step_all_us"
         res[key] = round(med, 2)
         res[key.replace("_us", "_gbs")] = round(nbytes / (med * 1e-6) / 1e9, 1)
+        key2 = "compress_select_compact_us" if agg == "group" else "compress_select_compact_all_us"
+        res[key2] = round(timed(step, args.compress_reps), 2)
     # the same step over an fp8 (E4M3FN) copy of the pool (agg "group")
     kvc = importlib.import_module("nanokv-llm_amd.layers.kv_cache")
     kq, vq = kvc.fp8_quantize(kg), kvc.fp8_quantize(vg)
@@ -352,9 +387,12 @@ def run_compress(args, dev):
     if not args.no_cpu_baseline:
         res["compress_cpu_baseline"] = cpu_compress_baseline()
     res.update({"compress_bytes": nbytes, "compress_sequences": m,
-                "compress_config": "agg group (importance summed over each GQA group, kept "
-                                   "set per KV head); compress_step_all_*: all-head importance; "
-                                   "compress_step_fp8_us: agg group over an fp8 pool"})
+                "compress_config": "the full step (compress_step + compress_finalize: tables, slots, "
+                                   "events); agg group (importance summed over each GQA group, "
+                                   "kept set per KV head); compress_step_all_*: all-head "
+                                   "importance; compress_select_compact_*: without the "
+                                   "finalize; compress_step_fp8_us: agg group over an fp8 pool "
+                                   "(select + compact)"})
     return res
 
 
@@ -745,27 +783,35 @@ def run_longctx(args, dev):
     step_ms = e0.elapsed_time(e1) / args.longctx_steps
     nbytes = wl_mod.decode_bytes(wl["context_lens"], Hq, Hk, D, width)
     parity = parity_sample(wl, bt, out, kc, vc, n=4)
-    # compression: the 20 longest sequences eligible under the engine's rule
+    # compression: the 20 longest sequences eligible under the engine's rule, checked against
+    # the oracle on a copy of their blocks, then timed as the full step (select + compact +
+    # table, slot and event update; the table rewrite undone outside the timed region)
+    sel_list = wl_mod.eligible_longest(wl["context_lens"].tolist(),
+                                       wl["tail_uncompressed"].tolist(), 20, B, 4)
     lens = wl["context_lens"].tolist()
-    tail_unc = wl["tail_uncompressed"].tolist()
-    elig = [i for i, n in enumerate(lens)
-            if n % B != B - 1 and tail_unc[i] >= 4 * B and n // B >= 4]
-    sel_list = sorted(sorted(elig, key=lambda i: (-lens[i], i))[:20])
+    comp_parity = {agg: compress_parity(q, kc, vc, bt, ctx, sel_list, agg, dev)
+                   for agg in ("group", "all")}
     sel = torch.tensor(sel_list, dtype=torch.int32, device=dev)
     base = ctx.clone()
     cl = ctx.clone()
+    bt_c = bt.clone()
     m = sel.numel()
     cws = torch.empty(cu.select_workspace_bytes(m, Hq, Hk, 4, B), dtype=torch.uint8, device=dev)
     imp = torch.empty(m, Hk, 4 * B - 1, dtype=torch.float32, device=dev)
     keep = torch.empty(m, Hk, 513, dtype=torch.int32, device=dev)
+    ev_c = torch.empty(m, 4 + width, dtype=torch.int32, device=dev)
+    slot_c = slots.clone()
     flush = torch.ones(128 * 1024 * 1024, dtype=torch.int32, device=dev)
     times = []
     for i in range(3 + args.compress_reps):
+        bt_c.copy_(bt)
         flush.sum()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record(stream)
-        cu.compress_step(q, kc, vc, bt, base, cl, sel, 4, 513, D ** -0.5, "group",
+        cu.compress_step(q, kc, vc, bt_c, base, cl, sel, 4, 513, D ** -0.5, "group",
                          importance=imp, keep_idx=keep, workspace=cws)
+        cu.compress_finalize(bt_c, base, sel, 513, B, 4, ev_c, rewrite_tables=True,
+                             slot_mapping=slot_c)
         b.record(stream)
         torch.cuda.synchronize()
         if i >= 3:
@@ -786,10 +832,12 @@ def run_longctx(args, dev):
     def device_step():
         cu.compress_schedule(ctx, tails_d, B, 4, 20, 1, counter, sel_d, n_sel, base_d,
                              policy="longest")
-        cu.compress_step(q, kc, vc, bt, base_d, cl, sel_d, 4, 513, D ** -0.5, "group",
+        cu.compress_step(q, kc, vc, bt_c, base_d, cl, sel_d, 4, 513, D ** -0.5, "group",
                          importance=imp20, keep_idx=keep20, workspace=cws20)
-        cu.compress_finalize(bt, base_d, sel_d, 513, B, 4, ev, rewrite_tables=False)
+        cu.compress_finalize(bt_c, base_d, sel_d, 513, B, 4, ev, rewrite_tables=True,
+                             slot_mapping=slot_c)
 
+    bt_c.copy_(bt)
     device_step()
     torch.cuda.synchronize()
     same_selection = sorted(x for x in sel_d.tolist() if x >= 0) == sel_list
@@ -798,6 +846,7 @@ def run_longctx(args, dev):
         device_step()
     gtimes = []
     for i in range(3 + args.compress_reps):
+        bt_c.copy_(bt)
         flush.sum()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record(stream)
@@ -817,6 +866,8 @@ def run_longctx(args, dev):
         "longctx_decode_gbs": round(gbs, 1),
         "longctx_pct_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 1),
         "longctx_parity_max_abs_err": parity,
+        "longctx_compress_parity_group": comp_parity["group"],
+        "longctx_compress_parity_all": comp_parity["all"],
         "longctx_compress_step_us": round(comp_us, 2),
         "longctx_compress_amortized_us_per_step": round(comp_us / 1024, 3),
         "longctx_compress_graph_us": round(statistics.median(gtimes), 2),

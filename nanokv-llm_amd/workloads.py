@@ -21,6 +21,9 @@ Workloads (sizes from the reference's Qwen3 geometries, block size 256):
                       of the sequences already compressed once (shorter context),
                       a pool sized to fill most of HBM with only the used blocks
                       written
+  compress_qwen3_32b_longctx  the compression step on that state: the 20 longest
+                      sequences eligible under the engine's rule, W = 4 blocks,
+                      keep 2*256+1, only the selected sequences owning blocks
 """
 from __future__ import annotations
 
@@ -243,3 +246,33 @@ def decode_qwen3_32b_longctx(seed=6, device="cpu", bs=500, n_blocks=None, frac_c
                 context_lens=ctx.to(torch.int32), block_tables=[table],
                 slot_mappings=[slot_of(table, ctx - 1)], scale=D ** -0.5, Hq=Hq, Hk=Hk,
                 compressed=compressed, tail_uncompressed=tail_unc, n_blocks=n_blocks)
+
+
+def eligible_longest(context_lens, tail_uncompressed, topk, block=BLOCK, window_blocks=4):
+    """The topk longest sequences (ties to the lower index) that the engine's scheduling rule
+    admits to a compression step (nanokvllm/engine/model_runner.py:313-323): len % B != B-1,
+    tokens since the last compression >= W*B and len // B >= W. Returned in batch order."""
+    lens = [int(x) for x in context_lens]
+    tails = [int(x) for x in tail_uncompressed]
+    elig = [i for i, n in enumerate(lens)
+            if n % block != block - 1 and tails[i] >= window_blocks * block
+            and n // block >= window_blocks]
+    return sorted(sorted(elig, key=lambda i: (-lens[i], i))[:topk])
+
+
+def compress_qwen3_32b_longctx(seed=6, device="cpu", topk=20):
+    """The compression step of the long-context decode state at Qwen3-32B geometry (Hq 64,
+    Hk 8, batch 500): the lengths, tails and q of decode_qwen3_32b_longctx(seed), the topk
+    longest eligible sequences selected, and a compact pool in which only those sequences own
+    blocks (whole tables, up to 64 blocks each; the others keep their lengths and no cache)."""
+    st = decode_qwen3_32b_longctx(seed=seed, alloc_caches=False)
+    lens = st["context_lens"]
+    sel = eligible_longest(lens.tolist(), st["tail_uncompressed"].tolist(), topk)
+    gen = torch.Generator().manual_seed(seed * 7 + 6)
+    lens_for_tables = [int(lens[i]) if i in sel else 0 for i in range(lens.numel())]
+    n_blocks = sum(math.ceil(c / BLOCK) for c in lens_for_tables) + 8
+    table = assign_blocks(lens_for_tables, n_blocks, gen)
+    k_cache, v_cache = _kv_pool((n_blocks, BLOCK, 8, HEAD_DIM), seed, device)
+    return dict(q=st["q"], k_cache=k_cache, v_cache=v_cache, context_lens=lens,
+                block_tables=table, seq_idx=sel, tail_uncompressed=st["tail_uncompressed"],
+                Hq=64, Hk=8)

@@ -24,6 +24,8 @@ How each function is pinned (tests/test_oracle_*.py):
                             GQA == MHA with repeated K/V heads
   varlen_prefill_ref        SDPA(is_causal) for Lq == Lk; last query row ==
                             decode; chunked == one-shot; float64 loops
+  varlen_prefill_rows_ref   the same rows of varlen_prefill_ref; each row ==
+                            decode over the keys it sees
   snapkv_ref / select_topk  float64 brute force on tiny windows with planted
                             sink / head-sum / scale / last-token cases;
                             bf16 path == fp32 path on well-separated scores

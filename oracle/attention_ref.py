@@ -90,3 +90,35 @@ def varlen_prefill_ref(q, k, v, cu_seqlens_q, cu_seqlens_k, scale, block_tables=
         p = torch.nan_to_num(p, nan=0.0)  # fully masked rows (Lk < Lq) -> 0
         out[q0:q1] = torch.bmm(p, Vh).permute(1, 0, 2)
     return out
+
+
+def varlen_prefill_rows_ref(q_rows, seq_of_row, pos_of_row, k_cache, v_cache, cu_seqlens_q,
+                            cu_seqlens_k, scale, block_tables):
+    """Selected output rows of varlen_prefill_ref (paged K/V), without the other rows.
+
+    Row r is query pos_of_row[r] (0-based within its chunk) of sequence seq_of_row[r]:
+    it sees keys 0 .. Lk-Lq+pos of that sequence (attention.py:96-102, bottom-right
+    causal). q_rows [R, Hq, D]; returns fp32 [R, Hq, D]. The K/V of each sequence are
+    gathered once for all of its rows, so long sequences cost O(rows * Lk).
+    """
+    R, Hq, D = q_rows.shape
+    Hk = k_cache.size(-2)
+    g = Hq // Hk
+    out = torch.zeros(R, Hq, D, dtype=torch.float32)
+    seq_of_row = torch.as_tensor(seq_of_row, dtype=torch.int64)
+    pos_of_row = torch.as_tensor(pos_of_row, dtype=torch.int64)
+    for i in sorted(set(seq_of_row.tolist())):
+        rows = (seq_of_row == i).nonzero().view(-1)
+        Lq = int(cu_seqlens_q[i + 1]) - int(cu_seqlens_q[i])
+        Lk = int(cu_seqlens_k[i + 1]) - int(cu_seqlens_k[i])
+        K = gather_paged_rows(k_cache, block_tables[i], Lk).float()
+        V = gather_paged_rows(v_cache, block_tables[i], Lk).float()
+        Kh = K.permute(1, 0, 2).repeat_interleave(g, dim=0)  # [Hq, Lk, D]
+        Vh = V.permute(1, 0, 2).repeat_interleave(g, dim=0)
+        Q = q_rows[rows].float().permute(1, 0, 2)  # [Hq, r, D]
+        s = torch.bmm(Q, Kh.transpose(1, 2)) * scale  # [Hq, r, Lk]
+        last = (Lk - Lq) + pos_of_row[rows].view(-1, 1)  # last visible key of each row
+        s = s.masked_fill(torch.arange(Lk).view(1, -1) > last, float("-inf"))
+        p = torch.nan_to_num(torch.softmax(s, dim=-1), nan=0.0)
+        out[rows] = torch.bmm(p, Vh).permute(1, 0, 2)
+    return out

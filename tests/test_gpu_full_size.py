@@ -4,7 +4,9 @@
   64 sequences against the fp32 oracle (max abs err <= 2e-2).
 * The compression step at batch 500 (seed 3: the 20 longest, W 4, keep 513), both
   aggregations: importance within rtol 1e-4 of the fp32 oracle, kept sets exact given the
-  scores, caches, lengths, events, block tables and slot maps bit-exact.
+  scores, caches, lengths, events, block tables and slot maps bit-exact. The same for the
+  long-context state at Qwen3-32B geometry (seed 6: Hq 64 over Hk 8, the 20 longest
+  eligible sequences).
 * Long-context decode at Qwen3-32B geometry (seed 6: batch 500, contexts log-uniform
   [1024, 16384], 20% compressed once): 72 of the 500 sequences against the oracle.
 * The same shape through a stack of Attention layers sharing one decode workspace.
@@ -63,20 +65,25 @@ def test_decode_qwen3_8b_all_sequences(nkv, dev):
     assert err <= TOL
 
 
-@pytest.mark.parametrize("agg", ["group", "all"])
-def test_compress_step_qwen3_8b_batch_500(nkv, dev, agg):
-    cw = wl_mod.compress_qwen3_8b(seed=3, device=dev, selected_only=True)
+def _check_compress_step(cw, dev, agg):
+    """The compression step (compress_step + compress_finalize with the table and slot
+    rewrite) on a compact copy of the state against the oracle: importance within rtol 1e-4
+    of the fp32 oracle, kept sets exact given the scores, caches, lengths, events, block
+    tables and slot maps bit-exact."""
     kc0, vc0 = cw["k_cache"].cpu(), cw["v_cache"].cpu()
     kg, vg = cw["k_cache"], cw["v_cache"]
     bt, lens, sel = cw["block_tables"], cw["context_lens"], cw["seq_idx"]
-    assert len(sel) == 20 and lens.numel() == 500
+    bs, Hq, D = cw["q"].shape
+    m = len(sel)
+    print(f"compression step: batch {bs}, Hq {Hq}, Hk {kg.size(2)}, {m} sequences, agg {agg}",
+          flush=True)
     btg, base = bt.to(dev), lens.to(dev)
     ctx = base.clone()
     seq_idx = torch.tensor(sel, dtype=torch.int32, device=dev)
-    slot_map = torch.arange(500, dtype=torch.int32, device=dev) * 3
+    slot_map = torch.arange(bs, dtype=torch.int32, device=dev) * 3
     keep, imp = cu.compress_step(cw["q"].to(dev), kg, vg, btg, base, ctx, seq_idx, 4, 513,
-                                 128 ** -0.5, agg)
-    events = torch.empty(20, 4 + bt.size(1), dtype=torch.int32, device=dev)
+                                 D ** -0.5, agg)
+    events = torch.empty(m, 4 + bt.size(1), dtype=torch.int32, device=dev)
     cu.compress_finalize(btg, base, seq_idx, 513, 256, 4, events, rewrite_tables=True,
                          slot_mapping=slot_map)
     torch.cuda.synchronize()
@@ -96,13 +103,34 @@ def test_compress_step_qwen3_8b_batch_500(nkv, dev, agg):
     assert torch.equal(ctx.cpu(), ctx_ref)
     assert cu.events_to_dicts(events, 0) == ev_ref
     bt_exp = bt.clone()
-    slot_exp = torch.arange(500, dtype=torch.int32) * 3
+    slot_exp = torch.arange(bs, dtype=torch.int32) * 3
     for ev in ev_ref:
         s, n = ev["batch_index"], ev["new_context_len"]
         bt_exp[s, ev["keep_blocks"]:] = -1
-        slot_exp[s] = int(bt[s, n // 256]) * 256 + n % 256
+        # the next token's slot; position n opens a freed block when n % 256 == 0
+        slot_exp[s] = -1 if n % 256 == 0 else int(bt[s, n // 256]) * 256 + n % 256
     assert torch.equal(btg.cpu(), bt_exp)
     assert torch.equal(slot_map.cpu(), slot_exp)
+
+
+@pytest.mark.parametrize("agg", ["group", "all"])
+def test_compress_step_qwen3_8b_batch_500(nkv, dev, agg):
+    cw = wl_mod.compress_qwen3_8b(seed=3, device=dev, selected_only=True)
+    assert len(cw["seq_idx"]) == 20 and cw["context_lens"].numel() == 500
+    _check_compress_step(cw, dev, agg)
+
+
+@pytest.mark.parametrize("agg", ["group", "all"])
+def test_compress_step_qwen3_32b_longctx_batch_500(nkv, dev, agg):
+    """The long-context state's compression step at its own geometry: Hq 64 over Hk 8
+    (group 8), the 20 longest eligible sequences (15-16k tokens, 64-block tables), window
+    4 blocks, keep 513."""
+    cw = wl_mod.compress_qwen3_32b_longctx(seed=6, device=dev)
+    assert len(cw["seq_idx"]) == 20 and cw["q"].shape == (500, 64, 128)
+    assert cw["block_tables"].size(1) == 64
+    _check_compress_step(cw, dev, agg)
+    del cw
+    torch.cuda.empty_cache()
 
 
 def test_decode_qwen3_32b_batch_500(nkv, dev):

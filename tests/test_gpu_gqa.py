@@ -85,7 +85,7 @@ def test_prefill_gqa_groups(nkv, dev, Hq, Hk, paged):
     assert (out.float().cpu() - ref).abs().max().item() <= TOL
 
 
-@pytest.mark.parametrize("Hq,Hk", [(24, 8), (40, 8), (48, 8), (56, 8), (128, 8)])
+@pytest.mark.parametrize("Hq,Hk", [(24, 8), (40, 8), (48, 8), (56, 8), (64, 8), (128, 8)])
 @pytest.mark.parametrize("agg", ["all", "group"])
 def test_compress_step_gqa_groups(nkv, dev, Hq, Hk, agg):
     wl = wl_mod.compress_workload(40, Hq, Hk, 1500, 4096, 6, seed=Hq + Hk, selected_only=True)

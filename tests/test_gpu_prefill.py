@@ -5,7 +5,7 @@ from types import SimpleNamespace
 import pytest
 import torch
 
-from oracle.attention_ref import store_kvcache_ref, varlen_prefill_ref
+from oracle.attention_ref import store_kvcache_ref, varlen_prefill_ref, varlen_prefill_rows_ref
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-2
@@ -227,3 +227,36 @@ def test_prefill_last_rows_match_decode_full_size(nkv, dev):
     dec = nkv.paged_decode(wl["q"][last].contiguous(), kc, vc, ctx, bt, wl["scale"])
     torch.cuda.synchronize()
     assert (dec.float() - out[last].float()).abs().max().item() <= TOL
+
+
+def test_prefill_chunked_sampled_rows_full_size(nkv, dev):
+    """The full chunked workload (16 sequences, 2048-token chunks after paged prefixes
+    U[0,8192], Lk up to ~10k): for every sequence its last 64 query rows and 64 random rows
+    against the oracle, max abs err <= 2e-2."""
+    wl = wl_mod.prefill_chunked_qwen3_8b(device=dev)
+    kc, vc = wl["k_cache"], wl["v_cache"]
+    nkv.store_kvcache(wl["key"], wl["value"], kc, vc, wl["slot_mapping"].to(dev))
+    out = nkv.varlen_prefill(wl["q"], kc, vc, wl["cu_seqlens_q"].to(dev),
+                             wl["cu_seqlens_k"].to(dev), wl["max_seqlen_q"], wl["scale"],
+                             block_tables=wl["block_tables"].to(dev))
+    torch.cuda.synchronize()
+    g = torch.Generator().manual_seed(55)
+    cq = wl["cu_seqlens_q"]
+    seq, pos = [], []
+    for i, lq in enumerate(wl["Lq"]):
+        picks = set(range(lq - 64, lq)) | set(torch.randperm(lq, generator=g)[:64].tolist())
+        seq += [i] * len(picks)
+        pos += sorted(picks)
+    rows = torch.tensor([int(cq[s]) + p for s, p in zip(seq, pos)])
+    kh, vh = kc.cpu(), vc.cpu()
+    err = 0.0
+    for i in range(len(wl["Lq"])):
+        sel = [r for r, s in enumerate(seq) if s == i]
+        ref = varlen_prefill_rows_ref(wl["q"][rows[sel]].cpu(), [i] * len(sel),
+                                      [pos[r] for r in sel], kh, vh, cq, wl["cu_seqlens_k"],
+                                      wl["scale"], wl["block_tables"])
+        e = (out[rows[sel].to(dev)].float().cpu() - ref).abs().max().item()
+        print(f"chunked seq {i}: Lk {wl['Lk'][i]}, {len(sel)} rows, max abs err {e:.2e}",
+              flush=True)
+        err = max(err, e)
+    assert max(wl["Lk"]) > 9000 and err <= TOL

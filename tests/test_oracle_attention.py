@@ -11,7 +11,7 @@ import torch
 import torch.nn.functional as F
 
 from oracle.attention_ref import (gather_paged_rows, paged_decode_ref, store_kvcache_ref,
-                                  varlen_prefill_ref)
+                                  varlen_prefill_ref, varlen_prefill_rows_ref)
 
 
 def _pool(nb, B, Hk, D, seed):
@@ -169,3 +169,27 @@ def test_prefill_chunk_bottom_right_and_decode_row():
     dec2 = paged_decode_ref(q[Lk - Lq:Lk - Lq + 1], kc, vc,
                             torch.tensor([Lk - Lq + 1], dtype=torch.int32), bt, 0.3)
     assert torch.allclose(chunk[0], dec2[0], atol=1e-5)
+
+
+def test_prefill_rows_equal_full_rows_and_decode():
+    """varlen_prefill_rows_ref: the sampled rows of varlen_prefill_ref (chunked, GQA, paged),
+    and each row equals decode over the keys it sees (Lk - Lq + pos + 1)."""
+    kc, vc = _pool(12, 8, 2, 16, 21)
+    g = torch.Generator().manual_seed(22)
+    Lq, Lk = [5, 9, 1], [11, 9, 30]
+    bt = torch.tensor([[3, 7, -1, -1], [0, 11, -1, -1], [9, 2, 5, 1]], dtype=torch.int32)
+    cq = torch.tensor([0, 5, 14, 15], dtype=torch.int32)
+    ck = torch.tensor([0, 11, 20, 50], dtype=torch.int32)
+    q = torch.randn(15, 4, 16, generator=g)
+    full = varlen_prefill_ref(q, kc, vc, cq, ck, 0.3, block_tables=bt)
+    picks = [(0, 0), (0, 4), (1, 8), (1, 2), (2, 0), (0, 2)]
+    seq = [s for s, _ in picks]
+    pos = [p for _, p in picks]
+    rows = torch.tensor([int(cq[s]) + p for s, p in picks])
+    got = varlen_prefill_rows_ref(q[rows], seq, pos, kc, vc, cq, ck, 0.3, bt)
+    assert torch.allclose(got, full[rows], atol=1e-6)
+    for r, (s, p) in enumerate(picks):
+        n = Lk[s] - Lq[s] + p + 1
+        dec = paged_decode_ref(q[rows[r]:rows[r] + 1], kc, vc, torch.tensor([n], dtype=torch.int32),
+                               bt[s:s + 1], 0.3)
+        assert torch.allclose(got[r], dec[0], atol=1e-5)
