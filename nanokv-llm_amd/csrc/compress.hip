@@ -784,8 +784,10 @@ __global__ __launch_bounds__(kSelThreads) void compress_group_kernel(
   __shared__ SelectLds L;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int kvh = blockIdx.x % Hk;
   const int j = blockIdx.x / Hk;
+  // workgroups go to the XCDs round-robin: rotating the head by the sequence gives each
+  // XCD's L2 every head's 256-byte column of the token rows instead of always the same one
+  const int kvh = (blockIdx.x + j) % Hk;
   if (block_tables && seq_idx[j] < 0) return;  // padding entry (uniform): nothing written
   const int Lw = window_blocks * block_size;
   const int n_cand = Lw - 1;
@@ -828,8 +830,8 @@ __global__ __launch_bounds__(kSelThreads) void compress_partial_kernel(
     float* __restrict__ partial) {
   __shared__ SelectLds L;
   const int lane = threadIdx.x & 63;
-  const int kvh = blockIdx.x % Hk;
   const int j = blockIdx.x / Hk;
+  const int kvh = (blockIdx.x + j) % Hk;  // rotated as in compress_group_kernel
   if (block_tables && seq_idx[j] < 0) return;  // padding entry (uniform): nothing written
   const int Lw = window_blocks * block_size;
   float gi[4];
@@ -859,7 +861,7 @@ __global__ __launch_bounds__(kSelThreads) void compress_sum_kernel(
   __shared__ SelectLds L;
   const int tid = threadIdx.x;
   const int j = blockIdx.x / n_units_per_seq;
-  const int kvh = blockIdx.x % n_units_per_seq;
+  const int kvh = (blockIdx.x + j) % n_units_per_seq;  // rotated as in compress_group_kernel
   if (block_tables && seq_idx[j] < 0) return;  // padding entry (uniform): nothing written
   const int Lw = window_blocks * block_size;
   const int n_cand = Lw - 1;
@@ -970,6 +972,9 @@ __global__ __launch_bounds__(256) void compress_compact_kernel(
 }
 
 // ---------------------------------------------------------------- finalize
+// One wave per selected sequence: the lanes walk its table row 64 entries at a time, the
+// freed block ids (entries past the kept blocks, in table order) are packed by a ballot
+// prefix count, and the row's tail is cleared by the same lanes after the reads.
 __global__ __launch_bounds__(64) void compress_finalize_kernel(
     int32_t* __restrict__ block_tables, int64_t bt_row_stride, int32_t max_blocks,
     const int32_t* __restrict__ base_context_lens, const int32_t* __restrict__ seq_idx,
@@ -977,36 +982,43 @@ __global__ __launch_bounds__(64) void compress_finalize_kernel(
     int32_t rewrite_tables, int32_t* __restrict__ slot_mapping, int32_t* __restrict__ events) {
   const int B = block_size;
   const int ev_len = 4 + max_blocks;
-  for (int j = threadIdx.x; j < m; j += blockDim.x) {
-    const int seq = seq_idx[j];
-    const int len = seq >= 0 ? base_context_lens[seq] : 0;  // seq -1: padding entry
-    int32_t* ev = events + (int64_t)j * ev_len;
-    int32_t* bt = block_tables + (int64_t)seq * bt_row_stride;
-    const int full = len / B, tail = len - (len / B) * B;
-    // same skip rule as the compaction: not compressible -> left unchanged and marked
-    // skipped (n_freed = -1), so the host changes none of its state; a padding entry
-    // (seq -1) reads [-1, 0, 0, 0, -1...]
-    if (full < window_blocks || full > max_blocks || (tail > 0 && full >= max_blocks)) {
+  const int j = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int seq = seq_idx[j];
+  const int len = seq >= 0 ? base_context_lens[seq] : 0;  // seq -1: padding entry
+  int32_t* ev = events + (int64_t)j * ev_len;
+  int32_t* bt = block_tables + (int64_t)(seq >= 0 ? seq : 0) * bt_row_stride;
+  const int full = len / B, tail = len - (len / B) * B;
+  // same skip rule as the compaction: not compressible -> left unchanged and marked
+  // skipped (n_freed = -1), so the host changes none of its state; a padding entry
+  // (seq -1) reads [-1, 0, 0, 0, -1...]
+  if (full < window_blocks || full > max_blocks || (tail > 0 && full >= max_blocks)) {
+    if (lane == 0) {
       ev[0] = seq; ev[1] = len; ev[2] = (len + B - 1) / B; ev[3] = seq >= 0 ? -1 : 0;
-      for (int i = 0; i < max_blocks; ++i) ev[4 + i] = -1;
-      continue;
     }
-    const int new_len = len - window_blocks * B + keep_tokens;
-    const int keep_blocks = (new_len + B - 1) / B;
-    int n = 0;
-    for (int i = keep_blocks; i < max_blocks; ++i) {
-      const int id = bt[i];
-      if (id >= 0) ev[4 + n++] = id;
-    }
-    for (int i = n; i < max_blocks; ++i) ev[4 + i] = -1;
-    ev[0] = seq; ev[1] = new_len; ev[2] = keep_blocks; ev[3] = n;
-    if (rewrite_tables)
-      for (int i = keep_blocks; i < max_blocks; ++i) bt[i] = -1;
-    if (slot_mapping) {
-      const int blk = new_len / B, off = new_len % B;
-      slot_mapping[seq] = (off == 0 || blk >= max_blocks || bt[blk] < 0) ? -1 : bt[blk] * B + off;
-    }
+    for (int i = lane; i < max_blocks; i += 64) ev[4 + i] = -1;
+    return;
   }
+  const int new_len = len - window_blocks * B + keep_tokens;
+  const int keep_blocks = (new_len + B - 1) / B;
+  int n = 0;  // freed ids packed so far (uniform)
+  for (int i0 = keep_blocks; i0 < max_blocks; i0 += 64) {
+    const int i = i0 + lane;
+    const int id = i < max_blocks ? bt[i] : -1;
+    const uint64_t valid = __builtin_amdgcn_ballot_w64(id >= 0);
+    if (id >= 0) ev[4 + n + __builtin_popcountll(valid & ((1ull << lane) - 1ull))] = id;
+    n += __builtin_popcountll(valid);
+  }
+  for (int i = n + lane; i < max_blocks; i += 64) ev[4 + i] = -1;
+  // the next token's slot, from an entry the rewrite keeps (blk < keep_blocks)
+  const int blk = new_len / B, off = new_len % B;
+  const int pb = (off == 0 || blk >= max_blocks) ? -1 : bt[blk];
+  if (lane == 0) {
+    ev[0] = seq; ev[1] = new_len; ev[2] = keep_blocks; ev[3] = n;
+    if (slot_mapping) slot_mapping[seq] = pb < 0 ? -1 : pb * B + off;
+  }
+  if (rewrite_tables)  // after this wave's reads of the row (program order within the wave)
+    for (int i = keep_blocks + lane; i < max_blocks; i += 64) bt[i] = -1;
 }
 
 // ----------------------------------------------------------------- schedule
@@ -1435,7 +1447,7 @@ extern "C" int nkv_compress_finalize(int32_t* block_tables, int64_t bt_row_strid
               "compress_finalize: null pointer");
   NKV_REQUIRE(bt_row_stride >= max_blocks_per_seq, NKV_EINVAL,
               "compress_finalize: bt_row_stride < max_blocks_per_seq");
-  hipLaunchKernelGGL(compress_finalize_kernel, dim3(1), dim3(64), 0, as_stream(stream),
+  hipLaunchKernelGGL(compress_finalize_kernel, dim3((unsigned)m), dim3(64), 0, as_stream(stream),
                      block_tables, bt_row_stride, max_blocks_per_seq, base_context_lens, seq_idx,
                      m, keep_tokens, block_size, window_blocks, rewrite_tables, slot_mapping,
                      events);

@@ -23,7 +23,8 @@ B, W = 256, 4
 
 
 @pytest.mark.parametrize("policy", ["first", "longest"])
-@pytest.mark.parametrize("bs,topk", [(1, 1), (37, 5), (500, 20), (3000, 64)])
+@pytest.mark.parametrize("bs,topk", [(1, 1), (37, 5), (500, 20), (1024, 64), (64, 64),
+                                     (1025, 20), (200, 65), (3000, 64)])
 def test_schedule_kernel_matches_oracle(dev, policy, bs, topk):
     rng = random.Random(bs * 3 + topk)
     counter_d = torch.zeros(1, dtype=torch.int32, device=dev)
