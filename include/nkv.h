@@ -73,6 +73,8 @@ int nkv_debug_flags(uint32_t* flags, int clear);
  * would write out of bounds there).
  * key/value rows may be strided views (e.g. the v part of a fused qkv
  * projection): element (i, h, d) lives at ptr[i*row_stride + h*head_dim + d].
+ * Elements are 2-byte (bf16 or fp16, the model's dtype): the rows are copied
+ * as they are.
  * Replaces: store_kvcache / store_kvcache_kernel,
  *           nanokvllm/layers/attention.py:10-40
  */
@@ -140,6 +142,21 @@ int nkv_qk_norm_rope_store(const void* q, int64_t q_row_stride, const void* k,
                            int64_t n_slots, int64_t n_tokens, int32_t n_q_heads,
                            int32_t n_kv_heads, int32_t head_dim, void* stream);
 
+/* fp16 model dtype: nkv_qk_norm_rope_store with q, k, v, the norm weights, q_out,
+ * k_out and the caches in fp16 and every rounding to fp16 (the reference's
+ * .to(orig_dtype) for an fp16 checkpoint). Replaces: the same calls
+ * (qwen3.py:109-113, layernorm.py:16-26, rotary_embedding.py:7-49,
+ * attention.py:71-73) when torch_dtype is float16 (model_runner.py:27). */
+int nkv_qk_norm_rope_store_f16(const void* q, int64_t q_row_stride, const void* k,
+                               int64_t k_row_stride, const void* v, int64_t v_row_stride,
+                               const int64_t* positions, const void* q_norm_weight,
+                               const void* k_norm_weight, float eps,
+                               const float* cos_sin_cache, int64_t max_position,
+                               void* q_out, int64_t q_out_row_stride, void* k_out,
+                               void* k_cache, void* v_cache, const int32_t* slot_mapping,
+                               int64_t n_slots, int64_t n_tokens, int32_t n_q_heads,
+                               int32_t n_kv_heads, int32_t head_dim, void* stream);
+
 /*
  * Paged decode attention (one query token per sequence, GQA, causal with the
  * new token already stored): for b < batch, query head h,
@@ -156,7 +173,9 @@ int nkv_qk_norm_rope_store(const void* q, int64_t q_row_stride, const void* k,
  * q[b,h,d] at q[b*q_row_stride + h*head_dim + d]; out likewise with
  * out_row_stride. head_dim 64, 128 or 256 (out then 2-, 4- or 8-byte aligned
  * with a row stride that is a multiple of head_dim/64); any GQA group
- * n_q_heads/n_kv_heads up to 16; block_size a multiple of 16. Block-table
+ * n_q_heads/n_kv_heads up to 256 (above 16 the group's query heads are split
+ * over ceil(g/16) waves, each reading the KV head's rows: K/V are then read
+ * ceil(g/16) times); block_size a multiple of 16. Block-table
  * entries outside [0, n_blocks) contribute nothing.
  * Replaces: flash_attn_with_kvcache(q.unsqueeze(1), k_cache, v_cache,
  *           cache_seqlens=context_lens, block_table=block_tables,
@@ -215,6 +234,21 @@ int nkv_paged_decode_fp8(const void* q, int64_t q_row_stride,
                          void* out, int64_t out_row_stride,
                          void* workspace, size_t workspace_bytes, void* stream);
 
+/* Paged decode for an fp16 model: nkv_paged_decode with q, the caches and out in
+ * fp16 (fp16 MFMA, fp32 softmax and accumulation). Same workspace size.
+ * Replaces: the same flash_attn_with_kvcache call (attention.py:104-107) with
+ * the fp16 pool the reference allocates for a float16 checkpoint
+ * (model_runner.py:27, 142-145). */
+int nkv_paged_decode_f16(const void* q, int64_t q_row_stride,
+                         const void* k_cache, const void* v_cache,
+                         const int32_t* block_tables, int64_t bt_row_stride,
+                         const int32_t* context_lens, int32_t batch,
+                         int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                         int32_t block_size, int32_t max_blocks_per_seq,
+                         int64_t n_blocks, float scale,
+                         void* out, int64_t out_row_stride,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
 /* The two stages nkv_paged_decode launches, exported so a caller can time or
  * schedule them separately. Same arguments as nkv_paged_decode.
  * Replaces: the same flash_attn_with_kvcache call (attention.py:104-107). */
@@ -244,7 +278,8 @@ int nkv_paged_decode_combine(const int32_t* context_lens, int32_t batch,
  * view of the qkv projection; paged caches share one stride). Table entries at or beyond
  * max_blocks_per_seq, negative, or past n_rows read as zero keys/values.
  * q/out are [sum Lq, Hq, D] with row strides. head_dim 64, 128 or 256; any
- * GQA group Hq/Hk up to 16. Rows with no visible key (Lk < Lq) are zero.
+ * GQA group Hq/Hk up to 128 (64 at head_dim 256: a tile holds 128 (64) query x
+ * head rows). Rows with no visible key (Lk < Lq) are zero.
  * Replaces: flash_attn_varlen_func(q, k, v, max_seqlen_q, cu_seqlens_q,
  *           max_seqlen_k, cu_seqlens_k, softmax_scale, causal=True,
  *           block_table), nanokvllm/layers/attention.py:96-102
@@ -273,6 +308,19 @@ int nkv_prefill_varlen_fp8(const void* q, int64_t q_row_stride,
                            int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
                            int32_t block_size, int64_t n_blocks, float scale, float k_scale,
                            float v_scale, void* out, int64_t out_row_stride, void* stream);
+
+/* Varlen causal prefill for an fp16 model: nkv_prefill_varlen with q, K/V (paged
+ * or contiguous) and out in fp16. Replaces: the flash_attn_varlen_func call
+ * (attention.py:96-102) for a float16 checkpoint (model_runner.py:27). */
+int nkv_prefill_varlen_f16(const void* q, int64_t q_row_stride,
+                           const void* k_cache, const void* v_cache, int64_t k_row_stride,
+                           int64_t v_row_stride,
+                           const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                           const int32_t* block_tables, int64_t bt_row_stride,
+                           int32_t max_blocks_per_seq, int32_t n_seqs, int32_t max_seqlen_q,
+                           int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                           int32_t block_size, int64_t n_rows, float scale,
+                           void* out, int64_t out_row_stride, void* stream);
 
 /* Aggregation of key importance over query heads (compression scoring). */
 #define NKV_AGG_ALL 0   /* sum over all Hq heads -> one kept set per sequence
@@ -330,7 +378,8 @@ int nkv_compress_topk(const float* importance, int32_t n_rows, int32_t n_cand,
  * two (agg "all": per-KV-head partial importance, then their sum and the
  * top-k) when W*B <= 1024 and B % 64 == 0 (the reference's W = 4, B = 256
  * qualifies); otherwise nkv_compress_score + nkv_compress_topk run on the
- * same workspace. Any GQA group Hq/Hk up to 16. Outputs are those of the two
+ * same workspace. Any GQA group Hq/Hk (the fused kernels take up to 16; larger
+ * groups score in passes of 16 query rows). Outputs are those of the two
  * calls:
  *   importance_out fp32 [m, n_sets, W*B-1],
  *   keep_idx int32 [m, n_sets, num_keep+2] = [0, ascending kept..., W*B-1].
@@ -352,6 +401,18 @@ int nkv_compress_select(const void* q, int64_t q_row_stride,
                         float scale, int32_t agg_mode, int32_t num_keep,
                         float* importance_out, int32_t* keep_idx,
                         void* workspace, size_t workspace_bytes, void* stream);
+/* nkv_compress_select with fp16 q and K (an fp16 pool). Replaces: the same
+ * scoring and selection for a float16 checkpoint. */
+int nkv_compress_select_f16(const void* q, int64_t q_row_stride,
+                            const void* k_cache, const int32_t* block_tables,
+                            int64_t bt_row_stride, int32_t max_blocks_per_seq,
+                            const int32_t* base_context_lens,
+                            const int32_t* seq_idx, int32_t m,
+                            int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                            int32_t block_size, int32_t window_blocks, int64_t n_blocks,
+                            float scale, int32_t agg_mode, int32_t num_keep,
+                            float* importance_out, int32_t* keep_idx,
+                            void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * SnapKV as the compression plug-in calls it (contiguous tensors): Q [m, Hq,
@@ -362,9 +423,9 @@ int nkv_compress_select(const void* q, int64_t q_row_stride,
  * importance_out fp32 [m, n_sets, n_cand] (n_sets 1 for ALL, Hk for GROUP),
  * keep_idx int32 [m, n_sets, num_keep + 1 + w] =
  *   [0, ascending top-num_keep (ties -> lower index), n_cand, ..., seq_len - 1].
- * window 1 is nkv_compress_select on the contiguous K; a window > 1 needs
- * seq_len a multiple of 256 and n_cand <= 4096. Workspace:
- * nkv_snapkv_workspace_bytes(...).
+ * window 1 is nkv_compress_select on the contiguous K; any seq_len (keys are
+ * scored in 256-key chunks, the last one masked) with n_cand <= 4096.
+ * Workspace: nkv_snapkv_workspace_bytes(...).
  * Replaces: SnapKV(Q, K, V, num_keep, window), nanokvllm/layers/CompressMethod.py:4-57
  *           (the policy API of CHANGE_LOG.md:197-208).
  */
@@ -375,6 +436,13 @@ int nkv_snapkv_select(const void* q, const void* k, int32_t m, int32_t n_q_heads
                       float scale, int32_t agg_mode, int32_t num_keep, float* importance_out,
                       int32_t* keep_idx, void* workspace, size_t workspace_bytes,
                       void* stream);
+/* nkv_snapkv_select with fp16 Q and K. Replaces: SnapKV (CompressMethod.py:4-57)
+ * on fp16 tensors. */
+int nkv_snapkv_select_f16(const void* q, const void* k, int32_t m, int32_t n_q_heads,
+                          int32_t n_kv_heads, int32_t head_dim, int32_t seq_len,
+                          int32_t window, float scale, int32_t agg_mode, int32_t num_keep,
+                          float* importance_out, int32_t* keep_idx, void* workspace,
+                          size_t workspace_bytes, void* stream);
 
 /*
  * One layer's compression step: nkv_compress_select (num_keep = keep_tokens-2)
@@ -395,6 +463,18 @@ int nkv_compress_step(const void* q, int64_t q_row_stride, void* k_cache, void* 
                       float scale, int32_t agg_mode, int32_t keep_tokens,
                       float* importance_out, int32_t* keep_idx,
                       void* workspace, size_t workspace_bytes, void* stream);
+/* nkv_compress_step with fp16 q and caches (the compaction moves 2-byte rows
+ * either way). Replaces: MyCompressCompact's per-layer work
+ * (compress_utils.py:100-263) for a float16 checkpoint. */
+int nkv_compress_step_f16(const void* q, int64_t q_row_stride, void* k_cache, void* v_cache,
+                          const int32_t* block_tables, int64_t bt_row_stride,
+                          int32_t max_blocks_per_seq, const int32_t* base_context_lens,
+                          int32_t* context_lens, const int32_t* seq_idx, int32_t m,
+                          int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                          int32_t block_size, int32_t window_blocks, int64_t n_blocks,
+                          float scale, int32_t agg_mode, int32_t keep_tokens,
+                          float* importance_out, int32_t* keep_idx,
+                          void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * In-place compaction of the window of each selected sequence, K and V:

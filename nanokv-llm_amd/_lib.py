@@ -47,11 +47,16 @@ SIGNATURES = {
     "nkv_qk_norm_rope_store": (C.c_int, [_p, _i64, _p, _i64, _p, _i64, _p, _p, _p, _f32, _p,
                                          _i64, _p, _i64, _p, _p, _p, _p, _i64, _i64, _i32,
                                          _i32, _i32, _p]),
+    "nkv_qk_norm_rope_store_f16": (C.c_int, [_p, _i64, _p, _i64, _p, _i64, _p, _p, _p, _f32, _p,
+                                             _i64, _p, _i64, _p, _p, _p, _p, _i64, _i64, _i32,
+                                             _i32, _i32, _p]),
     "nkv_paged_decode_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
     "nkv_paged_decode": (C.c_int, [_p, _i64, _p, _p, _p, _i64, _p, _i32, _i32, _i32, _i32, _i32,
                                    _i32, _i64, _f32, _p, _i64, _p, _sz, _p]),
     "nkv_paged_decode_noalloc": (C.c_int, [_p, _i64, _p, _p, _p, _i64, _p, _i32, _i32, _i32,
                                            _i32, _i32, _i32, _i64, _f32, _p, _i64, _p]),
+    "nkv_paged_decode_f16": (C.c_int, [_p, _i64, _p, _p, _p, _i64, _p, _i32, _i32, _i32, _i32,
+                                       _i32, _i32, _i64, _f32, _p, _i64, _p, _sz, _p]),
     "nkv_paged_decode_fp8": (C.c_int, [_p, _i64, _p, _p, _p, _i64, _p, _i32, _i32, _i32, _i32,
                                        _i32, _i32, _i64, _f32, _f32, _f32, _p, _i64, _p, _sz,
                                        _p]),
@@ -61,6 +66,9 @@ SIGNATURES = {
                                            _sz, _p]),
     "nkv_prefill_varlen": (C.c_int, [_p, _i64, _p, _p, _i64, _i64, _p, _p, _p, _i64, _i32, _i32,
                                      _i32, _i32, _i32, _i32, _i32, _i64, _f32, _p, _i64, _p]),
+    "nkv_prefill_varlen_f16": (C.c_int, [_p, _i64, _p, _p, _i64, _i64, _p, _p, _p, _i64, _i32,
+                                         _i32, _i32, _i32, _i32, _i32, _i32, _i64, _f32, _p,
+                                         _i64, _p]),
     "nkv_prefill_varlen_fp8": (C.c_int, [_p, _i64, _p, _p, _p, _p, _p, _i64, _i32, _i32, _i32,
                                          _i32, _i32, _i32, _i32, _i64, _f32, _f32, _f32, _p,
                                          _i64, _p]),
@@ -72,12 +80,20 @@ SIGNATURES = {
     "nkv_compress_select": (C.c_int, [_p, _i64, _p, _p, _i64, _i32, _p, _p, _i32, _i32, _i32,
                                       _i32, _i32, _i32, _i64, _f32, _i32, _i32, _p, _p, _p, _sz,
                                       _p]),
+    "nkv_compress_select_f16": (C.c_int, [_p, _i64, _p, _p, _i64, _i32, _p, _p, _i32, _i32, _i32,
+                                          _i32, _i32, _i32, _i64, _f32, _i32, _i32, _p, _p, _p,
+                                          _sz, _p]),
     "nkv_snapkv_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
     "nkv_snapkv_select": (C.c_int, [_p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _i32,
                                     _p, _p, _p, _sz, _p]),
+    "nkv_snapkv_select_f16": (C.c_int, [_p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32,
+                                        _i32, _p, _p, _p, _sz, _p]),
     "nkv_compress_step": (C.c_int, [_p, _i64, _p, _p, _p, _i64, _i32, _p, _p, _p, _i32, _i32, _i32,
                                     _i32, _i32, _i32, _i64, _f32, _i32, _i32, _p, _p, _p, _sz,
                                     _p]),
+    "nkv_compress_step_f16": (C.c_int, [_p, _i64, _p, _p, _p, _i64, _i32, _p, _p, _p, _i32, _i32,
+                                        _i32, _i32, _i32, _i32, _i64, _f32, _i32, _i32, _p, _p,
+                                        _p, _sz, _p]),
     "nkv_compress_step_fp8": (C.c_int, [_p, _i64, _p, _p, _p, _i64, _i32, _p, _p, _p, _i32, _i32,
                                         _i32, _i32, _i32, _i32, _i64, _f32, _f32, _i32, _i32, _p,
                                         _p, _p, _sz, _p]),
@@ -145,6 +161,14 @@ def require_device(device: torch.device, **tensors: torch.Tensor | None) -> None
     for name, t in tensors.items():
         if t is not None and t.device != device:
             raise ValueError(f"{name} is on {t.device}, expected {device}")
+
+
+def is_f16(t: torch.Tensor, what: str) -> bool:
+    """Activations (q, k, v, outputs) and 16-bit caches are bf16 or fp16, as the model's
+    dtype: True for fp16 (the kernels' _f16 entry points), False for bf16; raises otherwise."""
+    if t.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError(f"{what} must be bf16 or fp16, got {t.dtype}")
+    return t.dtype == torch.float16
 
 
 def need(cond: bool, msg: str) -> None:

@@ -44,7 +44,7 @@ constexpr int kMaxRows = 1024;  // rows per read-then-write round of a compactio
 // row of one sequence).
 // F8: K is fp8 (OCP E4M3FN) codes, widened to bf16 (exact) on load; the K scale is
 // folded into scale_log2 by the caller. D: head_dim (64, 128 or 256).
-template <bool F8, int D>
+template <bool F8, int D, bool H16 = false>
 __global__ __launch_bounds__(256) void compress_score_kernel(
     const bf16_t* __restrict__ q, int64_t q_row_stride, const void* __restrict__ k,
     const int32_t* __restrict__ block_tables, int64_t bt_row_stride, int32_t max_blocks,
@@ -52,6 +52,7 @@ __global__ __launch_bounds__(256) void compress_score_kernel(
     int32_t Hk, int32_t G, int32_t block_size, int32_t window_blocks, int64_t n_blocks,
     float scale_log2, int32_t n_cand, float* __restrict__ scores) {
   static_assert(compress_dim_ok(D), "head_dim 64, 128 or 256");
+  static_assert(!(F8 && H16), "fp8 caches are scored with bf16 queries");
   constexpr int kEl = F8 ? 1 : 2;
   constexpr int kLpr = D * kEl / 16;  // lanes per K row (16-byte loads)
   constexpr int kRpl = 64 / kLpr;     // K rows per load
@@ -60,7 +61,7 @@ __global__ __launch_bounds__(256) void compress_score_kernel(
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int Lw = window_blocks * block_size;
-  const int n_chunks = Lw / kChunk;
+  const int n_chunks = (Lw + kChunk - 1) / kChunk;  // the last one masked past Lw (contiguous K)
   const int c = blockIdx.x % n_chunks;
   const int kvh = (blockIdx.x / n_chunks) % Hk;
   const int j = blockIdx.x / (n_chunks * Hk);
@@ -93,7 +94,7 @@ __global__ __launch_bounds__(256) void compress_score_kernel(
   float* srow = scores + ((int64_t)j * Hq + (int64_t)kvh * G) * Lw + t0;
   if (!valid) {
     for (int i = threadIdx.x; i < G * kChunk; i += blockDim.x)
-      srow[(int64_t)(i / kChunk) * Lw + i % kChunk] = -INFINITY;
+      if (t0 + i % kChunk < Lw) srow[(int64_t)(i / kChunk) * Lw + i % kChunk] = -INFINITY;
     return;
   }
   // K rows are read whole (one head row per kLpr lanes: at head_dim 128, 256 bytes per
@@ -108,23 +109,26 @@ __global__ __launch_bounds__(256) void compress_score_kernel(
 #pragma unroll
     for (int r = 0; r < kNld; ++r) {
       const int key = wave * 64 + g * 16 + kRpl * r + lane / kLpr;
-      if constexpr (F8) {
-        kraw[g][r] = *reinterpret_cast<const u32x4_t*>(static_cast<const uint8_t*>(k) + base +
-                                                      key * tok_stride + (lane % kLpr) * 16);
-      } else {
-        kraw[g][r] = *reinterpret_cast<const u32x4_t*>(static_cast<const bf16_t*>(k) + base +
-                                                      key * tok_stride + (lane % kLpr) * 8);
+      kraw[g][r] = u32x4_t{0u, 0u, 0u, 0u};
+      if (t0 + key < Lw) {  // keys past the window (a contiguous tail chunk) read as 0
+        if constexpr (F8) {
+          kraw[g][r] = *reinterpret_cast<const u32x4_t*>(static_cast<const uint8_t*>(k) + base +
+                                                        key * tok_stride + (lane % kLpr) * 16);
+        } else {
+          kraw[g][r] = *reinterpret_cast<const u32x4_t*>(static_cast<const bf16_t*>(k) + base +
+                                                        key * tok_stride + (lane % kLpr) * 8);
+        }
       }
     }
   }
   __builtin_amdgcn_sched_barrier(0);  // all loads issued before the first MFMA
-  uint4 qreg[kKs];
+  u32x4_t qreg[kKs];
   auto load_q = [&](int h0) {  // query rows h0 .. h0+15 of the KV head as the MFMA A operand
     const int hr = h0 + (lane & 15);
     const int hc = hr < G ? hr : 0;  // MFMA rows >= G are computed and discarded
     const bf16_t* qp = q + qrow * q_row_stride + (int64_t)(kvh * G + hc) * D + (lane >> 4) * 8;
 #pragma unroll
-    for (int ks = 0; ks < kKs; ++ks) qreg[ks] = *reinterpret_cast<const uint4*>(qp + ks * 32);
+    for (int ks = 0; ks < kKs; ++ks) qreg[ks] = *reinterpret_cast<const u32x4_t*>(qp + ks * 32);
   };
   load_q(0);
 #pragma unroll
@@ -153,15 +157,14 @@ __global__ __launch_bounds__(256) void compress_score_kernel(
       f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < kKs; ++ks) {
-        const uint4 kb = *reinterpret_cast<const uint4*>(
+        const u32x4_t kb = *reinterpret_cast<const u32x4_t*>(
             &stage[(lane & 15) * kSR + (lane >> 4) * 8 + ks * 32]);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(qreg[ks]), as_bf16x8(kb), acc,
-                                                       0, 0, 0);
+        acc = mfma_16x16x32<H16>(qreg[ks], kb, acc);
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int h = h0 + (lane >> 4) * 4 + r;
-        if (h < G)
+        if (h < G && t < Lw)
           srow[(int64_t)h * Lw + tw] = (t == 0 || t >= n_cand) ? -INFINITY : acc[r] * scale_log2;
       }
     }
@@ -509,7 +512,7 @@ __device__ __forceinline__ void block_select(SelectLds& L, int n_cand, int num_k
 // (valid in lanes of row group 0). Uses L.red.
 // F8: the cache holds fp8 (OCP E4M3FN) codes, 128-byte head rows read by 8 lanes (8 rows
 // per load) and widened to bf16 when staged; the K scale is folded into scale_log2.
-template <bool F8>
+template <bool F8, bool H16>
 __device__ __forceinline__ void group_importance(
     SelectLds& L, const bf16_t* __restrict__ q, int64_t q_row_stride,
     const void* __restrict__ k, const int32_t* __restrict__ block_tables,
@@ -595,8 +598,7 @@ __device__ __forceinline__ void group_importance(
       for (int ks = 0; ks < 4; ++ks) {
         const u32x4_t kb =
             *reinterpret_cast<const u32x4_t*>(&stage[col * kStageRow + hg * 8 + ks * 32]);
-        a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8_v(qreg[ks]), as_bf16x8_v(kb), a,
-                                                     0, 0, 0);
+        a = mfma_16x16x32<H16>(qreg[ks], kb, a);
       }
       acc[g] = a;
     }
@@ -772,7 +774,7 @@ __device__ __forceinline__ void compact_unit(
 }
 
 // agg "group": score -> select -> (if k_cache_w) compact. Grid m * Hk.
-template <bool F8>
+template <bool F8, bool H16 = false>
 __global__ __launch_bounds__(kSelThreads) void compress_group_kernel(
     const bf16_t* __restrict__ q, int64_t q_row_stride, const void* __restrict__ k,
     const int32_t* __restrict__ block_tables, int64_t bt_row_stride, int32_t max_blocks,
@@ -802,7 +804,7 @@ __global__ __launch_bounds__(kSelThreads) void compress_group_kernel(
                           n_blocks);
   }
   float gi[4];
-  group_importance<F8>(L, q, q_row_stride, k, block_tables, bt_row_stride, max_blocks,
+  group_importance<F8, H16>(L, q, q_row_stride, k, block_tables, bt_row_stride, max_blocks,
                        base_context_lens, seq_idx, j, kvh, Hk, G, block_size, window_blocks,
                        n_blocks, scale_log2, gi);
   const int t0 = (tid >> 6) * kSelKeysPerWave;
@@ -821,7 +823,7 @@ __global__ __launch_bounds__(kSelThreads) void compress_group_kernel(
 }
 
 // agg "all", first kernel: each group's importance -> partial[j][kvh][Lw]. Grid m * Hk.
-template <bool F8>
+template <bool F8, bool H16 = false>
 __global__ __launch_bounds__(kSelThreads) void compress_partial_kernel(
     const bf16_t* __restrict__ q, int64_t q_row_stride, const void* __restrict__ k,
     const int32_t* __restrict__ block_tables, int64_t bt_row_stride, int32_t max_blocks,
@@ -835,7 +837,7 @@ __global__ __launch_bounds__(kSelThreads) void compress_partial_kernel(
   if (block_tables && seq_idx[j] < 0) return;  // padding entry (uniform): nothing written
   const int Lw = window_blocks * block_size;
   float gi[4];
-  group_importance<F8>(L, q, q_row_stride, k, block_tables, bt_row_stride, max_blocks,
+  group_importance<F8, H16>(L, q, q_row_stride, k, block_tables, bt_row_stride, max_blocks,
                        base_context_lens, seq_idx, j, kvh, Hk, G, block_size, window_blocks,
                        n_blocks, scale_log2, gi);
   float* prow = partial + ((int64_t)j * Hk + kvh) * Lw;
@@ -1187,7 +1189,7 @@ using namespace nkv;
 
 namespace nkv {
 // The score kernel's head_dim instance (64, 128 or 256; checked by the caller).
-template <bool F8>
+template <bool F8, bool H16 = false>
 static void launch_score(int32_t head_dim, unsigned grid, hipStream_t s, const bf16_t* q,
                          int64_t q_row_stride, const void* k, const int32_t* block_tables,
                          int64_t bt_row_stride, int32_t max_blocks,
@@ -1195,7 +1197,7 @@ static void launch_score(int32_t head_dim, unsigned grid, hipStream_t s, const b
                          int32_t G, int32_t block_size, int32_t window_blocks, int64_t n_blocks,
                          float scale_log2, int32_t n_cand, float* scores) {
 #define NKV_SCORE_LAUNCH(D)                                                                    \
-  hipLaunchKernelGGL((compress_score_kernel<F8, D>), dim3(grid), dim3(256), 0, s, q,             \
+  hipLaunchKernelGGL((compress_score_kernel<F8, D, H16>), dim3(grid), dim3(256), 0, s, q,        \
                      q_row_stride, k, block_tables, bt_row_stride, max_blocks,                   \
                      base_context_lens, seq_idx, Hk, G, block_size, window_blocks, n_blocks,     \
                      scale_log2, n_cand, scores)
@@ -1212,25 +1214,24 @@ extern "C" size_t nkv_compress_workspace_bytes(int32_t m, int32_t n_q_heads,
   return (size_t)m * n_q_heads * window_blocks * block_size * sizeof(float);
 }
 
-extern "C" int nkv_compress_score(const void* q, int64_t q_row_stride, const void* k_cache,
-                                  const int32_t* block_tables, int64_t bt_row_stride,
-                                  int32_t max_blocks_per_seq,
-                                  const int32_t* base_context_lens, const int32_t* seq_idx,
-                                  int32_t m, int32_t n_q_heads, int32_t n_kv_heads,
-                                  int32_t head_dim, int32_t block_size, int32_t window_blocks,
-                                  int64_t n_blocks, float scale, int32_t agg_mode,
-                                  float* importance_out, void* workspace, size_t workspace_bytes,
-                                  void* stream) {
-  clear_error();
+namespace nkv {
+template <bool H16>
+static int compress_score_impl(const void* q, int64_t q_row_stride, const void* k_cache,
+                               const int32_t* block_tables, int64_t bt_row_stride,
+                               int32_t max_blocks_per_seq, const int32_t* base_context_lens,
+                               const int32_t* seq_idx, int32_t m, int32_t n_q_heads,
+                               int32_t n_kv_heads, int32_t head_dim, int32_t block_size,
+                               int32_t window_blocks, int64_t n_blocks, float scale,
+                               int32_t agg_mode, float* importance_out, void* workspace,
+                               size_t workspace_bytes, void* stream) {
   NKV_REQUIRE(m >= 0 && n_q_heads > 0 && n_kv_heads > 0 && window_blocks > 0 && block_size > 0,
               NKV_EINVAL, "compress_score: bad sizes");
   if (m == 0) return NKV_OK;
   NKV_REQUIRE(compress_dim_ok(head_dim), NKV_EUNSUPPORTED,
               "compress_score: head_dim must be 64, 128 or 256 (got %d)", head_dim);
   NKV_REQUIRE(n_q_heads % n_kv_heads == 0, NKV_EINVAL, "compress_score: Hq %% Hk != 0");
-  const int g = n_q_heads / n_kv_heads;
-  NKV_REQUIRE(g <= 16, NKV_EUNSUPPORTED, "compress_score: GQA group %d above 16", g);
-  NKV_REQUIRE(block_size % kChunk == 0, NKV_EUNSUPPORTED,
+  const int g = n_q_heads / n_kv_heads;  // any group: query rows in passes of 16
+  NKV_REQUIRE(!block_tables || block_size % kChunk == 0, NKV_EUNSUPPORTED,
               "compress_score: block_size must be a multiple of 256");
   NKV_REQUIRE(agg_mode == NKV_AGG_ALL || agg_mode == NKV_AGG_GROUP, NKV_EINVAL,
               "compress_score: bad agg_mode %d", agg_mode);
@@ -1248,11 +1249,12 @@ extern "C" int nkv_compress_score(const void* q, int64_t q_row_stride, const voi
   NKV_REQUIRE(Lw >= 2, NKV_EINVAL, "compress_score: window too short");
   float* scores = (float*)workspace;
   hipStream_t s = as_stream(stream);
-  const unsigned grid = (unsigned)(m * n_kv_heads * (Lw / kChunk));
+  const unsigned grid = (unsigned)(m * n_kv_heads * ((Lw + kChunk - 1) / kChunk));
   const float sl2 = scale * kLog2e;
-  launch_score<false>(head_dim, grid, s, (const bf16_t*)q, q_row_stride, k_cache, block_tables,
-                      bt_row_stride, max_blocks_per_seq, base_context_lens, seq_idx, n_kv_heads,
-                      g, block_size, window_blocks, n_blocks, sl2, Lw - 1, scores);
+  launch_score<false, H16>(head_dim, grid, s, (const bf16_t*)q, q_row_stride, k_cache,
+                           block_tables, bt_row_stride, max_blocks_per_seq, base_context_lens,
+                           seq_idx, n_kv_heads, g, block_size, window_blocks, n_blocks, sl2,
+                           Lw - 1, scores);
   int rc = check_launch("nkv_compress_score");
   if (rc) return rc;
   const int n_sets = agg_mode == NKV_AGG_ALL ? 1 : n_kv_heads;
@@ -1261,6 +1263,24 @@ extern "C" int nkv_compress_score(const void* q, int64_t q_row_stride, const voi
                      (size_t)hps * 2 * sizeof(float), s, scores, n_q_heads, n_sets, Lw, Lw - 1,
                      importance_out);
   return check_launch("nkv_compress_score(importance)");
+}
+}  // namespace nkv
+
+extern "C" int nkv_compress_score(const void* q, int64_t q_row_stride, const void* k_cache,
+                                  const int32_t* block_tables, int64_t bt_row_stride,
+                                  int32_t max_blocks_per_seq,
+                                  const int32_t* base_context_lens, const int32_t* seq_idx,
+                                  int32_t m, int32_t n_q_heads, int32_t n_kv_heads,
+                                  int32_t head_dim, int32_t block_size, int32_t window_blocks,
+                                  int64_t n_blocks, float scale, int32_t agg_mode,
+                                  float* importance_out, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  clear_error();
+  return compress_score_impl<false>(q, q_row_stride, k_cache, block_tables, bt_row_stride,
+                                    max_blocks_per_seq, base_context_lens, seq_idx, m, n_q_heads,
+                                    n_kv_heads, head_dim, block_size, window_blocks, n_blocks,
+                                    scale, agg_mode, importance_out, workspace, workspace_bytes,
+                                    stream);
 }
 
 extern "C" int nkv_compress_topk(const float* importance, int32_t n_rows, int32_t n_cand,
@@ -1297,7 +1317,7 @@ extern "C" size_t nkv_compress_select_workspace_bytes(int32_t m, int32_t n_q_hea
 namespace nkv {
 // Launches the fused selection (and, with k_cache_w, the compaction) when the
 // shape allows it; returns 1 if the caller must take the general path.
-template <bool F8>
+template <bool F8, bool H16 = false>
 static int launch_fused(const void* q, int64_t q_row_stride, const void* k_cache,
                         const int32_t* block_tables, int64_t bt_row_stride,
                         int32_t max_blocks_per_seq, const int32_t* base_context_lens,
@@ -1317,14 +1337,14 @@ static int launch_fused(const void* q, int64_t q_row_stride, const void* k_cache
   const unsigned units = (unsigned)(m * n_kv_heads);
   float* partial = (float*)workspace;
   if (agg_mode == NKV_AGG_GROUP) {
-    hipLaunchKernelGGL((compress_group_kernel<F8>), dim3(units), dim3(kSelThreads), 0, s,
+    hipLaunchKernelGGL((compress_group_kernel<F8, H16>), dim3(units), dim3(kSelThreads), 0, s,
                        (const bf16_t*)q, q_row_stride, k_cache, block_tables, bt_row_stride,
                        max_blocks_per_seq, base_context_lens, seq_idx, n_kv_heads, g,
                        block_size, window_blocks, n_blocks, sl2, num_keep, importance_out,
                        keep_idx, k_cache_w, v_cache_w, context_lens);
     return check_launch("compress (group)") ? -1 : 0;
   }
-  hipLaunchKernelGGL((compress_partial_kernel<F8>), dim3(units), dim3(kSelThreads), 0, s,
+  hipLaunchKernelGGL((compress_partial_kernel<F8, H16>), dim3(units), dim3(kSelThreads), 0, s,
                      (const bf16_t*)q, q_row_stride, k_cache, block_tables, bt_row_stride,
                      max_blocks_per_seq, base_context_lens, seq_idx, n_kv_heads, g, block_size,
                      window_blocks, n_blocks, sl2, partial);
@@ -1339,16 +1359,17 @@ static int launch_fused(const void* q, int64_t q_row_stride, const void* k_cache
 }
 }  // namespace nkv
 
-extern "C" int nkv_compress_select(const void* q, int64_t q_row_stride, const void* k_cache,
-                                   const int32_t* block_tables, int64_t bt_row_stride,
-                                   int32_t max_blocks_per_seq, const int32_t* base_context_lens,
-                                   const int32_t* seq_idx, int32_t m, int32_t n_q_heads,
-                                   int32_t n_kv_heads, int32_t head_dim, int32_t block_size,
-                                   int32_t window_blocks, int64_t n_blocks, float scale,
-                                   int32_t agg_mode, int32_t num_keep, float* importance_out,
-                                   int32_t* keep_idx, void* workspace, size_t workspace_bytes,
-                                   void* stream) {
-  clear_error();
+namespace nkv {
+template <bool H16>
+static int compress_select_impl(const void* q, int64_t q_row_stride, const void* k_cache,
+                                const int32_t* block_tables, int64_t bt_row_stride,
+                                int32_t max_blocks_per_seq, const int32_t* base_context_lens,
+                                const int32_t* seq_idx, int32_t m, int32_t n_q_heads,
+                                int32_t n_kv_heads, int32_t head_dim, int32_t block_size,
+                                int32_t window_blocks, int64_t n_blocks, float scale,
+                                int32_t agg_mode, int32_t num_keep, float* importance_out,
+                                int32_t* keep_idx, void* workspace, size_t workspace_bytes,
+                                void* stream) {
   NKV_REQUIRE(m >= 0 && n_q_heads > 0 && n_kv_heads > 0 && window_blocks > 0 && block_size > 0,
               NKV_EINVAL, "compress_select: bad sizes");
   if (m == 0) return NKV_OK;
@@ -1371,20 +1392,58 @@ extern "C" int nkv_compress_select(const void* q, int64_t q_row_stride, const vo
   NKV_REQUIRE(workspace && workspace_bytes >= need, NKV_EWORKSPACE,
               "compress_select: workspace needs %zu bytes (got %zu)", need, workspace_bytes);
   hipStream_t s = as_stream(stream);
-  const int rc = launch_fused<false>(q, q_row_stride, k_cache, block_tables, bt_row_stride,
-                              max_blocks_per_seq, base_context_lens, seq_idx, m, n_q_heads,
-                              n_kv_heads, head_dim, block_size, window_blocks, n_blocks, scale,
-                              agg_mode, num_keep, importance_out, keep_idx, workspace, nullptr,
-                              nullptr, nullptr, s);
+  const int rc = launch_fused<false, H16>(q, q_row_stride, k_cache, block_tables,
+                                          bt_row_stride, max_blocks_per_seq, base_context_lens,
+                                          seq_idx, m, n_q_heads, n_kv_heads, head_dim,
+                                          block_size, window_blocks, n_blocks, scale, agg_mode,
+                                          num_keep, importance_out, keep_idx, workspace, nullptr,
+                                          nullptr, nullptr, s);
   if (rc <= 0) return rc < 0 ? NKV_ELAUNCH : NKV_OK;
   // general path: score + importance kernels, then the one-wave top-k
   const int n_sets = agg_mode == NKV_AGG_ALL ? 1 : n_kv_heads;
-  int e = nkv_compress_score(q, q_row_stride, k_cache, block_tables, bt_row_stride,
-                             max_blocks_per_seq, base_context_lens, seq_idx, m, n_q_heads,
-                             n_kv_heads, head_dim, block_size, window_blocks, n_blocks, scale,
-                             agg_mode, importance_out, workspace, workspace_bytes, stream);
+  int e = compress_score_impl<H16>(q, q_row_stride, k_cache, block_tables, bt_row_stride,
+                                   max_blocks_per_seq, base_context_lens, seq_idx, m, n_q_heads,
+                                   n_kv_heads, head_dim, block_size, window_blocks, n_blocks,
+                                   scale, agg_mode, importance_out, workspace, workspace_bytes,
+                                   stream);
   if (e) return e;
   return nkv_compress_topk(importance_out, m * n_sets, Lw - 1, num_keep, keep_idx, stream);
+}
+}  // namespace nkv
+
+extern "C" int nkv_compress_select(const void* q, int64_t q_row_stride, const void* k_cache,
+                                   const int32_t* block_tables, int64_t bt_row_stride,
+                                   int32_t max_blocks_per_seq, const int32_t* base_context_lens,
+                                   const int32_t* seq_idx, int32_t m, int32_t n_q_heads,
+                                   int32_t n_kv_heads, int32_t head_dim, int32_t block_size,
+                                   int32_t window_blocks, int64_t n_blocks, float scale,
+                                   int32_t agg_mode, int32_t num_keep, float* importance_out,
+                                   int32_t* keep_idx, void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+  clear_error();
+  return compress_select_impl<false>(q, q_row_stride, k_cache, block_tables, bt_row_stride,
+                                     max_blocks_per_seq, base_context_lens, seq_idx, m,
+                                     n_q_heads, n_kv_heads, head_dim, block_size, window_blocks,
+                                     n_blocks, scale, agg_mode, num_keep, importance_out,
+                                     keep_idx, workspace, workspace_bytes, stream);
+}
+
+extern "C" int nkv_compress_select_f16(const void* q, int64_t q_row_stride, const void* k_cache,
+                                       const int32_t* block_tables, int64_t bt_row_stride,
+                                       int32_t max_blocks_per_seq,
+                                       const int32_t* base_context_lens, const int32_t* seq_idx,
+                                       int32_t m, int32_t n_q_heads, int32_t n_kv_heads,
+                                       int32_t head_dim, int32_t block_size,
+                                       int32_t window_blocks, int64_t n_blocks, float scale,
+                                       int32_t agg_mode, int32_t num_keep,
+                                       float* importance_out, int32_t* keep_idx,
+                                       void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  return compress_select_impl<true>(q, q_row_stride, k_cache, block_tables, bt_row_stride,
+                                    max_blocks_per_seq, base_context_lens, seq_idx, m,
+                                    n_q_heads, n_kv_heads, head_dim, block_size, window_blocks,
+                                    n_blocks, scale, agg_mode, num_keep, importance_out,
+                                    keep_idx, workspace, workspace_bytes, stream);
 }
 
 extern "C" int nkv_compress_compact(void* k_cache, void* v_cache, const int32_t* block_tables,
@@ -1454,18 +1513,18 @@ extern "C" int nkv_compress_finalize(int32_t* block_tables, int64_t bt_row_strid
   return check_launch("nkv_compress_finalize");
 }
 
-extern "C" int nkv_compress_step(const void* q, int64_t q_row_stride, void* k_cache,
-                                 void* v_cache, const int32_t* block_tables,
-                                 int64_t bt_row_stride, int32_t max_blocks_per_seq,
-                                 const int32_t* base_context_lens, int32_t* context_lens,
-                                 const int32_t* seq_idx, int32_t m, int32_t n_q_heads,
-                                 int32_t n_kv_heads, int32_t head_dim, int32_t block_size,
-                                 int32_t window_blocks, int64_t n_blocks, float scale,
-                                 int32_t agg_mode, int32_t keep_tokens, float* importance_out,
-                                 int32_t* keep_idx, void* workspace, size_t workspace_bytes,
-                                 void* stream) {
-  using namespace nkv;
-  clear_error();
+namespace nkv {
+template <bool H16>
+static int compress_step_impl(const void* q, int64_t q_row_stride, void* k_cache,
+                              void* v_cache, const int32_t* block_tables,
+                              int64_t bt_row_stride, int32_t max_blocks_per_seq,
+                              const int32_t* base_context_lens, int32_t* context_lens,
+                              const int32_t* seq_idx, int32_t m, int32_t n_q_heads,
+                              int32_t n_kv_heads, int32_t head_dim, int32_t block_size,
+                              int32_t window_blocks, int64_t n_blocks, float scale,
+                              int32_t agg_mode, int32_t keep_tokens, float* importance_out,
+                              int32_t* keep_idx, void* workspace, size_t workspace_bytes,
+                              void* stream) {
   NKV_REQUIRE(m >= 0 && n_q_heads > 0 && n_kv_heads > 0 && window_blocks > 0 && block_size > 0,
               NKV_EINVAL, "compress_step: bad sizes");
   if (m == 0) return NKV_OK;
@@ -1491,24 +1550,63 @@ extern "C" int nkv_compress_step(const void* q, int64_t q_row_stride, void* k_ca
   NKV_REQUIRE(workspace && workspace_bytes >= need, NKV_EWORKSPACE,
               "compress_step: workspace needs %zu bytes (got %zu)", need, workspace_bytes);
   hipStream_t s = as_stream(stream);
-  int rc = launch_fused<false>(q, q_row_stride, k_cache, block_tables, bt_row_stride,
-                               max_blocks_per_seq, base_context_lens, seq_idx, m, n_q_heads,
-                               n_kv_heads, head_dim, block_size, window_blocks, n_blocks, scale,
-                               agg_mode, num_keep, importance_out, keep_idx, workspace, k_cache,
-                               v_cache, context_lens, s);
+  int rc = launch_fused<false, H16>(q, q_row_stride, k_cache, block_tables, bt_row_stride,
+                                    max_blocks_per_seq, base_context_lens, seq_idx, m,
+                                    n_q_heads, n_kv_heads, head_dim, block_size, window_blocks,
+                                    n_blocks, scale, agg_mode, num_keep, importance_out,
+                                    keep_idx, workspace, k_cache, v_cache, context_lens, s);
   if (rc < 0) return NKV_ELAUNCH;
   if (rc == 0) return NKV_OK;
-  // general path: selection, then the compaction kernel
-  rc = nkv_compress_select(q, q_row_stride, k_cache, block_tables, bt_row_stride,
-                           max_blocks_per_seq, base_context_lens, seq_idx, m, n_q_heads,
-                           n_kv_heads, head_dim, block_size, window_blocks, n_blocks, scale,
-                           agg_mode, num_keep, importance_out, keep_idx, workspace,
-                           workspace_bytes, stream);
+  // general path: selection, then the compaction kernel (2-byte rows move as bytes)
+  rc = compress_select_impl<H16>(q, q_row_stride, k_cache, block_tables, bt_row_stride,
+                                 max_blocks_per_seq, base_context_lens, seq_idx, m, n_q_heads,
+                                 n_kv_heads, head_dim, block_size, window_blocks, n_blocks,
+                                 scale, agg_mode, num_keep, importance_out, keep_idx, workspace,
+                                 workspace_bytes, stream);
   if (rc) return rc;
   return nkv_compress_compact(k_cache, v_cache, block_tables, bt_row_stride, max_blocks_per_seq,
                               base_context_lens, context_lens, seq_idx, m, keep_idx, n_sets,
                               keep_tokens, n_kv_heads, head_dim, block_size, window_blocks,
                               n_blocks, stream);
+}
+}  // namespace nkv
+
+extern "C" int nkv_compress_step(const void* q, int64_t q_row_stride, void* k_cache,
+                                 void* v_cache, const int32_t* block_tables,
+                                 int64_t bt_row_stride, int32_t max_blocks_per_seq,
+                                 const int32_t* base_context_lens, int32_t* context_lens,
+                                 const int32_t* seq_idx, int32_t m, int32_t n_q_heads,
+                                 int32_t n_kv_heads, int32_t head_dim, int32_t block_size,
+                                 int32_t window_blocks, int64_t n_blocks, float scale,
+                                 int32_t agg_mode, int32_t keep_tokens, float* importance_out,
+                                 int32_t* keep_idx, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+  nkv::clear_error();
+  return nkv::compress_step_impl<false>(q, q_row_stride, k_cache, v_cache, block_tables,
+                                        bt_row_stride, max_blocks_per_seq, base_context_lens,
+                                        context_lens, seq_idx, m, n_q_heads, n_kv_heads,
+                                        head_dim, block_size, window_blocks, n_blocks, scale,
+                                        agg_mode, keep_tokens, importance_out, keep_idx,
+                                        workspace, workspace_bytes, stream);
+}
+
+extern "C" int nkv_compress_step_f16(const void* q, int64_t q_row_stride, void* k_cache,
+                                     void* v_cache, const int32_t* block_tables,
+                                     int64_t bt_row_stride, int32_t max_blocks_per_seq,
+                                     const int32_t* base_context_lens, int32_t* context_lens,
+                                     const int32_t* seq_idx, int32_t m, int32_t n_q_heads,
+                                     int32_t n_kv_heads, int32_t head_dim, int32_t block_size,
+                                     int32_t window_blocks, int64_t n_blocks, float scale,
+                                     int32_t agg_mode, int32_t keep_tokens,
+                                     float* importance_out, int32_t* keep_idx, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  nkv::clear_error();
+  return nkv::compress_step_impl<true>(q, q_row_stride, k_cache, v_cache, block_tables,
+                                       bt_row_stride, max_blocks_per_seq, base_context_lens,
+                                       context_lens, seq_idx, m, n_q_heads, n_kv_heads,
+                                       head_dim, block_size, window_blocks, n_blocks, scale,
+                                       agg_mode, keep_tokens, importance_out, keep_idx,
+                                       workspace, workspace_bytes, stream);
 }
 
 extern "C" int nkv_compress_schedule(const int32_t* context_lens,
@@ -1632,12 +1730,13 @@ extern "C" size_t nkv_snapkv_workspace_bytes(int32_t m, int32_t n_q_heads, int32
   return scores > fused ? scores : fused;
 }
 
-extern "C" int nkv_snapkv_select(const void* q, const void* k, int32_t m, int32_t n_q_heads,
-                                 int32_t n_kv_heads, int32_t head_dim, int32_t seq_len,
-                                 int32_t window, float scale, int32_t agg_mode, int32_t num_keep,
-                                 float* importance_out, int32_t* keep_idx, void* workspace,
-                                 size_t workspace_bytes, void* stream) {
-  clear_error();
+namespace nkv {
+template <bool H16>
+static int snapkv_select_impl(const void* q, const void* k, int32_t m, int32_t n_q_heads,
+                              int32_t n_kv_heads, int32_t head_dim, int32_t seq_len,
+                              int32_t window, float scale, int32_t agg_mode, int32_t num_keep,
+                              float* importance_out, int32_t* keep_idx, void* workspace,
+                              size_t workspace_bytes, void* stream) {
   NKV_REQUIRE(m >= 0 && n_q_heads > 0 && n_kv_heads > 0 && seq_len > 0 && window > 0,
               NKV_EINVAL, "snapkv_select: bad sizes");
   if (m == 0) return NKV_OK;
@@ -1657,23 +1756,20 @@ extern "C" int nkv_snapkv_select(const void* q, const void* k, int32_t m, int32_
   NKV_REQUIRE(workspace && workspace_bytes >= need, NKV_EWORKSPACE,
               "snapkv_select: workspace needs %zu bytes (got %zu)", need, workspace_bytes);
   if (window == 1)  // the periodic step's own shape: fused when it fits
-    return nkv_compress_select(q, (int64_t)n_q_heads * head_dim, k, nullptr, 0, 0, nullptr,
-                               nullptr,
-                               m, n_q_heads, n_kv_heads, head_dim, seq_len, 1, 0, scale,
-                               agg_mode, num_keep, importance_out, keep_idx, workspace,
-                               workspace_bytes, stream);
-  NKV_REQUIRE(seq_len % kChunk == 0, NKV_EUNSUPPORTED,
-              "snapkv_select: seq_len must be a multiple of %d with a query window > 1 (got %d)",
-              kChunk, seq_len);
+    return compress_select_impl<H16>(q, (int64_t)n_q_heads * head_dim, k, nullptr, 0, 0,
+                                     nullptr, nullptr, m, n_q_heads, n_kv_heads, head_dim,
+                                     seq_len, 1, 0, scale, agg_mode, num_keep, importance_out,
+                                     keep_idx, workspace, workspace_bytes, stream);
   NKV_REQUIRE(n_cand <= 4096, NKV_EUNSUPPORTED, "snapkv_select: more than 4096 candidates");
   const int g = n_q_heads / n_kv_heads;
   const int rows = g * window;  // query rows per KV head
   float* scores = (float*)workspace;
   hipStream_t s = as_stream(stream);
-  const unsigned grid = (unsigned)(m * n_kv_heads * (seq_len / kChunk));
-  launch_score<false>(head_dim, grid, s, (const bf16_t*)q, (int64_t)n_q_heads * window * head_dim,
-                      k, nullptr, 0, 0, nullptr, nullptr, n_kv_heads, rows, seq_len, 1, 0,
-                      scale * kLog2e, n_cand, scores);
+  const unsigned grid = (unsigned)(m * n_kv_heads * ((seq_len + kChunk - 1) / kChunk));
+  launch_score<false, H16>(head_dim, grid, s, (const bf16_t*)q,
+                           (int64_t)n_q_heads * window * head_dim, k, nullptr, 0, 0, nullptr,
+                           nullptr, n_kv_heads, rows, seq_len, 1, 0, scale * kLog2e, n_cand,
+                           scores);
   int rc = check_launch("nkv_snapkv_select (score)");
   if (rc) return rc;
   const int n_sets = agg_mode == NKV_AGG_ALL ? 1 : n_kv_heads;
@@ -1691,4 +1787,27 @@ extern "C" int nkv_snapkv_select(const void* q, const void* k, int32_t m, int32_
                        importance_out, n_cand, num_keep, window, keep_idx);
   }
   return check_launch("nkv_snapkv_select (top-k)");
+}
+}  // namespace nkv
+
+extern "C" int nkv_snapkv_select(const void* q, const void* k, int32_t m, int32_t n_q_heads,
+                                 int32_t n_kv_heads, int32_t head_dim, int32_t seq_len,
+                                 int32_t window, float scale, int32_t agg_mode, int32_t num_keep,
+                                 float* importance_out, int32_t* keep_idx, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+  clear_error();
+  return snapkv_select_impl<false>(q, k, m, n_q_heads, n_kv_heads, head_dim, seq_len, window,
+                                   scale, agg_mode, num_keep, importance_out, keep_idx,
+                                   workspace, workspace_bytes, stream);
+}
+
+extern "C" int nkv_snapkv_select_f16(const void* q, const void* k, int32_t m, int32_t n_q_heads,
+                                     int32_t n_kv_heads, int32_t head_dim, int32_t seq_len,
+                                     int32_t window, float scale, int32_t agg_mode,
+                                     int32_t num_keep, float* importance_out, int32_t* keep_idx,
+                                     void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  return snapkv_select_impl<true>(q, k, m, n_q_heads, n_kv_heads, head_dim, seq_len, window,
+                                  scale, agg_mode, num_keep, importance_out, keep_idx,
+                                  workspace, workspace_bytes, stream);
 }

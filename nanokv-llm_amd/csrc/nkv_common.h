@@ -60,6 +60,73 @@ __device__ __forceinline__ bf16x8_t as_bf16x8_v(u32x4_t v) {
   return __builtin_bit_cast(bf16x8_t, v);
 }
 
+// ---------------------------------------------------------------- 16-bit element types
+// q, K, V and outputs are bf16 or fp16 (the model's dtype); a kernel instance takes one of
+// them as the template flag H16 (true: fp16) and the helpers below pick the matching
+// conversion or MFMA. The bits travel as raw uint16 either way.
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+
+// 16-bit value in the low / high half of a word -> fp32 (exact)
+template <bool H16>
+__device__ __forceinline__ float e16_lo(uint32_t w) {
+  if constexpr (H16) return (float)__builtin_bit_cast(f16x2_t, w)[0];
+  else return bf16_lo(w);
+}
+template <bool H16>
+__device__ __forceinline__ float e16_hi(uint32_t w) {
+  if constexpr (H16) return (float)__builtin_bit_cast(f16x2_t, w)[1];
+  else return bf16_hi(w);
+}
+
+// fp32 pair -> packed pair (lo in bits 0-15), round to nearest even: the hardware
+// conversions (v_cvt_f16_f32; for bf16 the packed bf16 conversion)
+template <bool H16>
+__device__ __forceinline__ uint32_t cvt_pk16(float lo, float hi) {
+  if constexpr (H16) {
+    const f16x2_t v = {(_Float16)lo, (_Float16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+  } else {
+    const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+}
+
+// v_mfma_f32_16x16x32_{bf16,f16}: 8 elements of A and B per lane (raw bits)
+template <bool H16>
+__device__ __forceinline__ f32x4_t mfma_16x16x32(u32x4_t a, u32x4_t b, f32x4_t c) {
+  if constexpr (H16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                   __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                    __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+// v_mfma_f32_16x16x16_{bf16,f16}: 4 elements of A and B per lane (raw bits)
+template <bool H16>
+__device__ __forceinline__ f32x4_t mfma_16x16x16(s16x4_t a, s16x4_t b, f32x4_t c) {
+  if constexpr (H16)
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4_t, a),
+                                                  __builtin_bit_cast(f16x4_t, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+
+// acc + lo + hi of a packed pair (v_dot2_f32_{bf16,f16} against (1, 1))
+template <bool H16>
+__device__ __forceinline__ float sum2_16(uint32_t pair, float acc) {
+  if constexpr (H16) {
+    const f16x2_t ones = {(_Float16)1.f, (_Float16)1.f};
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, pair), ones, acc, false);
+  } else {
+    const bf16x2_t ones = {(__bf16)1.f, (__bf16)1.f};
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pair), ones, acc, false);
+  }
+}
+
 // 64-lane wavefront reductions (butterfly over the whole wave).
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll

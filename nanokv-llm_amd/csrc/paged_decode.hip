@@ -64,6 +64,9 @@ constexpr int kWavesPerCU = 8;           // resident split waves per CU (2 per S
 constexpr int part_row(int D) { return D + 4; }
 constexpr bool decode_dim_ok(int D) { return D == 64 || D == 128 || D == 256; }
 constexpr int kMaxCols = 16;             // MFMA columns: query heads per wave at most
+constexpr int kMaxGroup = 256;           // GQA group at most (above 16: column groups)
+// Column groups per KV head: its G query heads over ceil(G / 16) waves when G > 16.
+constexpr int decode_ncg(int G) { return G > kMaxCols ? (G + kMaxCols - 1) / kMaxCols : 1; }
 
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
@@ -149,16 +152,17 @@ __device__ __forceinline__ int stage_off(int dim) {
 // G (query heads per KV head) is any value with HP*G <= 16: the columns past
 // HP*G are computed and dropped. D: head_dim (64, 128 or 256); a wave's piece of
 // a token row (HP*D elements) is 128 to 512 bytes.
-template <bool F8, int HP, int D>
+template <bool F8, int HP, int D, bool H16 = false>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2)))
 void paged_decode_split_kernel(
     const bf16_t* __restrict__ q, int64_t q_row_stride,
     const void* __restrict__ k_cache, const void* __restrict__ v_cache,
     const int32_t* __restrict__ block_tables, int64_t bt_row_stride,
     const int32_t* __restrict__ context_lens, int32_t batch, int32_t Hk, int32_t G,
-    int32_t block_size, int32_t max_blocks, int64_t n_blocks, int32_t min_chunks,
+    int32_t NCG, int32_t block_size, int32_t max_blocks, int64_t n_blocks, int32_t min_chunks,
     float scale_log2, float v_scale, float* __restrict__ part, i32x4v_t* __restrict__ desc) {
   static_assert(decode_dim_ok(D), "head_dim 64, 128 or 256");
+  static_assert(!(F8 && H16), "fp8 caches are read with bf16 queries");
   constexpr int kEl = F8 ? 1 : 2;              // bytes per cache element
   constexpr int kSeg = HP * D * kEl;           // bytes a wave reads of each token row
   static_assert(kSeg >= 64 && kSeg <= 512, "a wave's piece of a row is 64..512 bytes");
@@ -184,7 +188,8 @@ void paged_decode_split_kernel(
   const int lane = threadIdx.x;
   const int g4 = lane >> 4;   // key group: keys 4*g4 .. 4*g4+3 of a chunk
   const int col = lane & 15;  // MFMA column: query head (S^T, O^T) / key row (K)
-  const int HPG = HP * G;     // query heads (MFMA columns) of the wave's head group
+  // Column groups: the G > 16 query heads of a KV head are split over NCG = ceil(G / 16)
+  // waves of 16 MFMA columns (the last one fewer; HP = 1 then); NCG = 1 otherwise.
   const int row_b = Hk * D * kEl;  // bytes of one cache row (token)
   const int max_tokens = max_blocks * block_size;
 
@@ -192,14 +197,19 @@ void paged_decode_split_kernel(
   // chunk stream (sequence-major); waves p, p+NP, p+2NP, ... split it into
   // equal ranges, so the NP waves i*NP .. i*NP+NP-1 read the Hk heads of the
   // same cache blocks at the same time.
-  const int NP = Hk / HP;
+  const int NP = Hk * NCG / HP;
   const int grp = blockIdx.x % NP;
-  const int kvh0 = grp * HP;
+  const int kvh0 = (grp / NCG) * HP;
+  const int cg = grp - (grp / NCG) * NCG;  // column group
+  // MFMA columns that are query heads (= partial rows per wave and sequence)
+  const int HPG = NCG > 1 ? min(kMaxCols, G - cg * kMaxCols) : HP * G;
+  const int qh0 = kvh0 * G + cg * kMaxCols;  // query head of column 0
   const int wi = blockIdx.x / NP;
   const int Wh = gridDim.x / NP;
   if (wi >= Wh) return;
-  // partial rows of this head group: (wave + sequence) x HPG columns
-  float* gpart = part + (int64_t)grp * (Wh + batch) * HPG * kPartRow;
+  // partial rows of this head group: (wave + sequence) x HPG columns, after the groups of
+  // the query heads before qh0 (so the groups' regions add up to (waves + batch) x Hq rows)
+  float* gpart = part + (int64_t)(Wh + batch) * qh0 * kPartRow;
   SeqCursor cur;
   int T = 0;
   for (cur.cb = 0; cur.cb < batch; cur.cb += 64) {
@@ -250,7 +260,7 @@ void paged_decode_split_kernel(
     {
       const int hc = col < HPG ? col : 0;
       const u32x4_t* qp = reinterpret_cast<const u32x4_t*>(
-          q + (int64_t)b * q_row_stride + (int64_t)(kvh0 * G + hc) * D + g4 * 8);
+          q + (int64_t)b * q_row_stride + (int64_t)(qh0 + hc) * D + g4 * 8);
 #pragma unroll
       for (int ks = 0; ks < kKs; ++ks) qreg[ks] = qp[ks * 4];
     }
@@ -345,8 +355,7 @@ void paged_decode_split_kernel(
             const u32x4_t ka =
                 *reinterpret_cast<const u32x4_t*>(
                     &kbuf[hh][col * kVRow + stage_off<F8, D>(g4 * 8 + ks * 32)]);
-            a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8_v(ka), as_bf16x8_v(qreg[ks]), a,
-                                                         0, 0, 0);
+            a = mfma_16x16x32<H16>(ka, qreg[ks], a);
           }
           st[hh] = a;
         }
@@ -374,9 +383,7 @@ void paged_decode_split_kernel(
 #pragma unroll
           for (int db = 0; db < kDb; ++db) acc[db] *= alpha;
         }
-        const bf16x2v_t p01 = {(__bf16)p[0], (__bf16)p[1]};
-        const bf16x2v_t p23 = {(__bf16)p[2], (__bf16)p[3]};
-        const uint2 pw = {__builtin_bit_cast(uint32_t, p01), __builtin_bit_cast(uint32_t, p23)};
+        const uint2 pw = {cvt_pk16<H16>(p[0], p[1]), cvt_pk16<H16>(p[2], p[3])};
         if constexpr (kShared) {  // V over the K rows: the S^T reads above come first
 #pragma unroll
           for (int r = 0; r < kLoads; ++r) {
@@ -408,7 +415,7 @@ void paged_decode_split_kernel(
           for (int hh = 0; hh < HP; ++hh) {
             const i16x4_t va = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                 (lds_i16x4_t*)&vbuf[hh][tr_row * kVRow + stage_off<F8, D>(db * 16 + tr_col)]);
-            acc[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pbh[hh], acc[db], 0, 0, 0);
+            acc[db] = mfma_16x16x16<H16>(va, pbh[hh], acc[db]);
           }
         }
       };
@@ -446,9 +453,9 @@ void paged_decode_split_kernel(
       if (g4 == 0) *reinterpret_cast<float2*>(&pr[D]) = float2{m_run, l_run};
     }
     if (c_lo + n_seg == nc && lane < HP) {
-      const int64_t first = (int64_t)grp * (Wh + batch) * HPG + (int64_t)(w_first + b) * HPG +
+      const int64_t first = (int64_t)(Wh + batch) * qh0 + (int64_t)(w_first + b) * HPG +
                             lane * G;
-      desc[(int64_t)b * Hk + kvh0 + lane] =
+      desc[((int64_t)b * Hk + kvh0 + lane) * NCG + cg] =
           i32x4v_t{(int32_t)first, wi - w_first + 1, HPG, 0};
     }
     k += n_seg;
@@ -473,24 +480,29 @@ __device__ __forceinline__ void load_dims(const float* p, float (&v)[N]) {
     v[3] = t.w;
   }
 }
-// N output dims of one lane as bf16 (2, 4 or 8 bytes).
-template <int N>
+// N output dims of one lane as bf16 or fp16 (2, 4 or 8 bytes).
+template <bool H16>
+__device__ __forceinline__ uint32_t out_pk(float lo, float hi) {
+  if constexpr (H16) return cvt_pk16<true>(lo, hi);
+  else return pack_bf16x2(lo, hi);
+}
+template <int N, bool H16>
 __device__ __forceinline__ void store_dims(bf16_t* op, const float (&o)[N], float scale) {
   if constexpr (N == 1) {
-    *reinterpret_cast<uint16_t*>(op) = (uint16_t)(pack_bf16x2(o[0] * scale, 0.f) & 0xffffu);
+    *reinterpret_cast<uint16_t*>(op) = (uint16_t)(out_pk<H16>(o[0] * scale, 0.f) & 0xffffu);
   } else if constexpr (N == 2) {
-    *reinterpret_cast<uint32_t*>(op) = pack_bf16x2(o[0] * scale, o[1] * scale);
+    *reinterpret_cast<uint32_t*>(op) = out_pk<H16>(o[0] * scale, o[1] * scale);
   } else {
     *reinterpret_cast<uint2*>(op) =
-        uint2{pack_bf16x2(o[0] * scale, o[1] * scale), pack_bf16x2(o[2] * scale, o[3] * scale)};
+        uint2{out_pk<H16>(o[0] * scale, o[1] * scale), out_pk<H16>(o[2] * scale, o[3] * scale)};
   }
 }
 
 // Merge the partials of one (sequence, query head): O = sum_s 2^(m_s-M) O_s /
 // sum_s 2^(m_s-M) l_s. One wave per pair; lane l owns output dims N*l .. N*l+N-1.
-template <int D>
+template <int D, bool H16 = false>
 __global__ __launch_bounds__(64) void paged_decode_combine_kernel(
-    const int32_t* __restrict__ context_lens, int32_t Hq, int32_t Hk,
+    const int32_t* __restrict__ context_lens, int32_t Hq, int32_t Hk, int32_t NCG,
     const float* __restrict__ part, const i32x4v_t* __restrict__ desc,
     bf16_t* __restrict__ out, int64_t out_row_stride) {
   static_assert(decode_dim_ok(D), "head_dim 64, 128 or 256");
@@ -504,7 +516,9 @@ __global__ __launch_bounds__(64) void paged_decode_combine_kernel(
   // (m, l) pair and the first eight partial rows at once (the second).
   static_assert(kMaxSlots <= 128, "two partials per lane");
   const int ctx = context_lens[b];
-  const i32x4v_t d = desc[(int64_t)b * Hk + h / G];
+  const int hq = h % G;                         // query head within the KV head's group
+  const int cg = NCG > 1 ? hq / kMaxCols : 0;    // its column group (0 unless G > 16)
+  const i32x4v_t d = desc[((int64_t)b * Hk + h / G) * NCG + cg];
   bf16_t* op = out + (int64_t)b * out_row_stride + (int64_t)h * D + N * lane;
   float o[N];
 #pragma unroll
@@ -512,11 +526,11 @@ __global__ __launch_bounds__(64) void paged_decode_combine_kernel(
   // the descriptor is written by this call for every sequence with ctx > 0
   const int ns = ctx > 0 ? min(d.y, kMaxSlots) : 0;
   if (ns == 0) {
-    store_dims<N>(op, o, 0.f);
+    store_dims<N, H16>(op, o, 0.f);
     return;
   }
   const int64_t stride = (int64_t)d.z * kPartRow;  // floats between a head's partials
-  const float* pbase = part + ((int64_t)d.x + h % G) * kPartRow;
+  const float* pbase = part + ((int64_t)d.x + hq - cg * kMaxCols) * kPartRow;
   const float* po = pbase + N * lane;
   float2 ml0 = {-INFINITY, 0.f}, ml1 = {-INFINITY, 0.f};
   if (lane < ns) ml0 = *reinterpret_cast<const float2*>(pbase + lane * stride + D);
@@ -562,7 +576,7 @@ __global__ __launch_bounds__(64) void paged_decode_combine_kernel(
       }
     }
   }
-  store_dims<N>(op, o, L > 0.f ? 1.f / L : 0.f);
+  store_dims<N, H16>(op, o, L > 0.f ? 1.f / L : 0.f);
 }
 
 static int decode_check(const void* q, const void* k_cache, const void* v_cache,
@@ -577,8 +591,8 @@ static int decode_check(const void* q, const void* k_cache, const void* v_cache,
   NKV_REQUIRE(n_q_heads % n_kv_heads == 0, NKV_EINVAL,
               "paged_decode: n_q_heads %% n_kv_heads != 0 (%d, %d)", n_q_heads, n_kv_heads);
   const int g = n_q_heads / n_kv_heads;
-  NKV_REQUIRE(g <= kMaxCols, NKV_EUNSUPPORTED, "paged_decode: GQA group %d above %d", g,
-              kMaxCols);
+  NKV_REQUIRE(g <= kMaxGroup, NKV_EUNSUPPORTED, "paged_decode: GQA group %d above %d", g,
+              kMaxGroup);
   NKV_REQUIRE(block_size > 0 && block_size % kChunk == 0, NKV_EUNSUPPORTED,
               "paged_decode: block_size must be a multiple of 16 (got %d)", block_size);
   NKV_REQUIRE(max_blocks_per_seq > 0 && bt_row_stride >= max_blocks_per_seq, NKV_EINVAL,
@@ -664,6 +678,7 @@ static int decode_grid_of(int hp, int D) {
 // The launch a decode call makes: KV heads per wave, the grid and the smallest range.
 struct DecodePlan {
   int hp;          // KV heads per wave (1, 2 or 4)
+  int ncg;         // column groups per KV head (1 unless G > 16; then hp = 1)
   unsigned grid;   // one-wave workgroups
   int32_t min_chunks;
 };
@@ -692,11 +707,12 @@ static DecodePlan decode_plan(int32_t batch, int32_t Hq, int32_t Hk, int32_t max
   }
   DecodePlan p;
   p.hp = hp;
+  p.ncg = decode_ncg(g);
   p.min_chunks = decode_min_chunks(max_blocks, block_size);
   // Resident waves per head group, but no more than the table width lets receive a range
   // of min_chunks (small batches launch only the waves that can get work).
   const int resident = decode_grid_of<F8>(hp, D);
-  const int np = Hk / p.hp;
+  const int np = Hk * p.ncg / p.hp;
   const int64_t per =
       std::min<int64_t>(std::max(1, resident / np), decode_useful_waves(batch, max_blocks,
                                                                         block_size));
@@ -704,15 +720,19 @@ static DecodePlan decode_plan(int32_t batch, int32_t Hq, int32_t Hk, int32_t max
   return p;
 }
 
-// Bytes of the descriptors (one per sequence and KV head; 16-byte aligned) and of the
-// partial rows a plan writes: per head group (waves + batch) x HP*G rows, i.e.
-// grid * HP*G + batch * Hq rows in all.
-static size_t decode_desc_bytes(int32_t batch, int32_t Hk) {
-  return (size_t)batch * Hk * sizeof(i32x4v_t);
+// Bytes of the descriptors (one per sequence, KV head and column group; 16-byte aligned)
+// and of the partial rows a plan writes: each head group (waves + batch) x its columns,
+// i.e. (grid / head groups + batch) x Hq rows in all (grid * hp*g + batch * Hq for G <= 16;
+// at most grid * 16 + batch * Hq).
+static size_t decode_desc_bytes(int32_t batch, int32_t n_groups) {
+  return (size_t)batch * n_groups * sizeof(i32x4v_t);
 }
-static size_t decode_part_bytes(int64_t grid, int32_t hpg, int32_t batch, int32_t Hq,
-                                int32_t D) {
-  return (size_t)(grid * hpg + (int64_t)batch * Hq) * part_row(D) * sizeof(float);
+static size_t decode_part_bytes(int64_t waves, int32_t batch, int32_t Hq, int32_t D) {
+  return (size_t)((waves + batch) * (int64_t)Hq) * part_row(D) * sizeof(float);
+}
+// Waves per head group of a plan.
+static int64_t decode_waves(const DecodePlan& p, int32_t Hk) {
+  return (int64_t)p.grid / (Hk * p.ncg / p.hp);
 }
 
 }  // namespace nkv
@@ -724,19 +744,20 @@ extern "C" size_t nkv_paged_decode_workspace_bytes(int32_t batch, int32_t n_q_he
   if (batch <= 0 || n_q_heads <= 0 || max_blocks_per_seq <= 0 || block_size <= 0 ||
       !decode_dim_ok(head_dim))
     return 0;
-  // Whatever the plan: grid <= CUs * kWavesPerCU and grid <= useful * (head groups), with
-  // HP*G <= min(16, Hq) and (head groups) * HP*G = Hq; the descriptors at most batch * Hq.
+  // Whatever the plan: waves per head group x Hq <= grid x min(16, Hq) (a group's columns
+  // are at most 16 and the groups' columns add up to Hq), grid <= CUs * kWavesPerCU and
+  // grid <= useful * (head groups); the descriptors (per KV head and column group) at most
+  // batch * Hq.
   const int64_t resident = (int64_t)device_cus() * kWavesPerCU;
   const int64_t cols = std::min<int64_t>(
       resident * std::min(kMaxCols, n_q_heads),
       decode_useful_waves(batch, max_blocks_per_seq, block_size) * n_q_heads);
-  return decode_desc_bytes(batch, n_q_heads) +
-         decode_part_bytes(0, 0, batch, n_q_heads, head_dim) +
+  return decode_desc_bytes(batch, n_q_heads) + decode_part_bytes(0, batch, n_q_heads, head_dim) +
          (size_t)cols * part_row(head_dim) * sizeof(float);
 }
 
 namespace nkv {
-template <bool F8>
+template <bool F8, bool H16 = false>
 static int decode_split(const void* q, int64_t q_row_stride, const void* k_cache,
                         const void* v_cache, const int32_t* block_tables, int64_t bt_row_stride,
                         const int32_t* context_lens, int32_t batch, int32_t n_q_heads,
@@ -755,20 +776,21 @@ static int decode_split(const void* q, int64_t q_row_stride, const void* k_cache
   const int g = n_q_heads / n_kv_heads;
   const DecodePlan p = decode_plan<F8>(batch, n_q_heads, n_kv_heads, max_blocks_per_seq,
                                        block_size, head_dim);
-  const size_t desc_b = decode_desc_bytes(batch, n_kv_heads);
-  const size_t need = desc_b + decode_part_bytes(p.grid, p.hp * g, batch, n_q_heads, head_dim);
+  const size_t desc_b = decode_desc_bytes(batch, n_kv_heads * p.ncg);
+  const int64_t waves = decode_waves(p, n_kv_heads);
+  const size_t need = desc_b + decode_part_bytes(waves, batch, n_q_heads, head_dim);
   NKV_REQUIRE(workspace && workspace_bytes >= need, NKV_EWORKSPACE,
               "paged_decode: workspace needs %zu bytes (got %zu)", need, workspace_bytes);
-  NKV_REQUIRE((int64_t)p.grid * p.hp * g + (int64_t)batch * n_q_heads < (1ll << 31),
-              NKV_EUNSUPPORTED, "paged_decode: too many partial rows");
+  NKV_REQUIRE((waves + batch) * n_q_heads < (1ll << 31), NKV_EUNSUPPORTED,
+              "paged_decode: too many partial rows");
   i32x4v_t* desc = static_cast<i32x4v_t*>(workspace);
   float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + desc_b);
   const float scale_log2 = scale * k_scale * kLog2e;
   hipStream_t s = as_stream(stream);
 #define NKV_DECODE_LAUNCH(HP, D)                                                               \
-  hipLaunchKernelGGL((paged_decode_split_kernel<F8, HP, D>), dim3(p.grid), dim3(64), 0, s,      \
+  hipLaunchKernelGGL((paged_decode_split_kernel<F8, HP, D, H16>), dim3(p.grid), dim3(64), 0, s, \
                      (const bf16_t*)q, q_row_stride, k_cache, v_cache, block_tables,           \
-                     bt_row_stride, context_lens, batch, n_kv_heads, g, block_size,            \
+                     bt_row_stride, context_lens, batch, n_kv_heads, g, p.ncg, block_size,     \
                      max_blocks_per_seq, n_blocks, p.min_chunks, scale_log2, v_scale, part,    \
                      desc)
   if (head_dim == 64) {
@@ -796,6 +818,7 @@ static int decode_split(const void* q, int64_t q_row_stride, const void* k_cache
 
 // The combine of a split launched with the same arguments: the partial rows start after
 // the descriptors, whatever the plan.
+template <bool H16 = false>
 static int decode_combine(const int32_t* context_lens, int32_t batch, int32_t n_q_heads,
                           int32_t n_kv_heads, int32_t head_dim, int32_t block_size,
                           int32_t max_blocks_per_seq, void* out, int64_t out_row_stride,
@@ -803,8 +826,10 @@ static int decode_combine(const int32_t* context_lens, int32_t batch, int32_t n_
   NKV_REQUIRE(decode_dim_ok(head_dim), NKV_EUNSUPPORTED,
               "paged_decode: head_dim must be 64, 128 or 256 (got %d)", head_dim);
   NKV_REQUIRE(batch >= 0 && n_q_heads > 0 && n_kv_heads > 0 && n_q_heads % n_kv_heads == 0 &&
-                  n_q_heads / n_kv_heads <= kMaxCols && block_size > 0 && max_blocks_per_seq > 0,
+                  n_q_heads / n_kv_heads <= kMaxGroup && block_size > 0 &&
+                  max_blocks_per_seq > 0,
               NKV_EINVAL, "paged_decode_combine: bad sizes");
+  const int ncg = decode_ncg(n_q_heads / n_kv_heads);
   if (batch == 0) return NKV_OK;
   NKV_REQUIRE(out && context_lens, NKV_EINVAL, "paged_decode_combine: null pointer");
   // each lane stores D/64 consecutive bf16 (2, 4 or 8 bytes)
@@ -814,7 +839,7 @@ static int decode_combine(const int32_t* context_lens, int32_t batch, int32_t n_
               NKV_EINVAL,
               "paged_decode_combine: out must be %d-byte aligned with a row stride >= Hq*D "
               "that is a multiple of %d", 2 * al, al);
-  const size_t desc_b = decode_desc_bytes(batch, n_kv_heads);
+  const size_t desc_b = decode_desc_bytes(batch, n_kv_heads * ncg);
   NKV_REQUIRE(workspace && workspace_bytes > desc_b, NKV_EWORKSPACE,
               "paged_decode_combine: workspace of %zu bytes holds no partials",
               workspace_bytes);
@@ -822,9 +847,9 @@ static int decode_combine(const int32_t* context_lens, int32_t batch, int32_t n_
   const float* part = reinterpret_cast<const float*>(static_cast<const char*>(workspace) + desc_b);
   const dim3 grid((unsigned)(batch * n_q_heads));
 #define NKV_COMBINE_LAUNCH(D)                                                                  \
-  hipLaunchKernelGGL((paged_decode_combine_kernel<D>), grid, dim3(64), 0, as_stream(stream),    \
-                     context_lens, n_q_heads, n_kv_heads, part, desc, (bf16_t*)out,            \
-                     out_row_stride)
+  hipLaunchKernelGGL((paged_decode_combine_kernel<D, H16>), grid, dim3(64), 0,                 \
+                     as_stream(stream), context_lens, n_q_heads, n_kv_heads, ncg, part, desc,  \
+                     (bf16_t*)out, out_row_stride)
   if (head_dim == 64) NKV_COMBINE_LAUNCH(64);
   else if (head_dim == 128) NKV_COMBINE_LAUNCH(128);
   else NKV_COMBINE_LAUNCH(256);
@@ -873,6 +898,26 @@ extern "C" int nkv_paged_decode(const void* q, int64_t q_row_stride, const void*
   return nkv_paged_decode_combine(context_lens, batch, n_q_heads, n_kv_heads, head_dim,
                                   block_size, max_blocks_per_seq, out, out_row_stride, workspace,
                                   workspace_bytes, stream);
+}
+
+extern "C" int nkv_paged_decode_f16(const void* q, int64_t q_row_stride, const void* k_cache,
+                                    const void* v_cache, const int32_t* block_tables,
+                                    int64_t bt_row_stride, const int32_t* context_lens,
+                                    int32_t batch, int32_t n_q_heads, int32_t n_kv_heads,
+                                    int32_t head_dim, int32_t block_size,
+                                    int32_t max_blocks_per_seq, int64_t n_blocks, float scale,
+                                    void* out, int64_t out_row_stride, void* workspace,
+                                    size_t workspace_bytes, void* stream) {
+  nkv::clear_error();
+  int rc = nkv::decode_split<false, true>(q, q_row_stride, k_cache, v_cache, block_tables,
+                                          bt_row_stride, context_lens, batch, n_q_heads,
+                                          n_kv_heads, head_dim, block_size, max_blocks_per_seq,
+                                          n_blocks, scale, 1.f, 1.f, workspace, workspace_bytes,
+                                          stream);
+  if (rc) return rc;
+  return nkv::decode_combine<true>(context_lens, batch, n_q_heads, n_kv_heads, head_dim,
+                                   block_size, max_blocks_per_seq, out, out_row_stride,
+                                   workspace, workspace_bytes, stream);
 }
 
 extern "C" int nkv_paged_decode_fp8(const void* q, int64_t q_row_stride, const void* k_cache,
@@ -948,9 +993,9 @@ extern "C" int nkv_paged_decode_noalloc(const void* q, int64_t q_row_stride, con
   // the bytes this call's plan needs, against the array's fixed size
   const DecodePlan p = decode_plan<false>(batch, n_q_heads, n_kv_heads, max_blocks_per_seq,
                                           block_size, head_dim);
-  const size_t need = decode_desc_bytes(batch, n_kv_heads) +
-                      decode_part_bytes(p.grid, p.hp * (n_q_heads / n_kv_heads), batch,
-                                        n_q_heads, head_dim);
+  const size_t need = decode_desc_bytes(batch, n_kv_heads * p.ncg) +
+                      decode_part_bytes(decode_waves(p, n_kv_heads), batch, n_q_heads,
+                                        head_dim);
   NKV_REQUIRE(need <= kScratchBytes, NKV_EUNSUPPORTED,
               "paged_decode_noalloc: batch %d x %d query heads needs %zu bytes of partials, "
               "above the fixed %zu-byte array; use nkv_paged_decode with a workspace",

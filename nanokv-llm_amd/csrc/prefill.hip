@@ -68,16 +68,12 @@ typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
 typedef __attribute__((address_space(3))) u32x4_t lds_u32x4_t;
 typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
 
-__device__ __forceinline__ uint32_t pack2(float a, float b) {
-  const bf16x2v_t v = {(__bf16)a, (__bf16)b};
-  return __builtin_bit_cast(uint32_t, v);
-}
-// acc + lo + hi of a packed bf16 pair (v_dot2c_f32_bf16 against (1, 1))
-__device__ __forceinline__ float sum2_bf16(uint32_t pair, float acc) {
-  const bf16x2v_t ones = {(__bf16)1.f, (__bf16)1.f};
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v_t, pair), ones, acc, false);
+// Output pair: bf16 with the round-to-nearest-even of pack_bf16x2, or fp16.
+template <bool H16>
+__device__ __forceinline__ uint32_t out_pack(float a, float b) {
+  if constexpr (H16) return cvt_pk16<true>(a, b);
+  else return pack_bf16x2(a, b);
 }
 // Raw buffer descriptor over [base, base + bytes): loads past `bytes` return 0.
 __device__ __forceinline__ i32x4_t buffer_desc(const void* base, uint32_t bytes) {
@@ -96,7 +92,7 @@ __device__ __forceinline__ void load_to_lds(i32x4_t desc, uint32_t lds_addr, uin
                : "memory");
 }
 
-template <bool F8, int D>
+template <bool F8, int D, bool H16 = false>
 __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void prefill_varlen_kernel(
     const bf16_t* __restrict__ q, int64_t q_row_stride, const void* __restrict__ k_cache,
     const void* __restrict__ v_cache, int64_t k_row_stride, int64_t v_row_stride,
@@ -105,6 +101,7 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void prefill_varlen_kernel(
     int32_t block_size, int32_t max_blocks, int32_t n_limit, int32_t n_tiles, float scale_log2,
     float v_scale, bf16_t* __restrict__ out, int64_t out_row_stride) {
   static_assert(prefill_dim_ok(D), "head_dim 64, 128 or 256");
+  static_assert(!(F8 && H16), "fp8 caches are read with bf16 queries");
   constexpr int kEl = F8 ? 1 : 2;          // bytes per cache element
   constexpr int kRB = D * 2;               // bytes of a staged (bf16) K or V row
   constexpr int kNC = D / 8;               // 16-byte chunks per staged row
@@ -372,8 +369,7 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void prefill_varlen_kernel(
         f32x4_t a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < kKs; ++ks)
-          a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8_v(ka[ks]), as_bf16x8_v(qreg[rr][ks]),
-                                                       a, 0, 0, 0);
+          a = mfma_16x16x32<H16>(ka[ks], qreg[rr][ks], a);
         st[rr][h] = a;
       }
     }
@@ -441,10 +437,11 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void prefill_varlen_kernel(
 #pragma unroll
         for (int e = 0; e < 8; ++e)
           p[e] = fast_exp2(fmaf(sv[rr][8 * c + e], scale_log2, -mb[rr]));  // -inf -> 0
-        pb[rr] = u32x4_t{pack2(p[0], p[1]), pack2(p[2], p[3]), pack2(p[4], p[5]), pack2(p[6], p[7])};
+        pb[rr] = u32x4_t{cvt_pk16<H16>(p[0], p[1]), cvt_pk16<H16>(p[2], p[3]),
+                         cvt_pk16<H16>(p[4], p[5]), cvt_pk16<H16>(p[6], p[7])};
         float l = l_run[rr];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) l = sum2_bf16(pb[rr][e], l);
+        for (int e = 0; e < 4; ++e) l = sum2_16<H16>(pb[rr][e], l);
         l_run[rr] = l;
       }
 #pragma unroll
@@ -457,8 +454,7 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void prefill_varlen_kernel(
                             __builtin_bit_cast(uint2, v1).x, __builtin_bit_cast(uint2, v1).y};
 #pragma unroll
         for (int rr = 0; rr < kRG; ++rr)
-          acc[rr][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              as_bf16x8_v(va), as_bf16x8_v(pb[rr]), acc[rr][db], 0, 0, 0);
+          acc[rr][db] = mfma_16x16x32<H16>(va, pb[rr], acc[rr][db]);
       }
     }
     // next step's tile landed (own loads), then publish and free this stage
@@ -489,8 +485,8 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void prefill_varlen_kernel(
                  (int64_t)(kvh * G + head[rr]) * D + g4 * 4;
 #pragma unroll
     for (int db = 0; db < kDb; ++db) {
-      const uint2 w = {pack_bf16x2(acc[rr][db][0] * inv, acc[rr][db][1] * inv),
-                       pack_bf16x2(acc[rr][db][2] * inv, acc[rr][db][3] * inv)};
+      const uint2 w = {out_pack<H16>(acc[rr][db][0] * inv, acc[rr][db][1] * inv),
+                       out_pack<H16>(acc[rr][db][2] * inv, acc[rr][db][3] * inv)};
       *reinterpret_cast<uint2*>(op + db * 16) = w;
     }
   }
@@ -499,7 +495,7 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void prefill_varlen_kernel(
 }  // namespace nkv
 
 namespace nkv {
-template <bool F8>
+template <bool F8, bool H16 = false>
 static int prefill_launch(const void* q, int64_t q_row_stride, const void* k_cache,
                           const void* v_cache, int64_t k_row_stride, int64_t v_row_stride,
                           const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
@@ -509,7 +505,7 @@ static int prefill_launch(const void* q, int64_t q_row_stride, const void* k_cac
                           int32_t block_size, int64_t n_rows, float scale, float k_scale,
                           float v_scale, void* out, int64_t out_row_stride, void* stream) {
   constexpr int kEl = F8 ? 1 : 2;
-  const char* what = F8 ? "prefill_varlen_fp8" : "prefill_varlen";
+  const char* what = F8 ? "prefill_varlen_fp8" : H16 ? "prefill_varlen_f16" : "prefill_varlen";
   NKV_REQUIRE(n_seqs >= 0 && max_seqlen_q >= 0 && n_q_heads > 0 && n_kv_heads > 0, NKV_EINVAL,
               "%s: bad sizes", what);
   if (n_seqs == 0 || max_seqlen_q == 0) return NKV_OK;
@@ -517,7 +513,9 @@ static int prefill_launch(const void* q, int64_t q_row_stride, const void* k_cac
               "%s: head_dim must be 64, 128 or 256 (got %d)", what, head_dim);
   NKV_REQUIRE(n_q_heads % n_kv_heads == 0, NKV_EINVAL, "%s: Hq %% Hk != 0", what);
   const int g = n_q_heads / n_kv_heads;
-  NKV_REQUIRE(g <= 16, NKV_EUNSUPPORTED, "%s: GQA group %d above 16", what, g);
+  // a tile holds at least one query for all g heads of its KV head
+  NKV_REQUIRE(g <= prefill_tile_rows(head_dim), NKV_EUNSUPPORTED, "%s: GQA group %d above %d",
+              what, g, prefill_tile_rows(head_dim));
   NKV_REQUIRE(q && k_cache && v_cache && cu_seqlens_q && cu_seqlens_k && out, NKV_EINVAL,
               "%s: null pointer", what);
   NKV_REQUIRE(aligned16(q) && aligned16(k_cache) && aligned16(v_cache) && aligned16(out),
@@ -554,7 +552,7 @@ static int prefill_launch(const void* q, int64_t q_row_stride, const void* k_cac
   NKV_REQUIRE(grid < (1ll << 31), NKV_EUNSUPPORTED, "%s: grid too large", what);
   const float sl2 = scale * k_scale * kLog2e;
 #define NKV_PREFILL_LAUNCH(D)                                                                  \
-  hipLaunchKernelGGL((prefill_varlen_kernel<F8, D>), dim3((unsigned)grid), dim3(256), 0,         \
+  hipLaunchKernelGGL((prefill_varlen_kernel<F8, D, H16>), dim3((unsigned)grid), dim3(256), 0,    \
                      as_stream(stream), (const bf16_t*)q, q_row_stride, k_cache, v_cache,        \
                      k_row_stride, v_row_stride, cu_seqlens_q, cu_seqlens_k, block_tables,       \
                      bt_row_stride, n_kv_heads, g, block_size, max_blocks, n_limit, n_tiles, sl2, \
@@ -563,7 +561,8 @@ static int prefill_launch(const void* q, int64_t q_row_stride, const void* k_cac
   else if (head_dim == 128) NKV_PREFILL_LAUNCH(128);
   else NKV_PREFILL_LAUNCH(256);
 #undef NKV_PREFILL_LAUNCH
-  return check_launch(F8 ? "nkv_prefill_varlen_fp8" : "nkv_prefill_varlen");
+  return check_launch(F8 ? "nkv_prefill_varlen_fp8"
+                         : H16 ? "nkv_prefill_varlen_f16" : "nkv_prefill_varlen");
 }
 }  // namespace nkv
 
@@ -582,6 +581,24 @@ extern "C" int nkv_prefill_varlen(const void* q, int64_t q_row_stride, const voi
                                     bt_row_stride, max_blocks_per_seq, n_seqs, max_seqlen_q,
                                     n_q_heads, n_kv_heads, head_dim, block_size, n_rows, scale,
                                     1.f, 1.f, out, out_row_stride, stream);
+}
+
+extern "C" int nkv_prefill_varlen_f16(const void* q, int64_t q_row_stride, const void* k_cache,
+                                      const void* v_cache, int64_t k_row_stride,
+                                      int64_t v_row_stride, const int32_t* cu_seqlens_q,
+                                      const int32_t* cu_seqlens_k, const int32_t* block_tables,
+                                      int64_t bt_row_stride, int32_t max_blocks_per_seq,
+                                      int32_t n_seqs, int32_t max_seqlen_q, int32_t n_q_heads,
+                                      int32_t n_kv_heads, int32_t head_dim, int32_t block_size,
+                                      int64_t n_rows, float scale, void* out,
+                                      int64_t out_row_stride, void* stream) {
+  nkv::clear_error();
+  return nkv::prefill_launch<false, true>(q, q_row_stride, k_cache, v_cache, k_row_stride,
+                                          v_row_stride, cu_seqlens_q, cu_seqlens_k, block_tables,
+                                          bt_row_stride, max_blocks_per_seq, n_seqs,
+                                          max_seqlen_q, n_q_heads, n_kv_heads, head_dim,
+                                          block_size, n_rows, scale, 1.f, 1.f, out,
+                                          out_row_stride, stream);
 }
 
 extern "C" int nkv_prefill_varlen_fp8(const void* q, int64_t q_row_stride, const void* k_cache,

@@ -29,8 +29,23 @@ constexpr bool rope_dim_ok(int D) { return D == 64 || D == 128 || D == 256; }
 // units per block: one per group of D/16 lanes
 constexpr int rope_units_per_block(int D) { return kRopeThreads / (D / 16); }
 
-__device__ __forceinline__ float bf(uint32_t b16) { return __uint_as_float(b16 << 16); }
-__device__ __forceinline__ float round_bf(float f) { return bf(f32_to_bf16_bits(f)); }
+// One 16-bit element (low bits of b16) -> fp32, and fp32 rounded to the element type and
+// back (round to nearest even): bf16, or fp16 with H16.
+template <bool H16>
+__device__ __forceinline__ float el(uint32_t b16) {
+  if constexpr (H16) return (float)__builtin_bit_cast(_Float16, (uint16_t)b16);
+  else return __uint_as_float(b16 << 16);
+}
+template <bool H16>
+__device__ __forceinline__ float round_el(float f) {
+  if constexpr (H16) return (float)(_Float16)f;
+  else return el<false>(f32_to_bf16_bits(f));
+}
+template <bool H16>
+__device__ __forceinline__ uint32_t pack_el(float lo, float hi) {
+  if constexpr (H16) return cvt_pk16<true>(lo, hi);
+  else return pack_bf16x2(lo, hi);
+}
 
 struct RopeArgs {
   const bf16_t* q_in;
@@ -64,7 +79,7 @@ struct RopeArgs {
 // and the slot are loaded together; the cos|sin row (which needs the position)
 // is the only dependent load. One unit per group measured fastest at every size
 // (more units per group serialise their dependent loads).
-template <int D>
+template <int D, bool H16 = false>
 __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_store_kernel(const RopeArgs a) {
   // Every product is rounded on its own, as the reference's separate torch ops are:
   // no a*b - c*d -> fma contraction.
@@ -98,10 +113,10 @@ __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_store_kernel(const 
     float x[16];  // x[0..7] first half, x[8..15] the rotary partners
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      x[2 * e] = bf(vlo[e] & 0xffffu);
-      x[2 * e + 1] = bf(vlo[e] >> 16);
-      x[8 + 2 * e] = bf(vhi[e] & 0xffffu);
-      x[9 + 2 * e] = bf(vhi[e] >> 16);
+      x[2 * e] = el<H16>(vlo[e] & 0xffffu);
+      x[2 * e + 1] = el<H16>(vlo[e] >> 16);
+      x[8 + 2 * e] = el<H16>(vhi[e] & 0xffffu);
+      x[9 + 2 * e] = el<H16>(vhi[e] >> 16);
     }
     if (a.q_weight) {
       const bf16_t* w = is_q ? a.q_weight : a.k_weight;
@@ -115,10 +130,10 @@ __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_store_kernel(const 
       const float r = rsqrtf(ss * (1.0f / D) + a.eps);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        x[2 * e] = round_bf(round_bf(x[2 * e] * r) * bf(wlo[e] & 0xffffu));
-        x[2 * e + 1] = round_bf(round_bf(x[2 * e + 1] * r) * bf(wlo[e] >> 16));
-        x[8 + 2 * e] = round_bf(round_bf(x[8 + 2 * e] * r) * bf(whi[e] & 0xffffu));
-        x[9 + 2 * e] = round_bf(round_bf(x[9 + 2 * e] * r) * bf(whi[e] >> 16));
+        x[2 * e] = round_el<H16>(round_el<H16>(x[2 * e] * r) * el<H16>(wlo[e] & 0xffffu));
+        x[2 * e + 1] = round_el<H16>(round_el<H16>(x[2 * e + 1] * r) * el<H16>(wlo[e] >> 16));
+        x[8 + 2 * e] = round_el<H16>(round_el<H16>(x[8 + 2 * e] * r) * el<H16>(whi[e] & 0xffffu));
+        x[9 + 2 * e] = round_el<H16>(round_el<H16>(x[9 + 2 * e] * r) * el<H16>(whi[e] >> 16));
       }
     }
     const float cv[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
@@ -132,8 +147,8 @@ __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_store_kernel(const 
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      vlo[e] = pack_bf16x2(y[2 * e], y[2 * e + 1]);
-      vhi[e] = pack_bf16x2(y[8 + 2 * e], y[9 + 2 * e]);
+      vlo[e] = pack_el<H16>(y[2 * e], y[2 * e + 1]);
+      vhi[e] = pack_el<H16>(y[8 + 2 * e], y[9 + 2 * e]);
     }
   }
   if (is_q) {
@@ -157,17 +172,17 @@ __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_store_kernel(const 
 
 }  // namespace nkv
 
-extern "C" int nkv_qk_norm_rope_store(const void* q, int64_t q_row_stride, const void* k,
-                                      int64_t k_row_stride, const void* v, int64_t v_row_stride,
-                                      const int64_t* positions, const void* q_norm_weight,
-                                      const void* k_norm_weight, float eps,
-                                      const float* cos_sin_cache, int64_t max_position,
-                                      void* q_out, int64_t q_out_row_stride, void* k_out,
-                                      void* k_cache, void* v_cache, const int32_t* slot_mapping,
-                                      int64_t n_slots, int64_t n_tokens, int32_t n_q_heads,
-                                      int32_t n_kv_heads, int32_t head_dim, void* stream) {
-  using namespace nkv;
-  clear_error();
+namespace nkv {
+template <bool H16>
+static int qk_norm_rope_store_impl(const void* q, int64_t q_row_stride, const void* k,
+                                   int64_t k_row_stride, const void* v, int64_t v_row_stride,
+                                   const int64_t* positions, const void* q_norm_weight,
+                                   const void* k_norm_weight, float eps,
+                                   const float* cos_sin_cache, int64_t max_position,
+                                   void* q_out, int64_t q_out_row_stride, void* k_out,
+                                   void* k_cache, void* v_cache, const int32_t* slot_mapping,
+                                   int64_t n_slots, int64_t n_tokens, int32_t n_q_heads,
+                                   int32_t n_kv_heads, int32_t head_dim, void* stream) {
   NKV_REQUIRE(n_tokens >= 0 && n_q_heads > 0 && n_kv_heads > 0 && n_slots >= 0, NKV_EINVAL,
               "qk_norm_rope_store: bad sizes");
   if (n_tokens == 0) return NKV_OK;
@@ -221,13 +236,47 @@ extern "C" int nkv_qk_norm_rope_store(const void* q, int64_t q_row_stride, const
   a.Hq = n_q_heads;
   a.Hk = n_kv_heads;
   if (head_dim == 64)
-    hipLaunchKernelGGL(qk_norm_rope_store_kernel<64>, dim3(grid), dim3(kRopeThreads), 0,
+    hipLaunchKernelGGL((qk_norm_rope_store_kernel<64, H16>), dim3(grid), dim3(kRopeThreads), 0,
                        as_stream(stream), a);
   else if (head_dim == 128)
-    hipLaunchKernelGGL(qk_norm_rope_store_kernel<128>, dim3(grid), dim3(kRopeThreads), 0,
+    hipLaunchKernelGGL((qk_norm_rope_store_kernel<128, H16>), dim3(grid), dim3(kRopeThreads), 0,
                        as_stream(stream), a);
   else
-    hipLaunchKernelGGL(qk_norm_rope_store_kernel<256>, dim3(grid), dim3(kRopeThreads), 0,
+    hipLaunchKernelGGL((qk_norm_rope_store_kernel<256, H16>), dim3(grid), dim3(kRopeThreads), 0,
                        as_stream(stream), a);
-  return check_launch("nkv_qk_norm_rope_store");
+  return check_launch(H16 ? "nkv_qk_norm_rope_store_f16" : "nkv_qk_norm_rope_store");
+}
+}  // namespace nkv
+
+extern "C" int nkv_qk_norm_rope_store(const void* q, int64_t q_row_stride, const void* k,
+                                      int64_t k_row_stride, const void* v, int64_t v_row_stride,
+                                      const int64_t* positions, const void* q_norm_weight,
+                                      const void* k_norm_weight, float eps,
+                                      const float* cos_sin_cache, int64_t max_position,
+                                      void* q_out, int64_t q_out_row_stride, void* k_out,
+                                      void* k_cache, void* v_cache, const int32_t* slot_mapping,
+                                      int64_t n_slots, int64_t n_tokens, int32_t n_q_heads,
+                                      int32_t n_kv_heads, int32_t head_dim, void* stream) {
+  nkv::clear_error();
+  return nkv::qk_norm_rope_store_impl<false>(
+      q, q_row_stride, k, k_row_stride, v, v_row_stride, positions, q_norm_weight,
+      k_norm_weight, eps, cos_sin_cache, max_position, q_out, q_out_row_stride, k_out, k_cache,
+      v_cache, slot_mapping, n_slots, n_tokens, n_q_heads, n_kv_heads, head_dim, stream);
+}
+
+extern "C" int nkv_qk_norm_rope_store_f16(const void* q, int64_t q_row_stride, const void* k,
+                                          int64_t k_row_stride, const void* v,
+                                          int64_t v_row_stride, const int64_t* positions,
+                                          const void* q_norm_weight, const void* k_norm_weight,
+                                          float eps, const float* cos_sin_cache,
+                                          int64_t max_position, void* q_out,
+                                          int64_t q_out_row_stride, void* k_out, void* k_cache,
+                                          void* v_cache, const int32_t* slot_mapping,
+                                          int64_t n_slots, int64_t n_tokens, int32_t n_q_heads,
+                                          int32_t n_kv_heads, int32_t head_dim, void* stream) {
+  nkv::clear_error();
+  return nkv::qk_norm_rope_store_impl<true>(
+      q, q_row_stride, k, k_row_stride, v, v_row_stride, positions, q_norm_weight,
+      k_norm_weight, eps, cos_sin_cache, max_position, q_out, q_out_row_stride, k_out, k_cache,
+      v_cache, slot_mapping, n_slots, n_tokens, n_q_heads, n_kv_heads, head_dim, stream);
 }

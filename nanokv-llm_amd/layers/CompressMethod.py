@@ -7,10 +7,12 @@ nanokvllm/layers/CompressMethod.py:4-57: Q [m, Hq, window, D], K/V
 when the window is too short. The importance of a key sums, over the query
 window and the query heads, the softmax of the window queries' scores over
 keys 0 .. L-window-1 (key 0 masked). Runs on libnkv_amd.so
-(nkv_snapkv_select: MFMA scores, softmax, head and window sums and the top-k;
-window 1 with L <= 1024, L % 64 == 0 in one fused launch, otherwise
-L % 256 == 0 is required). Scores are fp32 (the reference computes them in
-bf16) and ties at the selection threshold go to the lower index.
+(nkv_snapkv_select, or nkv_snapkv_select_f16 for fp16 Q/K: MFMA scores,
+softmax, head and window sums and the top-k; window 1 with L <= 1024,
+L % 64 == 0 in one fused launch, any other L through 256-key score chunks
+with the last one masked). At most 4096 candidates (L - window). Scores are
+fp32 (the reference computes them in the input dtype) and ties at the
+selection threshold go to the lower index.
 """
 from __future__ import annotations
 
@@ -31,8 +33,10 @@ def SnapKV(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor | None = None, num_
         return False
     assert Hq % Hk == 0, f"GQA requires Hq % Hk == 0, but got Hq={Hq}, Hk={Hk}"
     _lib.require_device(K.device, Q=Q, V=V)
-    _lib.need(K.is_contiguous() and K.dtype == torch.bfloat16 and Q.dtype == torch.bfloat16,
-              "SnapKV: Q and K must be bf16, K contiguous")
+    f16 = _lib.is_f16(K, "SnapKV: K")
+    _lib.need(K.is_contiguous() and Q.dtype == K.dtype,
+              "SnapKV: Q and K must share one dtype (bf16 or fp16), K contiguous")
+    _lib.need(L - window <= 4096, "SnapKV: at most 4096 candidates (L - window)")
     _lib.need(Q.shape == (m, Hq, window, D) and Q.is_contiguous(),
               f"SnapKV: Q must be contiguous [{m}, {Hq}, {window}, {D}]")
     n_sets = 1 if agg == "all" else Hk
@@ -42,7 +46,8 @@ def SnapKV(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor | None = None, num_
     keep = torch.empty(m, n_sets, num_keep + 1 + window, dtype=torch.int32, device=K.device)
     ws_bytes = lib.nkv_snapkv_workspace_bytes(m, Hq, Hk, L, window)
     workspace = torch.empty(max(ws_bytes, 4), dtype=torch.uint8, device=K.device)
-    rc = lib.nkv_snapkv_select(Q.data_ptr(), K.data_ptr(), m, Hq, Hk, D, L, window, D ** -0.5,
+    fn = lib.nkv_snapkv_select_f16 if f16 else lib.nkv_snapkv_select
+    rc = fn(Q.data_ptr(), K.data_ptr(), m, Hq, Hk, D, L, window, D ** -0.5,
                                AGG_MODES[agg], num_keep, importance.data_ptr(), keep.data_ptr(),
                                workspace.data_ptr(), workspace.numel(), _lib.stream_of(K))
     _lib.check(rc, "SnapKV select")

@@ -25,7 +25,9 @@ def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
 
     Same checks as the reference (attention.py:33-40): last dim contiguous,
     head stride == head_dim, cache token stride == Hk*D, one slot per token.
-    An fp8 (float8_e4m3fn) cache stores E4M3FN(clamp(x / scale)).
+    bf16 or fp16 rows go to a cache of the same dtype (the copy moves 2-byte
+    elements); an fp8 (float8_e4m3fn) cache stores E4M3FN(clamp(x / scale)) of
+    bf16 rows.
     """
     N, num_heads, head_dim = key.shape
     D = num_heads * head_dim
@@ -48,7 +50,9 @@ def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
             head_dim, n_slots, float(k_scale), float(v_scale), _lib.stream_of(key))
         _lib.check(rc, "store_kvcache_fp8")
         return
-    assert key.dtype == _BF16 and value.dtype == _BF16 and k_cache.dtype == _BF16
+    _lib.is_f16(key, "store_kvcache: key")
+    _lib.need(value.dtype == key.dtype and k_cache.dtype == key.dtype,
+              "store_kvcache: key, value and the caches must share one dtype")
     rc = _lib.lib().nkv_store_kvcache(
         key.data_ptr(), key.stride(0), value.data_ptr(), value.stride(0),
         k_cache.data_ptr(), v_cache.data_ptr(), slot_mapping.data_ptr(), N,
@@ -61,14 +65,17 @@ def _decode_args(q, k_cache, block_tables, context_lens, v_cache=None, out=None)
                         context_lens=context_lens, out=out)
     bs, Hq, D = q.shape
     NB, B, Hk, Dk = k_cache.shape
-    _lib.need(q.dtype == _BF16, "paged_decode: q must be bf16")
+    _lib.is_f16(q, "paged_decode: q")
+    _lib.need(k_cache.dtype == q.dtype or (k_cache.dtype == torch.float8_e4m3fn
+                                           and q.dtype == _BF16),
+              "paged_decode: caches must have q's dtype (or fp8 with bf16 q)")
     if v_cache is not None:
         _lib.need(v_cache.shape == k_cache.shape and v_cache.dtype == k_cache.dtype
                   and v_cache.is_contiguous(),
                   "paged_decode: v_cache must be contiguous with k_cache's shape and dtype")
     if out is not None:
-        _lib.need(out.shape == q.shape and out.dtype == _BF16 and out.stride(-1) == 1
-                  and out.stride(1) == D, "paged_decode: out must be bf16 [bs, Hq, D], "
+        _lib.need(out.shape == q.shape and out.dtype == q.dtype and out.stride(-1) == 1
+                  and out.stride(1) == D, "paged_decode: out must be [bs, Hq, D] in q's dtype, "
                   "rows of contiguous heads")
     assert Dk == D and q.stride(-1) == 1 and q.stride(1) == D
     assert k_cache.is_contiguous()
@@ -136,7 +143,7 @@ def paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                  out: torch.Tensor | None = None,
                  workspace: torch.Tensor | None = None, k_scale: float = 1.0,
                  v_scale: float = 1.0) -> torch.Tensor:
-    """Paged GQA decode: q [bs, Hq, D] -> out [bs, Hq, D] (bf16).
+    """Paged GQA decode: q [bs, Hq, D] -> out [bs, Hq, D] (q's dtype: bf16 or fp16).
 
     Same math as flash_attn_with_kvcache(q.unsqueeze(1), k_cache, v_cache,
     cache_seqlens=context_lens, block_table=block_tables, softmax_scale=scale,
@@ -145,7 +152,7 @@ def paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     """
     bs, Hq, D, NB, B, Hk = _decode_args(q, k_cache, block_tables, context_lens, v_cache, out)
     if out is None:
-        out = torch.empty(bs, Hq, D, dtype=_BF16, device=q.device)
+        out = torch.empty(bs, Hq, D, dtype=q.dtype, device=q.device)
     if workspace is None:
         workspace = paged_decode_workspace(q, k_cache, block_tables)
     if k_cache.dtype == torch.float8_e4m3fn:
@@ -158,11 +165,12 @@ def paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
             _lib.stream_of(q))
         _lib.check(rc, "paged_decode_fp8")
         return out
-    rc = _lib.lib().nkv_paged_decode(
-        q.data_ptr(), q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(),
-        block_tables.data_ptr(), block_tables.stride(0), context_lens.data_ptr(), bs, Hq, Hk, D,
-        B, block_tables.size(1), NB, float(scale), out.data_ptr(), out.stride(0),
-        workspace.data_ptr(), workspace.numel(), _lib.stream_of(q))
+    fn = _lib.lib().nkv_paged_decode_f16 if q.dtype == torch.float16 else \
+        _lib.lib().nkv_paged_decode
+    rc = fn(q.data_ptr(), q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(),
+            block_tables.data_ptr(), block_tables.stride(0), context_lens.data_ptr(), bs, Hq, Hk,
+            D, B, block_tables.size(1), NB, float(scale), out.data_ptr(), out.stride(0),
+            workspace.data_ptr(), workspace.numel(), _lib.stream_of(q))
     _lib.check(rc, "paged_decode")
     return out
 
@@ -178,6 +186,7 @@ def varlen_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     they are [sum Lk, Hk, D] rows, each with its own row stride (k roped and
     contiguous, v a view of the qkv projection). Same math as
     flash_attn_varlen_func(..., causal=True, block_table) at attention.py:96-102.
+    q, k, v and the output are bf16 or fp16 (one dtype); an fp8 pool takes bf16 q.
     """
     N, Hq, D = q.shape
     _lib.require_device(q.device, k=k, v=v, cu_seqlens_q=cu_seqlens_q, cu_seqlens_k=cu_seqlens_k,
@@ -185,18 +194,19 @@ def varlen_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     assert q.stride(-1) == 1 and q.stride(1) == D
     assert cu_seqlens_q.dtype == torch.int32 and cu_seqlens_k.dtype == torch.int32
     n_seqs = cu_seqlens_q.numel() - 1
-    _lib.need(q.dtype == _BF16, "varlen_prefill: q must be bf16")
+    f16 = _lib.is_f16(q, "varlen_prefill: q")
     _lib.need(cu_seqlens_k.numel() == n_seqs + 1 and cu_seqlens_q.is_contiguous()
               and cu_seqlens_k.is_contiguous(),
               "varlen_prefill: cu_seqlens_q/k must be contiguous, one entry per sequence + 1")
     _lib.need(v.dtype == k.dtype, "varlen_prefill: k and v dtypes differ")
     if out is not None:
-        _lib.need(out.shape == q.shape and out.dtype == _BF16 and out.stride(-1) == 1
-                  and out.stride(1) == D, "varlen_prefill: out must be bf16 shaped like q, "
-                  "rows of contiguous heads")
+        _lib.need(out.shape == q.shape and out.dtype == q.dtype and out.stride(-1) == 1
+                  and out.stride(1) == D, "varlen_prefill: out must be shaped like q, in q's "
+                  "dtype, rows of contiguous heads")
     if block_tables is not None and k.dtype == torch.float8_e4m3fn:
         # fp8 pool: the kernel widens the codes as it stages them (no bf16 copy)
         NB, B, Hk, Dk = k.shape
+        _lib.need(not f16, "varlen_prefill: an fp8 pool is read with bf16 q")
         _lib.need(v.shape == k.shape and k.is_contiguous() and v.is_contiguous(),
                   "varlen_prefill: fp8 caches must be contiguous, v shaped like k")
         _lib.need(block_tables.dtype == torch.int32 and block_tables.stride(1) == 1,
@@ -214,7 +224,8 @@ def varlen_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     if block_tables is not None:
         NB, B, Hk, Dk = k.shape
         assert k.is_contiguous() and v.is_contiguous() and v.shape == k.shape
-        _lib.need(k.dtype == _BF16, "varlen_prefill: paged caches must be bf16 or fp8")
+        _lib.need(k.dtype == q.dtype, "varlen_prefill: paged caches must have q's dtype "
+                  "(or be fp8)")
         k_row_stride = v_row_stride = Hk * Dk
         n_rows = NB * B
         bt_ptr, bt_stride = block_tables.data_ptr(), block_tables.stride(0)
@@ -223,7 +234,7 @@ def varlen_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     else:
         _, Hk, Dk = k.shape
         assert v.shape == k.shape
-        _lib.need(k.dtype == _BF16, "varlen_prefill: contiguous k/v must be bf16")
+        _lib.need(k.dtype == q.dtype, "varlen_prefill: contiguous k/v must have q's dtype")
         assert k.stride(1) == Dk and k.stride(2) == 1 and v.stride(1) == Dk and v.stride(2) == 1
         k_row_stride, v_row_stride = k.stride(0), v.stride(0)
         n_rows = k.size(0)
@@ -231,8 +242,9 @@ def varlen_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         bt_ptr, bt_stride, max_blocks = None, 0, 0
     assert Dk == D
     if out is None:
-        out = torch.empty(N, Hq, D, dtype=_BF16, device=q.device)
-    rc = _lib.lib().nkv_prefill_varlen(
+        out = torch.empty(N, Hq, D, dtype=q.dtype, device=q.device)
+    fn = _lib.lib().nkv_prefill_varlen_f16 if f16 else _lib.lib().nkv_prefill_varlen
+    rc = fn(
         q.data_ptr(), q.stride(0), k.data_ptr(), v.data_ptr(), k_row_stride, v_row_stride,
         cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), bt_ptr, bt_stride, max_blocks, n_seqs,
         int(max_seqlen_q), Hq, Hk, D, B, n_rows, float(scale), out.data_ptr(), out.stride(0),

@@ -82,8 +82,12 @@ def _check_window_args(what, q, k_cache, v_cache, block_tables, base_context_len
               f"{what}: caches must be contiguous")
     if q is not None:
         D = k_cache.size(-1)
-        _lib.need(q.dtype == torch.bfloat16 and q.stride(-1) == 1 and q.stride(1) == D,
-                  f"{what}: q must be bf16 rows of contiguous heads")
+        _lib.is_f16(q, f"{what}: q")
+        _lib.need(q.stride(-1) == 1 and q.stride(1) == D,
+                  f"{what}: q must be rows of contiguous heads")
+        _lib.need(k_cache.dtype == q.dtype or (k_cache.dtype == torch.float8_e4m3fn
+                                               and q.dtype == torch.bfloat16),
+                  f"{what}: the caches must have q's dtype (or be fp8 with bf16 q)")
     m = seq_idx.numel()
     if importance is not None:
         _lib.need(importance.dtype == torch.float32 and importance.is_contiguous()
@@ -126,7 +130,8 @@ def compress_select(q, k_cache, block_tables, base_context_lens, seq_idx, window
     ws_bytes = select_workspace_bytes(m, Hq, Hk, window_blocks, B)
     if workspace is None:
         workspace = torch.empty(max(ws_bytes, 4), dtype=torch.uint8, device=q.device)
-    rc = L.nkv_compress_select(
+    fn = L.nkv_compress_select_f16 if q.dtype == torch.float16 else L.nkv_compress_select
+    rc = fn(
         q.data_ptr(), q.stride(0), k_cache.data_ptr(), block_tables.data_ptr(),
         block_tables.stride(0), block_tables.size(1), base_context_lens.data_ptr(),
         seq_idx.data_ptr(), m, Hq, Hk, D, B, window_blocks, NB, float(scale), AGG_MODES[agg],
@@ -186,7 +191,9 @@ def compress_step(q, k_cache, v_cache, block_tables, base_context_lens, context_
             _lib.stream_of(q))
         _lib.check(rc, "compress_step_fp8")
         return keep_idx, importance
-    rc = _lib.lib().nkv_compress_step(
+    fn = _lib.lib().nkv_compress_step_f16 if q.dtype == torch.float16 else \
+        _lib.lib().nkv_compress_step
+    rc = fn(
         q.data_ptr(), q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(), block_tables.data_ptr(),
         block_tables.stride(0), block_tables.size(1), base_context_lens.data_ptr(),
         context_lens.data_ptr(), seq_idx.data_ptr(), m, Hq, Hk, D, B, window_blocks, NB,

@@ -52,14 +52,15 @@ def fp8_dequantize(codes: torch.Tensor, scale: float = 1.0, out: torch.Tensor | 
 
 
 class KVCachePool:
-    """One K/V tensor for every layer (model_runner.py:133-152), bf16 or fp8."""
+    """One K/V tensor for every layer (model_runner.py:133-152): bf16 or fp16 (the model's
+    dtype, as the reference allocates it) or fp8."""
 
     def __init__(self, num_layers: int, num_kv_heads: int, head_dim: int, block_size: int = 256,
                  dtype: torch.dtype = torch.bfloat16, gpu_memory_utilization: float = 0.8,
                  num_blocks: int | None = None, device="cuda", k_scale: float = 1.0,
                  v_scale: float = 1.0):
-        if dtype not in (torch.bfloat16, FP8):
-            raise ValueError("the pool holds bf16 or float8_e4m3fn")
+        if dtype not in (torch.bfloat16, torch.float16, FP8):
+            raise ValueError("the pool holds bf16, fp16 or float8_e4m3fn")
         self.block_size, self.dtype = block_size, dtype
         itemsize = torch.tensor([], dtype=dtype).element_size()
         self.block_bytes = 2 * num_layers * block_size * num_kv_heads * head_dim * itemsize

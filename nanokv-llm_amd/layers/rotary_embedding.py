@@ -21,8 +21,8 @@ from .. import _lib
 _BF16 = torch.bfloat16
 
 
-def _rows(x: torch.Tensor, heads: int, head_dim: int):
-    assert x.dtype == _BF16 and x.dim() == 3 and x.size(1) == heads and x.size(2) == head_dim
+def _rows(x: torch.Tensor, heads: int, head_dim: int, dtype=_BF16):
+    assert x.dtype == dtype and x.dim() == 3 and x.size(1) == heads and x.size(2) == head_dim
     assert x.stride(2) == 1 and x.stride(1) == head_dim, "heads must be contiguous in a row"
     return x.data_ptr(), x.stride(0)
 
@@ -42,15 +42,19 @@ def qk_norm_rope_store(positions: torch.Tensor, q: torch.Tensor, k: torch.Tensor
     weights are None (the qkv_bias=True branch of qwen3.py:109). With caches,
     k' and v are written to row slot_mapping[i] (slot -1 skipped) as
     store_kvcache does. ``need_k=False`` skips the contiguous k' output (when
-    attention reads K back from the cache). v is returned unchanged.
+    attention reads K back from the cache). v is returned unchanged. q, k, v, the
+    norm weights, the outputs and the caches share one dtype, bf16 or fp16 (the
+    roundings are then to fp16).
     """
     N, Hq, D = q.shape
     Hk = k.size(1)
     _lib.require_device(q.device, k=k, v=v, positions=positions, cos_sin_cache=cos_sin_cache,
                         q_norm_weight=q_norm_weight, k_norm_weight=k_norm_weight,
                         k_cache=k_cache, v_cache=v_cache, slot_mapping=slot_mapping, q_out=q_out)
-    q_ptr, q_rs = _rows(q, Hq, D)
-    k_ptr, k_rs = _rows(k, Hk, D)
+    dt = q.dtype
+    f16 = _lib.is_f16(q, "qk_norm_rope_store: q")
+    q_ptr, q_rs = _rows(q, Hq, D, dt)
+    k_ptr, k_rs = _rows(k, Hk, D, dt)
     assert k.size(0) == N and positions.dtype == torch.int64 and positions.is_contiguous()
     assert positions.numel() == N
     cs = cos_sin_cache.reshape(cos_sin_cache.size(0), -1)
@@ -58,28 +62,29 @@ def qk_norm_rope_store(positions: torch.Tensor, q: torch.Tensor, k: torch.Tensor
     if (q_norm_weight is None) != (k_norm_weight is None):
         raise ValueError("give both q/k norm weights or neither")
     if q_norm_weight is not None:
-        assert q_norm_weight.dtype == _BF16 and k_norm_weight.dtype == _BF16
+        assert q_norm_weight.dtype == dt and k_norm_weight.dtype == dt
         assert q_norm_weight.is_contiguous() and k_norm_weight.is_contiguous()
         assert q_norm_weight.numel() == D and k_norm_weight.numel() == D
     if q_out is None:
-        q_out = torch.empty(N, Hq, D, dtype=_BF16, device=q.device)
-    _rows(q_out, Hq, D)
+        q_out = torch.empty(N, Hq, D, dtype=dt, device=q.device)
+    _rows(q_out, Hq, D, dt)
     _lib.need(q_out.size(0) == N, "qk_norm_rope_store: q_out needs one row per token")
     store = k_cache is not None and k_cache.numel() > 0
-    k_out = torch.empty(N, Hk, D, dtype=_BF16, device=q.device) if (need_k or not store) else None
+    k_out = torch.empty(N, Hk, D, dtype=dt, device=q.device) if (need_k or not store) else None
     v_ptr, v_rs = (0, 0)
     n_slots = 0
     if store:
         assert v is not None and slot_mapping is not None
-        v_ptr, v_rs = _rows(v, Hk, D)
+        v_ptr, v_rs = _rows(v, Hk, D, dt)
         _lib.need(v.size(0) == N, "qk_norm_rope_store: v needs one row per token")
-        assert k_cache.dtype == _BF16 and v_cache.dtype == _BF16
+        assert k_cache.dtype == dt and v_cache.dtype == dt
         assert k_cache.is_contiguous() and v_cache.is_contiguous()
         assert k_cache.size(-1) == D and k_cache.size(-2) == Hk and v_cache.shape == k_cache.shape
         assert slot_mapping.dtype == torch.int32 and slot_mapping.is_contiguous()
         assert slot_mapping.numel() == N
         n_slots = k_cache.numel() // (Hk * D)
-    rc = _lib.lib().nkv_qk_norm_rope_store(
+    fn = _lib.lib().nkv_qk_norm_rope_store_f16 if f16 else _lib.lib().nkv_qk_norm_rope_store
+    rc = fn(
         q_ptr, q_rs, k_ptr, k_rs, v_ptr or None, v_rs, positions.data_ptr(),
         q_norm_weight.data_ptr() if q_norm_weight is not None else None,
         k_norm_weight.data_ptr() if k_norm_weight is not None else None, float(eps),

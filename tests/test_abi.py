@@ -82,31 +82,32 @@ P = 0x10000  # a 16-byte aligned stand-in for a device pointer: never dereferenc
 EINVAL, EWORKSPACE, EUNSUPPORTED = -1, -3, -4
 
 
-def _prefill(**kw):
+def _prefill(f16=False, **kw):
     a = dict(q=P, qrs=4096, k=P, v=P, krs=1024, vrs=1024, cq=P, ck=P, bt=None, btrs=0, mb=0,
              n=1, mq=16, hq=32, hk=8, d=128, bs=256, rows=1000, scale=1.0, out=P, ors=4096)
     a.update(kw)
-    return ("nkv_prefill_varlen", [a[x] for x in ("q", "qrs", "k", "v", "krs", "vrs", "cq", "ck",
+    return ("nkv_prefill_varlen_f16" if f16 else "nkv_prefill_varlen", [a[x] for x in ("q", "qrs", "k", "v", "krs", "vrs", "cq", "ck",
                                                    "bt", "btrs", "mb", "n", "mq", "hq", "hk",
                                                    "d", "bs", "rows", "scale", "out", "ors")]
             + [None])
 
 
-def _decode(fp8=False, **kw):
+def _decode(fp8=False, f16=False, **kw):
     a = dict(q=P, qrs=4096, k=P, v=P, bt=P, btrs=32, ctx=P, b=4, hq=32, hk=8, d=128, bs=256,
              mb=32, nb=100, scale=1.0, ks=1.0, vs=1.0, out=P, ors=4096, ws=P, wsb=1 << 30)
     a.update(kw)
     names = ["q", "qrs", "k", "v", "bt", "btrs", "ctx", "b", "hq", "hk", "d", "bs", "mb", "nb",
              "scale"] + (["ks", "vs"] if fp8 else []) + ["out", "ors", "ws", "wsb"]
-    return ("nkv_paged_decode_fp8" if fp8 else "nkv_paged_decode", [a[x] for x in names] + [None])
+    name = "nkv_paged_decode_fp8" if fp8 else "nkv_paged_decode_f16" if f16 else "nkv_paged_decode"
+    return (name, [a[x] for x in names] + [None])
 
 
-def _cstep(**kw):
+def _cstep(f16=False, **kw):
     a = dict(q=P, qrs=4096, k=P, v=P, bt=P, btrs=32, mb=32, base=P, ctx=P, sel=P, m=2, hq=32,
              hk=8, d=128, bs=256, w=4, nb=100, scale=1.0, agg=1, keep=513, imp=P, keep_idx=P,
              ws=P, wsb=1 << 30)
     a.update(kw)
-    return ("nkv_compress_step", [a[x] for x in ("q", "qrs", "k", "v", "bt", "btrs", "mb", "base",
+    return ("nkv_compress_step_f16" if f16 else "nkv_compress_step", [a[x] for x in ("q", "qrs", "k", "v", "bt", "btrs", "mb", "base",
                                                   "ctx", "sel", "m", "hq", "hk", "d", "bs", "w",
                                                   "nb", "scale", "agg", "keep", "imp",
                                                   "keep_idx", "ws", "wsb")] + [None])
@@ -114,12 +115,16 @@ def _cstep(**kw):
 
 CASES = [
     (_prefill(d=96), EUNSUPPORTED, b"head_dim"),
-    (_prefill(hq=17, hk=1), EUNSUPPORTED, b"GQA group"),
+    (_prefill(hq=129, hk=1), EUNSUPPORTED, b"GQA group"),  # a 128-row tile holds one query
+    (_prefill(hq=65, hk=1, d=256, qrs=65 * 256, ors=65 * 256), EUNSUPPORTED, b"GQA group"),
+    (_prefill(f16=True, d=96), EUNSUPPORTED, b"head_dim"),
     (_prefill(q=P + 2), EINVAL, b"aligned"),
     (_prefill(qrs=1000), EINVAL, b"row strides"),
     (_prefill(bt=P, btrs=4, mb=4, bs=8), EUNSUPPORTED, b"multiple of 16"),
     (_prefill(bt=P, btrs=4, mb=4, vrs=2048), EINVAL, b"share one row stride"),
-    (_decode(hq=32, hk=1), EUNSUPPORTED, b"GQA group"),
+    (_decode(hq=257, hk=1, qrs=257 * 128, ors=257 * 128), EUNSUPPORTED, b"GQA group"),
+    (_decode(f16=True, d=96), EUNSUPPORTED, b"head_dim"),
+    (_decode(f16=True, wsb=16), EWORKSPACE, b"workspace"),
     (_decode(hq=24, hk=8, wsb=16), EWORKSPACE, b"workspace"),
     (_decode(bs=8), EUNSUPPORTED, b"multiple of 16"),
     (_decode(btrs=16), EINVAL, b"block table"),
@@ -128,6 +133,7 @@ CASES = [
     (_cstep(keep=2), EINVAL, b"keep_tokens"),
     (_cstep(agg=7), EINVAL, b"agg_mode"),
     (_cstep(hq=30), EINVAL, b"Hq % Hk"),
+    (_cstep(f16=True, agg=7), EINVAL, b"agg_mode"),
     (("nkv_compress_schedule", [P, P, 20000, 256, 4, 20, 1, 0, P, P, P, P, None]),
      EUNSUPPORTED, b"batch above"),
     (("nkv_compress_schedule", [P, P, 64, 256, 4, 20, 1, 3, P, P, P, P, None]),

@@ -184,10 +184,11 @@ def test_my_compress_compact_drop_in(nkv, dev):
 
 @pytest.mark.parametrize("window", [1, 2, 5, 8])
 @pytest.mark.parametrize("agg", ["all", "group"])
-@pytest.mark.parametrize("L", [1024, 2048])
+@pytest.mark.parametrize("L", [1024, 2048, 1000, 333])
 def test_snapkv_plugin_api(nkv, dev, window, agg, L):
     """SnapKV(Q, K, V, num_keep, window) (CompressMethod.py:4-57) with the reference's
-    query windows: importance within rtol 1e-4 of the oracle's fp32 SnapKV importance,
+    query windows and lengths that are not multiples of the 256-key score chunks (the last
+    chunk masked): importance within rtol 1e-4 of the oracle's fp32 SnapKV importance,
     the kept set exactly the oracle's selection on that importance, the window kept."""
     g = torch.Generator().manual_seed(9 + window + L)
     Q = torch.randn(3, 32, window, 128, generator=g).to(torch.bfloat16)

@@ -1,6 +1,8 @@
-"""GQA groups outside the powers of two: decode, prefill and the compression step against
-the oracle for g = 3, 5, 6, 7, 16, and Qwen3-14B geometry (40 query heads over 8 KV heads,
-g = 5) through Attention.forward.
+"""GQA groups outside the powers of two and above 16: decode, prefill and the compression
+step against the oracle for g = 3, 5, 6, 7, 16, 17, 20, 32, 64, 128 (decode splits a group
+above 16 over waves of 16 query heads; prefill tiles hold 128 query x head rows; the
+compression step scores such groups in passes of 16), and Qwen3-14B geometry (40 query
+heads over 8 KV heads, g = 5) through Attention.forward.
 
 The reference hands any Hq % Hk == 0 to flash-attn (nanokvllm/layers/attention.py:96-107)
 with head counts from the model config (nanokvllm/models/qwen3.py:53-60). Bars as in the rest
@@ -41,7 +43,8 @@ def _tables(rng, lens, B, n_blocks, width, pad=-1):
 
 
 @pytest.mark.parametrize("Hq,Hk", [(24, 8), (40, 8), (48, 8), (56, 8), (128, 8), (12, 4),
-                                   (10, 2), (7, 1), (16, 1)])
+                                   (10, 2), (7, 1), (16, 1), (17, 1), (40, 2), (64, 2), (64, 1),
+                                   (128, 1)])
 def test_decode_gqa_groups(nkv, dev, Hq, Hk):
     """Table widths both below and above the two-heads-per-wave threshold."""
     for width_blocks, bs, hi in ((4, 9, 1000), (32, 24, 8000)):
@@ -57,7 +60,8 @@ def test_decode_gqa_groups(nkv, dev, Hq, Hk):
         assert (out.float().cpu() - ref).abs().max().item() <= TOL
 
 
-@pytest.mark.parametrize("Hq,Hk", [(24, 8), (40, 8), (48, 8), (56, 8), (128, 8), (10, 2)])
+@pytest.mark.parametrize("Hq,Hk", [(24, 8), (40, 8), (48, 8), (56, 8), (128, 8), (10, 2),
+                                   (40, 2), (64, 2), (64, 1), (128, 1)])
 @pytest.mark.parametrize("paged", [True, False])
 def test_prefill_gqa_groups(nkv, dev, Hq, Hk, paged):
     rng = random.Random(Hq * 7 + Hk + int(paged))
@@ -85,7 +89,8 @@ def test_prefill_gqa_groups(nkv, dev, Hq, Hk, paged):
     assert (out.float().cpu() - ref).abs().max().item() <= TOL
 
 
-@pytest.mark.parametrize("Hq,Hk", [(24, 8), (40, 8), (48, 8), (56, 8), (64, 8), (128, 8)])
+@pytest.mark.parametrize("Hq,Hk", [(24, 8), (40, 8), (48, 8), (56, 8), (64, 8), (128, 8),
+                                   (64, 2), (40, 2)])
 @pytest.mark.parametrize("agg", ["all", "group"])
 def test_compress_step_gqa_groups(nkv, dev, Hq, Hk, agg):
     wl = wl_mod.compress_workload(40, Hq, Hk, 1500, 4096, 6, seed=Hq + Hk, selected_only=True)
