@@ -103,27 +103,44 @@ def paged_decode_workspace(q: torch.Tensor, k_cache: torch.Tensor,
 # One decode workspace per device, shared by every Attention layer: the layers of a step
 # run one after another on one stream, so no two decode calls use it at once (callers
 # that run layers concurrently on several streams pass their own workspaces to
-# paged_decode). It only grows; a replaced buffer is kept alive, because a HIP graph
-# captured earlier may still hold its address.
+# paged_decode). It only grows. A replaced buffer that a HIP graph captured (a decode call
+# ran during capture while it was current) is kept alive, because that graph still holds
+# its address; one that no capture saw is freed. release_retired_decode_workspaces() drops
+# the kept ones once the caller has dropped its graphs.
 _SHARED_WS: dict = {}
+_CAPTURED_WS: set = set()  # (device, data_ptr) of shared workspaces seen during a capture
 _RETIRED_WS: list = []
 
 
 def shared_decode_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     """The device's shared decode workspace, grown to at least ``nbytes``."""
     ws = _SHARED_WS.get(device)
+    capturing = torch.cuda.is_current_stream_capturing()
     if ws is None or ws.numel() < nbytes:
-        if torch.cuda.is_current_stream_capturing():
+        if capturing:
             raise _lib.NkvError(
                 "the shared decode workspace must be large enough before graph capture: "
                 "call reserve_decode_workspace (or run the largest batch eagerly) first")
         size = max(int(nbytes), 4)
         if ws is not None:
             size = max(size, 2 * ws.numel())  # few regrowths
-            _RETIRED_WS.append(ws)
+            key = (device, ws.data_ptr())
+            if key in _CAPTURED_WS:  # a captured graph may still read and write it
+                _CAPTURED_WS.discard(key)
+                _RETIRED_WS.append(ws)
         ws = torch.empty(size, dtype=torch.uint8, device=device)
         _SHARED_WS[device] = ws
+    if capturing:
+        _CAPTURED_WS.add((device, ws.data_ptr()))
     return ws
+
+
+def release_retired_decode_workspaces() -> int:
+    """Free the replaced shared workspaces that graphs captured; call after dropping every
+    graph captured before the last regrowth. Returns how many were released."""
+    n = len(_RETIRED_WS)
+    _RETIRED_WS.clear()
+    return n
 
 
 def reserve_decode_workspace(device, max_num_seqs: int, n_q_heads: int,
@@ -261,6 +278,16 @@ class Attention(nn.Module):
 
     def __init__(self, num_heads, head_dim, scale, num_kv_heads, vllm_config, num_layers):
         super().__init__()
+        # the kernels' limits, checked here rather than at the first forward or the first
+        # compression step mid-serving (include/nkv.h states each of them)
+        _lib.need(head_dim in (64, 128, 256), f"Attention: head_dim {head_dim} is not 64, "
+                  "128 or 256")
+        _lib.need(num_kv_heads > 0 and num_heads % num_kv_heads == 0,
+                  f"Attention: num_heads {num_heads} is not a multiple of num_kv_heads "
+                  f"{num_kv_heads}")
+        max_group = 64 if head_dim == 256 else 128  # a prefill tile's query x head rows
+        _lib.need(num_heads // num_kv_heads <= max_group,
+                  f"Attention: GQA group {num_heads // num_kv_heads} above {max_group}")
         self.num_heads = num_heads
         self.head_dim = head_dim
         self.scale = scale
@@ -275,6 +302,43 @@ class Attention(nn.Module):
             self.kv_compress_keep_blocks = vllm_config.kv_compress_keep_blocks
             self.kv_compress_keep_extra_tokens = vllm_config.kv_compress_keep_extra_tokens
             self.kv_compress_agg = getattr(vllm_config, "kv_compress_agg", "all")
+            W = self.kv_compress_window_blocks
+            _lib.need(0 < W <= 64, f"Attention: kv_compress_window_blocks {W} not in 1..64")
+            _lib.need(self.kv_compress_keep_blocks >= 0 and
+                      self.kv_compress_keep_extra_tokens >= 0,
+                      "Attention: kv_compress_keep_blocks and kv_compress_keep_extra_tokens "
+                      "must be >= 0")
+            _lib.need(self.kv_compress_agg in ("all", "group"),
+                      f"Attention: kv_compress_agg {self.kv_compress_agg!r} is not 'all' or "
+                      "'group'")
+        self._cache_checked = None  # (k_cache data_ptr, shape) whose geometry was checked
+
+    def _check_cache(self):
+        """The bound cache's geometry against the kernels' limits, once per binding: block
+        size a multiple of 16 (decode, prefill); with compression, a window of at most 4096
+        candidates (W*B - 1) and a block size the compression kernels take (a multiple of 64
+        with W*B <= 1024, or of 256)."""
+        kc = self.k_cache
+        key = (kc.data_ptr(), tuple(kc.shape))
+        if self._cache_checked == key:
+            return
+        _lib.need(kc.dim() == 4 and kc.size(2) == self.num_kv_heads and
+                  kc.size(3) == self.head_dim,
+                  f"Attention: k_cache must be [blocks, block_size, {self.num_kv_heads}, "
+                  f"{self.head_dim}], got {tuple(kc.shape)}")
+        B = kc.size(1)
+        _lib.need(B % 16 == 0, f"Attention: block_size {B} is not a multiple of 16")
+        if self.kv_compress_enabled:
+            Lw = self.kv_compress_window_blocks * B
+            keep = self.kv_compress_keep_blocks * B + self.kv_compress_keep_extra_tokens
+            _lib.need(Lw - 1 <= 4096, f"Attention: compression window of {Lw} tokens above "
+                      "4097")
+            _lib.need((B % 64 == 0 and Lw <= 1024) or B % 256 == 0,
+                      f"Attention: compression needs block_size a multiple of 64 (window <= "
+                      f"1024 tokens) or of 256, got {B}")
+            # keep >= Lw is the reference's no-op (SnapKV returns False, CompressMethod.py:17-18)
+            _lib.need(keep > 2, f"Attention: {keep} kept tokens (bos, selected, latest: > 2)")
+        self._cache_checked = key
 
     def _workspace(self, q, block_tables):
         """The device's decode workspace, shared with every other layer."""
@@ -288,6 +352,8 @@ class Attention(nn.Module):
         contiguously (no block table)."""
         context = get_context()
         k_cache, v_cache = self.k_cache, self.v_cache
+        if k_cache.numel():
+            self._check_cache()
         if k_cache.numel() and v_cache.numel() and not kv_stored:
             store_kvcache(k, v, k_cache, v_cache, context.slot_mapping, self.k_scale,
                           self.v_scale)
