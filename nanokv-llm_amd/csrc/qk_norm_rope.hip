@@ -78,7 +78,8 @@ struct RopeArgs {
 // [D/2+8i, D/2+8i+8) of the head (16-byte accesses). The head row, the position
 // and the slot are loaded together; the cos|sin row (which needs the position)
 // is the only dependent load. One unit per group measured fastest at every size
-// (more units per group serialise their dependent loads).
+// (more units per group serialise their dependent loads). Loads and stores are
+// non-temporal: every byte is touched once (4-5% faster than cached stores).
 template <int D, bool H16 = false>
 __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_store_kernel(const RopeArgs a) {
   // Every product is rounded on its own, as the reference's separate torch ops are:
@@ -153,20 +154,20 @@ __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_store_kernel(const 
   }
   if (is_q) {
     bf16_t* dst = a.q_out + (int64_t)t * a.q_out_row_stride + (int64_t)h * D;
-    *reinterpret_cast<u32x4_t*>(dst + 8 * l8) = vlo;
-    *reinterpret_cast<u32x4_t*>(dst + kH + 8 * l8) = vhi;
+    __builtin_nontemporal_store(vlo, reinterpret_cast<u32x4_t*>(dst + 8 * l8));
+    __builtin_nontemporal_store(vhi, reinterpret_cast<u32x4_t*>(dst + kH + 8 * l8));
     return;
   }
   NKV_DBG(sl < -1 || sl >= a.n_slots, NKV_DEBUG_SLOT);
   if (sl >= 0 && sl < a.n_slots) {  // -1 (padding) or out of range: skipped
     bf16_t* dst = (is_k ? a.k_cache : a.v_cache) + (sl * a.Hk + kvh) * (int64_t)D;
-    *reinterpret_cast<u32x4_t*>(dst + 8 * l8) = vlo;
-    *reinterpret_cast<u32x4_t*>(dst + kH + 8 * l8) = vhi;
+    __builtin_nontemporal_store(vlo, reinterpret_cast<u32x4_t*>(dst + 8 * l8));
+    __builtin_nontemporal_store(vhi, reinterpret_cast<u32x4_t*>(dst + kH + 8 * l8));
   }
   if (is_k && a.k_out) {
     bf16_t* dst = a.k_out + ((int64_t)t * a.Hk + kvh) * D;
-    *reinterpret_cast<u32x4_t*>(dst + 8 * l8) = vlo;
-    *reinterpret_cast<u32x4_t*>(dst + kH + 8 * l8) = vhi;
+    __builtin_nontemporal_store(vlo, reinterpret_cast<u32x4_t*>(dst + 8 * l8));
+    __builtin_nontemporal_store(vhi, reinterpret_cast<u32x4_t*>(dst + kH + 8 * l8));
   }
 }
 
