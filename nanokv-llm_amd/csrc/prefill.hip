@@ -327,10 +327,12 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void prefill_varlen_kernel(
 #pragma unroll
     for (int db = 0; db < kDb; ++db) acc[rr][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   float m_run[kRG], l_run[kRG];
+  float mb_run[kRG];  // m_run, or 0 while the row has no visible key
 #pragma unroll
   for (int rr = 0; rr < kRG; ++rr) {
     m_run[rr] = -INFINITY;
     l_run[rr] = 0.f;
+    mb_run[rr] = 0.f;
   }
 
   // Q is in registers before the loop: the empty asm uses pin the loads'
@@ -399,33 +401,35 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void prefill_varlen_kernel(
             if (s * kStep + 16 * h + 4 * g4 + r > lim) sv[rr][4 * h + r] = -INFINITY;
       }
     }
-    float cm[kRG];
-    bool raise[kRG];
-    bool any_raise = false;
+    // Each lane first tests its own 16 scores of a row group against the headroom; only
+    // when some lane's exceed it does the wave take the row maxima across the 4 lane groups
+    // (two permlane swaps) and rescale. The decisions are those of testing the row maxima
+    // every step, which rarely rise past the headroom after the first steps.
+    float lmax[kRG];
+    bool lraise = false;
 #pragma unroll
     for (int rr = 0; rr < kRG; ++rr) {
       const float* v = sv[rr];
-      const float cmax = fmax3(fmax3(fmax3(v[0], v[1], v[2]), fmax3(v[3], v[4], v[5]),
-                                     fmax3(v[6], v[7], v[8])),
-                               fmax3(v[9], v[10], v[11]),
-                               fmax3(fmax3(v[12], v[13], v[14]), v[15], -INFINITY));
-      cm[rr] = col_max4(cmax) * scale_log2;
-      raise[rr] = cm[rr] > m_run[rr] + kLazy;  // false while the row has no visible key
-      any_raise = any_raise || raise[rr];
+      lmax[rr] = fmax3(fmax3(fmax3(v[0], v[1], v[2]), fmax3(v[3], v[4], v[5]),
+                             fmax3(v[6], v[7], v[8])),
+                       fmax3(v[9], v[10], v[11]),
+                       fmax3(fmax3(v[12], v[13], v[14]), v[15], -INFINITY));
+      lraise = lraise || (lmax[rr] * scale_log2 > m_run[rr] + kLazy);
     }
-    if (__builtin_amdgcn_ballot_w64(any_raise) != 0) {
+    if (__builtin_amdgcn_ballot_w64(lraise) != 0) {
 #pragma unroll
       for (int rr = 0; rr < kRG; ++rr) {
-        const float alpha = raise[rr] ? fast_exp2(m_run[rr] - cm[rr]) : 1.f;  // exp2(-inf) = 0
-        m_run[rr] = raise[rr] ? cm[rr] : m_run[rr];
+        const float cm = col_max4(lmax[rr]) * scale_log2;
+        const bool raise = cm > m_run[rr] + kLazy;  // false while the row has no visible key
+        const float alpha = raise ? fast_exp2(m_run[rr] - cm) : 1.f;  // exp2(-inf) = 0
+        m_run[rr] = raise ? cm : m_run[rr];
+        mb_run[rr] = m_run[rr] == -INFINITY ? 0.f : m_run[rr];
         l_run[rr] *= alpha;
 #pragma unroll
         for (int db = 0; db < kDb; ++db) acc[rr][db] *= alpha;
       }
     }
-    float mb[kRG];
-#pragma unroll
-    for (int rr = 0; rr < kRG; ++rr) mb[rr] = m_run[rr] == -INFINITY ? 0.f : m_run[rr];
+    const float* mb = mb_run;
     // O^T[dims][rows] += V^T[dims][keys] P^T[keys][rows] per 32-key chunk c:
     // k-slot j of lane group g is key 32c+4g+j (j<4), or 32c+16+4g+(j-4)
 #pragma unroll
