@@ -1029,11 +1029,139 @@ __global__ __launch_bounds__(64) void compress_finalize_kernel(
 // counter advances; on every period-th step sequence i is eligible iff
 // len % B != B - 1, tail_uncompressed >= W*B and len / B >= W; the first topk
 // eligible in batch order (policy 0, the reference) or the topk longest
-// (policy 1, ties to the lower index) go to seq_idx, the rest is -1. One
-// workgroup; each sequence's eligibility key (its length, or -1) is staged in
-// LDS once; base_context_lens receives a copy of context_lens.
-constexpr int kSchedThreads = 1024;
+// (policy 1, ties to the lower index) go to seq_idx, the rest is -1; each
+// sequence's eligibility key is its length, or -1; base_context_lens receives a
+// copy of context_lens.
 constexpr int kSchedMaxBatch = 16384;  // eligibility keys staged in LDS (64 KiB)
+constexpr int kSchedSlots = 16;                      // sequences per lane, one-wave kernel
+constexpr int kSchedRegBatch = 64 * kSchedSlots;     // batches up to this: one wave
+
+__device__ __forceinline__ int sched_count(uint64_t m) { return __builtin_popcountll(m); }
+// Lanes below this one with their bit set in m.
+__device__ __forceinline__ int sched_below(uint64_t m) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                   __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// Batches up to kSchedRegBatch: one wave, no workgroup barriers. Lane l holds sequences
+// l + 64 s (s < kSchedSlots) in registers, all their loads issued together; every count is
+// a ballot over the wave. Policy 1 finds the take-th largest eligible length T bit by bit
+// (the largest T with at least `take` keys >= T), takes the keys above T and the
+// lowest-indexed ones equal to it, and ranks them (longest first, ties to the lower index)
+// with lane reads of the candidates when there are at most 64, through LDS otherwise.
+__global__ __launch_bounds__(64) void compress_schedule_wave_kernel(
+    const int32_t* __restrict__ context_lens, const int32_t* __restrict__ tail_uncompressed,
+    int32_t batch, int32_t block_size, int32_t window_blocks, int32_t topk, int32_t period,
+    int32_t policy, int32_t* __restrict__ step_counter, int32_t* __restrict__ seq_idx,
+    int32_t* __restrict__ n_selected, int32_t* __restrict__ base_context_lens) {
+  __shared__ int32_t cand[kSchedRegBatch];   // policy 1: the selected sequences, index order
+  __shared__ int32_t candk[kSchedRegBatch];  // and their lengths
+  const int lane = threadIdx.x;
+  int c = 0;
+  if (lane == 0) c = step_counter[0];
+  int len[kSchedSlots], tail[kSchedSlots];
+#pragma unroll
+  for (int s = 0; s < kSchedSlots; ++s) {
+    const int i = s * 64 + lane;
+    len[s] = i < batch ? context_lens[i] : 0;
+    tail[s] = i < batch ? tail_uncompressed[i] : 0;
+  }
+  c = __builtin_amdgcn_readfirstlane(c) + 1;
+  if (lane == 0) step_counter[0] = c;
+  const bool fire = c % period == 0;  // period > 0 (checked by the caller)
+  const int B = block_size;
+  const int min_tail = window_blocks * B;
+  int key[kSchedSlots];
+  int n_elig = 0, mx = 0;
+  const bool pow2 = (B & (B - 1)) == 0;  // uniform: shifts instead of divisions
+  const int b_log2 = __builtin_ctz((unsigned)B);
+#pragma unroll
+  for (int s = 0; s < kSchedSlots; ++s) {
+    const int i = s * 64 + lane;
+    if (base_context_lens && i < batch) base_context_lens[i] = len[s];
+    const int nb = pow2 ? len[s] >> b_log2 : len[s] / B;  // negative: never eligible
+    const int rem = len[s] - nb * B;
+    const bool ok = i < batch && fire && rem != B - 1 && tail[s] >= min_tail &&
+                    nb >= window_blocks;
+    key[s] = ok ? len[s] : -1;
+    n_elig += sched_count(__builtin_amdgcn_ballot_w64(ok));
+    mx = max(mx, key[s]);
+  }
+  const int take = min(n_elig, topk);
+  if (lane == 0) n_selected[0] = take;
+  for (int r = take + lane; r < topk; r += 64) seq_idx[r] = -1;  // unused slots
+  if (take == 0) return;  // uniform
+  if (policy == 0) {  // first `take` eligible in batch order
+    int rank = 0;
+#pragma unroll
+    for (int s = 0; s < kSchedSlots; ++s) {
+      const uint64_t m = __builtin_amdgcn_ballot_w64(key[s] >= 0);
+      const int pos = rank + sched_below(m);
+      if (key[s] >= 0 && pos < take) seq_idx[pos] = s * 64 + lane;
+      rank += sched_count(m);
+    }
+    return;
+  }
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) mx = max(mx, __shfl_xor(mx, o, 64));
+  mx = __builtin_amdgcn_readfirstlane(mx);
+  // T: the largest value with at least `take` eligible keys >= T
+  int T = 0;
+  for (int bit = 31 - __builtin_clz((uint32_t)mx | 1u); bit >= 0; --bit) {  // uniform
+    const int t = T | (1 << bit);
+    int cnt = 0;  // uniform: ballots and scalar bit counts, no cross-lane data movement
+#pragma unroll
+    for (int s = 0; s < kSchedSlots; ++s) cnt += sched_count(__builtin_amdgcn_ballot_w64(key[s] >= t));
+    if (cnt >= take) T = t;
+  }
+  // the keys above T, then the lowest-indexed ones equal to T, in index order
+  int n_gt = 0;
+#pragma unroll
+  for (int s = 0; s < kSchedSlots; ++s) n_gt += sched_count(__builtin_amdgcn_ballot_w64(key[s] > T));
+  int ties = take - n_gt;  // > 0
+  int pos = 0;
+#pragma unroll
+  for (int s = 0; s < kSchedSlots; ++s) {
+    const int k = key[s];
+    const uint64_t meq = __builtin_amdgcn_ballot_w64(k == T);
+    const bool sel = k > T || (k == T && sched_below(meq) < ties);
+    const uint64_t msel = __builtin_amdgcn_ballot_w64(sel);
+    const int p = pos + sched_below(msel);
+    if (sel) {
+      cand[p] = s * 64 + lane;
+      candk[p] = k;
+    }
+    pos += sched_count(msel);
+    ties -= min(sched_count(meq), ties);
+  }
+  __syncthreads();
+  if (take <= 64) {
+    const int my_cand = lane < take ? cand[lane] : -1;  // candidate `lane`
+    const int my_key = lane < take ? candk[lane] : -1;
+    int rank = 0;
+    for (int t = 0; t < take; ++t) {  // uniform
+      const int j = __builtin_amdgcn_readlane(my_cand, t);
+      const int lj = __builtin_amdgcn_readlane(my_key, t);
+      rank += lj > my_key || (lj == my_key && j < my_cand);
+    }
+    if (lane < take) seq_idx[rank] = my_cand;
+    return;
+  }
+  // longest first, ties to the lower index
+  for (int r = lane; r < take; r += 64) {
+    const int i = cand[r];
+    const int li = candk[r];
+    int rank = 0;
+    for (int t = 0; t < take; ++t) {
+      const int j = cand[t];
+      const int lj = candk[t];
+      rank += lj > li || (lj == li && j < i);
+    }
+    seq_idx[rank] = i;
+  }
+}
+
+constexpr int kSchedThreads = 1024;
 
 // Exclusive prefix sum of v over the workgroup in thread order; *total gets the sum.
 // Wave scans with shuffles, then the 16 wave totals through LDS (two barriers).
@@ -1060,9 +1188,10 @@ __device__ __forceinline__ int sched_scan(int v, int* wsum, int* total) {
   return off + incl - v;
 }
 
-// Each thread owns a contiguous range of sequences. Policy 1 finds the topk-th largest
-// length with a 4-bit radix select, takes the sequences above it and the lowest-indexed
-// ones equal to it, and ranks only those (written longest first).
+// Batches above kSchedRegBatch: one 1024-thread workgroup, each thread owning a contiguous
+// range of sequences. Policy 1 finds the topk-th largest length with a 4-bit radix select,
+// takes the sequences above it and the lowest-indexed ones equal to it, and ranks only those
+// (written longest first).
 __global__ __launch_bounds__(kSchedThreads) void compress_schedule_kernel(
     const int32_t* __restrict__ context_lens, const int32_t* __restrict__ tail_uncompressed,
     int32_t batch, int32_t block_size, int32_t window_blocks, int32_t topk, int32_t period,
@@ -1624,9 +1753,15 @@ extern "C" int nkv_compress_schedule(const int32_t* context_lens,
               kSchedMaxBatch);
   NKV_REQUIRE(context_lens && tail_uncompressed && step_counter && seq_idx && n_selected,
               NKV_EINVAL, "compress_schedule: null pointer");
-  hipLaunchKernelGGL(compress_schedule_kernel, dim3(1), dim3(kSchedThreads), 0, as_stream(stream),
-                     context_lens, tail_uncompressed, batch, block_size, window_blocks, topk,
-                     period, policy, step_counter, seq_idx, n_selected, base_context_lens);
+  if (batch <= kSchedRegBatch)
+    hipLaunchKernelGGL(compress_schedule_wave_kernel, dim3(1), dim3(64), 0, as_stream(stream),
+                       context_lens, tail_uncompressed, batch, block_size, window_blocks, topk,
+                       period, policy, step_counter, seq_idx, n_selected, base_context_lens);
+  else
+    hipLaunchKernelGGL(compress_schedule_kernel, dim3(1), dim3(kSchedThreads), 0,
+                       as_stream(stream), context_lens, tail_uncompressed, batch, block_size,
+                       window_blocks, topk, period, policy, step_counter, seq_idx, n_selected,
+                       base_context_lens);
   return check_launch("nkv_compress_schedule");
 }
 
