@@ -212,18 +212,18 @@ def test_pool_sizing_follows_the_reference_formula(nkv, dev, dtype):
     torch.cuda.empty_cache()
 
 
-@pytest.mark.parametrize("W,Hk", [(4, 8), (4, 4), (6, 8)])
+@pytest.mark.parametrize("W,Hq,Hk", [(4, 32, 8), (4, 32, 4), (6, 32, 8), (4, 64, 2)])
 @pytest.mark.parametrize("agg", ["all", "group"])
-def test_compress_step_over_fp8_pool(nkv, dev, agg, W, Hk):
+def test_compress_step_over_fp8_pool(nkv, dev, agg, W, Hq, Hk):
     """Compression on an fp8 pool: importance within rtol 1e-4 of the oracle's fp32 SnapKV on
     the fp32-dequantized window, kept sets bit-exact given those scores, and the 1-byte rows
     compacted bit-exactly; -1 padding in seq_idx skipped. Windows of 4 blocks take the fused
-    kernels, 6 blocks (1536 tokens) the general path."""
+    kernels, 6 blocks (1536 tokens) and GQA groups above 16 (64 over 2) the general path."""
     from oracle.compress_ref import (compress_compact_ref, gather_kv_by_slots_ref,
                                      get_tail_window_and_tail_slots_ref, select_topk_ref,
                                      snapkv_importance_ref)
     KEEP, ks = 2 * 256 + 1, 0.5
-    wl = wl_mod.compress_workload(32, 32, Hk, 1500, 4096, 6, 4, selected_only=True)
+    wl = wl_mod.compress_workload(32, Hq, Hk, 1500, 4096, 6, 4, selected_only=True)
     kq = fp8_ref.fp8_quantize_ref(wl["k_cache"], ks)
     vq = fp8_ref.fp8_quantize_ref(wl["v_cache"], 2.0)
     kg = kq.to(dev).view(torch.float8_e4m3fn)
