@@ -966,7 +966,7 @@ def main():
         "store_us": round(r["store_ms"] * 1e3, 2),
         "parity_max_abs_err": r["parity_max_abs_err"],
         "roofline": {
-            "kernel": "paged_decode_split_kernel<false, 2, 128>",
+            "kernel": "paged_decode_split_kernel<false, 2, 128, false>",
             "bound": "hbm",
             "achieved": round(split_gbs, 1),
             "peak": HBM_PEAK_GBS,
@@ -980,7 +980,7 @@ def main():
         "cpu_baseline": cpu,
         **comp,
         "prefill_roofline": {
-            "kernel": "prefill_varlen_kernel<false, 128>",
+            "kernel": "prefill_varlen_kernel<false, 128, false, true>",
             "bound": "mfma",
             "achieved": pre["prefill_chunked_tflops"],
             "peak": MFMA_BF16_PEAK_TFLOPS,
