@@ -138,7 +138,7 @@ def compress_qwen3_8b(seed=3, device="cpu", selected_only=True):
 
 
 def prefill_workload(n_seqs, Hq, Hk, len_lo, len_hi, seed, device="cpu", prefix_lo=None,
-                     prefix_hi=None, chunk=None, head_dim=HEAD_DIM):
+                     prefix_hi=None, chunk=None, head_dim=HEAD_DIM, block_size=BLOCK):
     """Varlen prefill over the paged cache.
 
     One-shot: Lq = Lk = L ~ U[len_lo, len_hi]. Chunked (chunk given): prefix
@@ -154,18 +154,19 @@ def prefill_workload(n_seqs, Hq, Hk, len_lo, len_hi, seed, device="cpu", prefix_
         P = torch.randint(prefix_lo, prefix_hi + 1, (n_seqs,), generator=gen).tolist()
         Lq = [chunk] * n_seqs
         Lk = [p + chunk for p in P]
-    need = sum(math.ceil(k / BLOCK) for k in Lk)
+    B = block_size
+    need = sum(math.ceil(k / B) for k in Lk)
     n_blocks = need + 8
-    table = assign_blocks(Lk, n_blocks, gen)
+    table = assign_blocks(Lk, n_blocks, gen, block=B)
     cu_q = torch.tensor([0] + list(torch.tensor(Lq).cumsum(0).tolist()), dtype=torch.int32)
     cu_k = torch.tensor([0] + list(torch.tensor(Lk).cumsum(0).tolist()), dtype=torch.int32)
     N = int(cu_q[-1])
     D = head_dim
     positions = torch.cat([torch.arange(k - q, k) for q, k in zip(Lq, Lk)])
     seq_of = torch.cat([torch.full((q,), i, dtype=torch.int64) for i, q in enumerate(Lq)])
-    blk = table.to(torch.int64)[seq_of, positions // BLOCK]
-    slots = (blk * BLOCK + positions % BLOCK).to(torch.int32)
-    k_cache, v_cache = _kv_pool((n_blocks, BLOCK, Hk, D), seed, device)
+    blk = table.to(torch.int64)[seq_of, positions // B]
+    slots = (blk * B + positions % B).to(torch.int32)
+    k_cache, v_cache = _kv_pool((n_blocks, B, Hk, D), seed, device)
     return dict(
         q=_randn((N, Hq, D), seed * 7 + 3, device),
         key=_randn((N, Hk, D), seed * 7 + 4, device),

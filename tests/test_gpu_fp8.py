@@ -127,11 +127,14 @@ def test_attention_with_fp8_pool(nkv, dev):
     assert (o.squeeze(1).float().cpu() - ref).abs().max().item() <= 2e-2
 
 
-def test_prefill_over_fp8_pool(nkv, dev):
+@pytest.mark.parametrize("B", [256, 16, 48])
+def test_prefill_over_fp8_pool(nkv, dev, B):
     """Chunked prefill reading a paged fp8 cache (the kernel widens the codes as it stages
-    them) vs the oracle on the fp32-dequantized cache."""
+    them) vs the oracle on the fp32-dequantized cache; block sizes whose 64-key steps
+    cross up to 4 blocks too."""
     from oracle.attention_ref import varlen_prefill_ref
-    wl = wl_mod.prefill_workload(3, 32, 8, 0, 0, seed=12, prefix_lo=0, prefix_hi=900, chunk=200)
+    wl = wl_mod.prefill_workload(3, 32, 8, 0, 0, seed=12, prefix_lo=0, prefix_hi=900, chunk=200,
+                                 block_size=B)
     kq = fp8_ref.fp8_quantize_ref(wl["k_cache"], 0.5)
     vq = fp8_ref.fp8_quantize_ref(wl["v_cache"], 2.0)
     fp8_ref.store_kvcache_fp8_ref(wl["key"], wl["value"], kq, vq, wl["slot_mapping"], 0.5, 2.0)

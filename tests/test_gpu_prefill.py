@@ -43,6 +43,17 @@ def test_prefill_paged_chunked(nkv, dev):
     assert _err(out, ref) <= TOL
 
 
+@pytest.mark.parametrize("B", [16, 48, 80, 272])
+def test_prefill_paged_block_sizes(nkv, dev, B):
+    """Block sizes other than 256: a 64-key step's rows of one wave stay in one block (B a
+    multiple of 16) while the step crosses up to 4 blocks (B = 16), every crossing counted
+    without branches; chunks after prefixes of up to 900 tokens."""
+    wl = wl_mod.prefill_workload(4, 32, 8, 0, 0, seed=21 + B, prefix_lo=0, prefix_hi=900,
+                                 chunk=200, block_size=B)
+    out, ref = _paged(nkv, dev, wl)
+    assert _err(out, ref) <= TOL
+
+
 def test_prefill_contiguous(nkv, dev):
     """No block table: K/V are the new rows themselves (attention.py:96-102 without cache)."""
     wl = wl_mod.prefill_workload(3, 32, 8, 1, 600, seed=13)
