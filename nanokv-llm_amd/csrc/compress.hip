@@ -1044,24 +1044,26 @@ __device__ __forceinline__ int sched_below(uint64_t m) {
 }
 
 // Batches up to kSchedRegBatch: one wave, no workgroup barriers. Lane l holds sequences
-// l + 64 s (s < kSchedSlots) in registers, all their loads issued together; every count is
+// l + 64 s (s < kSlots: 8 up to batch 512, 16 above) in registers, all their loads issued
+// together; every count is
 // a ballot over the wave. Policy 1 finds the take-th largest eligible length T bit by bit
 // (the largest T with at least `take` keys >= T), takes the keys above T and the
 // lowest-indexed ones equal to it, and ranks them (longest first, ties to the lower index)
 // with lane reads of the candidates when there are at most 64, through LDS otherwise.
+template <int kSlots>  // sequences per lane: batch <= 64 * kSlots
 __global__ __launch_bounds__(64) void compress_schedule_wave_kernel(
     const int32_t* __restrict__ context_lens, const int32_t* __restrict__ tail_uncompressed,
     int32_t batch, int32_t block_size, int32_t window_blocks, int32_t topk, int32_t period,
     int32_t policy, int32_t* __restrict__ step_counter, int32_t* __restrict__ seq_idx,
     int32_t* __restrict__ n_selected, int32_t* __restrict__ base_context_lens) {
-  __shared__ int32_t cand[kSchedRegBatch];   // policy 1: the selected sequences, index order
-  __shared__ int32_t candk[kSchedRegBatch];  // and their lengths
+  __shared__ int32_t cand[64 * kSlots];   // policy 1: the selected sequences, index order
+  __shared__ int32_t candk[64 * kSlots];  // and their lengths
   const int lane = threadIdx.x;
   int c = 0;
   if (lane == 0) c = step_counter[0];
-  int len[kSchedSlots], tail[kSchedSlots];
+  int len[kSlots], tail[kSlots];
 #pragma unroll
-  for (int s = 0; s < kSchedSlots; ++s) {
+  for (int s = 0; s < kSlots; ++s) {
     const int i = s * 64 + lane;
     len[s] = i < batch ? context_lens[i] : 0;
     tail[s] = i < batch ? tail_uncompressed[i] : 0;
@@ -1071,12 +1073,12 @@ __global__ __launch_bounds__(64) void compress_schedule_wave_kernel(
   const bool fire = c % period == 0;  // period > 0 (checked by the caller)
   const int B = block_size;
   const int min_tail = window_blocks * B;
-  int key[kSchedSlots];
+  int key[kSlots];
   int n_elig = 0, mx = 0;
   const bool pow2 = (B & (B - 1)) == 0;  // uniform: shifts instead of divisions
   const int b_log2 = __builtin_ctz((unsigned)B);
 #pragma unroll
-  for (int s = 0; s < kSchedSlots; ++s) {
+  for (int s = 0; s < kSlots; ++s) {
     const int i = s * 64 + lane;
     if (base_context_lens && i < batch) base_context_lens[i] = len[s];
     const int nb = pow2 ? len[s] >> b_log2 : len[s] / B;  // negative: never eligible
@@ -1094,7 +1096,7 @@ __global__ __launch_bounds__(64) void compress_schedule_wave_kernel(
   if (policy == 0) {  // first `take` eligible in batch order
     int rank = 0;
 #pragma unroll
-    for (int s = 0; s < kSchedSlots; ++s) {
+    for (int s = 0; s < kSlots; ++s) {
       const uint64_t m = __builtin_amdgcn_ballot_w64(key[s] >= 0);
       const int pos = rank + sched_below(m);
       if (key[s] >= 0 && pos < take) seq_idx[pos] = s * 64 + lane;
@@ -1111,17 +1113,17 @@ __global__ __launch_bounds__(64) void compress_schedule_wave_kernel(
     const int t = T | (1 << bit);
     int cnt = 0;  // uniform: ballots and scalar bit counts, no cross-lane data movement
 #pragma unroll
-    for (int s = 0; s < kSchedSlots; ++s) cnt += sched_count(__builtin_amdgcn_ballot_w64(key[s] >= t));
+    for (int s = 0; s < kSlots; ++s) cnt += sched_count(__builtin_amdgcn_ballot_w64(key[s] >= t));
     if (cnt >= take) T = t;
   }
   // the keys above T, then the lowest-indexed ones equal to T, in index order
   int n_gt = 0;
 #pragma unroll
-  for (int s = 0; s < kSchedSlots; ++s) n_gt += sched_count(__builtin_amdgcn_ballot_w64(key[s] > T));
+  for (int s = 0; s < kSlots; ++s) n_gt += sched_count(__builtin_amdgcn_ballot_w64(key[s] > T));
   int ties = take - n_gt;  // > 0
   int pos = 0;
 #pragma unroll
-  for (int s = 0; s < kSchedSlots; ++s) {
+  for (int s = 0; s < kSlots; ++s) {
     const int k = key[s];
     const uint64_t meq = __builtin_amdgcn_ballot_w64(k == T);
     const bool sel = k > T || (k == T && sched_below(meq) < ties);
@@ -1753,10 +1755,16 @@ extern "C" int nkv_compress_schedule(const int32_t* context_lens,
               kSchedMaxBatch);
   NKV_REQUIRE(context_lens && tail_uncompressed && step_counter && seq_idx && n_selected,
               NKV_EINVAL, "compress_schedule: null pointer");
-  if (batch <= kSchedRegBatch)
-    hipLaunchKernelGGL(compress_schedule_wave_kernel, dim3(1), dim3(64), 0, as_stream(stream),
-                       context_lens, tail_uncompressed, batch, block_size, window_blocks, topk,
-                       period, policy, step_counter, seq_idx, n_selected, base_context_lens);
+  if (batch <= kSchedRegBatch / 2)  // half the slots: half the compares of every count
+    hipLaunchKernelGGL(compress_schedule_wave_kernel<kSchedSlots / 2>, dim3(1), dim3(64), 0,
+                       as_stream(stream), context_lens, tail_uncompressed, batch, block_size,
+                       window_blocks, topk, period, policy, step_counter, seq_idx, n_selected,
+                       base_context_lens);
+  else if (batch <= kSchedRegBatch)
+    hipLaunchKernelGGL(compress_schedule_wave_kernel<kSchedSlots>, dim3(1), dim3(64), 0,
+                       as_stream(stream), context_lens, tail_uncompressed, batch, block_size,
+                       window_blocks, topk, period, policy, step_counter, seq_idx, n_selected,
+                       base_context_lens);
   else
     hipLaunchKernelGGL(compress_schedule_kernel, dim3(1), dim3(kSchedThreads), 0,
                        as_stream(stream), context_lens, tail_uncompressed, batch, block_size,
