@@ -249,8 +249,8 @@ def cpu_baseline(wl, bt, kc, vc, budget_s=12.0):
 
 
 def compress_parity(q, kg, vg, bt, lens, sel, agg, dev):
-    """The compression step (compress_step + compress_finalize with the table and slot
-    rewrite) once on a device copy of the selected sequences' blocks, against the oracle on a
+    """The last layer's compression step (compress_step with the finalize's table, slot and
+    event update in the same launch) once on a device copy of the selected sequences' blocks, against the oracle on a
     host copy of the same blocks: importance within rtol 1e-4 (max relative error reported),
     kept sets exact given the scores, caches, lengths, events, tables and slots bit-exact. The
     timed state is left untouched, so this works on a pool that fills most of HBM."""
@@ -272,10 +272,9 @@ def compress_parity(q, kg, vg, bt, lens, sel, agg, dev):
     ctx = base.clone()
     seq_idx = torch.tensor(sel, dtype=torch.int32, device=dev)
     slot_map = torch.arange(bs, dtype=torch.int32, device=dev) * 3
-    keep, imp = cu.compress_step(q, kc, vc, btg, base, ctx, seq_idx, 4, 513, D ** -0.5, agg)
     events = torch.empty(len(sel), 4 + bt.size(1), dtype=torch.int32, device=dev)
-    cu.compress_finalize(btg, base, seq_idx, 513, B, 4, events, rewrite_tables=True,
-                         slot_mapping=slot_map)
+    keep, imp = cu.compress_step(q, kc, vc, btg, base, ctx, seq_idx, 4, 513, D ** -0.5, agg,
+                                 events=events, rewrite_tables=True, slot_mapping=slot_map)
     torch.cuda.synchronize()
     st = torch.tensor(sel)
     slots, *_ = get_tail_window_and_tail_slots_ref(bt2, lens, st, B, 4)
@@ -305,10 +304,11 @@ def compress_parity(q, kg, vg, bt, lens, sel, agg, dev):
 
 def run_compress(args, dev):
     """One layer's compression step at batch 500 as the configuration states it: scoring,
-    top-k and compaction of the 20 longest sequences (window 4 blocks, keep 513), then the
-    block-table, slot-mapping and event update (compress_finalize), per KV head (agg "group",
-    the benchmark configuration) and with the reference's all-head importance (agg "all").
-    compress_select_compact_us: the same without the finalize launch."""
+    top-k and compaction of the 20 longest sequences (window 4 blocks, keep 513), and the
+    block-table, slot-mapping and event update, in one launch (the last layer's step), per
+    KV head (agg "group", the benchmark configuration) and with the reference's all-head
+    importance (agg "all"). compress_select_compact_us: the step without the update;
+    compress_step_two_launch_us: the update as compress_finalize's own launch."""
     cw = wl_mod.compress_qwen3_8b(seed=3, device=dev, selected_only=True)
     kg, vg = cw["k_cache"], cw["v_cache"]
     bt0 = cw["block_tables"].to(dev)
@@ -360,6 +360,11 @@ def run_compress(args, dev):
                              importance=imp, keep_idx=keep, workspace=ws)
 
         def full_step():
+            cu.compress_step(q, kg, vg, btg, base, ctx, sel, 4, 513, 128 ** -0.5, agg,
+                             importance=imp, keep_idx=keep, workspace=ws, events=events,
+                             rewrite_tables=True, slot_mapping=slot_map)
+
+        def two_launches():
             step()
             cu.compress_finalize(btg, base, sel, 513, 256, 4, events, rewrite_tables=True,
                                  slot_mapping=slot_map)
@@ -370,34 +375,30 @@ def run_compress(args, dev):
         res[key.replace("_us", "_gbs")] = round(nbytes / (med * 1e-6) / 1e9, 1)
         key2 = "compress_select_compact_us" if agg == "group" else "compress_select_compact_all_us"
         res[key2] = round(timed(step, args.compress_reps), 2)
+        if agg == "group":
+            res["compress_step_two_launch_us"] = round(timed(two_launches, args.compress_reps),
+                                                       2)
     # the same step over an fp8 (E4M3FN) copy of the pool (agg "group")
     kvc = importlib.import_module("nanokv-llm_amd.layers.kv_cache")
     kq, vq = kvc.fp8_quantize(kg), kvc.fp8_quantize(vg)
     imp = torch.empty(m, Hk, 1023, dtype=torch.float32, device=dev)
     keep = torch.empty(m, Hk, 513, dtype=torch.int32, device=dev)
-    times = []
-    for i in range(3 + args.compress_reps):
-        flush.sum()
-        a = torch.cuda.Event(enable_timing=True)
-        b = torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        cu.compress_step(q, kq, vq, btg, base, ctx, sel, 4, 513, 128 ** -0.5, "group",
-                         importance=imp, keep_idx=keep, workspace=ws)
-        b.record(stream)
-        torch.cuda.synchronize()
-        if i >= 3:
-            times.append(a.elapsed_time(b) * 1000.0)
-    res["compress_step_fp8_us"] = round(statistics.median(times), 2)
+    res["compress_step_fp8_us"] = round(timed(lambda: cu.compress_step(
+        q, kq, vq, btg, base, ctx, sel, 4, 513, 128 ** -0.5, "group", importance=imp,
+        keep_idx=keep, workspace=ws, events=events, rewrite_tables=True,
+        slot_mapping=slot_map), args.compress_reps), 2)
     del kq, vq
     if not args.no_cpu_baseline:
         res["compress_cpu_baseline"] = cpu_compress_baseline()
     res.update({"compress_bytes": nbytes, "compress_sequences": m,
-                "compress_config": "the full step (compress_step + compress_finalize: tables, slots, "
-                                   "events); agg group (importance summed over each GQA group, "
-                                   "kept set per KV head); compress_step_all_*: all-head "
-                                   "importance; compress_select_compact_*: without the "
-                                   "finalize; compress_step_fp8_us: agg group over an fp8 pool "
-                                   "(select + compact)"})
+                "compress_config": "the full step (select + compact + the finalize's tables, "
+                                   "slots and events, one launch); agg group (importance "
+                                   "summed over each GQA group, kept set per KV head); "
+                                   "compress_step_all_*: all-head importance; "
+                                   "compress_select_compact_*: without the finalize; "
+                                   "compress_step_two_launch_us: the finalize as its own "
+                                   "launch; compress_step_fp8_us: the full step, agg group, "
+                                   "over an fp8 pool"})
     return res
 
 
@@ -814,9 +815,8 @@ def run_longctx(args, dev):
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record(stream)
         cu.compress_step(q, kc, vc, bt_c, base, cl, sel, 4, 513, D ** -0.5, "group",
-                         importance=imp, keep_idx=keep, workspace=cws)
-        cu.compress_finalize(bt_c, base, sel, 513, B, 4, ev_c, rewrite_tables=True,
-                             slot_mapping=slot_c)
+                         importance=imp, keep_idx=keep, workspace=cws, events=ev_c,
+                         rewrite_tables=True, slot_mapping=slot_c)
         b.record(stream)
         torch.cuda.synchronize()
         if i >= 3:
@@ -838,9 +838,8 @@ def run_longctx(args, dev):
         cu.compress_schedule(ctx, tails_d, B, 4, 20, 1, counter, sel_d, n_sel, base_d,
                              policy="longest")
         cu.compress_step(q, kc, vc, bt_c, base_d, cl, sel_d, 4, 513, D ** -0.5, "group",
-                         importance=imp20, keep_idx=keep20, workspace=cws20)
-        cu.compress_finalize(bt_c, base_d, sel_d, 513, B, 4, ev, rewrite_tables=True,
-                             slot_mapping=slot_c)
+                         importance=imp20, keep_idx=keep20, workspace=cws20, events=ev,
+                         rewrite_tables=True, slot_mapping=slot_c)
 
     bt_c.copy_(bt)
     device_step()

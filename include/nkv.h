@@ -477,6 +477,45 @@ int nkv_compress_step_f16(const void* q, int64_t q_row_stride, void* k_cache, vo
                           void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * The last layer's compression step: nkv_compress_step followed by
+ * nkv_compress_finalize (same arguments, same effects), in the step's launch
+ * when it is fused (m <= 16384): the bookkeeping of each selected sequence is
+ * done by the last of its (sequence, KV head) workgroups to arrive, after all
+ * of them have read its block-table row, so it needs no launch of its own.
+ * Arrival counters are device-global and zero between calls; calls that
+ * overlap on one GPU (concurrent streams) must not. block_tables is written
+ * (rewrite_tables) as by nkv_compress_finalize.
+ * Replaces: MyCompressCompact on the last layer (layer_id + 1 == num_layers):
+ *           the per-layer work and the event construction,
+ *           nanokvllm/layers/compress_utils.py:100-290, with the table/slot
+ *           effect of Scheduler.postprocess + BlockManager.truncate_blocks
+ *           (nanokvllm/engine/scheduler.py:104-125,
+ *            nanokvllm/engine/block_manager.py:117-138)
+ */
+int nkv_compress_step_finalize(const void* q, int64_t q_row_stride, void* k_cache,
+                               void* v_cache, int32_t* block_tables, int64_t bt_row_stride,
+                               int32_t max_blocks_per_seq, const int32_t* base_context_lens,
+                               int32_t* context_lens, const int32_t* seq_idx, int32_t m,
+                               int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                               int32_t block_size, int32_t window_blocks, int64_t n_blocks,
+                               float scale, int32_t agg_mode, int32_t keep_tokens,
+                               float* importance_out, int32_t* keep_idx, void* workspace,
+                               size_t workspace_bytes, int32_t rewrite_tables,
+                               int32_t* slot_mapping, int32_t* events, void* stream);
+/* nkv_compress_step_finalize with fp16 q and caches. Replaces: as
+ * nkv_compress_step_finalize, for a float16 checkpoint. */
+int nkv_compress_step_finalize_f16(const void* q, int64_t q_row_stride, void* k_cache,
+                                   void* v_cache, int32_t* block_tables, int64_t bt_row_stride,
+                                   int32_t max_blocks_per_seq, const int32_t* base_context_lens,
+                                   int32_t* context_lens, const int32_t* seq_idx, int32_t m,
+                                   int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                                   int32_t block_size, int32_t window_blocks, int64_t n_blocks,
+                                   float scale, int32_t agg_mode, int32_t keep_tokens,
+                                   float* importance_out, int32_t* keep_idx, void* workspace,
+                                   size_t workspace_bytes, int32_t rewrite_tables,
+                                   int32_t* slot_mapping, int32_t* events, void* stream);
+
+/*
  * In-place compaction of the window of each selected sequence, K and V:
  * kept window token keep_idx[j,s,i] moves to window position i
  * (i < keep_tokens); tail token u (tail = len % B tokens, block
@@ -566,6 +605,22 @@ int nkv_compress_step_fp8(const void* q, int64_t q_row_stride, void* k_cache, vo
                           float scale, float k_scale, int32_t agg_mode, int32_t keep_tokens,
                           float* importance_out, int32_t* keep_idx, void* workspace,
                           size_t workspace_bytes, void* stream);
+/* nkv_compress_step_fp8 followed by nkv_compress_finalize, fused as in
+ * nkv_compress_step_finalize (same counters, same rule for overlapping calls).
+ * Replaces: MyCompressCompact on the last layer (compress_utils.py:100-290)
+ * over an fp8 pool, with the table/slot effect of Scheduler.postprocess +
+ * BlockManager.truncate_blocks (scheduler.py:104-125, block_manager.py:117-138). */
+int nkv_compress_step_finalize_fp8(const void* q, int64_t q_row_stride, void* k_cache,
+                                   void* v_cache, int32_t* block_tables, int64_t bt_row_stride,
+                                   int32_t max_blocks_per_seq, const int32_t* base_context_lens,
+                                   int32_t* context_lens, const int32_t* seq_idx, int32_t m,
+                                   int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                                   int32_t block_size, int32_t window_blocks, int64_t n_blocks,
+                                   float scale, float k_scale, int32_t agg_mode,
+                                   int32_t keep_tokens, float* importance_out, int32_t* keep_idx,
+                                   void* workspace, size_t workspace_bytes,
+                                   int32_t rewrite_tables, int32_t* slot_mapping,
+                                   int32_t* events, void* stream);
 
 /*
  * Per-step attention metadata built on the device from one packed int32

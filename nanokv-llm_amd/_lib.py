@@ -97,6 +97,16 @@ SIGNATURES = {
     "nkv_compress_step_fp8": (C.c_int, [_p, _i64, _p, _p, _p, _i64, _i32, _p, _p, _p, _i32, _i32,
                                         _i32, _i32, _i32, _i32, _i64, _f32, _f32, _i32, _i32, _p,
                                         _p, _p, _sz, _p]),
+    "nkv_compress_step_finalize": (C.c_int, [_p, _i64, _p, _p, _p, _i64, _i32, _p, _p, _p, _i32,
+                                             _i32, _i32, _i32, _i32, _i32, _i64, _f32, _i32,
+                                             _i32, _p, _p, _p, _sz, _i32, _p, _p, _p]),
+    "nkv_compress_step_finalize_f16": (C.c_int, [_p, _i64, _p, _p, _p, _i64, _i32, _p, _p, _p,
+                                                 _i32, _i32, _i32, _i32, _i32, _i32, _i64, _f32,
+                                                 _i32, _i32, _p, _p, _p, _sz, _i32, _p, _p, _p]),
+    "nkv_compress_step_finalize_fp8": (C.c_int, [_p, _i64, _p, _p, _p, _i64, _i32, _p, _p, _p,
+                                                 _i32, _i32, _i32, _i32, _i32, _i32, _i64, _f32,
+                                                 _f32, _i32, _i32, _p, _p, _p, _sz, _i32, _p, _p,
+                                                 _p]),
     "nkv_compress_compact": (C.c_int, [_p, _p, _p, _i64, _i32, _p, _p, _p, _i32, _p, _i32, _i32,
                                        _i32, _i32, _i32, _i32, _i64, _p]),
     "nkv_compress_finalize": (C.c_int, [_p, _i64, _i32, _p, _p, _i32, _i32, _i32, _i32, _i32, _p,

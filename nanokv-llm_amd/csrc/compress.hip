@@ -692,24 +692,39 @@ __device__ __forceinline__ void unit_row(const int32_t* win_pb, const int32_t* k
   if (src < 0 || dst < 0) src = dst = -1;
 }
 
-// Block ids of the unit (window blocks, then the tail block or -1) into win_pb; returns
+// Block id of the unit for thread t <= window_blocks (window block t, then the tail block;
+// -1 if missing) into pb_out, as a load whose value is first used by the caller; returns
 // false (nothing to do) when the sequence is not compressible or its table is too short.
-__device__ __forceinline__ bool unit_blocks(int32_t* win_pb, const int32_t* __restrict__ bt,
-                                            int len, int B, int window_blocks, int max_blocks,
-                                            int64_t n_blocks) {
+__device__ __forceinline__ bool unit_block_load(const int32_t* __restrict__ bt, int len, int B,
+                                                int window_blocks, int max_blocks,
+                                                int32_t& pb_out) {
   const int full = len / B;
   const int tail = len - full * B;
+  pb_out = -1;
   if (full < window_blocks || full > max_blocks || (tail > 0 && full >= max_blocks))
     return false;
-  const int wb0 = full - window_blocks;
+  if ((int)threadIdx.x < window_blocks) pb_out = bt[full - window_blocks + threadIdx.x];
+  else if ((int)threadIdx.x == window_blocks && tail > 0) pb_out = bt[full];
+  return true;
+}
+
+// unit_block_load's id into win_pb (threads t <= window_blocks).
+__device__ __forceinline__ void unit_block_store(int32_t* win_pb, int32_t pb, int len, int B,
+                                                 int window_blocks, int64_t n_blocks) {
   if ((int)threadIdx.x <= window_blocks) {
-    int32_t pb = -1;
-    if ((int)threadIdx.x < window_blocks) pb = bt[wb0 + threadIdx.x];
-    else if (tail > 0) pb = bt[full];
-    NKV_DBG(((int)threadIdx.x < window_blocks || tail > 0) && (pb < 0 || pb >= n_blocks),
+    NKV_DBG(((int)threadIdx.x < window_blocks || len % B > 0) && (pb < 0 || pb >= n_blocks),
             NKV_DEBUG_BLOCK);
     win_pb[threadIdx.x] = (pb >= 0 && pb < n_blocks) ? pb : -1;
   }
+}
+
+// Both: the block ids of the unit (window blocks, then the tail block or -1) into win_pb.
+__device__ __forceinline__ bool unit_blocks(int32_t* win_pb, const int32_t* __restrict__ bt,
+                                            int len, int B, int window_blocks, int max_blocks,
+                                            int64_t n_blocks) {
+  int32_t pb;
+  if (!unit_block_load(bt, len, B, window_blocks, max_blocks, pb)) return false;
+  unit_block_store(win_pb, pb, len, B, window_blocks, n_blocks);
   return true;
 }
 
@@ -773,6 +788,127 @@ __device__ __forceinline__ void compact_unit(
   if (kvh == 0 && tid == 0) context_lens[seq] = len - Lw + keep_tokens;
 }
 
+// ---------------------------------------------------------------- finalize
+// Bookkeeping of one selected sequence, by one wave: the events row, the next token's
+// slot and the table row's tail. fin_load reads what it needs (the row's entries from
+// keep_blocks on, the first 128 two per lane, and the entry of the next token's block);
+// fin_store writes, reading further entries of rows longer than that itself. A caller
+// can issue fin_load early and fin_store after every other reader of the row is done.
+struct FinRow {
+  int32_t seq, len, new_len, keep_blocks, skip;  // uniform over the wave
+  int32_t id0, id1;  // entries keep_blocks + lane and keep_blocks + 64 + lane (-1 past the row)
+  int32_t pb;        // entry of the block holding position new_len (-1: none)
+};
+
+// Arguments of the bookkeeping when a compression step launch carries it.
+struct FinArgs {
+  int32_t* block_tables;  // the tables the step reads, writable; null: no bookkeeping
+  int32_t* slot_mapping;  // optional
+  int32_t* events;        // [m, 4 + max_blocks]
+  int32_t rewrite_tables;
+};
+
+__device__ __forceinline__ FinRow fin_load(const int32_t* __restrict__ bt_row, int seq, int len,
+                                           int max_blocks, int keep_tokens, int B,
+                                           int window_blocks, int lane) {
+  FinRow f;
+  f.seq = seq;
+  f.len = len;
+  const int full = len / B, tail = len - (len / B) * B;
+  // the compaction's skip rule: not compressible -> left unchanged; seq -1 (padding) too
+  f.skip = seq < 0 || full < window_blocks || full > max_blocks ||
+           (tail > 0 && full >= max_blocks);
+  f.new_len = len - window_blocks * B + keep_tokens;
+  f.keep_blocks = (f.new_len + B - 1) / B;
+  f.id0 = f.id1 = f.pb = -1;
+  if (!f.skip) {
+    const int i0 = f.keep_blocks + lane;
+    if (i0 < max_blocks) f.id0 = bt_row[i0];
+    if (i0 + 64 < max_blocks) f.id1 = bt_row[i0 + 64];
+    const int blk = f.new_len / B;  // kept (blk < keep_blocks) whenever the slot exists
+    if (f.new_len % B != 0 && blk < max_blocks) f.pb = bt_row[blk];
+  }
+  return f;
+}
+
+// events row: [seq, new_len, keep_blocks, n_freed, freed ids..., -1...]; a sequence left
+// unchanged reads [seq, len, ceil(len/B), -1, -1...] and a padding entry [-1, 0, 0, 0, -1...]
+__device__ __forceinline__ void fin_store(const FinRow& f, int32_t* __restrict__ bt_row,
+                                          int32_t* __restrict__ ev, int max_blocks, int B,
+                                          int rewrite_tables, int32_t* __restrict__ slot_mapping,
+                                          int lane) {
+  if (f.skip) {
+    if (lane == 0) {
+      ev[0] = f.seq; ev[1] = f.len; ev[2] = (f.len + B - 1) / B; ev[3] = f.seq >= 0 ? -1 : 0;
+    }
+    for (int i = lane; i < max_blocks; i += 64) ev[4 + i] = -1;
+    return;
+  }
+  // freed ids (entries >= 0 past the kept blocks, in table order) packed by ballot
+  // prefix counts
+  int n = 0;  // uniform
+  auto pack = [&](int32_t id) {
+    const uint64_t valid = __builtin_amdgcn_ballot_w64(id >= 0);
+    if (id >= 0) ev[4 + n + __builtin_popcountll(valid & ((1ull << lane) - 1ull))] = id;
+    n += __builtin_popcountll(valid);
+  };
+  pack(f.id0);
+  pack(f.id1);
+  for (int i0 = f.keep_blocks + 128; i0 < max_blocks; i0 += 64) {
+    const int i = i0 + lane;
+    pack(i < max_blocks ? bt_row[i] : -1);
+  }
+  for (int i = n + lane; i < max_blocks; i += 64) ev[4 + i] = -1;
+  if (lane == 0) {
+    ev[0] = f.seq; ev[1] = f.new_len; ev[2] = f.keep_blocks; ev[3] = n;
+    if (slot_mapping) slot_mapping[f.seq] = f.pb < 0 ? -1 : f.pb * B + f.new_len % B;
+  }
+  if (rewrite_tables)  // after every read of the row (the loads above, in program order)
+    for (int i = f.keep_blocks + lane; i < max_blocks; i += 64) bt_row[i] = -1;
+}
+
+// One wave per selected sequence.
+__global__ __launch_bounds__(64) void compress_finalize_kernel(
+    int32_t* __restrict__ block_tables, int64_t bt_row_stride, int32_t max_blocks,
+    const int32_t* __restrict__ base_context_lens, const int32_t* __restrict__ seq_idx,
+    int32_t m, int32_t keep_tokens, int32_t block_size, int32_t window_blocks,
+    int32_t rewrite_tables, int32_t* __restrict__ slot_mapping, int32_t* __restrict__ events) {
+  const int j = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int seq = seq_idx[j];
+  const int len = seq >= 0 ? base_context_lens[seq] : 0;  // seq -1: padding entry
+  int32_t* bt = block_tables + (int64_t)(seq >= 0 ? seq : 0) * bt_row_stride;
+  const FinRow f = fin_load(bt, seq, len, max_blocks, keep_tokens, block_size, window_blocks,
+                            lane);
+  fin_store(f, bt, events + (int64_t)j * (4 + max_blocks), max_blocks, block_size,
+            rewrite_tables, slot_mapping, lane);
+}
+
+// Arrivals of the units of each selected sequence in a step launch that carries the
+// bookkeeping (FinArgs): the unit that arrives last does it, after every unit of the
+// sequence has read the table row. atomicInc wraps each counter back to 0 at its last
+// arrival, so the counters are zero between launches; launches that overlap on one GPU
+// share them and must not.
+constexpr int kFinMaxSeqs = 16384;
+static __device__ uint32_t fin_arrivals[kFinMaxSeqs];
+
+// Called by one thread once every table read of its unit has returned (the reads were
+// consumed before a workgroup barrier that precedes the call); true for the last arrival
+// of the n_units units of sequence j. The result is needed only at the end of the unit,
+// so the round trip overlaps the unit's work.
+__device__ __forceinline__ uint32_t fin_arrive(int j, int n_units) {
+  return atomicInc(&fin_arrivals[j], (uint32_t)(n_units - 1));
+}
+
+// The bookkeeping of a padding entry (seq -1), by wave 0 of its first unit.
+__device__ __forceinline__ void fin_padding(const FinArgs& fin, int j, int max_blocks, int B) {
+  if (threadIdx.x < 64) {
+    const FinRow f = fin_load(nullptr, -1, 0, max_blocks, 0, B, 1, threadIdx.x);
+    fin_store(f, nullptr, fin.events + (int64_t)j * (4 + max_blocks), max_blocks, B, 0, nullptr,
+              threadIdx.x);
+  }
+}
+
 // agg "group": score -> select -> (if k_cache_w) compact. Grid m * Hk.
 template <bool F8, bool H16 = false>
 __global__ __launch_bounds__(kSelThreads) void compress_group_kernel(
@@ -782,7 +918,7 @@ __global__ __launch_bounds__(kSelThreads) void compress_group_kernel(
     int32_t Hk, int32_t G, int32_t block_size, int32_t window_blocks, int64_t n_blocks, float scale_log2,
     int32_t num_keep, float* __restrict__ importance_out, int32_t* __restrict__ keep_idx,
     void* __restrict__ k_cache_w, void* __restrict__ v_cache_w,
-    int32_t* __restrict__ context_lens) {
+    int32_t* __restrict__ context_lens, FinArgs fin) {
   __shared__ SelectLds L;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -790,23 +926,36 @@ __global__ __launch_bounds__(kSelThreads) void compress_group_kernel(
   // workgroups go to the XCDs round-robin: rotating the head by the sequence gives each
   // XCD's L2 every head's 256-byte column of the token rows instead of always the same one
   const int kvh = (blockIdx.x + j) % Hk;
-  if (block_tables && seq_idx[j] < 0) return;  // padding entry (uniform): nothing written
+  if (block_tables && seq_idx[j] < 0) {  // padding entry (uniform): nothing else written
+    if (fin.block_tables && blockIdx.x % Hk == 0) fin_padding(fin, j, max_blocks, block_size);
+    return;
+  }
   const int Lw = window_blocks * block_size;
   const int n_cand = Lw - 1;
-  // compaction: the unit's block ids (published by the scoring's barriers), read while the
-  // scoring's loads are in flight; not compressible or inconsistent with the table width:
-  // left untouched
+  // compaction: the unit's block ids, loaded with the scoring's first loads; not
+  // compressible or inconsistent with the table width: left untouched
   bool compact = false;
-  if (k_cache_w) {
-    const int seq = seq_idx[j];
-    compact = unit_blocks(L.win_pb, block_tables + (int64_t)seq * bt_row_stride,
-                          base_context_lens[seq], block_size, window_blocks, max_blocks,
-                          n_blocks);
-  }
+  int32_t wpb = -1;
+  const int seq = block_tables ? seq_idx[j] : 0;  // no seq_idx for contiguous K
+  const int len = k_cache_w ? base_context_lens[seq] : 0;
+  if (k_cache_w)
+    compact = unit_block_load(block_tables + (int64_t)seq * bt_row_stride, len, block_size,
+                              window_blocks, max_blocks, wpb);
   float gi[4];
   group_importance<F8, H16>(L, q, q_row_stride, k, block_tables, bt_row_stride, max_blocks,
                        base_context_lens, seq_idx, j, kvh, Hk, G, block_size, window_blocks,
                        n_blocks, scale_log2, gi);
+  // published by the selection's barriers; stored only now so that the scoring's loads
+  // are not held behind this one
+  if (compact) unit_block_store(L.win_pb, wpb, len, block_size, window_blocks, n_blocks);
+  uint32_t fin_old = 0;  // every wave has read its table entries (the scoring's barriers)
+  FinRow fr{};
+  if (fin.block_tables && tid < 64) {
+    if (tid == 0) fin_old = fin_arrive(j, Hk);
+    // read by every unit, used by the last to arrive: the selection hides the round trip
+    fr = fin_load(fin.block_tables + (int64_t)seq * bt_row_stride, seq, len, max_blocks,
+                  num_keep + 2, block_size, window_blocks, lane);
+  }
   const int t0 = (tid >> 6) * kSelKeysPerWave;
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
@@ -820,6 +969,10 @@ __global__ __launch_bounds__(kSelThreads) void compress_group_kernel(
   if (compact)
     compact_unit<F8>(L, k_cache_w, v_cache_w, base_context_lens, context_lens, seq_idx, j, kvh,
                      num_keep + 2, Hk, block_size, window_blocks);
+  if (fin.block_tables && tid < 64 && __builtin_amdgcn_readfirstlane(fin_old) == (uint32_t)(Hk - 1))
+    fin_store(fr, fin.block_tables + (int64_t)fr.seq * bt_row_stride,
+              fin.events + (int64_t)j * (4 + max_blocks), max_blocks, block_size,
+              fin.rewrite_tables, fin.slot_mapping, lane);
 }
 
 // agg "all", first kernel: each group's importance -> partial[j][kvh][Lw]. Grid m * Hk.
@@ -859,21 +1012,26 @@ __global__ __launch_bounds__(kSelThreads) void compress_sum_kernel(
     int32_t* __restrict__ keep_idx, void* __restrict__ k_cache_w,
     void* __restrict__ v_cache_w, const int32_t* __restrict__ block_tables,
     int64_t bt_row_stride, int32_t max_blocks, const int32_t* __restrict__ base_context_lens,
-    int32_t* __restrict__ context_lens, const int32_t* __restrict__ seq_idx, int64_t n_blocks) {
+    int32_t* __restrict__ context_lens, const int32_t* __restrict__ seq_idx, int64_t n_blocks,
+    FinArgs fin) {
   __shared__ SelectLds L;
   const int tid = threadIdx.x;
   const int j = blockIdx.x / n_units_per_seq;
   const int kvh = (blockIdx.x + j) % n_units_per_seq;  // rotated as in compress_group_kernel
-  if (block_tables && seq_idx[j] < 0) return;  // padding entry (uniform): nothing written
+  if (block_tables && seq_idx[j] < 0) {  // padding entry (uniform): nothing else written
+    if (fin.block_tables && blockIdx.x % n_units_per_seq == 0)
+      fin_padding(fin, j, max_blocks, block_size);
+    return;
+  }
   const int Lw = window_blocks * block_size;
   const int n_cand = Lw - 1;
   bool compact = false;  // as in compress_group_kernel
-  if (k_cache_w) {
-    const int seq = seq_idx[j];
-    compact = unit_blocks(L.win_pb, block_tables + (int64_t)seq * bt_row_stride,
-                          base_context_lens[seq], block_size, window_blocks, max_blocks,
-                          n_blocks);
-  }
+  int32_t wpb = -1;
+  const int seq = block_tables ? seq_idx[j] : 0;
+  const int len = k_cache_w ? base_context_lens[seq] : 0;
+  if (k_cache_w)
+    compact = unit_block_load(block_tables + (int64_t)seq * bt_row_stride, len, block_size,
+                              window_blocks, max_blocks, wpb);
   const float* pj = partial + (int64_t)j * Hk * Lw;
   const bool writer = kvh == 0;
   float* irow = importance_out + (int64_t)j * n_cand;
@@ -889,11 +1047,24 @@ __global__ __launch_bounds__(kSelThreads) void compress_sum_kernel(
     L.imp[t] = v;
     if (writer && t < n_cand) irow[t] = v;
   }
+  if (compact) unit_block_store(L.win_pb, wpb, len, block_size, window_blocks, n_blocks);
   __syncthreads();
+  uint32_t fin_old = 0;  // the unit's table reads (wave 0's) preceded the barrier
+  FinRow fr{};
+  if (fin.block_tables && tid < 64) {
+    if (tid == 0) fin_old = fin_arrive(j, n_units_per_seq);
+    fr = fin_load(fin.block_tables + (int64_t)seq * bt_row_stride, seq, len, max_blocks,
+                  num_keep + 2, block_size, window_blocks, tid);  // as in the group kernel
+  }
   block_select(L, n_cand, num_keep, writer ? keep_idx + (int64_t)j * (num_keep + 2) : nullptr);
   if (compact)
     compact_unit<F8>(L, k_cache_w, v_cache_w, base_context_lens, context_lens, seq_idx, j, kvh,
                      num_keep + 2, Hk, block_size, window_blocks);
+  if (fin.block_tables && tid < 64 &&
+      __builtin_amdgcn_readfirstlane(fin_old) == (uint32_t)(n_units_per_seq - 1))
+    fin_store(fr, fin.block_tables + (int64_t)fr.seq * bt_row_stride,
+              fin.events + (int64_t)j * (4 + max_blocks), max_blocks, block_size,
+              fin.rewrite_tables, fin.slot_mapping, tid);
 }
 
 // ----------------------------------------------------------------- compact
@@ -971,56 +1142,6 @@ __global__ __launch_bounds__(256) void compress_compact_kernel(
 
   if (blockIdx.x % (2 * parts * Hk) == 0 && threadIdx.x == 0)
     context_lens[seq] = len - Lw + keep_tokens;
-}
-
-// ---------------------------------------------------------------- finalize
-// One wave per selected sequence: the lanes walk its table row 64 entries at a time, the
-// freed block ids (entries past the kept blocks, in table order) are packed by a ballot
-// prefix count, and the row's tail is cleared by the same lanes after the reads.
-__global__ __launch_bounds__(64) void compress_finalize_kernel(
-    int32_t* __restrict__ block_tables, int64_t bt_row_stride, int32_t max_blocks,
-    const int32_t* __restrict__ base_context_lens, const int32_t* __restrict__ seq_idx,
-    int32_t m, int32_t keep_tokens, int32_t block_size, int32_t window_blocks,
-    int32_t rewrite_tables, int32_t* __restrict__ slot_mapping, int32_t* __restrict__ events) {
-  const int B = block_size;
-  const int ev_len = 4 + max_blocks;
-  const int j = blockIdx.x;
-  const int lane = threadIdx.x;
-  const int seq = seq_idx[j];
-  const int len = seq >= 0 ? base_context_lens[seq] : 0;  // seq -1: padding entry
-  int32_t* ev = events + (int64_t)j * ev_len;
-  int32_t* bt = block_tables + (int64_t)(seq >= 0 ? seq : 0) * bt_row_stride;
-  const int full = len / B, tail = len - (len / B) * B;
-  // same skip rule as the compaction: not compressible -> left unchanged and marked
-  // skipped (n_freed = -1), so the host changes none of its state; a padding entry
-  // (seq -1) reads [-1, 0, 0, 0, -1...]
-  if (full < window_blocks || full > max_blocks || (tail > 0 && full >= max_blocks)) {
-    if (lane == 0) {
-      ev[0] = seq; ev[1] = len; ev[2] = (len + B - 1) / B; ev[3] = seq >= 0 ? -1 : 0;
-    }
-    for (int i = lane; i < max_blocks; i += 64) ev[4 + i] = -1;
-    return;
-  }
-  const int new_len = len - window_blocks * B + keep_tokens;
-  const int keep_blocks = (new_len + B - 1) / B;
-  int n = 0;  // freed ids packed so far (uniform)
-  for (int i0 = keep_blocks; i0 < max_blocks; i0 += 64) {
-    const int i = i0 + lane;
-    const int id = i < max_blocks ? bt[i] : -1;
-    const uint64_t valid = __builtin_amdgcn_ballot_w64(id >= 0);
-    if (id >= 0) ev[4 + n + __builtin_popcountll(valid & ((1ull << lane) - 1ull))] = id;
-    n += __builtin_popcountll(valid);
-  }
-  for (int i = n + lane; i < max_blocks; i += 64) ev[4 + i] = -1;
-  // the next token's slot, from an entry the rewrite keeps (blk < keep_blocks)
-  const int blk = new_len / B, off = new_len % B;
-  const int pb = (off == 0 || blk >= max_blocks) ? -1 : bt[blk];
-  if (lane == 0) {
-    ev[0] = seq; ev[1] = new_len; ev[2] = keep_blocks; ev[3] = n;
-    if (slot_mapping) slot_mapping[seq] = pb < 0 ? -1 : pb * B + off;
-  }
-  if (rewrite_tables)  // after this wave's reads of the row (program order within the wave)
-    for (int i = keep_blocks + lane; i < max_blocks; i += 64) bt[i] = -1;
 }
 
 // ----------------------------------------------------------------- schedule
@@ -1457,7 +1578,7 @@ static int launch_fused(const void* q, int64_t q_row_stride, const void* k_cache
                         int64_t n_blocks, float scale, int32_t agg_mode, int32_t num_keep,
                         float* importance_out, int32_t* keep_idx, void* workspace,
                         void* k_cache_w, void* v_cache_w, int32_t* context_lens,
-                        hipStream_t s) {
+                        hipStream_t s, const FinArgs& fin = FinArgs{}) {
   const int g = n_q_heads / n_kv_heads;
   const int Lw = window_blocks * block_size;
   const bool step = k_cache_w != nullptr;
@@ -1472,7 +1593,7 @@ static int launch_fused(const void* q, int64_t q_row_stride, const void* k_cache
                        (const bf16_t*)q, q_row_stride, k_cache, block_tables, bt_row_stride,
                        max_blocks_per_seq, base_context_lens, seq_idx, n_kv_heads, g,
                        block_size, window_blocks, n_blocks, sl2, num_keep, importance_out,
-                       keep_idx, k_cache_w, v_cache_w, context_lens);
+                       keep_idx, k_cache_w, v_cache_w, context_lens, fin);
     return check_launch("compress (group)") ? -1 : 0;
   }
   hipLaunchKernelGGL((compress_partial_kernel<F8, H16>), dim3(units), dim3(kSelThreads), 0, s,
@@ -1485,7 +1606,7 @@ static int launch_fused(const void* q, int64_t q_row_stride, const void* k_cache
                      0, s, (const float*)partial, n_kv_heads, per_seq, block_size,
                      window_blocks, num_keep, importance_out, keep_idx, k_cache_w, v_cache_w,
                      block_tables, bt_row_stride, max_blocks_per_seq, base_context_lens,
-                     context_lens, seq_idx, n_blocks);
+                     context_lens, seq_idx, n_blocks, fin);
   return check_launch("compress (sum)") ? -1 : 0;
 }
 }  // namespace nkv
@@ -1623,6 +1744,19 @@ extern "C" int nkv_compress_compact(void* k_cache, void* v_cache, const int32_t*
   return check_launch("nkv_compress_compact");
 }
 
+namespace nkv {
+static int launch_finalize(const FinArgs& fin, int64_t bt_row_stride, int32_t max_blocks_per_seq,
+                           const int32_t* base_context_lens, const int32_t* seq_idx, int32_t m,
+                           int32_t keep_tokens, int32_t block_size, int32_t window_blocks,
+                           hipStream_t s) {
+  hipLaunchKernelGGL(compress_finalize_kernel, dim3((unsigned)m), dim3(64), 0, s,
+                     fin.block_tables, bt_row_stride, max_blocks_per_seq, base_context_lens,
+                     seq_idx, m, keep_tokens, block_size, window_blocks, fin.rewrite_tables,
+                     fin.slot_mapping, fin.events);
+  return check_launch("nkv_compress_finalize");
+}
+}  // namespace nkv
+
 extern "C" int nkv_compress_finalize(int32_t* block_tables, int64_t bt_row_stride,
                                      int32_t max_blocks_per_seq,
                                      const int32_t* base_context_lens, const int32_t* seq_idx,
@@ -1637,11 +1771,9 @@ extern "C" int nkv_compress_finalize(int32_t* block_tables, int64_t bt_row_strid
               "compress_finalize: null pointer");
   NKV_REQUIRE(bt_row_stride >= max_blocks_per_seq, NKV_EINVAL,
               "compress_finalize: bt_row_stride < max_blocks_per_seq");
-  hipLaunchKernelGGL(compress_finalize_kernel, dim3((unsigned)m), dim3(64), 0, as_stream(stream),
-                     block_tables, bt_row_stride, max_blocks_per_seq, base_context_lens, seq_idx,
-                     m, keep_tokens, block_size, window_blocks, rewrite_tables, slot_mapping,
-                     events);
-  return check_launch("nkv_compress_finalize");
+  return launch_finalize(FinArgs{block_tables, slot_mapping, events, rewrite_tables},
+                         bt_row_stride, max_blocks_per_seq, base_context_lens, seq_idx, m,
+                         keep_tokens, block_size, window_blocks, as_stream(stream));
 }
 
 namespace nkv {
@@ -1655,7 +1787,7 @@ static int compress_step_impl(const void* q, int64_t q_row_stride, void* k_cache
                               int32_t window_blocks, int64_t n_blocks, float scale,
                               int32_t agg_mode, int32_t keep_tokens, float* importance_out,
                               int32_t* keep_idx, void* workspace, size_t workspace_bytes,
-                              void* stream) {
+                              void* stream, const FinArgs& fin = FinArgs{}) {
   NKV_REQUIRE(m >= 0 && n_q_heads > 0 && n_kv_heads > 0 && window_blocks > 0 && block_size > 0,
               NKV_EINVAL, "compress_step: bad sizes");
   if (m == 0) return NKV_OK;
@@ -1681,24 +1813,35 @@ static int compress_step_impl(const void* q, int64_t q_row_stride, void* k_cache
   NKV_REQUIRE(workspace && workspace_bytes >= need, NKV_EWORKSPACE,
               "compress_step: workspace needs %zu bytes (got %zu)", need, workspace_bytes);
   hipStream_t s = as_stream(stream);
+  // the bookkeeping rides in the fused launch (m within the arrival counters), else it
+  // follows as its own launch
+  const FinArgs fused_fin = m <= kFinMaxSeqs ? fin : FinArgs{};
   int rc = launch_fused<false, H16>(q, q_row_stride, k_cache, block_tables, bt_row_stride,
                                     max_blocks_per_seq, base_context_lens, seq_idx, m,
                                     n_q_heads, n_kv_heads, head_dim, block_size, window_blocks,
                                     n_blocks, scale, agg_mode, num_keep, importance_out,
-                                    keep_idx, workspace, k_cache, v_cache, context_lens, s);
+                                    keep_idx, workspace, k_cache, v_cache, context_lens, s,
+                                    fused_fin);
   if (rc < 0) return NKV_ELAUNCH;
-  if (rc == 0) return NKV_OK;
-  // general path: selection, then the compaction kernel (2-byte rows move as bytes)
-  rc = compress_select_impl<H16>(q, q_row_stride, k_cache, block_tables, bt_row_stride,
-                                 max_blocks_per_seq, base_context_lens, seq_idx, m, n_q_heads,
-                                 n_kv_heads, head_dim, block_size, window_blocks, n_blocks,
-                                 scale, agg_mode, num_keep, importance_out, keep_idx, workspace,
-                                 workspace_bytes, stream);
-  if (rc) return rc;
-  return nkv_compress_compact(k_cache, v_cache, block_tables, bt_row_stride, max_blocks_per_seq,
-                              base_context_lens, context_lens, seq_idx, m, keep_idx, n_sets,
-                              keep_tokens, n_kv_heads, head_dim, block_size, window_blocks,
-                              n_blocks, stream);
+  if (rc == 1) {
+    // general path: selection, then the compaction kernel (2-byte rows move as bytes)
+    rc = compress_select_impl<H16>(q, q_row_stride, k_cache, block_tables, bt_row_stride,
+                                   max_blocks_per_seq, base_context_lens, seq_idx, m, n_q_heads,
+                                   n_kv_heads, head_dim, block_size, window_blocks, n_blocks,
+                                   scale, agg_mode, num_keep, importance_out, keep_idx,
+                                   workspace, workspace_bytes, stream);
+    if (rc) return rc;
+    rc = nkv_compress_compact(k_cache, v_cache, block_tables, bt_row_stride,
+                              max_blocks_per_seq, base_context_lens, context_lens, seq_idx, m,
+                              keep_idx, n_sets, keep_tokens, n_kv_heads, head_dim, block_size,
+                              window_blocks, n_blocks, stream);
+    if (rc) return rc;
+  } else if (fused_fin.block_tables) {
+    return NKV_OK;
+  }
+  if (!fin.block_tables) return NKV_OK;
+  return launch_finalize(fin, bt_row_stride, max_blocks_per_seq, base_context_lens, seq_idx, m,
+                         keep_tokens, block_size, window_blocks, s);
 }
 }  // namespace nkv
 
@@ -1740,6 +1883,40 @@ extern "C" int nkv_compress_step_f16(const void* q, int64_t q_row_stride, void* 
                                        workspace, workspace_bytes, stream);
 }
 
+extern "C" int nkv_compress_step_finalize(
+    const void* q, int64_t q_row_stride, void* k_cache, void* v_cache, int32_t* block_tables,
+    int64_t bt_row_stride, int32_t max_blocks_per_seq, const int32_t* base_context_lens,
+    int32_t* context_lens, const int32_t* seq_idx, int32_t m, int32_t n_q_heads,
+    int32_t n_kv_heads, int32_t head_dim, int32_t block_size, int32_t window_blocks,
+    int64_t n_blocks, float scale, int32_t agg_mode, int32_t keep_tokens, float* importance_out,
+    int32_t* keep_idx, void* workspace, size_t workspace_bytes, int32_t rewrite_tables,
+    int32_t* slot_mapping, int32_t* events, void* stream) {
+  nkv::clear_error();
+  NKV_REQUIRE(events, NKV_EINVAL, "compress_step_finalize: null events");
+  return nkv::compress_step_impl<false>(
+      q, q_row_stride, k_cache, v_cache, block_tables, bt_row_stride, max_blocks_per_seq,
+      base_context_lens, context_lens, seq_idx, m, n_q_heads, n_kv_heads, head_dim, block_size,
+      window_blocks, n_blocks, scale, agg_mode, keep_tokens, importance_out, keep_idx, workspace,
+      workspace_bytes, stream, nkv::FinArgs{block_tables, slot_mapping, events, rewrite_tables});
+}
+
+extern "C" int nkv_compress_step_finalize_f16(
+    const void* q, int64_t q_row_stride, void* k_cache, void* v_cache, int32_t* block_tables,
+    int64_t bt_row_stride, int32_t max_blocks_per_seq, const int32_t* base_context_lens,
+    int32_t* context_lens, const int32_t* seq_idx, int32_t m, int32_t n_q_heads,
+    int32_t n_kv_heads, int32_t head_dim, int32_t block_size, int32_t window_blocks,
+    int64_t n_blocks, float scale, int32_t agg_mode, int32_t keep_tokens, float* importance_out,
+    int32_t* keep_idx, void* workspace, size_t workspace_bytes, int32_t rewrite_tables,
+    int32_t* slot_mapping, int32_t* events, void* stream) {
+  nkv::clear_error();
+  NKV_REQUIRE(events, NKV_EINVAL, "compress_step_finalize: null events");
+  return nkv::compress_step_impl<true>(
+      q, q_row_stride, k_cache, v_cache, block_tables, bt_row_stride, max_blocks_per_seq,
+      base_context_lens, context_lens, seq_idx, m, n_q_heads, n_kv_heads, head_dim, block_size,
+      window_blocks, n_blocks, scale, agg_mode, keep_tokens, importance_out, keep_idx, workspace,
+      workspace_bytes, stream, nkv::FinArgs{block_tables, slot_mapping, events, rewrite_tables});
+}
+
 extern "C" int nkv_compress_schedule(const int32_t* context_lens,
                                      const int32_t* tail_uncompressed, int32_t batch,
                                      int32_t block_size, int32_t window_blocks, int32_t topk,
@@ -1777,18 +1954,18 @@ extern "C" int nkv_compress_schedule(const int32_t* context_lens,
 // scoring (k_scale folded into the score scale), then importance, top-k, and the
 // compaction of the 1-byte rows. Windows of up to 1024 tokens take the fused kernels
 // (as nkv_compress_step), longer ones the four-kernel general path; same results.
-extern "C" int nkv_compress_step_fp8(const void* q, int64_t q_row_stride, void* k_cache,
-                                     void* v_cache, const int32_t* block_tables,
-                                     int64_t bt_row_stride, int32_t max_blocks_per_seq,
-                                     const int32_t* base_context_lens, int32_t* context_lens,
-                                     const int32_t* seq_idx, int32_t m, int32_t n_q_heads,
-                                     int32_t n_kv_heads, int32_t head_dim, int32_t block_size,
-                                     int32_t window_blocks, int64_t n_blocks, float scale,
-                                     float k_scale, int32_t agg_mode, int32_t keep_tokens,
-                                     float* importance_out, int32_t* keep_idx, void* workspace,
-                                     size_t workspace_bytes, void* stream) {
-  using namespace nkv;
-  clear_error();
+namespace nkv {
+static int compress_step_fp8_impl(const void* q, int64_t q_row_stride, void* k_cache,
+                                  void* v_cache, const int32_t* block_tables,
+                                  int64_t bt_row_stride, int32_t max_blocks_per_seq,
+                                  const int32_t* base_context_lens, int32_t* context_lens,
+                                  const int32_t* seq_idx, int32_t m, int32_t n_q_heads,
+                                  int32_t n_kv_heads, int32_t head_dim, int32_t block_size,
+                                  int32_t window_blocks, int64_t n_blocks, float scale,
+                                  float k_scale, int32_t agg_mode, int32_t keep_tokens,
+                                  float* importance_out, int32_t* keep_idx, void* workspace,
+                                  size_t workspace_bytes, void* stream,
+                                  const FinArgs& fin = FinArgs{}) {
   NKV_REQUIRE(m >= 0 && n_q_heads > 0 && n_kv_heads > 0 && window_blocks > 0 &&
                   block_size > 0 && k_scale > 0.f,
               NKV_EINVAL, "compress_step_fp8: bad sizes");
@@ -1821,13 +1998,18 @@ extern "C" int nkv_compress_step_fp8(const void* q, int64_t q_row_stride, void* 
   NKV_REQUIRE(workspace && workspace_bytes >= need, NKV_EWORKSPACE,
               "compress_step_fp8: workspace needs %zu bytes (got %zu)", need, workspace_bytes);
   hipStream_t s = as_stream(stream);
+  const FinArgs fused_fin = m <= kFinMaxSeqs ? fin : FinArgs{};  // as compress_step_impl
   int rc = launch_fused<true>(q, q_row_stride, k_cache, block_tables, bt_row_stride,
                               max_blocks_per_seq, base_context_lens, seq_idx, m, n_q_heads,
                               n_kv_heads, head_dim, block_size, window_blocks, n_blocks,
                               scale * k_scale, agg_mode, num_keep, importance_out, keep_idx,
-                              workspace, k_cache, v_cache, context_lens, s);
+                              workspace, k_cache, v_cache, context_lens, s, fused_fin);
   if (rc < 0) return NKV_ELAUNCH;
-  if (rc == 0) return NKV_OK;
+  if (rc == 0) {
+    if (fused_fin.block_tables || !fin.block_tables) return NKV_OK;
+    return launch_finalize(fin, bt_row_stride, max_blocks_per_seq, base_context_lens, seq_idx,
+                           m, keep_tokens, block_size, window_blocks, s);
+  }
   // general path: score, importance, top-k, compaction
   float* scores = (float*)workspace;
   const unsigned sgrid = (unsigned)(m * n_kv_heads * (Lw / kChunk));
@@ -1857,7 +2039,48 @@ extern "C" int nkv_compress_step_fp8(const void* q, int64_t q_row_stride, void* 
   else if (max_rows <= 768) NKV_COMPACT8_LAUNCH(12);
   else NKV_COMPACT8_LAUNCH(16);
 #undef NKV_COMPACT8_LAUNCH
-  return check_launch("nkv_compress_step_fp8 (compact)");
+  rc = check_launch("nkv_compress_step_fp8 (compact)");
+  if (rc || !fin.block_tables) return rc;
+  return launch_finalize(fin, bt_row_stride, max_blocks_per_seq, base_context_lens, seq_idx, m,
+                         keep_tokens, block_size, window_blocks, s);
+}
+}  // namespace nkv
+
+extern "C" int nkv_compress_step_fp8(const void* q, int64_t q_row_stride, void* k_cache,
+                                     void* v_cache, const int32_t* block_tables,
+                                     int64_t bt_row_stride, int32_t max_blocks_per_seq,
+                                     const int32_t* base_context_lens, int32_t* context_lens,
+                                     const int32_t* seq_idx, int32_t m, int32_t n_q_heads,
+                                     int32_t n_kv_heads, int32_t head_dim, int32_t block_size,
+                                     int32_t window_blocks, int64_t n_blocks, float scale,
+                                     float k_scale, int32_t agg_mode, int32_t keep_tokens,
+                                     float* importance_out, int32_t* keep_idx, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  nkv::clear_error();
+  return nkv::compress_step_fp8_impl(q, q_row_stride, k_cache, v_cache, block_tables,
+                                     bt_row_stride, max_blocks_per_seq, base_context_lens,
+                                     context_lens, seq_idx, m, n_q_heads, n_kv_heads, head_dim,
+                                     block_size, window_blocks, n_blocks, scale, k_scale,
+                                     agg_mode, keep_tokens, importance_out, keep_idx, workspace,
+                                     workspace_bytes, stream);
+}
+
+extern "C" int nkv_compress_step_finalize_fp8(
+    const void* q, int64_t q_row_stride, void* k_cache, void* v_cache, int32_t* block_tables,
+    int64_t bt_row_stride, int32_t max_blocks_per_seq, const int32_t* base_context_lens,
+    int32_t* context_lens, const int32_t* seq_idx, int32_t m, int32_t n_q_heads,
+    int32_t n_kv_heads, int32_t head_dim, int32_t block_size, int32_t window_blocks,
+    int64_t n_blocks, float scale, float k_scale, int32_t agg_mode, int32_t keep_tokens,
+    float* importance_out, int32_t* keep_idx, void* workspace, size_t workspace_bytes,
+    int32_t rewrite_tables, int32_t* slot_mapping, int32_t* events, void* stream) {
+  nkv::clear_error();
+  NKV_REQUIRE(events, NKV_EINVAL, "compress_step_finalize_fp8: null events");
+  return nkv::compress_step_fp8_impl(
+      q, q_row_stride, k_cache, v_cache, block_tables, bt_row_stride, max_blocks_per_seq,
+      base_context_lens, context_lens, seq_idx, m, n_q_heads, n_kv_heads, head_dim, block_size,
+      window_blocks, n_blocks, scale, k_scale, agg_mode, keep_tokens, importance_out, keep_idx,
+      workspace, workspace_bytes, stream,
+      nkv::FinArgs{block_tables, slot_mapping, events, rewrite_tables});
 }
 
 // SnapKV as called directly (the plug-in API): Q [m, Hq, window, D], contiguous K

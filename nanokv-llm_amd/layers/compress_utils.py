@@ -160,11 +160,14 @@ def compress_compact(k_cache, v_cache, block_tables, base_context_lens, context_
 
 def compress_step(q, k_cache, v_cache, block_tables, base_context_lens, context_lens, seq_idx,
                   window_blocks, keep_tokens, scale, agg="all", importance=None, keep_idx=None,
-                  workspace=None, k_scale=1.0):
+                  workspace=None, k_scale=1.0, events=None, rewrite_tables=True,
+                  slot_mapping=None):
     """compress_select + compress_compact in one call (fused on the GPU).
 
     Returns (keep_idx, importance) like compress_select; the caches and
-    context_lens are updated like compress_compact.
+    context_lens are updated like compress_compact. With ``events`` (the last
+    layer) the call also does compress_finalize's bookkeeping (events, table
+    and slot rewrite), inside the fused launch.
     """
     m = seq_idx.numel()
     NB, B, Hk, D = k_cache.shape
@@ -181,35 +184,50 @@ def compress_step(q, k_cache, v_cache, block_tables, base_context_lens, context_
     ws_bytes = select_workspace_bytes(m, Hq, Hk, window_blocks, B)
     if workspace is None:
         workspace = torch.empty(max(ws_bytes, 4), dtype=torch.uint8, device=q.device)
+    fin = []  # the bookkeeping's arguments, appended to the step's
+    if events is not None:
+        _check_finalize_args(block_tables, base_context_lens, seq_idx, events, slot_mapping)
+        fin = [int(bool(rewrite_tables)), _lib.ptr(slot_mapping), events.data_ptr()]
+    name = "nkv_compress_step" + ("_finalize" if fin else "")
     if k_cache.dtype == torch.float8_e4m3fn:  # fp8 pool (K read as code * k_scale)
-        rc = _lib.lib().nkv_compress_step_fp8(
+        name += "_fp8"
+        rc = getattr(_lib.lib(), name)(
             q.data_ptr(), q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(),
             block_tables.data_ptr(), block_tables.stride(0), block_tables.size(1),
             base_context_lens.data_ptr(), context_lens.data_ptr(), seq_idx.data_ptr(), m, Hq, Hk,
             D, B, window_blocks, NB, float(scale), float(k_scale), AGG_MODES[agg], keep_tokens,
             importance.data_ptr(), keep_idx.data_ptr(), workspace.data_ptr(), workspace.numel(),
-            _lib.stream_of(q))
-        _lib.check(rc, "compress_step_fp8")
+            *fin, _lib.stream_of(q))
+        _lib.check(rc, name[4:])
         return keep_idx, importance
-    fn = _lib.lib().nkv_compress_step_f16 if q.dtype == torch.float16 else \
-        _lib.lib().nkv_compress_step
-    rc = fn(
+    if q.dtype == torch.float16:
+        name += "_f16"
+    rc = getattr(_lib.lib(), name)(
         q.data_ptr(), q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(), block_tables.data_ptr(),
         block_tables.stride(0), block_tables.size(1), base_context_lens.data_ptr(),
         context_lens.data_ptr(), seq_idx.data_ptr(), m, Hq, Hk, D, B, window_blocks, NB,
         float(scale), AGG_MODES[agg], keep_tokens, importance.data_ptr(), keep_idx.data_ptr(),
-        workspace.data_ptr(), workspace.numel(), _lib.stream_of(q))
-    _lib.check(rc, "compress_step")
+        workspace.data_ptr(), workspace.numel(), *fin, _lib.stream_of(q))
+    _lib.check(rc, name[4:])
     return keep_idx, importance
 
 
-def compress_finalize(block_tables, base_context_lens, seq_idx, keep_tokens, block_size,
-                      window_blocks, events, rewrite_tables=True, slot_mapping=None):
+def _check_finalize_args(block_tables, base_context_lens, seq_idx, events, slot_mapping):
     _lib.require_device(block_tables.device, base_context_lens=base_context_lens,
                         seq_idx=seq_idx, events=events, slot_mapping=slot_mapping)
     _lib.need(all(t.dtype == torch.int32 for t in (block_tables, base_context_lens, seq_idx,
                                                    events)),
               "compress_finalize: tables, lengths, seq_idx and events must be int32")
+    _lib.need(slot_mapping is None or slot_mapping.dtype == torch.int32,
+              "compress_finalize: slot_mapping must be int32")
+    _lib.need(events.is_contiguous() and events.numel() >= seq_idx.numel() *
+              (4 + block_tables.size(1)),
+              "compress_finalize: events needs [m, 4 + max_blocks] int32 entries")
+
+
+def compress_finalize(block_tables, base_context_lens, seq_idx, keep_tokens, block_size,
+                      window_blocks, events, rewrite_tables=True, slot_mapping=None):
+    _check_finalize_args(block_tables, base_context_lens, seq_idx, events, slot_mapping)
     rc = _lib.lib().nkv_compress_finalize(
         block_tables.data_ptr(), block_tables.stride(0), block_tables.size(1),
         base_context_lens.data_ptr(), seq_idx.data_ptr(), seq_idx.numel(), keep_tokens,
@@ -289,14 +307,14 @@ def MyCompressCompact(q_current: torch.Tensor, k_cache: torch.Tensor, v_cache: t
     ws_bytes = select_workspace_bytes(m, Hq, Hk, window_blocks, B)
     buf = _buffers(context, selected, device, m, n_sets, window_tokens - 1, keep_tokens,
                    ws_bytes, 4 + context.block_tables.size(1))
+    last = layer_id + 1 >= num_layers  # the last layer also does the bookkeeping (:266-288)
     compress_step(q_current, k_cache, v_cache, context.block_tables, base, context.context_lens,
                   buf.seq_idx, window_blocks, keep_tokens, D ** -0.5, agg,
                   importance=buf.importance, keep_idx=buf.keep_idx, workspace=buf.workspace,
-                  k_scale=k_scale)
-    if layer_id + 1 >= num_layers:
-        compress_finalize(context.block_tables, base, buf.seq_idx, keep_tokens, B, window_blocks,
-                          buf.events, rewrite_tables=rewrite_tables,
-                          slot_mapping=context.slot_mapping if rewrite_tables else None)
+                  k_scale=k_scale, events=buf.events if last else None,
+                  rewrite_tables=rewrite_tables,
+                  slot_mapping=context.slot_mapping if rewrite_tables else None)
+    if last:
         if device_sel is not None:  # read by the host after the step, no sync here
             context.compression_events_device = buf.events
         else:
