@@ -331,24 +331,31 @@ def run_compress(args, dev):
                                                      cw["context_lens"], cw["seq_idx"], agg, dev)
            for agg in ("group", "all")}
 
-    def timed(fn, reps):
-        times = []
+    def timed_many(fns, reps):
+        """Median µs of each variant; the variants' reps interleave (order reversed every
+        other round) so that a drift of the clock over the run weighs on all alike."""
+        times = {n: [] for n in fns}
+        order = list(fns)
         for i in range(3 + reps):
-            btg.copy_(bt0)  # the finalize's table rewrite is undone outside the timed region
-            # evict the window from the 256 MB last-level cache by READING 512 MiB: the
-            # cache is left holding clean lines, as after the decode kernels that run
-            # between compression steps (a fill would leave 256 MB of dirty lines
-            # whose write-back would overlap the step)
-            flush.sum()
-            a = torch.cuda.Event(enable_timing=True)
-            b = torch.cuda.Event(enable_timing=True)
-            a.record(stream)
-            fn()
-            b.record(stream)
-            torch.cuda.synchronize()
-            if i >= 3:
-                times.append(a.elapsed_time(b) * 1000.0)
-        return statistics.median(times)
+            for n in (order if i % 2 == 0 else order[::-1]):
+                btg.copy_(bt0)  # the finalize's table rewrite is undone outside the timed region
+                # evict the window from the 256 MB last-level cache by READING 512 MiB: the
+                # cache is left holding clean lines, as after the decode kernels that run
+                # between compression steps (a fill would leave 256 MB of dirty lines
+                # whose write-back would overlap the step)
+                flush.sum()
+                a = torch.cuda.Event(enable_timing=True)
+                b = torch.cuda.Event(enable_timing=True)
+                a.record(stream)
+                fns[n]()
+                b.record(stream)
+                torch.cuda.synchronize()
+                if i >= 3:
+                    times[n].append(a.elapsed_time(b) * 1000.0)
+        return {n: statistics.median(t) for n, t in times.items()}
+
+    def timed(fn, reps):
+        return timed_many({"": fn}, reps)[""]
 
     for agg in ("group", "all"):
         n_sets = 1 if agg == "all" else Hk
@@ -369,15 +376,18 @@ def run_compress(args, dev):
             cu.compress_finalize(btg, base, sel, 513, 256, 4, events, rewrite_tables=True,
                                  slot_mapping=slot_map)
 
-        med = timed(full_step, args.compress_reps)
+        variants = {"full": full_step, "step": step}
+        if agg == "group":
+            variants["two"] = two_launches
+        t = timed_many(variants, args.compress_reps)
+        med = t["full"]
         key = "compress_step_us" if agg == "group" else "compress_step_all_us"
         res[key] = round(med, 2)
         res[key.replace("_us", "_gbs")] = round(nbytes / (med * 1e-6) / 1e9, 1)
         key2 = "compress_select_compact_us" if agg == "group" else "compress_select_compact_all_us"
-        res[key2] = round(timed(step, args.compress_reps), 2)
+        res[key2] = round(t["step"], 2)
         if agg == "group":
-            res["compress_step_two_launch_us"] = round(timed(two_launches, args.compress_reps),
-                                                       2)
+            res["compress_step_two_launch_us"] = round(t["two"], 2)
     # the same step over an fp8 (E4M3FN) copy of the pool (agg "group")
     kvc = importlib.import_module("nanokv-llm_amd.layers.kv_cache")
     kq, vq = kvc.fp8_quantize(kg), kvc.fp8_quantize(vg)
