@@ -174,8 +174,8 @@ def test_decode_and_step_metadata():
 
 @pytest.mark.parametrize("policy", ["first", "longest"])
 def test_schedule_oracle_matches_host_scheduler(policy):
-    """The schedule oracle (the device kernel's checker) and the host CompressionScheduler
-    make the same choice on random states, firing on the same steps."""
+    """The schedule oracle (what the device kernel is tested against) and the host
+    CompressionScheduler make the same choice on random states, firing on the same steps."""
     gen = torch.Generator().manual_seed(3 if policy == "first" else 4)
     sched = hooks.CompressionScheduler(_cfg(period=2, topk=5), policy=policy)
     counter = 0
