@@ -531,11 +531,20 @@ __device__ __forceinline__ void group_importance(
   bool valid = t0 < Lw;
   if (block_tables) {
     const int seq = seq_idx[j];
+    // the table row's first 128 entries (two per lane) are loaded with the length, so the
+    // wave's block id needs no round trip after it
+    const int32_t* bt_row = block_tables + (int64_t)(seq >= 0 ? seq : 0) * bt_row_stride;
+    const int32_t e0 = (seq >= 0 && lane < max_blocks) ? bt_row[lane] : -1;
+    const int32_t e1 = (seq >= 0 && lane + 64 < max_blocks) ? bt_row[lane + 64] : -1;
     const int len = seq >= 0 ? base_context_lens[seq] : 0;  // seq -1: padding entry
     const int full = len / block_size;
     int64_t pb = -1;
-    if (valid && full >= window_blocks && full <= max_blocks)
-      pb = block_tables[(int64_t)seq * bt_row_stride + full - window_blocks + t0 / block_size];
+    if (valid && full >= window_blocks && full <= max_blocks) {
+      const int e = full - window_blocks + t0 / block_size;  // wave-uniform entry
+      pb = e < 64    ? __builtin_amdgcn_readlane(e0, e)
+           : e < 128 ? __builtin_amdgcn_readlane(e1, e - 64)
+                     : bt_row[e];
+    }
     NKV_DBG(valid && seq >= 0 && full >= window_blocks && full <= max_blocks &&
                 (pb < 0 || pb >= n_blocks),
             NKV_DEBUG_BLOCK);
@@ -932,8 +941,13 @@ __global__ __launch_bounds__(kSelThreads) void compress_group_kernel(
   }
   const int Lw = window_blocks * block_size;
   const int n_cand = Lw - 1;
-  // compaction: the unit's block ids, loaded with the scoring's first loads; not
-  // compressible or inconsistent with the table width: left untouched
+  float gi[4];
+  group_importance<F8, H16>(L, q, q_row_stride, k, block_tables, bt_row_stride, max_blocks,
+                       base_context_lens, seq_idx, j, kvh, Hk, G, block_size, window_blocks,
+                       n_blocks, scale_log2, gi);
+  // compaction: the unit's block ids, loaded now (the selection hides the round trip, and
+  // the scoring's chain to its K loads stays short); not compressible or inconsistent with
+  // the table width: left untouched
   bool compact = false;
   int32_t wpb = -1;
   const int seq = block_tables ? seq_idx[j] : 0;  // no seq_idx for contiguous K
@@ -941,21 +955,6 @@ __global__ __launch_bounds__(kSelThreads) void compress_group_kernel(
   if (k_cache_w)
     compact = unit_block_load(block_tables + (int64_t)seq * bt_row_stride, len, block_size,
                               window_blocks, max_blocks, wpb);
-  float gi[4];
-  group_importance<F8, H16>(L, q, q_row_stride, k, block_tables, bt_row_stride, max_blocks,
-                       base_context_lens, seq_idx, j, kvh, Hk, G, block_size, window_blocks,
-                       n_blocks, scale_log2, gi);
-  // published by the selection's barriers; stored only now so that the scoring's loads
-  // are not held behind this one
-  if (compact) unit_block_store(L.win_pb, wpb, len, block_size, window_blocks, n_blocks);
-  uint32_t fin_old = 0;  // every wave has read its table entries (the scoring's barriers)
-  FinRow fr{};
-  if (fin.block_tables && tid < 64) {
-    if (tid == 0) fin_old = fin_arrive(j, Hk);
-    // read by every unit, used by the last to arrive: the selection hides the round trip
-    fr = fin_load(fin.block_tables + (int64_t)seq * bt_row_stride, seq, len, max_blocks,
-                  num_keep + 2, block_size, window_blocks, lane);
-  }
   const int t0 = (tid >> 6) * kSelKeysPerWave;
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
@@ -966,6 +965,18 @@ __global__ __launch_bounds__(kSelThreads) void compress_group_kernel(
   float* irow = importance_out + ((int64_t)j * Hk + kvh) * n_cand;
   for (int t = tid; t < n_cand; t += kSelThreads) irow[t] = L.imp[t];
   block_select(L, n_cand, num_keep, keep_idx + ((int64_t)j * Hk + kvh) * (num_keep + 2));
+  if (compact) {  // uniform
+    unit_block_store(L.win_pb, wpb, len, block_size, window_blocks, n_blocks);
+    __syncthreads();
+  }
+  uint32_t fin_old = 0;  // every table read of the unit has returned (the barriers before)
+  FinRow fr{};
+  if (fin.block_tables && tid < 64) {
+    if (tid == 0) fin_old = fin_arrive(j, Hk);
+    // read by every unit, used by the last to arrive: the compaction hides the round trip
+    fr = fin_load(fin.block_tables + (int64_t)seq * bt_row_stride, seq, len, max_blocks,
+                  num_keep + 2, block_size, window_blocks, lane);
+  }
   if (compact)
     compact_unit<F8>(L, k_cache_w, v_cache_w, base_context_lens, context_lens, seq_idx, j, kvh,
                      num_keep + 2, Hk, block_size, window_blocks);
