@@ -302,6 +302,67 @@ def compress_parity(q, kg, vg, bt, lens, sel, agg, dev):
             "lengths_events_tables_slots_exact": meta}
 
 
+def compress_in_graph(args, dev, flush, n_in=10):
+    """The full step inside a larger graph, as it runs in a decode step's graph (whose own
+    launch is paid once for the whole step): n_in steps captured in one graph, per step. The
+    state is the whole batch-500 decode state (every sequence's blocks in the pool); step i
+    compresses its own 20 sequences, ranks 20i .. 20i+19 by length (step 0: the 20 longest,
+    the configuration's selection), so every step reads cold windows, and has its own copy
+    of the tables (restored outside the timed region)."""
+    cw = wl_mod.compress_workload(500, 32, 8, 1500, 4096, 20, 3, dev, selected_only=False)
+    kg, vg, q = cw["k_cache"], cw["v_cache"], cw["q"].to(dev)
+    lens = cw["context_lens"].tolist()
+    order = sorted(range(len(lens)), key=lambda i: (-lens[i], i))
+    sels = [torch.tensor(sorted(order[20 * i:20 * i + 20]), dtype=torch.int32, device=dev)
+            for i in range(n_in)]
+    bt0 = cw["block_tables"].to(dev)
+    bts = [bt0.clone() for _ in range(n_in)]
+    base = cw["context_lens"].to(dev)
+    ctx = base.clone()
+    Hq, Hk = q.size(1), kg.size(2)
+    ws = torch.empty(cu.select_workspace_bytes(20, Hq, Hk, 4, 256), dtype=torch.uint8,
+                     device=dev)
+    events = torch.empty(20, 4 + bt0.size(1), dtype=torch.int32, device=dev)
+    slot_map = torch.zeros(base.numel(), dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream()
+    res = {}
+    for agg in ("group", "all"):
+        n_sets = 1 if agg == "all" else Hk
+        imp = torch.empty(20, n_sets, 1023, dtype=torch.float32, device=dev)
+        keep = torch.empty(20, n_sets, 513, dtype=torch.int32, device=dev)
+
+        def steps():
+            for sel, btx in zip(sels, bts):
+                cu.compress_step(q, kg, vg, btx, base, ctx, sel, 4, 513, 128 ** -0.5, agg,
+                                 importance=imp, keep_idx=keep, workspace=ws, events=events,
+                                 rewrite_tables=True, slot_mapping=slot_map)
+
+        steps()  # every kernel loaded before the capture
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            steps()
+        times = []
+        for i in range(3 + args.compress_reps):
+            for btx in bts:
+                btx.copy_(bt0)
+            flush.sum()
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            graph.replay()
+            b.record(stream)
+            torch.cuda.synchronize()
+            if i >= 3:
+                times.append(a.elapsed_time(b) * 1000.0 / n_in)
+        del graph
+        key = "compress_step_in_graph_us" if agg == "group" else "compress_step_all_in_graph_us"
+        res[key] = round(statistics.median(times), 2)
+    del kg, vg, cw
+    torch.cuda.empty_cache()
+    return res
+
+
 def run_compress(args, dev):
     """One layer's compression step at batch 500 as the configuration states it: scoring,
     top-k and compaction of the 20 longest sequences (window 4 blocks, keep 513), and the
@@ -398,6 +459,7 @@ def run_compress(args, dev):
         keep_idx=keep, workspace=ws, events=events, rewrite_tables=True,
         slot_mapping=slot_map), args.compress_reps), 2)
     del kq, vq
+    res.update(compress_in_graph(args, dev, flush))
     if not args.no_cpu_baseline:
         res["compress_cpu_baseline"] = cpu_compress_baseline()
     res.update({"compress_bytes": nbytes, "compress_sequences": m,
@@ -408,7 +470,10 @@ def run_compress(args, dev):
                                    "compress_select_compact_*: without the finalize; "
                                    "compress_step_two_launch_us: the finalize as its own "
                                    "launch; compress_step_fp8_us: the full step, agg group, "
-                                   "over an fp8 pool"})
+                                   "over an fp8 pool; *_in_graph_us: per step, ten full "
+                                   "steps of the whole batch-500 state in one graph, each "
+                                   "on its own 20 sequences (the 20 longest, then the next "
+                                   "ranks; cold windows)"})
     return res
 
 
