@@ -980,7 +980,8 @@ __global__ __launch_bounds__(kSelThreads) void compress_group_kernel(
   if (compact)
     compact_unit<F8>(L, k_cache_w, v_cache_w, base_context_lens, context_lens, seq_idx, j, kvh,
                      num_keep + 2, Hk, block_size, window_blocks);
-  if (fin.block_tables && tid < 64 && __builtin_amdgcn_readfirstlane(fin_old) == (uint32_t)(Hk - 1))
+  if (fin.block_tables && tid < 64 &&
+      (uint32_t)__builtin_amdgcn_readfirstlane(fin_old) == (uint32_t)(Hk - 1))
     fin_store(fr, fin.block_tables + (int64_t)fr.seq * bt_row_stride,
               fin.events + (int64_t)j * (4 + max_blocks), max_blocks, block_size,
               fin.rewrite_tables, fin.slot_mapping, lane);
@@ -1072,7 +1073,7 @@ __global__ __launch_bounds__(kSelThreads) void compress_sum_kernel(
     compact_unit<F8>(L, k_cache_w, v_cache_w, base_context_lens, context_lens, seq_idx, j, kvh,
                      num_keep + 2, Hk, block_size, window_blocks);
   if (fin.block_tables && tid < 64 &&
-      __builtin_amdgcn_readfirstlane(fin_old) == (uint32_t)(n_units_per_seq - 1))
+      (uint32_t)__builtin_amdgcn_readfirstlane(fin_old) == (uint32_t)(n_units_per_seq - 1))
     fin_store(fr, fin.block_tables + (int64_t)fr.seq * bt_row_stride,
               fin.events + (int64_t)j * (4 + max_blocks), max_blocks, block_size,
               fin.rewrite_tables, fin.slot_mapping, tid);
