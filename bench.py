@@ -1084,7 +1084,7 @@ def main():
             "unit": "GB/s",
             "frac": round(split_gbs / HBM_PEAK_GBS, 4),
             "traffic": measured_traffic("paged_decode_qwen3_8b_bs64.txt",
-                                        "paged_decode_split_kernel<false, 2, 128>"),
+                                        "paged_decode_split_kernel<false, 2, 128, false>"),
             "avg_us": round(r["split_ms"] * 1e3, 2),
             "algorithmic_bytes": r["split_bytes"],
         },
