@@ -39,6 +39,9 @@ cu = importlib.import_module("nanokv-llm_amd.layers.compress_utils")
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 METRIC = "paged decode-attn GB/s (% HBM peak) @Qwen3-8B; KV-compress step µs @bs500"
+# the dominant kernel of the decode workload (the roofline line), as rocprofv3 names it
+DECODE_KERNEL = "paged_decode_split_kernel<false, 2, 128, false>"
+DECODE_PROFILE = "paged_decode_qwen3_8b_bs64.txt"
 
 
 def measured_traffic(profile, kernel):
@@ -1077,14 +1080,13 @@ def main():
         "store_us": round(r["store_ms"] * 1e3, 2),
         "parity_max_abs_err": r["parity_max_abs_err"],
         "roofline": {
-            "kernel": "paged_decode_split_kernel<false, 2, 128, false>",
+            "kernel": DECODE_KERNEL,
             "bound": "hbm",
             "achieved": round(split_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(split_gbs / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic("paged_decode_qwen3_8b_bs64.txt",
-                                        "paged_decode_split_kernel<false, 2, 128, false>"),
+            "traffic": measured_traffic(DECODE_PROFILE, DECODE_KERNEL),
             "avg_us": round(r["split_ms"] * 1e3, 2),
             "algorithmic_bytes": r["split_bytes"],
         },
