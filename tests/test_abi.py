@@ -188,3 +188,17 @@ def test_debug_library_matches_and_release_reports_no_debug_checks():
     dbg = ctypes.CDLL(L.DEBUG_LIB_PATH)
     dbg.nkv_debug_flags.argtypes = [ctypes.c_void_p, ctypes.c_int32]
     assert dbg.nkv_debug_flags(None, 0) == EINVAL  # checked before the device is touched
+
+
+def test_step_finalize_needs_events():
+    """The last layer's fused step refuses a missing events buffer before any launch."""
+    from importlib import import_module
+    lib = import_module("nanokv-llm_amd._lib").lib()
+    args = [None, 0, None, None, None, 0, 1, None, None, None, 1, 32, 8, 128, 256, 4, 1, 1.0,
+            1, 513, None, None, None, 0, 1, None, None, None]
+    assert lib.nkv_compress_step_finalize(*args) == -1
+    assert b"events" in lib.nkv_last_error()
+    assert lib.nkv_compress_step_finalize_f16(*args) == -1
+    fp8_args = args[:18] + [1.0] + args[18:]  # k_scale after scale
+    assert lib.nkv_compress_step_finalize_fp8(*fp8_args) == -1
+    assert b"events" in lib.nkv_last_error()
