@@ -164,9 +164,10 @@ def test_fused_finalize_general_path(nkv, dev):
 
 
 def test_fused_finalize_consecutive_calls(nkv, dev):
-    """Three calls in a row with other sizes: 40 sequences x 8 KV heads (320 workgroups,
-    more than the CUs), then 7 x 4, then 12 x 8; each equals the two launches."""
-    for seed, bs, Hk, topk in ((26, 80, 8, 40), (27, 20, 4, 7), (28, 30, 8, 12)):
+    """Calls in a row with other sizes: 40 sequences x 8 KV heads (320 workgroups, more
+    than the CUs), then 7 x 4, 3 x 1 (one unit per sequence: every arrival is the last),
+    then 12 x 8; each equals the two launches."""
+    for seed, bs, Hk, topk in ((26, 80, 8, 40), (27, 20, 4, 7), (29, 8, 1, 3), (28, 30, 8, 12)):
         q, kc, vc, bt, lens, sel = _state(seed, bs=bs, Hq=4 * Hk, Hk=Hk, topk=topk)
-        _compare(dev, q, kc, vc, bt, lens, sel, "group" if Hk == 8 else "all", 2 * 256 + 1,
+        _compare(dev, q, kc, vc, bt, lens, sel, "group" if Hk in (8, 1) else "all", 2 * 256 + 1,
                  256)
