@@ -168,12 +168,18 @@ def test_compress_step_sweep(nkv, dev, case, D):
     if case % 3 == 0:
         padded.insert(rng.randrange(0, len(padded) + 1), -1)
     print(f"compress case {case}: D={D} B={B} W={W} keep={keep} Hk={Hk} G={G} agg={agg} "
-          f"sel={padded}", flush=True)
+          f"sel={padded} last_layer={case % 2 == 1}", flush=True)
     base = torch.tensor(lens, dtype=torch.int32)
     kg, vg, ctx = kc.to(dev), vc.to(dev), base.clone().to(dev)
     seq_idx = torch.tensor(padded, dtype=torch.int32, device=dev)
-    keep_idx, imp = cu.compress_step(q.to(dev), kg, vg, bt.to(dev), base.to(dev), ctx, seq_idx, W,
-                                     keep, D ** -0.5, agg)
+    # odd cases: the last layer's step, with the finalize's events, table and slot rewrite
+    last = case % 2 == 1
+    btg = bt.to(dev)
+    events = torch.full((len(padded), 4 + width), 77, dtype=torch.int32, device=dev)
+    slot_map = torch.arange(bs, dtype=torch.int32, device=dev) * 5 + 3
+    fin = dict(events=events, rewrite_tables=True, slot_mapping=slot_map) if last else {}
+    keep_idx, imp = cu.compress_step(q.to(dev), kg, vg, btg, base.to(dev), ctx, seq_idx, W,
+                                     keep, D ** -0.5, agg, **fin)
     torch.cuda.synchronize()
     real = [i for i, s in enumerate(padded) if s >= 0]
     imp, keep_idx = imp.cpu()[real], keep_idx.cpu()[real]
@@ -184,7 +190,16 @@ def test_compress_step_sweep(nkv, dev, case, D):
     assert torch.allclose(imp, ref_imp, rtol=1e-4, atol=1e-7)
     assert torch.equal(keep_idx[..., 1:-1].long(), select_topk_ref(imp, keep - 2))
     ctx_ref = base.clone()
-    compress_compact_ref(None, kc, vc, bt, base, ctx_ref, sel, B, W, keep_blocks, extra, 0, 2,
-                         keep_idx=keep_idx.long())
+    _, _, ev_ref = compress_compact_ref(None, kc, vc, bt, base, ctx_ref, sel, B, W, keep_blocks,
+                                        extra, 0, 1 if last else 2, keep_idx=keep_idx.long())
     assert torch.equal(kg.cpu(), kc) and torch.equal(vg.cpu(), vc)
     assert torch.equal(ctx.cpu(), ctx_ref)
+    if last:  # events (padding rows skipped), freed table entries -1, the next token's slot
+        assert cu.events_to_dicts(events, 0) == ev_ref
+        bt_exp = bt.clone()
+        slot_exp = torch.arange(bs, dtype=torch.int32) * 5 + 3
+        for ev in ev_ref:
+            i, n = ev["batch_index"], ev["new_context_len"]
+            bt_exp[i, ev["keep_blocks"]:] = -1
+            slot_exp[i] = -1 if n % B == 0 else int(bt[i, n // B]) * B + n % B
+        assert torch.equal(btg.cpu(), bt_exp) and torch.equal(slot_map.cpu(), slot_exp)
