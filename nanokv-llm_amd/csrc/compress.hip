@@ -24,7 +24,10 @@
 //    any destination row is written (s_waitcnt 0 + barrier), which gives the
 //    reference's two-phase index_select().clone() / index_copy_ semantics
 //    without a staging buffer, at one read + one write per moved byte.
-//  * finalize (last layer): events, freed blocks, block-table and slot rewrite.
+//  * finalize (last layer): events, freed blocks, block-table and slot rewrite;
+//    its own one-wave-per-sequence launch, or, on the fused path, done inside
+//    the step's launch by the last (sequence, KV head) workgroup of each
+//    sequence to arrive (self-resetting arrival counters, no fences).
 #include "nkv_common.h"
 
 namespace nkv {
