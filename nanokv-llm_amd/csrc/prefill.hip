@@ -6,14 +6,14 @@
 // j of a sequence with Lq queries and Lk keys sees keys 0 .. Lk-Lq+j).
 //
 // MI355X design (MFMA-bound):
-//  * Workgroup = (sequence, tile of floor(128/g) queries, KV head) x 4 waves.
-//    The tile's 128 "rows" are its queries for all g query heads of the KV
+//  * Workgroup = (sequence, tile of floor(R/g) queries, KV head) x 4 waves.
+//    The tile's R "rows" are its queries for all g query heads of the KV
 //    head, query-major (row r = query r/g, head r%g; rows past the tile's
 //    queries x g are computed and dropped), so one K/V tile in LDS serves g
-//    heads (GQA sharing) for any g <= 16. Wave w owns two 16-row groups.
-//    head_dim D is 64, 128 or 256 (a template parameter); at 256 a wave owns
-//    one 16-row group (64-row tiles) and the 128 KiB ring leaves one
-//    workgroup per CU.
+//    heads (GQA sharing). Wave w owns three 16-row groups at head_dim 128
+//    (R = 192), two at 64 and in the fp8 instance (R = 128), one at 256
+//    (R = 64, and the 128 KiB ring leaves one workgroup per CU). head_dim D
+//    is 64, 128 or 256 (a template parameter).
 //  * Keys advance in 64-key steps. Each step's K and V tiles (2 x 16 KiB at
 //    D = 128) go from HBM straight into LDS with gfx950's 16-byte buffer-load-to-LDS
 //    (no staging registers, no LDS write instructions) through a ring of
@@ -49,11 +49,18 @@ constexpr int kStep = 64;                 // keys per step
 constexpr int kStages = 2;                // LDS ring depth (steps)
 constexpr int kBufferFlags = 0x00020000;  // raw buffer descriptor word 3 for gfx950
 constexpr bool prefill_dim_ok(int D) { return D == 64 || D == 128 || D == 256; }
-// 16-row groups per wave: two (32 rows), one at head_dim 256 (its O^T and Q^T registers
+// 16-row groups per wave: three at head_dim 128 (each K and V^T read from LDS serves three
+// MFMAs; bit-identical to two, at par to 2% faster), two at 64 and in the fp8 instance (whose
+// staging registers leave no room for a third), one at 256 (its O^T and Q^T registers
 // would not fit two waves per SIMD otherwise)
-constexpr int prefill_row_groups(int D) { return D == 256 ? 1 : 2; }
+constexpr int prefill_row_groups(int D, bool F8) {
+  return D == 256 ? 1 : (D == 128 && !F8 ? 3 : 2);
+}
 // rows (query, head pairs) of a workgroup's tile: 4 waves
-constexpr int prefill_tile_rows(int D) { return 64 * prefill_row_groups(D); }
+constexpr int prefill_tile_rows(int D, bool F8) { return 64 * prefill_row_groups(D, F8); }
+// largest GQA group, the same for every instance of a head_dim: each tile holds at least
+// one query for all g heads of its KV head
+constexpr int prefill_max_group(int D) { return D == 256 ? 64 : 128; }
 // XOR applied to the 16-byte chunk index of LDS row r (even: chunk pairs stay together).
 // Keeps the K row reads and the V transpose reads free of bank conflicts: 2*(r & 7) for
 // 256- and 512-byte rows, 2*((r >> 1) & 3) for 128-byte rows (two rows per bank line).
@@ -105,7 +112,7 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void prefill_varlen_kernel(
   constexpr int kEl = F8 ? 1 : 2;          // bytes per cache element
   constexpr int kRB = D * 2;               // bytes of a staged (bf16) K or V row
   constexpr int kNC = D / 8;               // 16-byte chunks per staged row
-  constexpr int kRG = prefill_row_groups(D);
+  constexpr int kRG = prefill_row_groups(D, F8);
   constexpr int kTileB = kStep * kRB;      // bytes of one K or V tile
   constexpr int kStageB = 2 * kTileB;      // K tile then V tile
   constexpr int kKs = D / 32;              // k-steps of S^T
@@ -115,7 +122,7 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void prefill_varlen_kernel(
   constexpr int kLpr8 = D / 16;            // F8: lanes per row (16 codes each)
   constexpr int kRpl8 = 64 / kLpr8;        // F8: rows per load
   constexpr int kNl8 = 16 / kRpl8;         // F8: loads per wave per tile
-  const int QT = prefill_tile_rows(D) / G;  // queries per tile
+  const int QT = prefill_tile_rows(D, F8) / G;  // queries per tile
   __shared__ __attribute__((aligned(1024))) char ring[kStages * kStageB];
 
   const int tid = threadIdx.x;
@@ -527,8 +534,8 @@ static int prefill_launch(const void* q, int64_t q_row_stride, const void* k_cac
   NKV_REQUIRE(n_q_heads % n_kv_heads == 0, NKV_EINVAL, "%s: Hq %% Hk != 0", what);
   const int g = n_q_heads / n_kv_heads;
   // a tile holds at least one query for all g heads of its KV head
-  NKV_REQUIRE(g <= prefill_tile_rows(head_dim), NKV_EUNSUPPORTED, "%s: GQA group %d above %d",
-              what, g, prefill_tile_rows(head_dim));
+  NKV_REQUIRE(g <= prefill_max_group(head_dim), NKV_EUNSUPPORTED, "%s: GQA group %d above %d",
+              what, g, prefill_max_group(head_dim));
   NKV_REQUIRE(q && k_cache && v_cache && cu_seqlens_q && cu_seqlens_k && out, NKV_EINVAL,
               "%s: null pointer", what);
   NKV_REQUIRE(aligned16(q) && aligned16(k_cache) && aligned16(v_cache) && aligned16(out),
@@ -559,7 +566,7 @@ static int prefill_launch(const void* q, int64_t q_row_stride, const void* k_cac
   // paged: valid block ids are [0, n_rows / block_size); contiguous: valid rows
   const int32_t n_limit = (int32_t)std::min<int64_t>(block_tables ? n_rows / block_size : n_rows,
                                                      INT32_MAX);
-  const int qt = prefill_tile_rows(head_dim) / g;
+  const int qt = prefill_tile_rows(head_dim, F8) / g;
   const int n_tiles = (max_seqlen_q + qt - 1) / qt;
   const int64_t grid = (int64_t)n_seqs * n_tiles * n_kv_heads;
   NKV_REQUIRE(grid < (1ll << 31), NKV_EUNSUPPORTED, "%s: grid too large", what);

@@ -285,7 +285,7 @@ class Attention(nn.Module):
         _lib.need(num_kv_heads > 0 and num_heads % num_kv_heads == 0,
                   f"Attention: num_heads {num_heads} is not a multiple of num_kv_heads "
                   f"{num_kv_heads}")
-        max_group = 64 if head_dim == 256 else 128  # a prefill tile's query x head rows
+        max_group = 64 if head_dim == 256 else 128  # prefill: every tile holds a query per head
         _lib.need(num_heads // num_kv_heads <= max_group,
                   f"Attention: GQA group {num_heads // num_kv_heads} above {max_group}")
         self.num_heads = num_heads

@@ -115,7 +115,7 @@ def _cstep(f16=False, **kw):
 
 CASES = [
     (_prefill(d=96), EUNSUPPORTED, b"head_dim"),
-    (_prefill(hq=129, hk=1), EUNSUPPORTED, b"GQA group"),  # a 128-row tile holds one query
+    (_prefill(hq=129, hk=1), EUNSUPPORTED, b"GQA group"),  # at most 128 (the fp8 tile's rows)
     (_prefill(hq=65, hk=1, d=256, qrs=65 * 256, ors=65 * 256), EUNSUPPORTED, b"GQA group"),
     (_prefill(f16=True, d=96), EUNSUPPORTED, b"head_dim"),
     (_prefill(q=P + 2), EINVAL, b"aligned"),
