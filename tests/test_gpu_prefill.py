@@ -87,6 +87,47 @@ def test_prefill_edge_lengths(nkv, dev):
     assert torch.equal(o[0], v[0].repeat_interleave(Hq // Hk, dim=0))
 
 
+@pytest.mark.parametrize("Hq,Hk,fp8", [(8, 8, False), (32, 8, False), (64, 8, False),
+                                       (32, 8, True)])
+def test_prefill_tile_boundaries(nkv, dev, Hq, Hk, fp8):
+    """Query counts at and around the tile sizes of the instance: floor(192/g) queries a tile
+    at head_dim 128 (192, 48 and 24 at g = 1, 4, 8) and floor(128/g) over an fp8 pool (32 at
+    g = 4), each chunk after its own paged prefix, so the causal diagonal meets the 64-key
+    steps at different offsets."""
+    from oracle import fp8_ref
+    D, B = 128, 64
+    g = torch.Generator().manual_seed(31 + Hq + int(fp8))
+    Lq = [23, 24, 25, 31, 32, 33, 47, 48, 49, 95, 96, 97, 191, 192, 193]
+    pre = [0, 64, 5, 100, 0, 31, 0, 200, 1, 0, 7, 63, 0, 128, 9]
+    Lk = [a + b for a, b in zip(Lq, pre)]
+    cu_q = torch.tensor([0] + torch.tensor(Lq).cumsum(0).tolist(), dtype=torch.int32)
+    cu_k = torch.tensor([0] + torch.tensor(Lk).cumsum(0).tolist(), dtype=torch.int32)
+    width = max((k + B - 1) // B for k in Lk)
+    n_blocks = sum((k + B - 1) // B for k in Lk) + 2
+    perm = torch.randperm(n_blocks, generator=g).tolist()
+    rows = []
+    for k in Lk:
+        nb = (k + B - 1) // B
+        rows.append([perm.pop() for _ in range(nb)] + [-1] * (width - nb))
+    bt = torch.tensor(rows, dtype=torch.int32)
+    q = torch.randn(int(cu_q[-1]), Hq, D, generator=g).to(torch.bfloat16)
+    kc = torch.randn(n_blocks, B, Hk, D, generator=g).to(torch.bfloat16)
+    vc = torch.randn(n_blocks, B, Hk, D, generator=g).to(torch.bfloat16)
+    print(f"prefill tile boundaries Hq={Hq} Hk={Hk} fp8={fp8}", flush=True)
+    if fp8:
+        kq, vq = fp8_ref.fp8_quantize_ref(kc, 1.0), fp8_ref.fp8_quantize_ref(vc, 1.0)
+        kg = kq.to(dev).view(torch.float8_e4m3fn)
+        vg = vq.to(dev).view(torch.float8_e4m3fn)
+        kc = kq.view(torch.float8_e4m3fn).float()
+        vc = vq.view(torch.float8_e4m3fn).float()
+    else:
+        kg, vg = kc.to(dev), vc.to(dev)
+    out = nkv.varlen_prefill(q.to(dev), kg, vg, cu_q.to(dev), cu_k.to(dev), max(Lq),
+                             D ** -0.5, block_tables=bt.to(dev))
+    ref = varlen_prefill_ref(q.float(), kc, vc, cu_q, cu_k, D ** -0.5, block_tables=bt)
+    assert _err(out, ref) <= TOL
+
+
 def test_prefill_strided_q_and_out(nkv, dev):
     """q is a view into a fused qkv buffer and out a view into a wider buffer."""
     wl = wl_mod.prefill_workload(2, 32, 8, 100, 400, seed=15)
